@@ -1,0 +1,198 @@
+"""Benchmark: DSINE AngMF propagate on one MI355X.
+
+A step is one pass of the hot path over one batch: one angmf_propagate call
+(workload 2: B=1, 256x256, k=5, fp32) through the C ABI, inputs resident in
+HBM.  To keep the 256 MB Infinity Cache from serving the inputs, each step
+reads a different one of `--sets` input copies (together > 512 MB); the warm
+number (same inputs every step) is reported beside it.
+
+Prints one JSON line (rank 0):
+  value       Mpixel/s over the timed region (host clock, K steps)
+  roofline    HBM roofline of the kernel: algorithmic bytes per launch /
+              average launch duration from HIP events around each launch
+  cpu_baseline  the CPU oracle (double-precision restatement of the
+              reference's CPU twin), one thread, on a bounded sample
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBPS = 8000.0
+
+
+def cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "unknown"
+
+
+def cpu_baseline(w, inp, seconds: float, nthreads: int = 1):
+    """Time the oracle on whole images of the workload until `seconds` of
+    CPU work; returns (Mpixel/s, passes)."""
+    import oracle
+    passes = 0
+    t0 = time.perf_counter()
+    while True:
+        oracle.angmf_propagate(inp["pred_norm"], inp["prob"], inp["xy"], inp["angle"],
+                               inp["ray"], inp["intrinsics"], w.H, w.W, w.k,
+                               nthreads=nthreads)
+        passes += 1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    return passes * w.B * w.HW * w.calls / el / 1e6, passes, el
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--workload", type=int, default=2)
+    ap.add_argument("--sets", type=int, default=0, help="rotating input sets (0 = auto, > 512 MB)")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--no-cpu", action="store_true")
+    args = ap.parse_args()
+
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+              "the op shards by frames or row bands with no collective on the path, "
+              "so run --gpus 1", file=sys.stderr)
+        return 2
+
+    import torch
+    from brovisionml_amd import _lib, workloads as wl
+
+    if not torch.cuda.is_available():
+        print("bench.py: no HIP device", file=sys.stderr)
+        return 1
+    dev = torch.device("cuda:0")
+    _lib.load()
+
+    w = wl.WORKLOADS[args.workload]
+    inp = wl.make_inputs(w)
+    fu, cu, fv, cv = inp["intrinsics"]
+    B, H, W, k = w.B, w.H, w.W, w.k
+    bytes_per_call = w.algorithmic_bytes(shared_ray=True) // w.calls
+    set_bytes = bytes_per_call
+    nsets = args.sets or max(2, int(np.ceil(512e6 / set_bytes)))
+
+    def dev_set():
+        return {key: torch.from_numpy(np.ascontiguousarray(inp[key])).to(dev)
+                for key in ("pred_norm", "prob", "xy", "angle", "ray")}
+
+    base = dev_set()
+    sets = [base] + [{key: t.clone() for key, t in base.items()} for _ in range(nsets - 1)]
+    outs = [torch.empty_like(s["pred_norm"]) for s in sets]
+    stream = torch.cuda.current_stream(dev)
+    sptr = stream.cuda_stream
+
+    def launch(i: int) -> None:
+        s = sets[i]
+        pn = s["pred_norm"]
+        for c in range(w.calls):
+            dst = outs[i]
+            st = _lib.angmf_propagate_f32(
+                pn.data_ptr(), s["prob"].data_ptr(), s["xy"].data_ptr(), s["angle"].data_ptr(),
+                s["ray"].data_ptr(), fu, cu, fv, cv, B, H, W, k, 0, dst.data_ptr(),
+                _lib.DEFAULT, sptr)
+            if st != 0:
+                raise RuntimeError(f"angmf_propagate_f32 failed: {st} {_lib.last_error()}")
+            pn = dst
+
+    def timed(rotate: bool, steps: int):
+        starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+        ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for i in range(steps):
+            starts[i].record(stream)
+            launch(i % nsets if rotate else 0)
+            ends[i].record(stream)
+        torch.cuda.synchronize()
+        wall = time.perf_counter() - t0
+        ev = [s.elapsed_time(e) for s, e in zip(starts, ends)]
+        return wall, float(np.mean(ev)) / w.calls, float(np.median(ev)) / w.calls
+
+    for i in range(args.warmup):
+        launch(i % nsets)
+    torch.cuda.synchronize()
+
+    wall, ev_mean_ms, ev_med_ms = timed(True, args.steps)
+    for i in range(args.warmup):
+        launch(0)
+    wall_w, ev_mean_w, ev_med_w = timed(False, args.steps)
+
+    ms_per_step = wall * 1e3 / args.steps
+    mpix = B * H * W * w.calls * args.steps / wall / 1e6
+    achieved = bytes_per_call / (ev_mean_ms * 1e-3) / 1e9
+    achieved_w = bytes_per_call / (ev_mean_w * 1e-3) / 1e9
+
+    line = {
+        "metric": "Mpixel/s (+ achieved HBM GB/s, % of peak), DSINE propagation 256x256 k=5 fp32",
+        "value": round(mpix, 2),
+        "unit": "Mpixel/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {
+            "workload": w.name, "B": B, "H": H, "W": W, "k": k, "calls_per_step": w.calls,
+            "ray": "shared", "inputs": f"{nsets} rotating HBM-resident copies "
+            f"({nsets * set_bytes / 1e6:.0f} MB > 256 MB Infinity Cache)",
+        },
+        "roofline": {
+            "bound": "hbm",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBPS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBPS, 4),
+            "traffic": None,
+            "kernel": f"angmf_f32_kernel<{k}>",
+            "bytes_per_launch": bytes_per_call,
+            "launch_us_mean": round(ev_mean_ms * 1e3, 3),
+            "launch_us_median": round(ev_med_ms * 1e3, 3),
+        },
+        "warm": {
+            "value": round(B * H * W * w.calls * args.steps / wall_w / 1e6, 2),
+            "launch_us_mean": round(ev_mean_w * 1e3, 3),
+            "achieved_gbps": round(achieved_w, 1),
+        },
+        "gpu": torch.cuda.get_device_name(dev),
+    }
+
+    if not args.no_cpu:
+        v1, passes, el = cpu_baseline(w, inp, args.cpu_seconds, 1)
+        line["cpu_baseline"] = {
+            "value": round(v1, 4), "unit": "Mpixel/s", "cores": 1, "kind": "port",
+            "sample": f"{passes} passes over the {w.name} input ({H}x{W}, k={k}), "
+                      f"{el:.1f} s, oracle restatement of src/dsine_ops.cpp in double",
+            "cpu": cpu_model(),
+            "host_threads": os.cpu_count(),
+        }
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -1,0 +1,78 @@
+"""ctypes binding of the C ABI declared in include/bvml_dsine.h.
+
+The library is the in-tree build product brovisionml_amd/lib/libbvml_dsine.so.
+There is no fallback: if it is missing, every entry point raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+from .build import LIB
+
+# Status codes (include/bvml_dsine.h)
+OK = 0
+ENULL = -1
+ESHAPE = -2
+EK = -3
+ESIZE = -4
+EALIAS = -5
+EFLAGS = -6
+EPARAM = -7
+
+DEFAULT = 0
+FP64 = 1
+
+# Every symbol include/bvml_dsine.h declares.
+EXPORTS = (
+    "bvml_dsine_ray_relu_f32",
+    "bvml_dsine_angmf_propagate_f32",
+    "bvml_dsine_last_error",
+    "bvml_dsine_version",
+)
+
+_lib = None
+
+
+def load(path: str = LIB) -> ctypes.CDLL:
+    """Load (once) and type the native library; raises if it was not built."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"brovisionml_amd: native library {path} is missing; run "
+            "`python -m brovisionml_amd.build` (hipcc, gfx950) first")
+    lib = ctypes.CDLL(path)
+    vp, i, ll, d, u = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_double, ctypes.c_uint
+    lib.bvml_dsine_ray_relu_f32.argtypes = [vp, vp, i, i, i, ll, vp]
+    lib.bvml_dsine_ray_relu_f32.restype = i
+    lib.bvml_dsine_angmf_propagate_f32.argtypes = [
+        vp, vp, vp, vp, vp, d, d, d, d, i, i, i, i, ll, vp, u, vp]
+    lib.bvml_dsine_angmf_propagate_f32.restype = i
+    lib.bvml_dsine_last_error.argtypes = []
+    lib.bvml_dsine_last_error.restype = ctypes.c_char_p
+    lib.bvml_dsine_version.argtypes = []
+    lib.bvml_dsine_version.restype = ctypes.c_char_p
+    _lib = lib
+    return lib
+
+
+def last_error() -> str:
+    return load().bvml_dsine_last_error().decode()
+
+
+def ray_relu_f32(normal: int, ray: int, B: int, H: int, W: int,
+                 ray_bstride: int, stream: int = 0) -> int:
+    """Raw call; pointers are integer device addresses. Returns the status."""
+    return load().bvml_dsine_ray_relu_f32(normal, ray, B, H, W, ray_bstride, stream)
+
+
+def angmf_propagate_f32(pred_norm: int, prob: int, xy: int, angle: int, ray: int,
+                        fu: float, cu: float, fv: float, cv: float,
+                        B: int, H: int, W: int, k: int, ray_bstride: int,
+                        out: int, flags: int = DEFAULT, stream: int = 0) -> int:
+    """Raw call; pointers are integer device addresses. Returns the status."""
+    return load().bvml_dsine_angmf_propagate_f32(
+        pred_norm, prob, xy, angle, ray, fu, cu, fv, cv, B, H, W, k,
+        ray_bstride, out, flags, stream)

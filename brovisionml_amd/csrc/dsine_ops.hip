@@ -1,0 +1,812 @@
+// MI355X (gfx950) kernels for brovisionml's DSINE surface-normal ops and the
+// C ABI that launches them (include/bvml_dsine.h).
+//
+// Two ops, both per-pixel geometry on the /8 NRN grid, fp32 NCHW planes:
+//   ray_relu         in-place camera-facing clamp (src/dsine_ops.cpp:55-76)
+//   angmf_propagate  fused k x k neighbour rotate + RayReLU + prob-weighted
+//                    sum + renormalise (src/dsine_ops.cpp:78-172)
+//
+// angmf_propagate is HBM-bound (436 B/px at k=5) with a VALU budget of
+// roughly 120 lane-instructions per neighbour at 70 % of 8 TB/s, so the
+// reference's double-precision formulation (about 380 per neighbour) cannot be
+// used as the fast path.  The fast kernel instead
+//   * stages the tile's replicate-padded pred_norm halo in LDS once, as
+//     per-source records: the unit normal m, g = P0.m (P0 = the source pixel's
+//     ray at depth 1), and the products ifu*mx, ifv*my, g*ifu, g*ifv;
+//   * evaluates each neighbour in fp32 with an algebraically reduced axis:
+//     the reference's axis normalize(du + dz*tu, dv + dz*tv, dz) with
+//     dz = num/dd equals sign(dd) * normalize(V) where
+//     V = (g*xs/fu - q*tu0, g*ys/fv - q*tv0, -q), q = xs*mx/fu + ys*my/fv on the
+//     RAW xy pair and tu0, tv0 the source ray -- the xy normalisation and the
+//     quadratic terms cancel exactly, and V.m == 0, so Rodrigues reduces to
+//     m*cos(t) + (V x m)*sin(t)/|V|;
+//   * flags every pixel whose fp32 result could miss the reference by more
+//     than the parity tolerance -- a neighbour with |dd| near 0 (the axis
+//     flips sign there), a near-zero xy pair or normal (the reference's
+//     clamps take over), a non-finite value, or an accumulator that is small
+//     compared with the root-sum-square of its terms (the final normalise
+//     amplifies fp32 rounding by 1/|acc|) -- and recomputes flagged pixels in
+//     double precision in the reference's own operation order, one neighbour
+//     per lane of the wave that owns the pixel, with a wave-wide reduction.
+// The double-precision body is also available as its own kernel
+// (BVML_DSINE_FP64), which reproduces the CPU reference to a few ulps.
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <string>
+
+#include "bvml_dsine.h"
+
+namespace {
+
+// src/dsine_ops.cpp:27: the float 1e-2f, widened to double where the
+// reference does arithmetic in double.
+constexpr float kRayEpsF = 1e-2f;
+
+// |dd| below this (in the fp32 evaluation, where dd is O(1) with an absolute
+// error of a few 1e-7) sends the pixel to the double-precision path.
+constexpr float kDdTau = 2e-5f;
+
+// Raw xy pairs with |xy|^2 below this, and normals with |m|^2 below kMinM2,
+// are left to the double-precision path, where the reference's 1e-12 clamps
+// stop normalising.
+constexpr float kMinXY2 = 1e-20f;
+constexpr float kMinM2 = 1e-16f;
+
+// A pixel is recomputed in double when |acc|^2 < kAccRatio2 * sum(wi^2),
+// wi = prob / |m'| being each term's weight after RayReLU.  fp32 gives each
+// term an error of a few 1e-7; the final normalise divides their sum by |acc|.
+constexpr float kAccRatio2 = 1e-2f;
+
+// ---------------------------------------------------------------------------
+// Double-precision reference body
+// ---------------------------------------------------------------------------
+
+// std::max(a, b) == (a < b) ? b : a -- returns a when a is NaN, as the
+// reference CPU path does (fmax would not).
+__device__ __forceinline__ double smax(double a, double b) { return (a < b) ? b : a; }
+
+// One neighbour's RayReLU'd rotated normal, in the operation order of
+// src/dsine_ops.cpp:110-160 (axis :110-138, axis_angle_to_matrix :31-51,
+// rotate + renormalise :140-148, RayReLU :150-160).  Contraction is off so
+// the sign-deciding dd is bit-identical to the CPU's.
+__device__ __forceinline__ void nbr_ref_f64(double nx, double ny, double nz,
+                                            double pix_x, double pix_y,
+                                            double xs, double ys, double theta,
+                                            double rx, double ry, double rz,
+                                            double fu, double cu, double fv,
+                                            double cv, double& ox, double& oy,
+                                            double& oz) {
+#pragma clang fp contract(off)
+    const double xyinv = 1.0 / smax(sqrt(xs * xs + ys * ys), 1e-12);
+    xs *= xyinv;
+    ys *= xyinv;
+    const double du = xs / fu;
+    const double dv = ys / fv;
+    const double tu = (pix_x + xs - cu) / fu;
+    const double tv = (pix_y + ys - cv) / fv;
+    const double num = -(du * nx + dv * ny);
+    double dd = tu * nx + tv * ny + nz;
+    if (fabs(dd) < 1e-8) {
+        const double sgn = (dd > 0.0) ? 1.0 : (dd < 0.0 ? -1.0 : 0.0);
+        dd = 1e-8 * sgn;
+    }
+    const double dz = num / dd;
+    double axx = du + dz * tu;
+    double axy = dv + dz * tv;
+    double axz = dz;
+    const double an = sqrt(axx * axx + axy * axy + axz * axz);
+    const double ainv = 1.0 / smax(an, 1e-12);
+    axx *= ainv;
+    axy *= ainv;
+    axz *= ainv;
+    if (!isfinite(axx) || !isfinite(axy) || !isfinite(axz)) axx = axy = axz = 0.0;
+
+    // axis_angle_to_matrix(axis * theta), quaternion form.
+    const double vx = axx * theta, vy = axy * theta, vz = axz * theta;
+    const double angle = sqrt(vx * vx + vy * vy + vz * vz);
+    const double half = angle * 0.5;
+    double s;
+    if (angle < 1e-6)
+        s = 0.5 - (angle * angle) / 48.0;
+    else
+        s = sin(half) / angle;
+    const double qr = cos(half);
+    const double qi = vx * s, qj = vy * s, qk = vz * s;
+    const double two_s = 2.0 / (qr * qr + qi * qi + qj * qj + qk * qk);
+    const double R0 = 1.0 - two_s * (qj * qj + qk * qk);
+    const double R1 = two_s * (qi * qj - qk * qr);
+    const double R2 = two_s * (qi * qk + qj * qr);
+    const double R3 = two_s * (qi * qj + qk * qr);
+    const double R4 = 1.0 - two_s * (qi * qi + qk * qk);
+    const double R5 = two_s * (qj * qk - qi * qr);
+    const double R6 = two_s * (qi * qk - qj * qr);
+    const double R7 = two_s * (qj * qk + qi * qr);
+    const double R8 = 1.0 - two_s * (qi * qi + qj * qj);
+
+    double rnx = R0 * nx + R1 * ny + R2 * nz;
+    double rny = R3 * nx + R4 * ny + R5 * nz;
+    double rnz = R6 * nx + R7 * ny + R8 * nz;
+    const double rinv = 1.0 / smax(sqrt(rnx * rnx + rny * rny + rnz * rnz), 1e-12);
+    rnx *= rinv;
+    rny *= rinv;
+    rnz *= rinv;
+
+    const double nn = sqrt(rnx * rnx + rny * rny + rnz * rnz);
+    const double rr = sqrt(rx * rx + ry * ry + rz * rz);
+    const double denom = smax(nn * rr, 1e-8);
+    const double cs = (rnx * rx + rny * ry + rnz * rz) / denom;
+    const double relu_cm = smax(cs - (double)kRayEpsF, 0.0) + (double)kRayEpsF;
+    const double dcoef = relu_cm - cs;
+    double mx = rnx + rx * dcoef, my = rny + ry * dcoef, mz = rnz + rz * dcoef;
+    const double minv = 1.0 / smax(sqrt(mx * mx + my * my + mz * mz), 1e-12);
+    ox = mx * minv;
+    oy = my * minv;
+    oz = mz * minv;
+}
+
+__device__ __forceinline__ int clampi(int v, int lo, int hi) {
+    return v < lo ? lo : (v > hi ? hi : v);
+}
+
+// Per-launch constants of angmf_propagate.
+struct AngmfArgs {
+    const float* pn;   // pred_norm
+    const float* pr;   // prob
+    const float* xy;   // raw xy
+    const float* ang;  // angle
+    const float* ray;
+    float* out;
+    double fu, cu, fv, cv;
+    long long ray_bstride;
+    long long HW;
+    int B, H, W;
+    // fp32 kernel: TW x TH output tile per workgroup, M groups of 64 pixels,
+    // one wave per (group, window row) -> 64*M*K threads.
+    int TW, TH, M, tiles_x, tiles_per_img, nblocks;
+    float ifu, ifv;    // 1/fu, 1/fv
+    float tu_c, tv_c;  // (0.5 - cu)/fu, (0.5 - cv)/fv: source ray tu0 = sx*ifu + tu_c
+};
+
+// ---------------------------------------------------------------------------
+// Double-precision kernel: one pixel per thread, reference order throughout.
+// ---------------------------------------------------------------------------
+template <int K>
+__global__ __launch_bounds__(256) void angmf_f64_kernel(AngmfArgs a) {
+#pragma clang fp contract(off)
+    constexpr int P = K / 2, K2 = K * K;
+    const long long HW = a.HW;
+    const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= (long long)a.B * HW) return;
+    const int b = (int)(gid / HW);
+    const long long p = gid - (long long)b * HW;
+    const int y = (int)(p / a.W), x = (int)(p - (long long)y * a.W);
+    const float* pn = a.pn + (size_t)b * 3 * HW;
+    const float* pr = a.pr + (size_t)b * K2 * HW;
+    const float* xyp = a.xy + (size_t)b * 2 * K2 * HW;
+    const float* ap = a.ang + (size_t)b * K2 * HW;
+    const float* rp = a.ray + (size_t)b * a.ray_bstride;
+    float* op = a.out + (size_t)b * 3 * HW;
+
+    const double rx = rp[p], ry = rp[HW + p], rz = rp[2 * HW + p];
+    double acc0 = 0.0, acc1 = 0.0, acc2 = 0.0;
+    for (int n = 0; n < K2; ++n) {
+        const int ky = n / K, kx = n - ky * K;
+        const int sy = clampi(y - P + ky, 0, a.H - 1);
+        const int sx = clampi(x - P + kx, 0, a.W - 1);
+        const long long sp = (long long)sy * a.W + sx;
+        double mx, my, mz;
+        nbr_ref_f64(pn[sp], pn[HW + sp], pn[2 * HW + sp], sx + 0.5, sy + 0.5,
+                    xyp[(size_t)n * HW + p], xyp[(size_t)(K2 + n) * HW + p],
+                    ap[(size_t)n * HW + p], rx, ry, rz, a.fu, a.cu, a.fv, a.cv,
+                    mx, my, mz);
+        const double w = pr[(size_t)n * HW + p];
+        acc0 += w * mx;
+        acc1 += w * my;
+        acc2 += w * mz;
+    }
+    const double inv = 1.0 / smax(sqrt(acc0 * acc0 + acc1 * acc1 + acc2 * acc2), 1e-12);
+    op[p] = (float)(acc0 * inv);
+    op[HW + p] = (float)(acc1 * inv);
+    op[2 * HW + p] = (float)(acc2 * inv);
+}
+
+// ---------------------------------------------------------------------------
+// fp32 fast kernel
+// ---------------------------------------------------------------------------
+
+// Workgroups go to the 8 XCDs round-robin (blockIdx % 8).  Give each XCD a
+// contiguous run of logical tiles so tiles that share halo rows and columns
+// share that XCD's L2.
+__device__ __forceinline__ int xcd_remap(int bid, int nb) {
+    const int q = nb >> 3, r = nb & 7;
+    const int xcd = bid & 7, i = bid >> 3;
+    return xcd * q + (xcd < r ? xcd : r) + i;
+}
+
+__device__ __forceinline__ float rsq(float x) { return __builtin_amdgcn_rsqf(x); }
+
+// Load base[byte_off / 4] with a uniform base pointer and a 32-bit per-lane
+// byte offset, which maps onto the scalar-base + vector-offset load form.
+__device__ __forceinline__ float ldf(const float* base, uint32_t byte_off) {
+    return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+
+// Raw buffer load of one fp32 plane: the descriptor (base, HW*4 bytes) is
+// wave-uniform and lives in scalar registers, the lane supplies a 32-bit byte
+// offset; an offset past the plane reads 0 instead of faulting.
+constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw-buffer descriptor word 3
+
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const float* plane, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(plane), (short)0, (int)bytes,
+                                             kBufferWord3);
+}
+
+__device__ __forceinline__ float ldb(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, 0));
+}
+
+__device__ __forceinline__ void stf(float* base, uint32_t byte_off, float v) {
+    *reinterpret_cast<float*>(reinterpret_cast<char*>(base) + byte_off) = v;
+}
+
+// sin and cos of t for |t| <= 3.2 (callers send larger |t| to the double
+// path).  Half-angle polynomials in u = h^2, h = t/2 in [0, 1.6]: Chebyshev
+// fits (computed for this kernel) with sin(h) = h + h^3 S(u) to 8e-9 and
+// cos(h) = 1 + u C(u) to 5e-10; then sin t = 2 sin h cos h and
+// cos t = cos^2 h - sin^2 h.  fp32 angular error of (cos t, sin t) <= 1.8e-7.
+__device__ __forceinline__ void sincos_small(float t, float& st, float& ct) {
+    const float h = 0.5f * t, u = h * h;
+    float p = fmaf(u, 2.630318e-06f, -0.00019821344f);
+    p = fmaf(u, p, 0.008333231f);
+    p = fmaf(u, p, -0.16666666f);
+    const float s = fmaf(h * u, p, h);
+    float q = fmaf(u, -2.625131e-07f, 2.4772546e-05f);
+    q = fmaf(u, q, -0.0013888624f);
+    q = fmaf(u, q, 0.041666657f);
+    q = fmaf(u, q, -0.5f);
+    const float c = fmaf(u, q, 1.0f);
+    const float sc = s * c;
+    st = sc + sc;
+    ct = fmaf(c, c, -(s * s));
+}
+
+__device__ __forceinline__ unsigned long long uniform64(unsigned long long v) {
+    const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
+    const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
+    return ((unsigned long long)hi << 32) | lo;
+}
+
+// LDS plan of the fp32 kernel, in 16-byte units:
+//   smask[16]        u64 flagged-pixel mask per 64-pixel group (8 units)
+//   rec0[ncell]      (mx, my, mz, g)  unit source normal, g = P0 . m
+//   rec1[ncell]      (mx/fu, my/fv, g/fu, g/fv)
+//   rec2[ncell]      raw source normal (for the double-precision recompute)
+//   sray[64*M]       this tile's rays (rx, ry, rz, 1/max(|r|, 1e-8))
+//   part[K][64*M]    per-window-row fp32 partial (acc.xyz, sum wi^2 or NaN)
+//   fixp[M][K][PPR]  per-window-row fp64 partial of a flagged pixel (3 doubles)
+//   stu[nw], stv[nh] source-column tu0 and source-row tv0
+// ncell = (TH+2P) x (TW+2P) is the replicate-padded source window of the tile.
+struct LdsPlan {
+    int rec0, rec1, rec2, sray, part, fixp, tuv, total;
+};
+
+__host__ __device__ inline LdsPlan lds_plan(int K, int TW, int TH, int M) {
+    const int P = K / 2, nw = TW + 2 * P, nh = TH + 2 * P, ncell = nw * nh, npx = 64 * M;
+    const int ppr = (K <= 8) ? 8 : 4;
+    LdsPlan L;
+    L.rec0 = 8;
+    L.rec1 = L.rec0 + ncell;
+    L.rec2 = L.rec1 + ncell;
+    L.sray = L.rec2 + ncell;
+    L.part = L.sray + npx;
+    L.fixp = L.part + K * npx;
+    L.tuv = L.fixp + (M * K * ppr * 3 + 1) / 2;
+    L.total = L.tuv + (nw + nh + 3) / 4;
+    return L;
+}
+
+// One source cell of the tile window: unit normal, ray products, raw normal.
+__device__ __forceinline__ void stage_cell(const AngmfArgs& a, float4* rec0, float4* rec1,
+                                           float4* rec2, float* stu, float* stv, int i,
+                                           int hy, int hx, int sy, int sx, float mx,
+                                           float my, float mz) {
+    const float tu0 = fmaf((float)sx, a.ifu, a.tu_c);
+    const float tv0 = fmaf((float)sy, a.ifv, a.tv_c);
+    if (hy == 0) stu[hx] = tu0;
+    if (hx == 0) stv[hy] = tv0;
+    const float m2 = fmaf(mx, mx, fmaf(my, my, mz * mz));
+    // Degenerate or non-finite normals become m = 0, g = 0: every neighbour
+    // that reads them then has dd == 0 and is flagged.
+    const bool ok = (m2 >= kMinM2) && (m2 <= 1e30f);
+    const float inv = rsq(ok ? m2 : 1.0f);
+    const float ux = ok ? mx * inv : 0.0f;
+    const float uy = ok ? my * inv : 0.0f;
+    const float uz = ok ? mz * inv : 0.0f;
+    const float g = fmaf(tu0, ux, fmaf(tv0, uy, uz));
+    rec0[i] = make_float4(ux, uy, uz, g);
+    rec1[i] = make_float4(ux * a.ifu, uy * a.ifv, g * a.ifu, g * a.ifv);
+    rec2[i] = make_float4(mx, my, mz, 0.0f);
+}
+
+// Occupancy target: 16 waves per CU hold one 16-wave block; k = 5 needs 20
+// (two 10-wave blocks, the 256x256 shape in one round), i.e. <= 96 VGPRs.
+template <int K>
+constexpr int kWavesPerEU = (K == 5) ? 5 : 4;
+
+template <int K>
+__global__ __launch_bounds__(64 * K * (16 / K))
+__attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(AngmfArgs a) {
+    constexpr int P = K / 2, K2 = K * K;
+    constexpr int LPG = (K <= 8) ? 8 : 16;  // lanes per flagged pixel in the recompute
+    constexpr int PPR = 64 / LPG;           // flagged pixels per recompute pass
+    extern __shared__ float4 smem[];
+    const int TW = a.TW, TH = a.TH, M = a.M;
+    const int nw = TW + 2 * P, nh = TH + 2 * P, ncell = nw * nh;
+    const int npx = 64 * M;
+    const LdsPlan L = lds_plan(K, TW, TH, M);
+    unsigned long long* smask = reinterpret_cast<unsigned long long*>(smem);
+    float4* rec0 = smem + L.rec0;
+    float4* rec1 = smem + L.rec1;
+    float4* rec2 = smem + L.rec2;
+    float4* sray = smem + L.sray;
+    float4* part = smem + L.part;
+    double* fixp = reinterpret_cast<double*>(smem + L.fixp);
+    float* stu = reinterpret_cast<float*>(smem + L.tuv);
+    float* stv = stu + nw;
+
+    const int lb = xcd_remap(blockIdx.x, a.nblocks);
+    const int b = lb / a.tiles_per_img;
+    const int t_in = lb - b * a.tiles_per_img;
+    const int tyi = t_in / a.tiles_x;
+    const int ty0 = tyi * TH;
+    const int tx0 = (t_in - tyi * a.tiles_x) * TW;
+    const long long HW = a.HW;
+    const float* pn = a.pn + (size_t)b * 3 * HW;
+    const float* pr = a.pr + (size_t)b * K2 * HW;
+    const float* xyp = a.xy + (size_t)b * 2 * K2 * HW;
+    const float* ap = a.ang + (size_t)b * K2 * HW;
+    const float* rp = a.ray + (size_t)b * a.ray_bstride;
+    float* op = a.out + (size_t)b * 3 * HW;
+    const int W = a.W, H = a.H;
+    const int nthr = (int)blockDim.x;
+
+    // ---- this lane's pixel and window row ----------------------------------
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int lane = threadIdx.x & 63;
+    const int ky = __builtin_amdgcn_readfirstlane(wave / M);
+    const int gi = wave - ky * M;
+    const int j = gi * 64 + lane;
+    const int ty = j / TW, tx = j - ty * TW;
+    const int y = ty0 + ty, x = tx0 + tx;
+    const bool valid = (ty < TH) && (y < H) && (x < W);
+    const uint32_t pb = valid ? (uint32_t)(y * W + x) * 4u : 0u;
+
+    // ---- prologue: loads in the order they are needed --------------------
+    // (vmcnt retires in order, so the window loads go first and the 4K
+    // row loads, consumed last, stay in flight through the staging math).
+    const int c0 = threadIdx.x, c1 = threadIdx.x + nthr;
+    int hy0 = 0, hx0 = 0, sy0 = 0, sx0 = 0, hy1 = 0, hx1 = 0, sy1 = 0, sx1 = 0;
+    float m0x = 0.f, m0y = 0.f, m0z = 0.f, m1x = 0.f, m1y = 0.f, m1z = 0.f;
+    if (c0 < ncell) {
+        hy0 = c0 / nw;
+        hx0 = c0 - hy0 * nw;
+        sy0 = clampi(ty0 - P + hy0, 0, H - 1);
+        sx0 = clampi(tx0 - P + hx0, 0, W - 1);
+        const uint32_t sb = (uint32_t)(sy0 * W + sx0) * 4u;
+        m0x = ldf(pn, sb);
+        m0y = ldf(pn + HW, sb);
+        m0z = ldf(pn + 2 * HW, sb);
+    }
+    if (c1 < ncell) {
+        hy1 = c1 / nw;
+        hx1 = c1 - hy1 * nw;
+        sy1 = clampi(ty0 - P + hy1, 0, H - 1);
+        sx1 = clampi(tx0 - P + hx1, 0, W - 1);
+        const uint32_t sb = (uint32_t)(sy1 * W + sx1) * 4u;
+        m1x = ldf(pn, sb);
+        m1y = ldf(pn + HW, sb);
+        m1z = ldf(pn + 2 * HW, sb);
+    }
+    float4 rv = make_float4(0.f, 0.f, 0.f, 0.f);
+    bool rvalid = false;
+    if (threadIdx.x < npx) {
+        const int ity = threadIdx.x / TW, itx = threadIdx.x - ity * TW;
+        const int iy = ty0 + ity, ix = tx0 + itx;
+        rvalid = ity < TH && iy < H && ix < W;
+        if (rvalid) {
+            const uint32_t ib = (uint32_t)(iy * W + ix) * 4u;
+            rv.x = ldf(rp, ib);
+            rv.y = ldf(rp + HW, ib);
+            rv.z = ldf(rp + 2 * HW, ib);
+        }
+    }
+    float xs[K], ys[K], th[K], wt[K];
+#pragma unroll
+    for (int kx = 0; kx < K; ++kx) xs[kx] = ys[kx] = th[kx] = wt[kx] = 0.f;
+    if (valid) {
+        const size_t n0 = (size_t)ky * K;
+        const uint32_t pbytes = (uint32_t)HW * 4u;
+#pragma unroll
+        for (int kx = 0; kx < K; ++kx) {
+            xs[kx] = ldb(plane_rsrc(xyp + (n0 + kx) * HW, pbytes), pb);
+            ys[kx] = ldb(plane_rsrc(xyp + (K2 + n0 + kx) * HW, pbytes), pb);
+            th[kx] = ldb(plane_rsrc(ap + (n0 + kx) * HW, pbytes), pb);
+            wt[kx] = ldb(plane_rsrc(pr + (n0 + kx) * HW, pbytes), pb);
+        }
+    }
+
+    // ---- stage the tile's source window and rays --------------------------
+    if (c0 < ncell) stage_cell(a, rec0, rec1, rec2, stu, stv, c0, hy0, hx0, sy0, sx0, m0x, m0y, m0z);
+    if (c1 < ncell) stage_cell(a, rec0, rec1, rec2, stu, stv, c1, hy1, hx1, sy1, sx1, m1x, m1y, m1z);
+    for (int i = c0 + 2 * nthr; i < ncell; i += nthr) {
+        const int hy = i / nw, hx = i - hy * nw;
+        const int sy = clampi(ty0 - P + hy, 0, H - 1), sx = clampi(tx0 - P + hx, 0, W - 1);
+        const uint32_t sb = (uint32_t)(sy * W + sx) * 4u;
+        stage_cell(a, rec0, rec1, rec2, stu, stv, i, hy, hx, sy, sx, ldf(pn, sb),
+                   ldf(pn + HW, sb), ldf(pn + 2 * HW, sb));
+    }
+    if (threadIdx.x < npx) {
+        // cos(v', r) = v'.r / max(|v'||r|, 1e-8) with |v'| = 1
+        if (rvalid)
+            rv.w = 1.0f / fmaxf(sqrtf(fmaf(rv.x, rv.x, fmaf(rv.y, rv.y, rv.z * rv.z))), 1e-8f);
+        sray[threadIdx.x] = rv;
+    }
+    __syncthreads();
+
+    // ---- phase A: one window row (ky) of one pixel per lane, fp32 ----------
+    float4 res = make_float4(0.f, 0.f, 0.f, 0.f);
+    if (valid) {
+        const float4 r = sray[j];
+        const float rsx = r.x * r.w, rsy = r.y * r.w, rsz = r.z * r.w;
+        const float tv0 = stv[ty + ky];
+        const int cb = (ty + ky) * nw + tx;
+        float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, q2 = 0.f;
+        bool bad = false;
+#pragma unroll
+        for (int kx = 0; kx < K; ++kx) {
+            const float4 r0 = rec0[cb + kx];
+            const float4 r1 = rec1[cb + kx];
+            const float tu0 = stu[tx + kx];
+            const float xsv = xs[kx], ysv = ys[kx], t = th[kx];
+
+            // axis = sign(dd) * V/|V|
+            const float s = fmaf(xsv, xsv, ysv * ysv);
+            const float lam = rsq(fmaxf(s, 1e-24f));
+            const float q = fmaf(xsv, r1.x, ysv * r1.y);
+            const float dd = fmaf(lam, q, r0.w);
+            bad |= !(fabsf(dd) >= kDdTau) | (s < kMinXY2) | !(fabsf(t) <= 3.2f);
+            const float Vx = fmaf(r1.z, xsv, -q * tu0);
+            const float Vy = fmaf(r1.w, ysv, -q * tv0);
+            const float n2 = fmaf(Vx, Vx, fmaf(Vy, Vy, q * q));
+            const float ia = copysignf(rsq(n2), dd);
+            float st, ct;
+            sincos_small(t, st, ct);
+            const float S = st * ia;
+            // v' = m cos(t) + (V x m) sin(t)/|V|,  V = (Vx, Vy, -q)
+            const float cx = fmaf(Vy, r0.z, q * r0.y);
+            const float cy = fmaf(-q, r0.x, -Vx * r0.z);
+            const float cz = fmaf(Vx, r0.y, -Vy * r0.x);
+            const float vx = fmaf(cx, S, r0.x * ct);
+            const float vy = fmaf(cy, S, r0.y * ct);
+            const float vz = fmaf(cz, S, r0.z * ct);
+            // RayReLU against this pixel's ray
+            const float cs = fmaf(vx, rsx, fmaf(vy, rsy, vz * rsz));
+            const float dc = fmaxf(kRayEpsF - cs, 0.0f);
+            const float mx = fmaf(r.x, dc, vx);
+            const float my = fmaf(r.y, dc, vy);
+            const float mz = fmaf(r.z, dc, vz);
+            const float wi = wt[kx] * rsq(fmaf(mx, mx, fmaf(my, my, mz * mz)));
+            acc0 = fmaf(mx, wi, acc0);
+            acc1 = fmaf(my, wi, acc1);
+            acc2 = fmaf(mz, wi, acc2);
+            q2 = fmaf(wi, wi, q2);
+        }
+        res = make_float4(acc0, acc1, acc2, bad ? __builtin_nanf("") : q2);
+    }
+    part[ky * npx + j] = res;
+    __syncthreads();
+
+    // ---- phase B: reduce the K rows, write unflagged pixels ----------------
+    if (ky == 0) {
+        bool flag = false;
+        if (valid) {
+            float4 sm = part[j];
+#pragma unroll
+            for (int rr = 1; rr < K; ++rr) {
+                const float4 t = part[rr * npx + j];
+                sm.x += t.x;
+                sm.y += t.y;
+                sm.z += t.z;
+                sm.w += t.w;
+            }
+            const float a2 = fmaf(sm.x, sm.x, fmaf(sm.y, sm.y, sm.z * sm.z));
+            flag = !(a2 >= kAccRatio2 * sm.w) || !(a2 <= 1e37f);
+            if (!flag) {
+                const float inv = rsq(fmaxf(a2, 1e-24f));
+                stf(op, pb, sm.x * inv);
+                stf(op + HW, pb, sm.y * inv);
+                stf(op + 2 * HW, pb, sm.z * inv);
+            }
+        }
+        const unsigned long long m = __ballot(flag);
+        if (lane == 0) smask[gi] = m;
+    }
+    __syncthreads();
+
+    // ---- phase C: double-precision recompute of flagged pixels -------------
+    // Each wave (gi, ky) evaluates row ky of up to PPR flagged pixels of its
+    // group per pass, one neighbour per lane, in the reference's operation
+    // order (source normals and rays from the LDS window, the per-neighbour
+    // planes re-read from L2).  Row partials meet in LDS and the ky == 0 wave
+    // writes the pixel.
+    int maxc = 0;
+    for (int g = 0; g < M; ++g) {
+        const int c = __popcll(uniform64(smask[g]));
+        maxc = c > maxc ? c : maxc;
+    }
+    if (maxc == 0) return;
+    const unsigned long long gmask = uniform64(smask[gi]);
+    const int cnt = __popcll(gmask);
+    const int slot = lane / LPG, kxl = lane - slot * LPG;
+    unsigned long long rest = gmask;
+    for (int base = 0; base < maxc; base += PPR) {
+        int src = 0, fin_src = 0;
+#pragma unroll
+        for (int sidx = 0; sidx < PPR; ++sidx) {
+            const int bitpos = rest ? __ffsll((long long)rest) - 1 : 0;
+            if (rest) rest &= rest - 1;
+            if (sidx == slot) src = bitpos;
+            if (sidx == lane) fin_src = bitpos;
+        }
+        const bool has = (base + slot) < cnt && kxl < K;
+        double p0 = 0.0, p1 = 0.0, p2 = 0.0;
+        if (has) {
+            const int jj = gi * 64 + src;
+            const int fty = jj / TW, ftx = jj - fty * TW;
+            // this neighbour's inputs, re-read (the block just read them: L2)
+            const uint32_t fb = (uint32_t)((ty0 + fty) * W + tx0 + ftx) * 4u;
+            const size_t n = (size_t)ky * K + kxl;
+            const float fxs = ldf(xyp + n * HW, fb);
+            const float fys = ldf(xyp + (K2 + n) * HW, fb);
+            const float fth = ldf(ap + n * HW, fb);
+            const float fwt = ldf(pr + n * HW, fb);
+            const int sy = clampi(ty0 + fty - P + ky, 0, H - 1);
+            const int sx = clampi(tx0 + ftx - P + kxl, 0, W - 1);
+            const float4 m = rec2[(fty + ky) * nw + ftx + kxl];
+            const float4 r = sray[jj];
+            double ox, oy, oz;
+            nbr_ref_f64(m.x, m.y, m.z, sx + 0.5, sy + 0.5, fxs, fys, fth, r.x, r.y, r.z,
+                        a.fu, a.cu, a.fv, a.cv, ox, oy, oz);
+            const double w = fwt;
+            p0 = w * ox;
+            p1 = w * oy;
+            p2 = w * oz;
+        }
+#pragma unroll
+        for (int off = LPG / 2; off > 0; off >>= 1) {
+            p0 += __shfl_xor(p0, off, 64);
+            p1 += __shfl_xor(p1, off, 64);
+            p2 += __shfl_xor(p2, off, 64);
+        }
+        if (kxl == 0 && (base + slot) < cnt) {
+            double* f = fixp + ((gi * K + ky) * PPR + slot) * 3;
+            f[0] = p0;
+            f[1] = p1;
+            f[2] = p2;
+        }
+        __syncthreads();
+        if (ky == 0 && lane < PPR && base + lane < cnt) {
+            double a0 = 0.0, a1 = 0.0, a2 = 0.0;
+            for (int rr = 0; rr < K; ++rr) {
+                const double* f = fixp + ((gi * K + rr) * PPR + lane) * 3;
+                a0 += f[0];
+                a1 += f[1];
+                a2 += f[2];
+            }
+            const double inv = 1.0 / smax(sqrt(a0 * a0 + a1 * a1 + a2 * a2), 1e-12);
+            const int jj = gi * 64 + fin_src;
+            const int fty = jj / TW, ftx = jj - fty * TW;
+            const uint32_t fb = (uint32_t)((ty0 + fty) * W + tx0 + ftx) * 4u;
+            stf(op, fb, (float)(a0 * inv));
+            stf(op + HW, fb, (float)(a1 * inv));
+            stf(op + 2 * HW, fb, (float)(a2 * inv));
+        }
+        __syncthreads();
+    }
+}
+
+// ---------------------------------------------------------------------------
+// RayReLU: double precision, reference order; memory-bound (36 B/px).
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void ray_relu_kernel(float* normal, const float* ray,
+                                                       long long HW, long long total,
+                                                       long long ray_bstride) {
+#pragma clang fp contract(off)
+    const long long gid = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= total) return;
+    const long long b = gid / HW;
+    const long long p = gid - b * HW;
+    float* n = normal + b * 3 * HW;
+    const float* r = ray + b * ray_bstride;
+    const double nx = n[p], ny = n[HW + p], nz = n[2 * HW + p];
+    const double rx = r[p], ry = r[HW + p], rz = r[2 * HW + p];
+    const double nn = sqrt(nx * nx + ny * ny + nz * nz);
+    const double rr = sqrt(rx * rx + ry * ry + rz * rz);
+    const double denom = smax(nn * rr, 1e-8);
+    const double cs = (nx * rx + ny * ry + nz * rz) / denom;
+    const double relu_cm = smax(cs - (double)kRayEpsF, 0.0) + (double)kRayEpsF;
+    const double dcoef = relu_cm - cs;
+    const double mx = nx + rx * dcoef, my = ny + ry * dcoef, mz = nz + rz * dcoef;
+    const double inv = 1.0 / smax(sqrt(mx * mx + my * my + mz * mz), 1e-12);
+    n[p] = (float)(mx * inv);
+    n[HW + p] = (float)(my * inv);
+    n[2 * HW + p] = (float)(mz * inv);
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+    return a0 < b0 + bbytes && b0 < a0 + abytes;
+}
+
+template <int K>
+hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
+    if (fp64) {
+        const long long total = (long long)a.B * a.HW;
+        const long long grid = (total + 255) / 256;
+        hipLaunchKernelGGL(angmf_f64_kernel<K>, dim3((unsigned)grid), dim3(256), 0, s, a);
+        return hipGetLastError();
+    }
+    const size_t lds = (size_t)lds_plan(K, a.TW, a.TH, a.M).total * 16;
+    hipLaunchKernelGGL(angmf_f32_kernel<K>, dim3((unsigned)a.nblocks), dim3(64 * a.M * K),
+                       lds, s, a);
+    return hipGetLastError();
+}
+
+// Tile of the fp32 kernel: wide images take 64 x M tiles (each wave one
+// 256 B row segment per plane); narrow ones full-width tiles of TH rows with
+// the fewest idle lanes.  At most 16 waves (M*K) per workgroup.
+void choose_tile(AngmfArgs& a, int K) {
+    const int mmax = 16 / K;
+    if (a.W > 128) {
+        a.TW = 64;
+        a.M = mmax < 2 ? mmax : 2;
+        a.TH = a.M;
+    } else {
+        double best = -1.0;
+        for (int th = 1; th <= a.H && th <= 64 * mmax; ++th) {
+            const int npx = a.W * th;
+            const int m = (npx + 63) / 64;
+            if (m > mmax) break;
+            const double util = (double)npx / (64.0 * m);
+            if (util >= best) {
+                best = util;
+                a.TH = th;
+                a.M = m;
+            }
+        }
+        a.TW = a.W;
+    }
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* bvml_dsine_last_error(void) { return g_last_error.c_str(); }
+
+const char* bvml_dsine_version(void) { return "0.1.0"; }
+
+int bvml_dsine_ray_relu_f32(float* normal, const float* ray, int B, int H, int W,
+                            long long ray_bstride, void* stream) {
+    if (B < 0 || H < 0 || W < 0)
+        return fail(BVML_DSINE_ESHAPE, "ray_relu: B, H and W must be >= 0");
+    if (ray_bstride < 0)
+        return fail(BVML_DSINE_ESHAPE, "ray_relu: ray_bstride must be >= 0");
+    const long long HW = (long long)H * W;
+    if (B == 0 || HW == 0) return BVML_DSINE_OK;
+    if (!normal || !ray) return fail(BVML_DSINE_ENULL, "ray_relu: normal and ray must be non-NULL");
+    const long long total = (long long)B * HW;
+    if (total > (long long)INT_MAX * 256)
+        return fail(BVML_DSINE_ESIZE, "ray_relu: B*H*W too large for one launch");
+    const size_t nbytes = (size_t)B * 3 * HW * sizeof(float);
+    const size_t rbytes = ((size_t)(B - 1) * ray_bstride + 3 * HW) * sizeof(float);
+    if (overlaps(normal, nbytes, ray, rbytes))
+        return fail(BVML_DSINE_EALIAS, "ray_relu: normal and ray overlap");
+    const long long grid = (total + 255) / 256;
+    hipLaunchKernelGGL(ray_relu_kernel, dim3((unsigned)grid), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), normal, ray, HW, total, ray_bstride);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return fail((int)e, std::string("ray_relu launch: ") + hipGetErrorString(e));
+    return BVML_DSINE_OK;
+}
+
+int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
+                                   const float* xy, const float* angle,
+                                   const float* ray, double fu, double cu,
+                                   double fv, double cv, int B, int H, int W,
+                                   int k, long long ray_bstride, float* out,
+                                   unsigned flags, void* stream) {
+    if (flags & ~BVML_DSINE_FP64)
+        return fail(BVML_DSINE_EFLAGS, "angmf_propagate: unknown flag bits");
+    if (B < 0 || H < 0 || W < 0)
+        return fail(BVML_DSINE_ESHAPE, "angmf_propagate: B, H and W must be >= 0");
+    if (ray_bstride < 0)
+        return fail(BVML_DSINE_ESHAPE, "angmf_propagate: ray_bstride must be >= 0");
+    if (!(k == 1 || k == 3 || k == 5 || k == 7 || k == 9))
+        return fail(BVML_DSINE_EK, "angmf_propagate: k must be one of 1, 3, 5, 7, 9");
+    const long long HW = (long long)H * W;
+    if (B == 0 || HW == 0) return BVML_DSINE_OK;
+    if (!pred_norm || !prob || !xy || !angle || !ray || !out)
+        return fail(BVML_DSINE_ENULL, "angmf_propagate: all tensors must be non-NULL");
+    const long long K2 = (long long)k * k;
+    const long long total = (long long)B * HW;
+    if (total > (long long)INT_MAX * 64 || HW >= (1LL << 30))
+        return fail(BVML_DSINE_ESIZE, "angmf_propagate: B*H*W too large for one launch");
+    const size_t f = sizeof(float);
+    const size_t out_b = (size_t)B * 3 * HW * f;
+    const size_t pn_b = (size_t)B * 3 * HW * f;
+    const size_t pr_b = (size_t)B * K2 * HW * f;
+    const size_t xy_b = (size_t)B * 2 * K2 * HW * f;
+    const size_t an_b = (size_t)B * K2 * HW * f;
+    const size_t ry_b = ((size_t)(B - 1) * ray_bstride + 3 * HW) * f;
+    if (overlaps(out, out_b, pred_norm, pn_b) || overlaps(out, out_b, prob, pr_b) ||
+        overlaps(out, out_b, xy, xy_b) || overlaps(out, out_b, angle, an_b) ||
+        overlaps(out, out_b, ray, ry_b))
+        return fail(BVML_DSINE_EALIAS, "angmf_propagate: out overlaps an input");
+
+    AngmfArgs a{};
+    a.pn = pred_norm; a.pr = prob; a.xy = xy; a.ang = angle; a.ray = ray; a.out = out;
+    a.fu = fu; a.cu = cu; a.fv = fv; a.cv = cv;
+    a.ray_bstride = ray_bstride;
+    a.HW = HW; a.B = B; a.H = H; a.W = W;
+    a.ifu = (float)(1.0 / fu);
+    a.ifv = (float)(1.0 / fv);
+    a.tu_c = (float)((0.5 - cu) / fu);
+    a.tv_c = (float)((0.5 - cv) / fv);
+    choose_tile(a, k);
+    a.tiles_x = (W + a.TW - 1) / a.TW;
+    const long long tiles_y = (H + a.TH - 1) / a.TH;
+    const long long tpi = (long long)a.tiles_x * tiles_y;
+    if (tpi * B > INT_MAX) return fail(BVML_DSINE_ESIZE, "angmf_propagate: too many tiles");
+    a.tiles_per_img = (int)tpi;
+    a.nblocks = (int)(tpi * B);
+
+    // The fp32 path assumes intrinsics in the range real cameras produce;
+    // anything else runs the double-precision kernel (same results as the
+    // reference, which accepts any value).
+    const bool sane = std::isfinite(fu) && std::isfinite(fv) && std::isfinite(cu) &&
+                      std::isfinite(cv) && std::fabs(fu) >= 1e-3 && std::fabs(fu) <= 1e7 &&
+                      std::fabs(fv) >= 1e-3 && std::fabs(fv) <= 1e7 &&
+                      std::fabs(cu) <= 1e7 && std::fabs(cv) <= 1e7;
+    const bool fp64 = (flags & BVML_DSINE_FP64) || !sane;
+    hipStream_t s = static_cast<hipStream_t>(stream);
+    hipError_t e;
+    switch (k) {
+        case 1: e = launch_angmf<1>(a, fp64, s); break;
+        case 3: e = launch_angmf<3>(a, fp64, s); break;
+        case 5: e = launch_angmf<5>(a, fp64, s); break;
+        case 7: e = launch_angmf<7>(a, fp64, s); break;
+        default: e = launch_angmf<9>(a, fp64, s); break;
+    }
+    if (e != hipSuccess)
+        return fail((int)e, std::string("angmf_propagate launch: ") + hipGetErrorString(e));
+    return BVML_DSINE_OK;
+}
+
+}  // extern "C"

@@ -1,0 +1,137 @@
+"""Python mirror of brovisionml's DSINE op interface on HIP device tensors.
+
+Same names, argument meaning and error behaviour as the C++ entry points in
+include/brovisionml/dsine_ops.h (the reference's
+include/brovisionml/dsine_ops.h:19-54):
+
+  ray_relu(normal, ray, H, W)                    in place
+  angmf_propagate(pred_norm, prob, xy, angle, ray, fu, cu, fv, cv, H, W, out)
+
+Tensors are torch tensors on a HIP device (torch is only the allocator and
+stream provider here), fp32, contiguous, in the reference's NCHW layout:
+(1, C*H*W), (C, H, W), or batched (B, C, H, W) / (B, C*H*W).  A batch of B
+samples is inferred from pred_norm / normal; the window size k from prob.
+`ray` may hold one map (3*H*W, shared) or one per sample.
+
+Errors raise RuntimeError with the reference's "dsine ops: " prefix
+(src/dsine_ops.cpp:18-22).  CPU tensors raise: this library is the HIP
+device path only (brovisionml keeps its CPU twin).
+"""
+from __future__ import annotations
+
+import math
+
+from . import _lib
+
+_WHO = "dsine ops: "
+
+
+def _fail(msg: str):
+    raise RuntimeError(_WHO + msg)
+
+
+def _check_tensors(op: str, tensors) -> None:
+    dev = tensors[0].device
+    for t in tensors[1:]:
+        if t.device != dev:
+            if op == "ray_relu":
+                _fail("ray_relu: normal and ray must share a device")
+            _fail(f"{op}: all inputs must share a device")
+    if dev.type != "cuda":
+        _fail(f"{op}: tensors are on the {dev.type.upper()}; this library "
+              "implements the HIP device path only")
+    import torch
+    for t in tensors:
+        if t.dtype != torch.float32:
+            _fail(f"{op}: tensors must be float32")
+        if not t.is_contiguous():
+            _fail(f"{op}: tensors must be contiguous")
+
+
+def _stream_of(t) -> int:
+    import torch
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _ray_stride(op: str, ray, B: int, HW: int) -> int:
+    if ray.numel() == 3 * HW:
+        return 0
+    if ray.numel() == 3 * HW * B:
+        return 3 * HW
+    _fail(f"{op}: ray must hold 3*H*W or B*3*H*W elements")
+
+
+def _raise_status(op: str, status: int) -> None:
+    if status != _lib.OK:
+        _fail(f"{op}: {_lib.last_error()} (status {status})")
+
+
+def ray_relu(normal, ray, H: int, W: int) -> None:
+    """RayReLU (eps 1e-2) in place on `normal` (src/dsine_ops.cpp:55-76)."""
+    _check_tensors("ray_relu", [normal, ray])
+    HW = H * W
+    if HW == 0:
+        return
+    if normal.numel() % (3 * HW):
+        _fail("ray_relu: normal must hold B*3*H*W elements")
+    B = normal.numel() // (3 * HW)
+    bstride = _ray_stride("ray_relu", ray, B, HW)
+    with _device(normal):
+        st = _lib.ray_relu_f32(normal.data_ptr(), ray.data_ptr(), B, H, W, bstride,
+                               _stream_of(normal))
+    _raise_status("ray_relu", st)
+
+
+def angmf_propagate(pred_norm, prob, xy, angle, ray, fu: float, cu: float,
+                    fv: float, cv: float, H: int, W: int, out=None, *,
+                    precise: bool = False):
+    """Fused AngMF propagate (src/dsine_ops.cpp:78-172).  Returns `out`
+    (allocated like pred_norm when None; must not alias any input).
+    precise=True runs the double-precision kernel."""
+    _check_tensors("angmf_propagate", [pred_norm, prob, xy, angle, ray])
+    import torch
+    HW = H * W
+    if out is None:
+        out = torch.empty_like(pred_norm)
+    elif out.device != pred_norm.device or out.dtype != pred_norm.dtype \
+            or not out.is_contiguous() or out.numel() != pred_norm.numel():
+        _fail("angmf_propagate: out must match pred_norm's device, dtype and size")
+    if HW == 0:
+        return out
+    if pred_norm.numel() % (3 * HW):
+        _fail("angmf_propagate: pred_norm must hold B*3*H*W elements")
+    B = pred_norm.numel() // (3 * HW)
+    if B == 0:
+        return out
+    if prob.numel() % (B * HW):
+        _fail("angmf_propagate: prob must hold B*k*k*H*W elements")
+    K2 = prob.numel() // (B * HW)
+    k = math.isqrt(K2)
+    if k * k != K2:
+        _fail("angmf_propagate: prob channel count is not a square")
+    if xy.numel() != 2 * K2 * B * HW or angle.numel() != K2 * B * HW:
+        _fail("angmf_propagate: xy must hold 2*k*k and angle k*k planes per sample")
+    bstride = _ray_stride("angmf_propagate", ray, B, HW)
+    flags = _lib.FP64 if precise else _lib.DEFAULT
+    with _device(pred_norm):
+        st = _lib.angmf_propagate_f32(
+            pred_norm.data_ptr(), prob.data_ptr(), xy.data_ptr(), angle.data_ptr(),
+            ray.data_ptr(), float(fu), float(cu), float(fv), float(cv), B, H, W, k,
+            bstride, out.data_ptr(), flags, _stream_of(pred_norm))
+    _raise_status("angmf_propagate", st)
+    return out
+
+
+class _device:
+    """Make the tensor's device current for the launch."""
+
+    def __init__(self, t):
+        self.t = t
+
+    def __enter__(self):
+        import torch
+        self.ctx = torch.cuda.device(self.t.device)
+        self.ctx.__enter__()
+
+    def __exit__(self, *exc):
+        self.ctx.__exit__(*exc)

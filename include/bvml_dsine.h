@@ -1,0 +1,90 @@
+/*
+ * bvml_dsine.h -- C ABI of the MI355X (gfx950) DSINE surface-normal ops.
+ *
+ * These entry points are the drop-in boundary for brovisionml's two GPU
+ * kernels.  They replace the launchers the reference declares in
+ * src/dsine_ops_cuda.h:13-23 (detail::ray_relu_cuda, detail::angmf_propagate_cuda)
+ * and implemented in src/dsine_ops.cu:159-191; the C++ layer
+ * (include/brovisionml/dsine_ops.h) forwards to them with the reference's own
+ * signatures.  Plain pointers and scalars only: every pointer is a device
+ * pointer (hipMalloc'd, or any HIP-visible device allocation) to contiguous
+ * fp32 NCHW planes, every call is asynchronous on `stream` (NULL = the null
+ * stream, as the reference launches on the default stream), and nothing
+ * throws.
+ *
+ * Layout (H, W: the /8 grid; HW = H*W; K2 = k*k; sample b of B):
+ *   pred_norm  b*3*HW      + c*HW      + y*W + x     c in [0,3)
+ *   prob       b*K2*HW     + n*HW      + ...         n = ky*k + kx
+ *   xy         b*2*K2*HW   + n*HW (xs), (K2+n)*HW (ys)
+ *   angle      b*K2*HW     + n*HW
+ *   ray        b*ray_bstride + c*HW    (ray_bstride 0 = one ray shared by all)
+ *   out        b*3*HW      + c*HW
+ * With B = 1, k = 5 and ray_bstride = 0 this is exactly the reference's
+ * (1, C*H*W) tensor layout (include/brovisionml/dsine_ops.h:35-46).
+ *
+ * Return value: 0 on success; a negative BVML_DSINE_E* code for a rejected
+ * argument (nothing is launched); a positive hipError_t value when the HIP
+ * runtime reports an error at launch.  bvml_dsine_last_error() returns the
+ * calling thread's message for the last non-zero status.
+ */
+#ifndef BVML_DSINE_H
+#define BVML_DSINE_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BVML_DSINE_OK 0
+#define BVML_DSINE_ENULL (-1)     /* a required pointer is NULL */
+#define BVML_DSINE_ESHAPE (-2)    /* B, H or W negative */
+#define BVML_DSINE_EK (-3)        /* k not one of 1, 3, 5, 7, 9 */
+#define BVML_DSINE_ESIZE (-4)     /* a plane index or grid would overflow */
+#define BVML_DSINE_EALIAS (-5)    /* out overlaps an input */
+#define BVML_DSINE_EFLAGS (-6)    /* unknown flag bits */
+#define BVML_DSINE_EPARAM (-7)    /* fu/fv zero or non-finite, cu/cv non-finite */
+
+/* Flag bits for bvml_dsine_angmf_propagate_f32. */
+#define BVML_DSINE_DEFAULT 0u
+/* Run every neighbour in double precision in the reference's operation
+ * order (one pixel per lane, no fp32 fast path): the parity anchor. */
+#define BVML_DSINE_FP64 1u
+
+/*
+ * RayReLU in place (eps = 1e-2), B samples.
+ * Replaces detail::ray_relu_cuda (src/dsine_ops_cuda.h:13-14,
+ * src/dsine_ops.cu:159-168); arithmetic of src/dsine_ops.cpp:55-76.
+ *   normal : B x 3 x HW, read and written
+ *   ray    : 3 x HW per sample at ray + b*ray_bstride (0 = shared)
+ * HW == 0 or B == 0 returns 0 without launching (src/dsine_ops.cu:162).
+ */
+int bvml_dsine_ray_relu_f32(float* normal, const float* ray, int B, int H,
+                            int W, long long ray_bstride, void* stream);
+
+/*
+ * Fused AngMF propagate, B samples, odd window k.
+ * Replaces detail::angmf_propagate_cuda (src/dsine_ops_cuda.h:16-23,
+ * src/dsine_ops.cu:170-191); arithmetic of src/dsine_ops.cpp:78-172, with
+ * k generalising the reference's fixed 5x5 window (src/dsine_ops.cpp:24-26).
+ * fu, cu, fv, cv: the grid-scaled intrinsics the caller computes at
+ * src/dsine_refine.cpp:232-237, shared by all samples.
+ * `out` is caller-allocated (B x 3 x HW) and must not overlap any input
+ * (the reference allocates it per call, src/dsine_ops.cu:178).
+ */
+int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
+                                   const float* xy, const float* angle,
+                                   const float* ray, double fu, double cu,
+                                   double fv, double cv, int B, int H, int W,
+                                   int k, long long ray_bstride, float* out,
+                                   unsigned flags, void* stream);
+
+/* Message for the calling thread's last non-zero status ("" if none). */
+const char* bvml_dsine_last_error(void);
+
+/* Library version string, e.g. "0.1.0". */
+const char* bvml_dsine_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BVML_DSINE_H */
