@@ -58,9 +58,17 @@ constexpr float kMinXY2 = 1e-20f;
 constexpr float kMinM2 = 1e-16f;
 
 // A pixel is recomputed in double when |acc|^2 < kAccRatio2 * sum(wi^2),
-// wi = prob / |m'| being each term's weight after RayReLU.  fp32 gives each
-// term an error of a few 1e-7; the final normalise divides their sum by |acc|.
-constexpr float kAccRatio2 = 1e-2f;
+// wi = prob / |m'| being each term's weight after RayReLU: each term carries
+// an fp32 error of at most about 3e-7 * wi (measured), their sum is divided
+// by |acc|, so unflagged pixels stay below 3e-7 / sqrt(kAccRatio2) = 7e-6.
+constexpr float kAccRatio2 = 2e-3f;
+
+// The rotation axis is V = m x N, N = D x P0 the normal of the plane through
+// the source pixel's ray P0 and the image-plane step D = (xs/fu, ys/fv, 0);
+// fp32 gives it a relative error of about 1e-7 / sin(m, N).  Where
+// |V| < kAxisK * |D| (sin(m, N) below about kAxisK / 1.3), or |dd| < kDdTau,
+// V and the sign of dd are recomputed in double for that neighbour.
+constexpr float kAxisK2 = 4e-4f;  // kAxisK = 0.02
 
 // ---------------------------------------------------------------------------
 // Double-precision reference body
@@ -170,6 +178,7 @@ struct AngmfArgs {
     int TW, TH, M, tiles_x, tiles_per_img, nblocks;
     float ifu, ifv;    // 1/fu, 1/fv
     float tu_c, tv_c;  // (0.5 - cu)/fu, (0.5 - cv)/fv: source ray tu0 = sx*ifu + tu_c
+    double ifu64, ifv64;
 };
 
 // ---------------------------------------------------------------------------
@@ -281,63 +290,140 @@ __device__ __forceinline__ unsigned long long uniform64(unsigned long long v) {
     return ((unsigned long long)hi << 32) | lo;
 }
 
-// LDS plan of the fp32 kernel, in 16-byte units:
+// 1/sqrt(x) in double: the hardware estimate refined by two Newton steps.
+__device__ __forceinline__ double rsq64(double x) {
+    double y = __builtin_amdgcn_rsq(x);
+    double e = fma(-x * y, y, 1.0);
+    y = fma(0.5 * y, e, y);
+    e = fma(-x * y, y, 1.0);
+    return fma(0.5 * y, e, y);
+}
+
+// sin and cos of t for |t| <= 3.2 in double: the half-angle scheme of
+// sincos_small with degree-17/16 Chebyshev fits (computed for this kernel;
+// sin h to 2e-18, cos h to 2e-17 on |h| <= 1.6).
+__device__ __forceinline__ void sincos_small64(double t, double& st, double& ct) {
+    const double h = 0.5 * t, u = h * h;
+    double p = 2.7284852642995796443e-15;
+    p = fma(u, p, -7.6437284923156877094e-13);
+    p = fma(u, p, 1.6058969595887581407e-10);
+    p = fma(u, p, -2.5052107495717588328e-8);
+    p = fma(u, p, 2.7557319218192719186e-6);
+    p = fma(u, p, -0.00019841269841251311898);
+    p = fma(u, p, 0.0083333333333333107506);
+    p = fma(u, p, -0.16666666666666666622);
+    const double s = fma(h * u, p, h);
+    double q = 4.6220697732871493978e-14;
+    q = fma(u, q, -1.1464231827944265041e-11);
+    q = fma(u, q, 2.087661624946805833e-9);
+    q = fma(u, q, -2.7557317537571715429e-7);
+    q = fma(u, q, 0.000024801587290607644376);
+    q = fma(u, q, -0.0013888888888853772382);
+    q = fma(u, q, 0.041666666666666238695);
+    q = fma(u, q, -0.49999999999999999144);
+    const double c = fma(u, q, 1.0);
+    const double sc = s * c;
+    st = sc + sc;
+    ct = fma(c, c, -(s * s));
+}
+
+// The neighbour term of the double-precision recompute, in the reduced form
+// of the fast path carried out in double (about 1e-15 from the reference).
+// Returns false, leaving the outputs unset, where the reference's clamps,
+// its NaN/Inf handling or the Taylor branch of its rotation could matter --
+// a near-zero or non-finite normal, xy pair or ray, |dd| < 4e-8 (the
+// reference clamps |dd| < 1e-8), or |theta| > 3.2 -- and the caller then runs
+// nbr_ref_f64 instead.
+__device__ __forceinline__ bool nbr_fast_f64(float mxf, float myf, float mzf, int sx, int sy,
+                                             float xsf, float ysf, float thf, float rxf,
+                                             float ryf, float rzf, const AngmfArgs& a,
+                                             double& ox, double& oy, double& oz) {
+    const double mx = mxf, my = myf, mz = mzf, xs = xsf, ys = ysf, t = thf;
+    const double rx = rxf, ry = ryf, rz = rzf;
+    const double m2 = mx * mx + my * my + mz * mz;
+    const double s = xs * xs + ys * ys;
+    const double r2 = rx * rx + ry * ry + rz * rz;
+    if (!(m2 >= 1e-16 && m2 <= 1e30 && s >= 1e-20 && s <= 1e30 && r2 >= 1e-16 &&
+          r2 <= 1e30 && fabs(t) <= 3.2))
+        return false;
+    const double im = rsq64(m2);
+    const double ux = mx * im, uy = my * im, uz = mz * im;
+    const double tu0 = (sx + 0.5 - a.cu) * a.ifu64;
+    const double tv0 = (sy + 0.5 - a.cv) * a.ifv64;
+    const double g = fma(tu0, ux, fma(tv0, uy, uz));
+    const double du = xs * a.ifu64, dv = ys * a.ifv64;
+    const double q = fma(du, ux, dv * uy);
+    const double dd = fma(rsq64(s), q, g);
+    if (!(fabs(dd) >= 4e-8)) return false;
+    const double Vx = fma(g, du, -q * tu0);
+    const double Vy = fma(g, dv, -q * tv0);
+    const double ia = copysign(rsq64(fma(Vx, Vx, fma(Vy, Vy, q * q))), dd);
+    double st, ct;
+    sincos_small64(t, st, ct);
+    const double S = st * ia;
+    const double vx = fma(fma(Vy, uz, q * uy), S, ux * ct);
+    const double vy = fma(fma(-q, ux, -Vx * uz), S, uy * ct);
+    const double vz = fma(fma(Vx, uy, -Vy * ux), S, uz * ct);
+    const double cs = fma(vx, rx, fma(vy, ry, vz * rz)) * rsq64(r2);
+    const double dc = fmax((double)kRayEpsF - cs, 0.0);
+    const double px = fma(rx, dc, vx), py = fma(ry, dc, vy), pz = fma(rz, dc, vz);
+    const double p2 = fma(px, px, fma(py, py, pz * pz));
+    if (!(p2 >= 1e-20)) return false;
+    const double ip = rsq64(p2);
+    ox = px * ip;
+    oy = py * ip;
+    oz = pz * ip;
+    return true;
+}
+
+// The axis of one neighbour in double for the fp32 path, where fp32 cannot
+// be trusted with it (|dd| near 0: its sign flips the axis; m nearly
+// parallel to N: V = m x N loses its relative precision).  Same reduced form,
+// from the raw inputs.  Writes the unit V (times sign(dd)) to V*, and sets
+// `bad` where |dd| or |V| is so small that the reference's 1e-8 / 1e-12
+// clamps can decide the result.
+__device__ __forceinline__ void precise_axis(float mx, float my, float mz, int sx, int sy,
+                                             float xs, float ys, const AngmfArgs& a,
+                                             float& Vx, float& Vy, float& Vz, bool& bad) {
+    const double tu0 = (sx + 0.5 - a.cu) * a.ifu64;
+    const double tv0 = (sy + 0.5 - a.cv) * a.ifv64;
+    const double du = (double)xs * a.ifu64, dv = (double)ys * a.ifv64;
+    const double g = fma(tu0, (double)mx, fma(tv0, (double)my, (double)mz));
+    const double q = fma(du, (double)mx, dv * (double)my);
+    const double s = fma((double)xs, (double)xs, (double)ys * (double)ys);
+    const double dd = fma(rsq64(fmax(s, 1e-24)), q, g);
+    const double vx = fma(g, du, -q * tu0), vy = fma(g, dv, -q * tv0), vz = -q;
+    const double nn = fma(vx, vx, fma(vy, vy, vz * vz));
+    if (!(fabs(dd) >= 4e-8) || !(nn >= 1e-22 * dd * dd)) {
+        bad = true;
+        return;
+    }
+    const double inv = copysign(rsq64(nn), dd);
+    Vx = (float)(vx * inv);
+    Vy = (float)(vy * inv);
+    Vz = (float)(vz * inv);
+}
+
+// LDS of the fp32 kernel, in 16-byte units:
 //   smask[16]        u64 flagged-pixel mask per 64-pixel group (8 units)
-//   rec0[ncell]      (mx, my, mz, g)  unit source normal, g = P0 . m
-//   rec1[ncell]      (mx/fu, my/fv, g/fu, g/fv)
-//   rec2[ncell]      raw source normal (for the double-precision recompute)
-//   sray[64*M]       this tile's rays (rx, ry, rz, 1/max(|r|, 1e-8))
 //   part[K][64*M]    per-window-row fp32 partial (acc.xyz, sum wi^2 or NaN)
 //   fixp[M][K][PPR]  per-window-row fp64 partial of a flagged pixel (3 doubles)
-//   stu[nw], stv[nh] source-column tu0 and source-row tv0
-// ncell = (TH+2P) x (TW+2P) is the replicate-padded source window of the tile.
-struct LdsPlan {
-    int rec0, rec1, rec2, sray, part, fixp, tuv, total;
-};
-
-__host__ __device__ inline LdsPlan lds_plan(int K, int TW, int TH, int M) {
-    const int P = K / 2, nw = TW + 2 * P, nh = TH + 2 * P, ncell = nw * nh, npx = 64 * M;
+__host__ __device__ inline int lds_units(int K, int M) {
     const int ppr = (K <= 8) ? 8 : 4;
-    LdsPlan L;
-    L.rec0 = 8;
-    L.rec1 = L.rec0 + ncell;
-    L.rec2 = L.rec1 + ncell;
-    L.sray = L.rec2 + ncell;
-    L.part = L.sray + npx;
-    L.fixp = L.part + K * npx;
-    L.tuv = L.fixp + (M * K * ppr * 3 + 1) / 2;
-    L.total = L.tuv + (nw + nh + 3) / 4;
-    return L;
+    return 8 + K * 64 * M + (M * K * ppr * 3 + 1) / 2;
 }
 
-// One source cell of the tile window: unit normal, ray products, raw normal.
-__device__ __forceinline__ void stage_cell(const AngmfArgs& a, float4* rec0, float4* rec1,
-                                           float4* rec2, float* stu, float* stv, int i,
-                                           int hy, int hx, int sy, int sx, float mx,
-                                           float my, float mz) {
-    const float tu0 = fmaf((float)sx, a.ifu, a.tu_c);
-    const float tv0 = fmaf((float)sy, a.ifv, a.tv_c);
-    if (hy == 0) stu[hx] = tu0;
-    if (hx == 0) stv[hy] = tv0;
-    const float m2 = fmaf(mx, mx, fmaf(my, my, mz * mz));
-    // Degenerate or non-finite normals become m = 0, g = 0: every neighbour
-    // that reads them then has dd == 0 and is flagged.
-    const bool ok = (m2 >= kMinM2) && (m2 <= 1e30f);
-    const float inv = rsq(ok ? m2 : 1.0f);
-    const float ux = ok ? mx * inv : 0.0f;
-    const float uy = ok ? my * inv : 0.0f;
-    const float uz = ok ? mz * inv : 0.0f;
-    const float g = fmaf(tu0, ux, fmaf(tv0, uy, uz));
-    rec0[i] = make_float4(ux, uy, uz, g);
-    rec1[i] = make_float4(ux * a.ifu, uy * a.ifv, g * a.ifu, g * a.ifv);
-    rec2[i] = make_float4(mx, my, mz, 0.0f);
-}
-
-// Occupancy target: 16 waves per CU hold one 16-wave block; k = 5 needs 20
-// (two 10-wave blocks, the 256x256 shape in one round), i.e. <= 96 VGPRs.
+// Occupancy target: k = 5 runs two 10-wave workgroups per CU (the 256x256
+// shape in a single round), which needs 20 waves per CU, i.e. <= 96 VGPRs.
 template <int K>
 constexpr int kWavesPerEU = (K == 5) ? 5 : 4;
 
+// One workgroup = M groups of 64 output pixels (a TW x TH tile of one
+// sample) x K waves, wave (ky, group) handling window row ky of one pixel per
+// lane.  Each lane loads the row's K source normals (L1/L2 hits: the window
+// rows of neighbouring pixels overlap) and the 4K per-neighbour planes, in the
+// order it consumes them, and accumulates the row's fp32 partial; the K
+// partials meet in LDS.
 template <int K>
 __global__ __launch_bounds__(64 * K * (16 / K))
 __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(AngmfArgs a) {
@@ -346,18 +432,10 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(Angmf
     constexpr int PPR = 64 / LPG;           // flagged pixels per recompute pass
     extern __shared__ float4 smem[];
     const int TW = a.TW, TH = a.TH, M = a.M;
-    const int nw = TW + 2 * P, nh = TH + 2 * P, ncell = nw * nh;
     const int npx = 64 * M;
-    const LdsPlan L = lds_plan(K, TW, TH, M);
     unsigned long long* smask = reinterpret_cast<unsigned long long*>(smem);
-    float4* rec0 = smem + L.rec0;
-    float4* rec1 = smem + L.rec1;
-    float4* rec2 = smem + L.rec2;
-    float4* sray = smem + L.sray;
-    float4* part = smem + L.part;
-    double* fixp = reinterpret_cast<double*>(smem + L.fixp);
-    float* stu = reinterpret_cast<float*>(smem + L.tuv);
-    float* stv = stu + nw;
+    float4* part = smem + 8;
+    double* fixp = reinterpret_cast<double*>(part + K * npx);
 
     const int lb = xcd_remap(blockIdx.x, a.nblocks);
     const int b = lb / a.tiles_per_img;
@@ -373,9 +451,7 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(Angmf
     const float* rp = a.ray + (size_t)b * a.ray_bstride;
     float* op = a.out + (size_t)b * 3 * HW;
     const int W = a.W, H = a.H;
-    const int nthr = (int)blockDim.x;
 
-    // ---- this lane's pixel and window row ----------------------------------
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
     const int ky = __builtin_amdgcn_readfirstlane(wave / M);
@@ -386,124 +462,79 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(Angmf
     const bool valid = (ty < TH) && (y < H) && (x < W);
     const uint32_t pb = valid ? (uint32_t)(y * W + x) * 4u : 0u;
 
-    // ---- prologue: loads in the order they are needed --------------------
-    // (vmcnt retires in order, so the window loads go first and the 4K
-    // row loads, consumed last, stay in flight through the staging math).
-    const int c0 = threadIdx.x, c1 = threadIdx.x + nthr;
-    int hy0 = 0, hx0 = 0, sy0 = 0, sx0 = 0, hy1 = 0, hx1 = 0, sy1 = 0, sx1 = 0;
-    float m0x = 0.f, m0y = 0.f, m0z = 0.f, m1x = 0.f, m1y = 0.f, m1z = 0.f;
-    if (c0 < ncell) {
-        hy0 = c0 / nw;
-        hx0 = c0 - hy0 * nw;
-        sy0 = clampi(ty0 - P + hy0, 0, H - 1);
-        sx0 = clampi(tx0 - P + hx0, 0, W - 1);
-        const uint32_t sb = (uint32_t)(sy0 * W + sx0) * 4u;
-        m0x = ldf(pn, sb);
-        m0y = ldf(pn + HW, sb);
-        m0z = ldf(pn + 2 * HW, sb);
-    }
-    if (c1 < ncell) {
-        hy1 = c1 / nw;
-        hx1 = c1 - hy1 * nw;
-        sy1 = clampi(ty0 - P + hy1, 0, H - 1);
-        sx1 = clampi(tx0 - P + hx1, 0, W - 1);
-        const uint32_t sb = (uint32_t)(sy1 * W + sx1) * 4u;
-        m1x = ldf(pn, sb);
-        m1y = ldf(pn + HW, sb);
-        m1z = ldf(pn + 2 * HW, sb);
-    }
-    float4 rv = make_float4(0.f, 0.f, 0.f, 0.f);
-    bool rvalid = false;
-    if (threadIdx.x < npx) {
-        const int ity = threadIdx.x / TW, itx = threadIdx.x - ity * TW;
-        const int iy = ty0 + ity, ix = tx0 + itx;
-        rvalid = ity < TH && iy < H && ix < W;
-        if (rvalid) {
-            const uint32_t ib = (uint32_t)(iy * W + ix) * 4u;
-            rv.x = ldf(rp, ib);
-            rv.y = ldf(rp + HW, ib);
-            rv.z = ldf(rp + 2 * HW, ib);
-        }
-    }
-    float xs[K], ys[K], th[K], wt[K];
-#pragma unroll
-    for (int kx = 0; kx < K; ++kx) xs[kx] = ys[kx] = th[kx] = wt[kx] = 0.f;
+    // ---- phase A: window row ky of this lane's pixel, fp32 -----------------
+    float4 res = make_float4(0.f, 0.f, 0.f, 0.f);
     if (valid) {
+        const int sy = clampi(y - P + ky, 0, H - 1);
+        const uint32_t rowb = (uint32_t)(sy * W);
+        // loads in consumption order: ray, then per neighbour its source
+        // normal and its 4 planes
+        const float rx = ldf(rp, pb), ry = ldf(rp + HW, pb), rz = ldf(rp + 2 * HW, pb);
+        float mxs[K], mys[K], mzs[K], xs[K], ys[K], th[K], wt[K];
         const size_t n0 = (size_t)ky * K;
         const uint32_t pbytes = (uint32_t)HW * 4u;
 #pragma unroll
         for (int kx = 0; kx < K; ++kx) {
+            const uint32_t sb = (rowb + (uint32_t)clampi(x - P + kx, 0, W - 1)) * 4u;
+            mxs[kx] = ldf(pn, sb);
+            mys[kx] = ldf(pn + HW, sb);
+            mzs[kx] = ldf(pn + 2 * HW, sb);
             xs[kx] = ldb(plane_rsrc(xyp + (n0 + kx) * HW, pbytes), pb);
             ys[kx] = ldb(plane_rsrc(xyp + (K2 + n0 + kx) * HW, pbytes), pb);
             th[kx] = ldb(plane_rsrc(ap + (n0 + kx) * HW, pbytes), pb);
             wt[kx] = ldb(plane_rsrc(pr + (n0 + kx) * HW, pbytes), pb);
         }
-    }
-
-    // ---- stage the tile's source window and rays --------------------------
-    if (c0 < ncell) stage_cell(a, rec0, rec1, rec2, stu, stv, c0, hy0, hx0, sy0, sx0, m0x, m0y, m0z);
-    if (c1 < ncell) stage_cell(a, rec0, rec1, rec2, stu, stv, c1, hy1, hx1, sy1, sx1, m1x, m1y, m1z);
-    for (int i = c0 + 2 * nthr; i < ncell; i += nthr) {
-        const int hy = i / nw, hx = i - hy * nw;
-        const int sy = clampi(ty0 - P + hy, 0, H - 1), sx = clampi(tx0 - P + hx, 0, W - 1);
-        const uint32_t sb = (uint32_t)(sy * W + sx) * 4u;
-        stage_cell(a, rec0, rec1, rec2, stu, stv, i, hy, hx, sy, sx, ldf(pn, sb),
-                   ldf(pn + HW, sb), ldf(pn + 2 * HW, sb));
-    }
-    if (threadIdx.x < npx) {
         // cos(v', r) = v'.r / max(|v'||r|, 1e-8) with |v'| = 1
-        if (rvalid)
-            rv.w = 1.0f / fmaxf(sqrtf(fmaf(rv.x, rv.x, fmaf(rv.y, rv.y, rv.z * rv.z))), 1e-8f);
-        sray[threadIdx.x] = rv;
-    }
-    __syncthreads();
-
-    // ---- phase A: one window row (ky) of one pixel per lane, fp32 ----------
-    float4 res = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (valid) {
-        const float4 r = sray[j];
-        const float rsx = r.x * r.w, rsy = r.y * r.w, rsz = r.z * r.w;
-        const float tv0 = stv[ty + ky];
-        const int cb = (ty + ky) * nw + tx;
+        const float ir = 1.0f / fmaxf(sqrtf(fmaf(rx, rx, fmaf(ry, ry, rz * rz))), 1e-8f);
+        const float rsx = rx * ir, rsy = ry * ir, rsz = rz * ir;
+        const float tv0 = fmaf((float)sy, a.ifv, a.tv_c);
         float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, q2 = 0.f;
         bool bad = false;
 #pragma unroll
         for (int kx = 0; kx < K; ++kx) {
-            const float4 r0 = rec0[cb + kx];
-            const float4 r1 = rec1[cb + kx];
-            const float tu0 = stu[tx + kx];
+            const int sx = clampi(x - P + kx, 0, W - 1);
+            const float tu0 = fmaf((float)sx, a.ifu, a.tu_c);
+            const float mx = mxs[kx], my = mys[kx], mz = mzs[kx];
             const float xsv = xs[kx], ysv = ys[kx], t = th[kx];
-
-            // axis = sign(dd) * V/|V|
+            // The fast path takes unit source normals (every normal this op
+            // or RayReLU writes is one); others go to the double path.
+            const float m2 = fmaf(mx, mx, fmaf(my, my, mz * mz));
+            const float g = fmaf(tu0, mx, fmaf(tv0, my, mz));  // P0 . m
+            const float du = xsv * a.ifu, dv = ysv * a.ifv;
+            const float q = fmaf(du, mx, dv * my);
             const float s = fmaf(xsv, xsv, ysv * ysv);
-            const float lam = rsq(fmaxf(s, 1e-24f));
-            const float q = fmaf(xsv, r1.x, ysv * r1.y);
-            const float dd = fmaf(lam, q, r0.w);
-            bad |= !(fabsf(dd) >= kDdTau) | (s < kMinXY2) | !(fabsf(t) <= 3.2f);
-            const float Vx = fmaf(r1.z, xsv, -q * tu0);
-            const float Vy = fmaf(r1.w, ysv, -q * tv0);
-            const float n2 = fmaf(Vx, Vx, fmaf(Vy, Vy, q * q));
-            const float ia = copysignf(rsq(n2), dd);
+            const float dd = fmaf(rsq(fmaxf(s, 1e-24f)), q, g);
+            bad |= !(fabsf(m2 - 1.0f) <= 1e-5f) | (s < kMinXY2) | !(fabsf(t) <= 3.2f);
+            // axis = sign(dd) * V/|V|,  V = (g du - q tu0, g dv - q tv0, -q) = m x N
+            float Vx = fmaf(g, du, -q * tu0);
+            float Vy = fmaf(g, dv, -q * tv0);
+            float Vz = -q;
+            float n2 = fmaf(Vx, Vx, fmaf(Vy, Vy, q * q));
+            float sg = dd;
+            if (__builtin_expect(!(fabsf(dd) >= kDdTau) | !(n2 >= kAxisK2 * fmaf(du, du, dv * dv)),
+                                 0)) {
+                precise_axis(mx, my, mz, sx, sy, xsv, ysv, a, Vx, Vy, Vz, bad);
+                n2 = 1.0f;
+                sg = 1.0f;
+            }
+            const float ia = copysignf(rsq(n2), sg);
             float st, ct;
             sincos_small(t, st, ct);
             const float S = st * ia;
-            // v' = m cos(t) + (V x m) sin(t)/|V|,  V = (Vx, Vy, -q)
-            const float cx = fmaf(Vy, r0.z, q * r0.y);
-            const float cy = fmaf(-q, r0.x, -Vx * r0.z);
-            const float cz = fmaf(Vx, r0.y, -Vy * r0.x);
-            const float vx = fmaf(cx, S, r0.x * ct);
-            const float vy = fmaf(cy, S, r0.y * ct);
-            const float vz = fmaf(cz, S, r0.z * ct);
+            // v' = m cos(t) + (V x m) sin(t)/|V|
+            const float vx = fmaf(fmaf(Vy, mz, -Vz * my), S, mx * ct);
+            const float vy = fmaf(fmaf(Vz, mx, -Vx * mz), S, my * ct);
+            const float vz = fmaf(fmaf(Vx, my, -Vy * mx), S, mz * ct);
             // RayReLU against this pixel's ray
             const float cs = fmaf(vx, rsx, fmaf(vy, rsy, vz * rsz));
             const float dc = fmaxf(kRayEpsF - cs, 0.0f);
-            const float mx = fmaf(r.x, dc, vx);
-            const float my = fmaf(r.y, dc, vy);
-            const float mz = fmaf(r.z, dc, vz);
-            const float wi = wt[kx] * rsq(fmaf(mx, mx, fmaf(my, my, mz * mz)));
-            acc0 = fmaf(mx, wi, acc0);
-            acc1 = fmaf(my, wi, acc1);
-            acc2 = fmaf(mz, wi, acc2);
+            const float px = fmaf(rx, dc, vx);
+            const float py = fmaf(ry, dc, vy);
+            const float pz = fmaf(rz, dc, vz);
+            const float wi = wt[kx] * rsq(fmaf(px, px, fmaf(py, py, pz * pz)));
+            acc0 = fmaf(px, wi, acc0);
+            acc1 = fmaf(py, wi, acc1);
+            acc2 = fmaf(pz, wi, acc2);
             q2 = fmaf(wi, wi, q2);
         }
         res = make_float4(acc0, acc1, acc2, bad ? __builtin_nanf("") : q2);
@@ -539,11 +570,10 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(Angmf
     __syncthreads();
 
     // ---- phase C: double-precision recompute of flagged pixels -------------
-    // Each wave (gi, ky) evaluates row ky of up to PPR flagged pixels of its
-    // group per pass, one neighbour per lane, in the reference's operation
-    // order (source normals and rays from the LDS window, the per-neighbour
-    // planes re-read from L2).  Row partials meet in LDS and the ky == 0 wave
-    // writes the pixel.
+    // Each wave (group, ky) evaluates row ky of up to PPR flagged pixels of
+    // its group per pass, one neighbour per lane (inputs re-read; the block
+    // has just read them, so from L2); row partials meet in LDS and the
+    // ky == 0 wave writes the pixel.
     int maxc = 0;
     for (int g = 0; g < M; ++g) {
         const int c = __popcll(uniform64(smask[g]));
@@ -563,26 +593,25 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(Angmf
             if (sidx == slot) src = bitpos;
             if (sidx == lane) fin_src = bitpos;
         }
-        const bool has = (base + slot) < cnt && kxl < K;
         double p0 = 0.0, p1 = 0.0, p2 = 0.0;
-        if (has) {
+        if ((base + slot) < cnt && kxl < K) {
             const int jj = gi * 64 + src;
             const int fty = jj / TW, ftx = jj - fty * TW;
-            // this neighbour's inputs, re-read (the block just read them: L2)
-            const uint32_t fb = (uint32_t)((ty0 + fty) * W + tx0 + ftx) * 4u;
+            const int fy = ty0 + fty, fx = tx0 + ftx;
+            const int sy = clampi(fy - P + ky, 0, H - 1);
+            const int sx = clampi(fx - P + kxl, 0, W - 1);
+            const uint32_t fb = (uint32_t)(fy * W + fx) * 4u;
+            const uint32_t sb = (uint32_t)(sy * W + sx) * 4u;
             const size_t n = (size_t)ky * K + kxl;
-            const float fxs = ldf(xyp + n * HW, fb);
-            const float fys = ldf(xyp + (K2 + n) * HW, fb);
-            const float fth = ldf(ap + n * HW, fb);
-            const float fwt = ldf(pr + n * HW, fb);
-            const int sy = clampi(ty0 + fty - P + ky, 0, H - 1);
-            const int sx = clampi(tx0 + ftx - P + kxl, 0, W - 1);
-            const float4 m = rec2[(fty + ky) * nw + ftx + kxl];
-            const float4 r = sray[jj];
+            const float mx = ldf(pn, sb), my = ldf(pn + HW, sb), mz = ldf(pn + 2 * HW, sb);
+            const float xsv = ldf(xyp + n * HW, fb), ysv = ldf(xyp + (K2 + n) * HW, fb);
+            const float thv = ldf(ap + n * HW, fb), wv = ldf(pr + n * HW, fb);
+            const float rx = ldf(rp, fb), ry = ldf(rp + HW, fb), rz = ldf(rp + 2 * HW, fb);
             double ox, oy, oz;
-            nbr_ref_f64(m.x, m.y, m.z, sx + 0.5, sy + 0.5, fxs, fys, fth, r.x, r.y, r.z,
-                        a.fu, a.cu, a.fv, a.cv, ox, oy, oz);
-            const double w = fwt;
+            if (!nbr_fast_f64(mx, my, mz, sx, sy, xsv, ysv, thv, rx, ry, rz, a, ox, oy, oz))
+                nbr_ref_f64(mx, my, mz, sx + 0.5, sy + 0.5, xsv, ysv, thv, rx, ry, rz, a.fu,
+                            a.cu, a.fv, a.cv, ox, oy, oz);
+            const double w = wv;
             p0 = w * ox;
             p1 = w * oy;
             p2 = w * oz;
@@ -671,7 +700,7 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
         hipLaunchKernelGGL(angmf_f64_kernel<K>, dim3((unsigned)grid), dim3(256), 0, s, a);
         return hipGetLastError();
     }
-    const size_t lds = (size_t)lds_plan(K, a.TW, a.TH, a.M).total * 16;
+    const size_t lds = (size_t)lds_units(K, a.M) * 16;
     hipLaunchKernelGGL(angmf_f32_kernel<K>, dim3((unsigned)a.nblocks), dim3(64 * a.M * K),
                        lds, s, a);
     return hipGetLastError();
@@ -777,6 +806,8 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
     a.HW = HW; a.B = B; a.H = H; a.W = W;
     a.ifu = (float)(1.0 / fu);
     a.ifv = (float)(1.0 / fv);
+    a.ifu64 = 1.0 / fu;
+    a.ifv64 = 1.0 / fv;
     a.tu_c = (float)((0.5 - cu) / fu);
     a.tv_c = (float)((0.5 - cv) / fv);
     choose_tile(a, k);
