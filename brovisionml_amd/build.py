@@ -32,7 +32,9 @@ HIP_FLAGS = [
 ]
 
 SOURCES = [
-    os.path.join(CSRC, "dsine_ops.hip"),
+    os.path.join(CSRC, "dsine_ops.hip"),   # kernels + C ABI
+    os.path.join(CSRC, "dsine_ops.cpp"),   # C++ drop-in (brovisionml::dsine)
+    os.path.join(CSRC, "tensor.cpp"),      # brotensor::Tensor subset
 ]
 
 

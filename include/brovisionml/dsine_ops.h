@@ -1,0 +1,60 @@
+#pragma once
+
+// DSINE NRN device ops on MI355X (gfx950) -- drop-in for brovisionml's
+// include/brovisionml/dsine_ops.h:17-56: the same namespace, names and
+// signatures, so src/dsine_refine.cpp:242 and :271-272 compile against it
+// unchanged.  Tensors are (1, C*H*W) fp32 NCHW on the HIP device; both ops
+// are asynchronous on the null stream, like the reference's default-stream
+// launches (src/dsine_ops.cu:2-4).
+//
+// Errors throw std::runtime_error prefixed "dsine ops: " (argument and device
+// checks, src/dsine_ops.cpp:18-22) or "dsine hip: " (a HIP runtime error at
+// launch; the reference's "dsine cuda: ", src/dsine_ops.cu:25-29).  Tensors
+// on the CPU throw: this library is the device path; brovisionml's CPU twin
+// (src/dsine_ops.cpp:55-172) stays where it is.
+
+#include "brotensor/tensor.h"
+
+namespace brovisionml::dsine {
+
+// RayReLU (eps 1e-2) of a (1, 3*H*W) unit-normal map against the L2-normalised
+// 3-channel ray_8, in place -- include/brovisionml/dsine_ops.h:19-26.
+void ray_relu(brotensor::Tensor& normal, const brotensor::Tensor& ray,
+              int H, int W);
+
+// Fused AngMF propagate over the 5x5 window -- include/brovisionml/dsine_ops.h:28-54.
+//   pred_norm (1, 3HW), prob (1, 25HW) sigmoid(prob_head), xy (1, 50HW) raw
+//   [xs(25), ys(25)], angle (1, 25HW) sigmoid(angle_head)*pi, ray (1, 3HW);
+//   fu, cu, fv, cv the grid-scaled intrinsics (src/dsine_refine.cpp:232-237).
+// `out` becomes (1, 3HW) on the device: its buffer is reused when it already
+// has that shape on the device and does not alias an input, else (re)allocated
+// (the reference allocates a zeroed one per call, src/dsine_ops.cu:178).
+void angmf_propagate(const brotensor::Tensor& pred_norm,
+                     const brotensor::Tensor& prob,
+                     const brotensor::Tensor& xy,
+                     const brotensor::Tensor& angle,
+                     const brotensor::Tensor& ray,
+                     double fu, double cu, double fv, double cv,
+                     int H, int W,
+                     brotensor::Tensor& out);
+
+namespace detail {
+
+// The launchers the dispatch above calls; they replace
+// detail::ray_relu_cuda / detail::angmf_propagate_cuda (src/dsine_ops_cuda.h:13-23)
+// with the same parameter lists and forward to the C ABI (include/bvml_dsine.h).
+void ray_relu_gpu(brotensor::Tensor& normal, const brotensor::Tensor& ray,
+                  int H, int W);
+
+void angmf_propagate_gpu(const brotensor::Tensor& pred_norm,
+                         const brotensor::Tensor& prob,
+                         const brotensor::Tensor& xy,
+                         const brotensor::Tensor& angle,
+                         const brotensor::Tensor& ray,
+                         double fu, double cu, double fv, double cv,
+                         int H, int W,
+                         brotensor::Tensor& out);
+
+}  // namespace detail
+
+}  // namespace brovisionml::dsine

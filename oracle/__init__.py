@@ -4,43 +4,22 @@ ctypes binding of oracle/_build/liboracle_dsine.so, the double-precision C
 restatement of brovisionml's CPU twin (src/dsine_ops.cpp:24-172).  Only the
 tests, the smoke check and the CPU-baseline leg of the benchmark may use it,
 as the checker or the timed CPU reference; the product never does.
+
+`Oracle(path)` binds any build of oracle/dsine_ops_oracle.c (the mutation
+test loads deliberately broken ones); the module-level functions use the
+default build.
 """
 from __future__ import annotations
 
 import ctypes
 import os
+import subprocess
 
 import numpy as np
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 LIB = os.path.join(HERE, "_build", "liboracle_dsine.so")
-
-_lib = None
-
-
-def load() -> ctypes.CDLL:
-    global _lib
-    if _lib is not None:
-        return _lib
-    if not os.path.exists(LIB):
-        raise RuntimeError(f"oracle library {LIB} missing; run `make -C oracle`")
-    lib = ctypes.CDLL(LIB)
-    vp, i, ll, d = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_double
-    lib.oracle_axis_angle_to_matrix.argtypes = [d, d, d, vp]
-    lib.oracle_axis_angle_to_matrix.restype = None
-    lib.oracle_axis.argtypes = [d] * 11 + [vp]
-    lib.oracle_axis.restype = None
-    lib.oracle_ray_relu_vec.argtypes = [d] * 6 + [vp]
-    lib.oracle_ray_relu_vec.restype = None
-    lib.oracle_neighbour.argtypes = [d] * 15 + [vp]
-    lib.oracle_neighbour.restype = None
-    lib.oracle_ray_relu_f32.argtypes = [vp, vp, i, i, i, ll]
-    lib.oracle_ray_relu_f32.restype = None
-    lib.oracle_angmf_propagate_rows_f32.argtypes = [
-        vp, vp, vp, vp, vp, d, d, d, d, i, i, i, i, ll, vp, vp, i, i, i]
-    lib.oracle_angmf_propagate_rows_f32.restype = None
-    _lib = lib
-    return lib
+SOURCE = os.path.join(HERE, "dsine_ops_oracle.c")
 
 
 def _ptr(a: np.ndarray) -> int:
@@ -48,65 +27,127 @@ def _ptr(a: np.ndarray) -> int:
 
 
 def _f32c(a) -> np.ndarray:
-    a = np.ascontiguousarray(a, dtype=np.float32)
-    return a
+    return np.ascontiguousarray(a, dtype=np.float32)
 
 
-def axis_angle_to_matrix(v) -> np.ndarray:
-    R = np.zeros(9, dtype=np.float64)
-    load().oracle_axis_angle_to_matrix(float(v[0]), float(v[1]), float(v[2]), _ptr(R))
-    return R.reshape(3, 3)
+def compile_variant(out_path: str, mutation: int = 0) -> str:
+    """Build the oracle with ORACLE_MUTATION=mutation into out_path (gcc, the
+    flags of oracle/Makefile)."""
+    subprocess.run(["gcc", "-O2", "-std=c11", "-fPIC", "-ffp-contract=off", "-fno-fast-math",
+                    "-fopenmp", "-shared", f"-DORACLE_MUTATION={mutation}", "-o", out_path,
+                    SOURCE, "-lm"], check=True)
+    return out_path
 
 
-def axis(n, pix, xy, intr) -> np.ndarray:
-    a = np.zeros(3, dtype=np.float64)
-    fu, cu, fv, cv = intr
-    load().oracle_axis(float(n[0]), float(n[1]), float(n[2]), float(pix[0]), float(pix[1]),
-                       float(xy[0]), float(xy[1]), fu, cu, fv, cv, _ptr(a))
-    return a
+class Oracle:
+    def __init__(self, path: str = LIB):
+        if not os.path.exists(path):
+            raise RuntimeError(f"oracle library {path} missing; run `make -C oracle`")
+        lib = ctypes.CDLL(path)
+        vp, i, ll, d = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_double
+        lib.oracle_axis_angle_to_matrix.argtypes = [d, d, d, vp]
+        lib.oracle_axis_angle_to_matrix.restype = None
+        lib.oracle_axis.argtypes = [d] * 11 + [vp]
+        lib.oracle_axis.restype = None
+        lib.oracle_ray_relu_vec.argtypes = [d] * 6 + [vp]
+        lib.oracle_ray_relu_vec.restype = None
+        lib.oracle_neighbour.argtypes = [d] * 15 + [vp]
+        lib.oracle_neighbour.restype = None
+        lib.oracle_ray_relu_f32.argtypes = [vp, vp, i, i, i, ll]
+        lib.oracle_ray_relu_f32.restype = None
+        lib.oracle_angmf_propagate_rows_f32.argtypes = [
+            vp, vp, vp, vp, vp, d, d, d, d, i, i, i, i, ll, vp, vp, i, i, i]
+        lib.oracle_angmf_propagate_rows_f32.restype = None
+        self.lib = lib
+
+    def axis_angle_to_matrix(self, v) -> np.ndarray:
+        R = np.zeros(9, dtype=np.float64)
+        self.lib.oracle_axis_angle_to_matrix(float(v[0]), float(v[1]), float(v[2]), _ptr(R))
+        return R.reshape(3, 3)
+
+    def axis(self, n, pix, xy, intr) -> np.ndarray:
+        a = np.zeros(3, dtype=np.float64)
+        fu, cu, fv, cv = intr
+        self.lib.oracle_axis(float(n[0]), float(n[1]), float(n[2]), float(pix[0]),
+                             float(pix[1]), float(xy[0]), float(xy[1]), fu, cu, fv, cv, _ptr(a))
+        return a
+
+    def ray_relu_vec(self, n, r) -> np.ndarray:
+        o = np.zeros(3, dtype=np.float64)
+        self.lib.oracle_ray_relu_vec(*(float(v) for v in n), *(float(v) for v in r), _ptr(o))
+        return o
+
+    def neighbour(self, n, pix, xy, theta, r, intr) -> np.ndarray:
+        o = np.zeros(3, dtype=np.float64)
+        fu, cu, fv, cv = intr
+        self.lib.oracle_neighbour(float(n[0]), float(n[1]), float(n[2]), float(pix[0]),
+                                  float(pix[1]), float(xy[0]), float(xy[1]), float(theta),
+                                  float(r[0]), float(r[1]), float(r[2]), fu, cu, fv, cv, _ptr(o))
+        return o
+
+    def ray_relu(self, normal, ray, H: int, W: int) -> np.ndarray:
+        """RayReLU(normal) as a new float32 array of normal's shape.
+        ray: 3*H*W (shared) or B*3*H*W (per sample)."""
+        n = _f32c(normal).copy()
+        r = _f32c(ray)
+        HW = H * W
+        B = n.size // (3 * HW) if HW else 0
+        bstride = 0 if r.size == 3 * HW else 3 * HW
+        self.lib.oracle_ray_relu_f32(_ptr(n), _ptr(r), B, H, W, bstride)
+        return n
+
+    def angmf_propagate(self, pred_norm, prob, xy, angle, ray, intr, H: int, W: int,
+                        k: int = 5, rows=None, nthreads: int = 1, return_acc: bool = False):
+        """angmf_propagate over all B samples (inferred from pred_norm).
+        rows=(y0, y1) limits the output rows computed (others stay NaN).
+        Returns out (float32, pred_norm's shape) [and the double accumulator]."""
+        pn, pr, xyp, ap, rp = (_f32c(a) for a in (pred_norm, prob, xy, angle, ray))
+        HW = H * W
+        B = pn.size // (3 * HW)
+        bstride = 0 if rp.size == 3 * HW else 3 * HW
+        out = np.full(pn.shape, np.nan, dtype=np.float32)
+        acc = np.full(pn.shape, np.nan, dtype=np.float64) if return_acc else None
+        y0, y1 = rows if rows is not None else (0, H)
+        fu, cu, fv, cv = intr
+        self.lib.oracle_angmf_propagate_rows_f32(
+            _ptr(pn), _ptr(pr), _ptr(xyp), _ptr(ap), _ptr(rp), fu, cu, fv, cv, B, H, W, k,
+            bstride, _ptr(out), _ptr(acc) if acc is not None else None, y0, y1, nthreads)
+        return (out, acc) if return_acc else out
 
 
-def ray_relu_vec(n, r) -> np.ndarray:
-    o = np.zeros(3, dtype=np.float64)
-    load().oracle_ray_relu_vec(*(float(v) for v in n), *(float(v) for v in r), _ptr(o))
-    return o
+_default = None
 
 
-def neighbour(n, pix, xy, theta, r, intr) -> np.ndarray:
-    o = np.zeros(3, dtype=np.float64)
-    fu, cu, fv, cv = intr
-    load().oracle_neighbour(float(n[0]), float(n[1]), float(n[2]), float(pix[0]),
-                            float(pix[1]), float(xy[0]), float(xy[1]), float(theta),
-                            float(r[0]), float(r[1]), float(r[2]), fu, cu, fv, cv, _ptr(o))
-    return o
+def default() -> Oracle:
+    global _default
+    if _default is None:
+        _default = Oracle(LIB)
+    return _default
 
 
-def ray_relu(normal: np.ndarray, ray: np.ndarray, H: int, W: int) -> np.ndarray:
-    """Returns RayReLU(normal) (a new float32 array of normal's shape).
-    ray: 3*H*W (shared) or B*3*H*W (per sample)."""
-    n = _f32c(normal).copy()
-    r = _f32c(ray)
-    HW = H * W
-    B = n.size // (3 * HW) if HW else 0
-    bstride = 0 if r.size == 3 * HW else 3 * HW
-    load().oracle_ray_relu_f32(_ptr(n), _ptr(r), B, H, W, bstride)
-    return n
+def load():
+    return default().lib
 
 
-def angmf_propagate(pred_norm, prob, xy, angle, ray, intr, H: int, W: int, k: int = 5,
-                    rows=None, nthreads: int = 1, return_acc: bool = False):
-    """Oracle angmf_propagate over all B samples (inferred from pred_norm).
-    rows=(y0, y1) limits the output rows computed (others stay NaN).
-    Returns out (float32, pred_norm's shape) [and the double accumulator]."""
-    pn, pr, xyp, ap, rp = (_f32c(a) for a in (pred_norm, prob, xy, angle, ray))
-    HW = H * W
-    B = pn.size // (3 * HW)
-    bstride = 0 if rp.size == 3 * HW else 3 * HW
-    out = np.full(pn.shape, np.nan, dtype=np.float32)
-    acc = np.full(pn.shape, np.nan, dtype=np.float64) if return_acc else None
-    y0, y1 = rows if rows is not None else (0, H)
-    fu, cu, fv, cv = intr
-    load().oracle_angmf_propagate_rows_f32(
-        _ptr(pn), _ptr(pr), _ptr(xyp), _ptr(ap), _ptr(rp), fu, cu, fv, cv, B, H, W, k,
-        bstride, _ptr(out), _ptr(acc) if acc is not None else None, y0, y1, nthreads)
-    return (out, acc) if return_acc else out
+def axis_angle_to_matrix(v):
+    return default().axis_angle_to_matrix(v)
+
+
+def axis(n, pix, xy, intr):
+    return default().axis(n, pix, xy, intr)
+
+
+def ray_relu_vec(n, r):
+    return default().ray_relu_vec(n, r)
+
+
+def neighbour(n, pix, xy, theta, r, intr):
+    return default().neighbour(n, pix, xy, theta, r, intr)
+
+
+def ray_relu(normal, ray, H, W):
+    return default().ray_relu(normal, ray, H, W)
+
+
+def angmf_propagate(*args, **kwargs):
+    return default().angmf_propagate(*args, **kwargs)

@@ -29,9 +29,20 @@
 #include <stddef.h>
 #include <stdint.h>
 
+/* ORACLE_MUTATION (default 0) plants one deliberate mistake for the
+ * mutation test (tests/test_oracle_pins.py), which checks that the pins
+ * catch it; the oracle used everywhere else is built with 0. */
+#ifndef ORACLE_MUTATION
+#define ORACLE_MUTATION 0
+#endif
+
 /* src/dsine_ops.cpp:27 -- constexpr float kRayEps = 1e-2f, used in double
  * expressions, so the effective constant is (double)1e-2f. */
+#if ORACLE_MUTATION == 5
+static const double kRayEpsF = 1e-2; /* mutation: the CUDA twin's double eps */
+#else
 static const float kRayEpsF = 1e-2f;
+#endif
 
 /* std::max(a, b) == (a < b) ? b : a */
 static inline double smax(double a, double b) { return (a < b) ? b : a; }
@@ -53,9 +64,15 @@ void oracle_axis_angle_to_matrix(double ax, double ay, double az, double R[9])
     const double i = ax * s, j = ay * s, k = az * s;
     const double two_s = 2.0 / (r * r + i * i + j * j + k * k);
     R[0] = 1.0 - two_s * (j * j + k * k);
+#if ORACLE_MUTATION == 1 /* mutation: transposed R */
+    R[3] = two_s * (i * j - k * r);
+    R[2] = two_s * (i * k + j * r);
+    R[1] = two_s * (i * j + k * r);
+#else
     R[1] = two_s * (i * j - k * r);
     R[2] = two_s * (i * k + j * r);
     R[3] = two_s * (i * j + k * r);
+#endif
     R[4] = 1.0 - two_s * (i * i + k * k);
     R[5] = two_s * (j * k - i * r);
     R[6] = two_s * (i * k - j * r);
@@ -77,10 +94,18 @@ void oracle_axis(double nx, double ny, double nz, double pix_x, double pix_y,
     const double dv_over_fv = ys / fv;
     const double term_u = (pix_x + xs - cu) / fu;
     const double term_v = (pix_y + ys - cv) / fv;
+#if ORACLE_MUTATION == 2 /* mutation: sign of num */
+    const double num = (du_over_fu * nx + dv_over_fv * ny);
+#else
     const double num = -(du_over_fu * nx + dv_over_fv * ny);
+#endif
     double dd = term_u * nx + term_v * ny + nz;
     if (fabs(dd) < 1e-8) {
+#if ORACLE_MUTATION == 6 /* mutation: sgn(0) = +1 */
+        const double sgn = (dd >= 0.0) ? 1.0 : -1.0;
+#else
         const double sgn = (dd > 0.0) ? 1.0 : (dd < 0.0 ? -1.0 : 0.0);
+#endif
         dd = 1e-8 * sgn;
     }
     const double dz = num / dd;
@@ -128,8 +153,12 @@ void oracle_neighbour(double nx, double ny, double nz, double pix_x,
     double rnx = R[0] * nx + R[1] * ny + R[2] * nz;
     double rny = R[3] * nx + R[4] * ny + R[5] * nz;
     double rnz = R[6] * nx + R[7] * ny + R[8] * nz;
+#if ORACLE_MUTATION == 7 /* mutation: no renormalise after rotating */
+    const double rinv = 1.0;
+#else
     const double rinv =
         1.0 / smax(sqrt(rnx * rnx + rny * rny + rnz * rnz), 1e-12);
+#endif
     rnx *= rinv; rny *= rinv; rnz *= rinv;
     oracle_ray_relu_vec(rnx, rny, rnz, rx, ry, rz, out);
 }
@@ -167,12 +196,20 @@ static void angmf_pixel(const float *pn, const float *pr, const float *xyp,
     const double rx = rp[p], ry = rp[HW + p], rz = rp[2 * HW + p];
     double acc0 = 0.0, acc1 = 0.0, acc2 = 0.0;
     for (int n = 0; n < K2; ++n) {
+#if ORACLE_MUTATION == 4 /* mutation: column-major slots */
+        const int kx = n / k, ky = n % k;
+#else
         const int ky = n / k, kx = n % k;
+#endif
         const int sy = imin(imax(y - P + ky, 0), H - 1); /* replicate */
         const int sx = imin(imax(x - P + kx, 0), W - 1);
         const size_t sp = (size_t)sy * W + sx;
         const double nx = pn[sp], ny = pn[HW + sp], nz = pn[2 * HW + sp];
+#if ORACLE_MUTATION == 3 /* mutation: unclamped pixel centre */
+        const double pix_x = (x - P + kx) + 0.5, pix_y = (y - P + ky) + 0.5;
+#else
         const double pix_x = sx + 0.5, pix_y = sy + 0.5;
+#endif
         const double xs = xyp[(size_t)n * HW + p];
         const double ys = xyp[(size_t)(K2 + n) * HW + p];
         const double theta = ap[(size_t)n * HW + p];

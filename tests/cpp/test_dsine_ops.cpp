@@ -1,0 +1,226 @@
+// Drop-in test of brovisionml::dsine::{ray_relu, angmf_propagate} (the C++
+// surface of include/brovisionml/dsine_ops.h), in the style of the
+// reference's tests (tests/test_dsine_refine.cpp:48-53: CHECK + failure count).
+//
+//   test_dsine_ops cpu   error behaviour; makes no GPU call
+//   test_dsine_ops gpu   the refiner's call pattern (src/dsine_refine.cpp:241-273:
+//                        ray_relu once, then chained angmf_propagate calls)
+//                        on a 60x80 grid against the CPU oracle (links
+//                        oracle/_build/liboracle_dsine.so; test-only)
+
+#include "brovisionml/dsine_ops.h"
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdio>
+#include <cstring>
+#include <random>
+#include <stdexcept>
+#include <string>
+#include <vector>
+
+extern "C" {
+void oracle_ray_relu_f32(float* normal, const float* ray, int B, int H, int W,
+                         long long ray_bstride);
+void oracle_angmf_propagate_f32(const float* pred_norm, const float* prob, const float* xy,
+                                const float* angle, const float* ray, double fu, double cu,
+                                double fv, double cv, int B, int H, int W, int k,
+                                long long ray_bstride, float* out);
+}
+
+using brotensor::Device;
+using brotensor::Tensor;
+namespace ops = brovisionml::dsine;
+
+static int g_failures = 0;
+
+#define CHECK(cond) do {                                                    \
+    if (!(cond)) {                                                          \
+        std::printf("  FAIL  %s:%d  %s\n", __FILE__, __LINE__, #cond);      \
+        ++g_failures;                                                       \
+    }                                                                       \
+} while (0)
+
+template <class F>
+static bool throws_with(F f, const char* prefix, const char* needle) {
+    try {
+        f();
+    } catch (const std::runtime_error& e) {
+        const std::string m = e.what();
+        const bool ok = m.rfind(prefix, 0) == 0 && m.find(needle) != std::string::npos;
+        if (!ok) std::printf("    message was: %s\n", m.c_str());
+        return ok;
+    }
+    return false;
+}
+
+// A tensor that claims to live on the device without touching the GPU: only
+// the device tag matters for the dispatch checks exercised in cpu mode.
+static Tensor fake_device(int rows, int cols) {
+    Tensor t = Tensor::mat(rows, cols);
+    t.device = Device::HIP;
+    return t;
+}
+
+static void test_errors() {
+    std::printf("  error behaviour\n");
+    const int H = 4, W = 6, HW = H * W;
+    Tensor n = Tensor::mat(1, 3 * HW), r = Tensor::mat(1, 3 * HW);
+    Tensor pr = Tensor::mat(1, 25 * HW), xy = Tensor::mat(1, 50 * HW), an = Tensor::mat(1, 25 * HW);
+    Tensor out;
+    // CPU tensors: this library is the device path.
+    CHECK(throws_with([&] { ops::ray_relu(n, r, H, W); }, "dsine ops: ", "CPU"));
+    CHECK(throws_with([&] { ops::angmf_propagate(n, pr, xy, an, r, 1, 1, 1, 1, H, W, out); },
+                      "dsine ops: ", "CPU"));
+    // Device mismatch (src/dsine_ops.cpp:180-181, 200-202).
+    Tensor dn = fake_device(1, 3 * HW);
+    CHECK(throws_with([&] { ops::ray_relu(dn, r, H, W); }, "dsine ops: ",
+                      "normal and ray must share a device"));
+    CHECK(throws_with([&] { ops::angmf_propagate(dn, pr, xy, an, r, 1, 1, 1, 1, H, W, out); },
+                      "dsine ops: ", "all inputs must share a device"));
+    // Wrong sizes are rejected before any launch.
+    Tensor dr = fake_device(1, 3 * HW), dpr = fake_device(1, 25 * HW), dxy = fake_device(1, 49 * HW);
+    Tensor dan = fake_device(1, 25 * HW);
+    CHECK(throws_with([&] { ops::angmf_propagate(dn, dpr, dxy, dan, dr, 1, 1, 1, 1, H, W, out); },
+                      "dsine ops: ", "xy holds"));
+    CHECK(throws_with([&] { ops::ray_relu(dn, dr, H + 1, W); }, "dsine ops: ", "normal holds"));
+    CHECK(throws_with([&] { ops::ray_relu(dn, dr, -1, W); }, "dsine ops: ", "H and W"));
+}
+
+// Unit normals, sigmoid probs, raw xy, angles, ray_8 of a 480x640 image
+// (intrins_from_fov + build_ray8, src/dsine_preprocess.cpp:35-46,
+// src/dsine_decoder.cpp:242-293).
+struct Inputs {
+    int H, W;
+    double fu, cu, fv, cv;
+    std::vector<float> n, prob, xy, angle, ray;
+};
+
+static Inputs make_inputs(int H, int W, unsigned seed) {
+    Inputs in;
+    in.H = H;
+    in.W = W;
+    const int HW = H * W, origH = 8 * H, origW = 8 * W;
+    const double kPi = 3.14159265358979323846;
+    const double f = (std::max(origH, origW) / 2.0) / std::tan((60.0 / 2.0) * kPi / 180.0);
+    const float fx = static_cast<float>(f), cx = static_cast<float>(origW / 2.0 - 0.5),
+                cy = static_cast<float>(origH / 2.0 - 0.5);
+    const double sw = static_cast<double>(W) / origW, sh = static_cast<double>(H) / origH;
+    in.fu = fx * sw;
+    in.cu = (cx + 0.5) * sw;
+    in.fv = fx * sh;
+    in.cv = (cy + 0.5) * sh;
+    std::mt19937 rng(seed);
+    std::normal_distribution<double> nd;
+    in.n.resize(3 * HW);
+    for (int p = 0; p < HW; ++p) {
+        const double a = nd(rng), b = nd(rng), c = nd(rng), l = std::sqrt(a * a + b * b + c * c);
+        in.n[p] = static_cast<float>(a / l);
+        in.n[HW + p] = static_cast<float>(b / l);
+        in.n[2 * HW + p] = static_cast<float>(c / l);
+    }
+    in.prob.resize(25 * HW);
+    for (auto& v : in.prob) v = static_cast<float>(1.0 / (1.0 + std::exp(-nd(rng))));
+    in.xy.resize(50 * HW);
+    for (auto& v : in.xy) v = static_cast<float>(nd(rng));
+    in.angle.resize(25 * HW);
+    for (auto& v : in.angle) v = static_cast<float>(0.1 * nd(rng));
+    in.ray.resize(3 * HW);
+    for (int y = 0; y < H; ++y)
+        for (int x = 0; x < W; ++x) {
+            const int p = y * W + x;
+            const double rx = static_cast<float>(((x + 0.5) - in.cu) / in.fu);
+            const double ry = static_cast<float>(((y + 0.5) - in.cv) / in.fv);
+            const double inv = 1.0 / std::max(std::sqrt(rx * rx + ry * ry + 1.0), 1e-12);
+            in.ray[p] = static_cast<float>(rx * inv);
+            in.ray[HW + p] = static_cast<float>(ry * inv);
+            in.ray[2 * HW + p] = static_cast<float>(1.0 * inv);
+        }
+    return in;
+}
+
+static Tensor upload(const std::vector<float>& v) {
+    Tensor t = Tensor::mat(1, static_cast<int>(v.size()));
+    std::memcpy(t.host_f32_mut(), v.data(), v.size() * sizeof(float));
+    return t.to(Device::HIP);
+}
+
+static double max_abs(const Tensor& dev, const std::vector<float>& want) {
+    Tensor h = dev.to(Device::CPU);
+    double m = 0.0;
+    for (std::size_t i = 0; i < want.size(); ++i)
+        m = std::max(m, std::fabs(static_cast<double>(h.host_f32()[i]) - want[i]));
+    return m;
+}
+
+static void test_refiner_call_pattern() {
+    std::printf("  refiner call pattern on the device (60x80)\n");
+    const int H = 60, W = 80;
+    Inputs in = make_inputs(H, W, 7);
+    Tensor ray = upload(in.ray), prob = upload(in.prob), xy = upload(in.xy), angle = upload(in.angle);
+    // pred_norm = RayReLU(decoder normal)
+    Tensor pred_norm = upload(in.n);
+    ops::ray_relu(pred_norm, ray, H, W);
+    std::vector<float> want_n = in.n;
+    oracle_ray_relu_f32(want_n.data(), in.ray.data(), 1, H, W, 0);
+    const double e0 = max_abs(pred_norm, want_n);
+    std::printf("    ray_relu max-abs %.3e\n", e0);
+    CHECK(e0 <= 2.5e-7);
+    // chained angmf_propagate (out feeds the next call, src/dsine_refine.cpp:271-273)
+    std::vector<float> want_out(3 * H * W);
+    for (int it = 0; it < 3; ++it) {
+        Tensor new_pred;
+        ops::angmf_propagate(pred_norm, prob, xy, angle, ray, in.fu, in.cu, in.fv, in.cv, H, W,
+                             new_pred);
+        CHECK(new_pred.device == Device::HIP && new_pred.rows == 1 && new_pred.cols == 3 * H * W);
+        oracle_angmf_propagate_f32(want_n.data(), in.prob.data(), in.xy.data(), in.angle.data(),
+                                   in.ray.data(), in.fu, in.cu, in.fv, in.cv, 1, H, W, 5, 0,
+                                   want_out.data());
+        const double e = max_abs(new_pred, want_out);
+        std::printf("    angmf_propagate call %d max-abs %.3e\n", it, e);
+        CHECK(e <= 1e-5);
+        // the oracle chains its own output; the device chains the device's
+        pred_norm = std::move(new_pred);
+        want_n = want_out;
+    }
+    // An `out` of the right shape on the device is reused, not reallocated.
+    Tensor out = Tensor::zeros_on(Device::HIP, 1, 3 * H * W);
+    void* before = out.data;
+    ops::angmf_propagate(pred_norm, prob, xy, angle, ray, in.fu, in.cu, in.fv, in.cv, H, W, out);
+    CHECK(out.data == before);
+    // ... but never when it aliases pred_norm (the reference reallocates).
+    Tensor alias = pred_norm;
+    ops::angmf_propagate(pred_norm, prob, xy, angle, ray, in.fu, in.cu, in.fv, in.cv, H, W, alias);
+    CHECK(alias.data != pred_norm.data);
+    CHECK(hipDeviceSynchronize() == hipSuccess);
+}
+
+int main(int argc, char** argv) {
+    const std::string mode = argc > 1 ? argv[1] : "cpu";
+    std::printf("test_dsine_ops (%s):\n", mode.c_str());
+    try {
+        if (mode == "cpu") {
+            test_errors();
+        } else if (mode == "gpu") {
+            int n = 0;
+            if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {
+                std::printf("  no HIP device\n");
+                return 2;
+            }
+            test_refiner_call_pattern();
+        } else {
+            std::printf("  unknown mode\n");
+            return 2;
+        }
+    } catch (const std::exception& e) {
+        std::printf("  error: %s\n", e.what());
+        return 1;
+    }
+    if (g_failures == 0) {
+        std::printf("  OK\n");
+        return 0;
+    }
+    std::printf("  %d failure(s)\n", g_failures);
+    return 1;
+}

@@ -1,0 +1,92 @@
+"""The C ABI library loads, exports every entry point include/bvml_dsine.h
+declares, and rejects bad arguments before touching the GPU (all calls here
+fail validation, so none launches; the runs need no device).  Also runs the
+C++ drop-in's error-path test (tests/cpp, cpu mode)."""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from brovisionml_amd import _lib
+from brovisionml_amd.build import LIB, ROOT
+
+HEADER = os.path.join(ROOT, "include", "bvml_dsine.h")
+CPP_TEST = os.path.join(ROOT, "tests", "cpp", "_build", "test_dsine_ops")
+
+
+def declared_functions():
+    text = open(HEADER).read()
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(bvml_dsine_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_binding_exports():
+    assert declared_functions() == sorted(_lib.EXPORTS)
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(LIB)
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+    out = subprocess.run(["nm", "-D", "--defined-only", LIB], stdout=subprocess.PIPE, text=True,
+                         check=True).stdout
+    for name in declared_functions():
+        assert re.search(rf"\bT {name}\b", out), name
+
+
+def test_version():
+    assert _lib.load().bvml_dsine_version().decode() == "0.1.0"
+
+
+FAKE = 0x10000  # never dereferenced: validation fails or the call is a no-op first
+
+
+def angmf(**kw):
+    args = dict(pred_norm=FAKE, prob=FAKE + 0x100000, xy=FAKE + 0x200000, angle=FAKE + 0x300000,
+                ray=FAKE + 0x400000, fu=100.0, cu=10.0, fv=100.0, cv=10.0, B=1, H=4, W=4, k=5,
+                ray_bstride=0, out=FAKE + 0x500000, flags=0, stream=0)
+    args.update(kw)
+    return _lib.angmf_propagate_f32(**args)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(B=-1), _lib.ESHAPE), (dict(H=-2), _lib.ESHAPE), (dict(ray_bstride=-3), _lib.ESHAPE),
+    (dict(k=4), _lib.EK), (dict(k=11), _lib.EK), (dict(k=0), _lib.EK),
+    (dict(prob=0), _lib.ENULL), (dict(out=0), _lib.ENULL),
+    (dict(flags=4), _lib.EFLAGS),
+    (dict(out=FAKE), _lib.EALIAS),                  # out == pred_norm
+    (dict(out=FAKE + 0x200000 + 64), _lib.EALIAS),  # inside xy
+    (dict(H=1 << 16, W=1 << 14), _lib.ESIZE),       # plane of 2^30 pixels
+])
+def test_angmf_rejects(kw, code):
+    assert angmf(**kw) == code
+    assert _lib.last_error().startswith("angmf_propagate: ")
+
+
+def test_empty_shapes_are_no_ops():
+    # the reference returns before launching when H*W == 0 (src/dsine_ops.cu:162,179)
+    assert angmf(H=0) == _lib.OK
+    assert angmf(W=0, pred_norm=0) == _lib.OK
+    assert angmf(B=0) == _lib.OK
+    assert _lib.ray_relu_f32(0, 0, 1, 0, 5, 0) == _lib.OK
+
+
+@pytest.mark.parametrize("args,code", [
+    ((FAKE, FAKE + 0x10000, -1, 2, 2, 0), _lib.ESHAPE),
+    ((0, FAKE, 1, 2, 2, 0), _lib.ENULL),
+    ((FAKE, FAKE + 8, 1, 2, 2, 0), _lib.EALIAS),
+    ((FAKE, FAKE + 0x10000, 1, 2, 2, -1), _lib.ESHAPE),
+])
+def test_ray_relu_rejects(args, code):
+    assert _lib.ray_relu_f32(*args) == code
+    assert _lib.last_error().startswith("ray_relu: ")
+
+
+def test_cpp_dropin_error_paths():
+    assert os.path.exists(CPP_TEST), "build() compiles tests/cpp/test_dsine_ops"
+    proc = subprocess.run([CPP_TEST, "cpu"], stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                          text=True, timeout=120)
+    assert proc.returncode == 0, proc.stdout

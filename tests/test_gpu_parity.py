@@ -7,6 +7,7 @@ seeded fp32 inputs; NaN patterns must match.  The double-precision kernel
 """
 from __future__ import annotations
 
+import glob
 import os
 import sys
 
@@ -243,3 +244,34 @@ def test_ray_relu(cuda, B, H, W):
     say(f"    max-abs {max_abs:.3e}")
     assert nan_mm == 0
     assert max_abs <= 2.5e-7
+
+
+GOLDEN = sorted(glob.glob(os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden",
+                                       "angmf_*.npz")))
+
+
+@pytest.mark.parametrize("path", GOLDEN, ids=[os.path.basename(p) for p in GOLDEN])
+def test_angmf_golden_fixture(cuda, path):
+    d = np.load(path)
+    H, W, k = int(d["H"]), int(d["W"]), int(d["k"])
+    say(f"[gpu] angmf golden {os.path.basename(path)}")
+    inp = {key: d[key] for key in ("pred_norm", "prob", "xy", "angle", "ray")}
+    inp["intrinsics"] = tuple(d["intr"])
+    B = inp["pred_norm"].shape[0]
+    got = run_gpu(inp, H, W, cuda, ray=d["ray"].reshape(-1))
+    max_abs, max_deg, nan_mm = compare(got.reshape(B, 3, -1), d["expect_out"])
+    say(f"    max-abs {max_abs:.3e}  max-angle {max_deg:.3e} deg")
+    assert nan_mm == 0
+    assert max_abs <= TOL_ABS and max_deg <= TOL_DEG
+
+
+def test_cpp_dropin_on_device(cuda):
+    """The C++ surface (include/brovisionml/dsine_ops.h) in the refiner's call
+    pattern against the oracle (tests/cpp/test_dsine_ops.cpp, gpu mode)."""
+    import subprocess
+    exe = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cpp", "_build", "test_dsine_ops")
+    say("[gpu] C++ drop-in test_dsine_ops gpu")
+    proc = subprocess.run([exe, "gpu"], stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True,
+                          timeout=110)
+    say(proc.stdout)
+    assert proc.returncode == 0, proc.stdout
