@@ -41,6 +41,23 @@ def cpu_model() -> str:
     return platform.processor() or "unknown"
 
 
+PROFILE = os.path.join(ROOT, "profiles", "angmf_f32_k5_256x256_traffic.json")
+
+
+def traffic_from_profile(w):
+    """HBM bytes per launch from the committed rocprofv3 --pmc summary
+    (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the same counters on a
+    plain copy of known size), if it covers this workload."""
+    try:
+        with open(PROFILE) as f:
+            p = json.load(f)
+    except (OSError, ValueError):
+        return None
+    if p.get("workload") != w.name:
+        return None
+    return p.get("traffic_bytes_per_launch")
+
+
 def cpu_baseline(w, inp, seconds: float, nthreads: int = 1):
     """Time the oracle on whole images of the workload until `seconds` of
     CPU work; returns (Mpixel/s, passes)."""
@@ -67,6 +84,9 @@ def main() -> int:
     ap.add_argument("--sets", type=int, default=0, help="rotating input sets (0 = auto, > 512 MB)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--calib", action="store_true",
+                    help="also run 10 plain device copies of one launch's byte count "
+                         "(the reference kernel for the FETCH_SIZE / WRITE_SIZE scale)")
     args = ap.parse_args()
 
     if args.gpus != 1:
@@ -138,6 +158,14 @@ def main() -> int:
         launch(0)
     wall_w, ev_mean_w, ev_med_w = timed(False, args.steps)
 
+    if args.calib:
+        n = bytes_per_call // 4
+        src = torch.ones(n, dtype=torch.float32, device=dev)
+        dst = torch.empty_like(src)
+        for _ in range(10):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+
     ms_per_step = wall * 1e3 / args.steps
     mpix = B * H * W * w.calls * args.steps / wall / 1e6
     achieved = bytes_per_call / (ev_mean_ms * 1e-3) / 1e9
@@ -167,7 +195,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": None,
+            "traffic": traffic_from_profile(w),
             "kernel": f"angmf_f32_kernel<{k}>",
             "bytes_per_launch": bytes_per_call,
             "launch_us_mean": round(ev_mean_ms * 1e3, 3),
