@@ -47,10 +47,6 @@ namespace {
 // reference does arithmetic in double.
 constexpr float kRayEpsF = 1e-2f;
 
-// |dd| below this (in the fp32 evaluation, where dd is O(1) with an absolute
-// error of a few 1e-7) sends the pixel to the double-precision path.
-constexpr float kDdTau = 2e-5f;
-
 // Raw xy pairs with |xy|^2 below this, and normals with |m|^2 below kMinM2,
 // are left to the double-precision path, where the reference's 1e-12 clamps
 // stop normalising.
@@ -63,12 +59,13 @@ constexpr float kMinM2 = 1e-16f;
 // by |acc|, so unflagged pixels stay below 3e-7 / sqrt(kAccRatio2) = 7e-6.
 constexpr float kAccRatio2 = 2e-3f;
 
-// The rotation axis is V = m x N, N = D x P0 the normal of the plane through
-// the source pixel's ray P0 and the image-plane step D = (xs/fu, ys/fv, 0);
-// fp32 gives it a relative error of about 1e-7 / sin(m, N).  Where
-// |V| < kAxisK * |D| (sin(m, N) below about kAxisK / 1.3), or |dd| < kDdTau,
-// V and the sign of dd are recomputed in double for that neighbour.
-constexpr float kAxisK2 = 4e-4f;  // kAxisK = 0.02
+// dd = g + q/|xy| is formed from g and q that are accurate to their own
+// relative precision, so fp32 gets its sign right unless |dd| < kDdRel * |g|;
+// below kDdAbs the reference's own rounding (and its 1e-8 clamp) can decide.
+// In either case V and the sign are recomputed in double for that neighbour,
+// and the pixel goes to the reference-order path if |dd| < 4e-8 there.
+constexpr float kDdRel = 1e-5f;
+constexpr float kDdAbs = 1e-6f;
 
 // ---------------------------------------------------------------------------
 // Double-precision reference body
@@ -179,6 +176,7 @@ struct AngmfArgs {
     float ifu, ifv;    // 1/fu, 1/fv
     float tu_c, tv_c;  // (0.5 - cu)/fu, (0.5 - cv)/fv: source ray tu0 = sx*ifu + tu_c
     double ifu64, ifv64;
+    double hc_u, hc_v;  // 0.5 - cu, 0.5 - cv
 };
 
 // ---------------------------------------------------------------------------
@@ -487,21 +485,28 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(Angmf
         // cos(v', r) = v'.r / max(|v'||r|, 1e-8) with |v'| = 1
         const float ir = 1.0f / fmaxf(sqrtf(fmaf(rx, rx, fmaf(ry, ry, rz * rz))), 1e-8f);
         const float rsx = rx * ir, rsy = ry * ir, rsz = rz * ir;
-        const float tv0 = fmaf((float)sy, a.ifv, a.tv_c);
+        // (s + 0.5 - c)/f as the reference forms it: exactly 0 at the principal point
+        const double tv0d = ((double)sy + a.hc_v) * a.ifv64;
+        const float tv0 = (float)tv0d;
         float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, q2 = 0.f;
         bool bad = false;
 #pragma unroll
         for (int kx = 0; kx < K; ++kx) {
             const int sx = clampi(x - P + kx, 0, W - 1);
-            const float tu0 = fmaf((float)sx, a.ifu, a.tu_c);
+            const double tu0d = ((double)sx + a.hc_u) * a.ifu64;
+            const float tu0 = (float)tu0d;
             const float mx = mxs[kx], my = mys[kx], mz = mzs[kx];
             const float xsv = xs[kx], ysv = ys[kx], t = th[kx];
             // The fast path takes unit source normals (every normal this op
             // or RayReLU writes is one); others go to the double path.
             const float m2 = fmaf(mx, mx, fmaf(my, my, mz * mz));
-            const float g = fmaf(tu0, mx, fmaf(tv0, my, mz));  // P0 . m
-            const float du = xsv * a.ifu, dv = ysv * a.ifv;
-            const float q = fmaf(du, mx, dv * my);
+            // g = P0 . m and q = D . m cancel when the surface is edge-on to
+            // the rays; formed in double (exact products of the fp32 inputs)
+            // they keep their relative precision, and so does V below.
+            const double du64 = (double)xsv * a.ifu64, dv64 = (double)ysv * a.ifv64;
+            const float g = (float)fma(tu0d, (double)mx, fma(tv0d, (double)my, (double)mz));
+            const float q = (float)fma(du64, (double)mx, dv64 * (double)my);
+            const float du = (float)du64, dv = (float)dv64;
             const float s = fmaf(xsv, xsv, ysv * ysv);
             const float dd = fmaf(rsq(fmaxf(s, 1e-24f)), q, g);
             bad |= !(fabsf(m2 - 1.0f) <= 1e-5f) | (s < kMinXY2) | !(fabsf(t) <= 3.2f);
@@ -511,13 +516,15 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(Angmf
             float Vz = -q;
             float n2 = fmaf(Vx, Vx, fmaf(Vy, Vy, q * q));
             float sg = dd;
-            if (__builtin_expect(!(fabsf(dd) >= kDdTau) | !(n2 >= kAxisK2 * fmaf(du, du, dv * dv)),
-                                 0)) {
+            if (__builtin_expect(!(fabsf(dd) >= fmaxf(kDdRel * fabsf(g), kDdAbs)), 0)) {
                 precise_axis(mx, my, mz, sx, sy, xsv, ysv, a, Vx, Vy, Vz, bad);
                 n2 = 1.0f;
                 sg = 1.0f;
             }
-            const float ia = copysignf(rsq(n2), sg);
+            // 1/|V| with one Newton step: its rounding scales the rotation
+            float ia = rsq(n2);
+            ia = fmaf(0.5f * ia, fmaf(-n2 * ia, ia, 1.0f), ia);
+            ia = copysignf(ia, sg);
             float st, ct;
             sincos_small(t, st, ct);
             const float S = st * ia;
@@ -808,6 +815,8 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
     a.ifv = (float)(1.0 / fv);
     a.ifu64 = 1.0 / fu;
     a.ifv64 = 1.0 / fv;
+    a.hc_u = 0.5 - cu;
+    a.hc_v = 0.5 - cv;
     a.tu_c = (float)((0.5 - cu) / fu);
     a.tv_c = (float)((0.5 - cv) / fv);
     choose_tile(a, k);
