@@ -28,6 +28,10 @@ HIP_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    # leading scalar kernel arguments (up to 14 dwords) arrive preloaded in
+    # SGPRs; the code object keeps a prologue that loads them on firmware
+    # without the feature
+    "-mllvm", "-amdgpu-kernarg-preload-count=10",
     "-Wall",
 ]
 

@@ -48,24 +48,25 @@ namespace {
 constexpr float kRayEpsF = 1e-2f;
 
 // Raw xy pairs with |xy|^2 below this, and normals with |m|^2 below kMinM2,
-// are left to the double-precision path, where the reference's 1e-12 clamps
-// stop normalising.
-constexpr float kMinXY2 = 1e-20f;
-constexpr float kMinM2 = 1e-16f;
+// go to the reference-order path: the reference's 1e-12 clamps stop
+// normalising them.
+constexpr double kMinXY2 = 1e-20;
+constexpr double kMinM2 = 1e-16;
 
-// A pixel is recomputed in double when |acc|^2 < kAccRatio2 * sum(wi^2),
-// wi = prob / |m'| being each term's weight after RayReLU: each term carries
-// an fp32 error of at most about 3e-7 * wi (measured), their sum is divided
-// by |acc|, so unflagged pixels stay below 3e-7 / sqrt(kAccRatio2) = 7e-6.
-constexpr float kAccRatio2 = 2e-3f;
+// The fast path's terms are within about 1e-14 * wi of the reference's
+// (wi = prob / |m'|, each term's weight after RayReLU), and the final
+// normalise divides their sum by |acc|: a pixel with
+// |acc|^2 < kAccRatio2 * sum(wi^2) goes to the reference-order path, so the
+// rest stay within 1e-14 / sqrt(kAccRatio2) = 1e-6.
+constexpr double kAccRatio2 = 1e-16;
 
-// dd = g + q/|xy| is formed from g and q that are accurate to their own
-// relative precision, so fp32 gets its sign right unless |dd| < kDdRel * |g|;
-// below kDdAbs the reference's own rounding (and its 1e-8 clamp) can decide.
-// In either case V and the sign are recomputed in double for that neighbour,
-// and the pixel goes to the reference-order path if |dd| < 4e-8 there.
-constexpr float kDdRel = 1e-5f;
-constexpr float kDdAbs = 1e-6f;
+// The reference clamps |dd| < 1e-8 (src/dsine_ops.cpp:120-123), where the
+// reduced axis no longer holds: a neighbour with |dd| below kDdMin sends its
+// pixel to the reference-order path.  The fast path's dd is within about
+// 1e-14 of the reference's, so the sign of every other dd is the reference's,
+// and so is the axis -- including where m is nearly parallel to
+// N = D x P0 (g and q both small), since dd = g + q/|xy| is small then too.
+constexpr double kDdMin = 1.01e-8;
 
 // ---------------------------------------------------------------------------
 // Double-precision reference body
@@ -235,8 +236,6 @@ __device__ __forceinline__ int xcd_remap(int bid, int nb) {
     return xcd * q + (xcd < r ? xcd : r) + i;
 }
 
-__device__ __forceinline__ float rsq(float x) { return __builtin_amdgcn_rsqf(x); }
-
 // Load base[byte_off / 4] with a uniform base pointer and a 32-bit per-lane
 // byte offset, which maps onto the scalar-base + vector-offset load form.
 __device__ __forceinline__ float ldf(const float* base, uint32_t byte_off) {
@@ -261,27 +260,6 @@ __device__ __forceinline__ void stf(float* base, uint32_t byte_off, float v) {
     *reinterpret_cast<float*>(reinterpret_cast<char*>(base) + byte_off) = v;
 }
 
-// sin and cos of t for |t| <= 3.2 (callers send larger |t| to the double
-// path).  Half-angle polynomials in u = h^2, h = t/2 in [0, 1.6]: Chebyshev
-// fits (computed for this kernel) with sin(h) = h + h^3 S(u) to 8e-9 and
-// cos(h) = 1 + u C(u) to 5e-10; then sin t = 2 sin h cos h and
-// cos t = cos^2 h - sin^2 h.  fp32 angular error of (cos t, sin t) <= 1.8e-7.
-__device__ __forceinline__ void sincos_small(float t, float& st, float& ct) {
-    const float h = 0.5f * t, u = h * h;
-    float p = fmaf(u, 2.630318e-06f, -0.00019821344f);
-    p = fmaf(u, p, 0.008333231f);
-    p = fmaf(u, p, -0.16666666f);
-    const float s = fmaf(h * u, p, h);
-    float q = fmaf(u, -2.625131e-07f, 2.4772546e-05f);
-    q = fmaf(u, q, -0.0013888624f);
-    q = fmaf(u, q, 0.041666657f);
-    q = fmaf(u, q, -0.5f);
-    const float c = fmaf(u, q, 1.0f);
-    const float sc = s * c;
-    st = sc + sc;
-    ct = fmaf(c, c, -(s * s));
-}
-
 __device__ __forceinline__ unsigned long long uniform64(unsigned long long v) {
     const unsigned lo = __builtin_amdgcn_readfirstlane((unsigned)v);
     const unsigned hi = __builtin_amdgcn_readfirstlane((unsigned)(v >> 32));
@@ -297,9 +275,17 @@ __device__ __forceinline__ double rsq64(double x) {
     return fma(0.5 * y, e, y);
 }
 
-// sin and cos of t for |t| <= 3.2 in double: the half-angle scheme of
-// sincos_small with degree-17/16 Chebyshev fits (computed for this kernel;
-// sin h to 2e-18, cos h to 2e-17 on |h| <= 1.6).
+// 1/sqrt(x) in double with one Newton step (about 1e-14 relative).
+__device__ __forceinline__ double rsq64_1(double x) {
+    const double y = __builtin_amdgcn_rsq(x);
+    return fma(0.5 * y, fma(-x * y, y, 1.0), y);
+}
+
+// sin and cos of t for |t| <= 3.2 in double (callers send larger |t| to the
+// reference-order path).  Half-angle polynomials in u = h^2, h = t/2 in
+// [0, 1.6]: degree-17/16 Chebyshev fits (computed for this kernel) with
+// sin h to 2e-18 and cos h to 2e-17; then sin t = 2 sin h cos h and
+// cos t = cos^2 h - sin^2 h.
 __device__ __forceinline__ void sincos_small64(double t, double& st, double& ct) {
     const double h = 0.5 * t, u = h * h;
     double p = 2.7284852642995796443e-15;
@@ -325,96 +311,28 @@ __device__ __forceinline__ void sincos_small64(double t, double& st, double& ct)
     ct = fma(c, c, -(s * s));
 }
 
-// The neighbour term of the double-precision recompute, in the reduced form
-// of the fast path carried out in double (about 1e-15 from the reference).
-// Returns false, leaving the outputs unset, where the reference's clamps,
-// its NaN/Inf handling or the Taylor branch of its rotation could matter --
-// a near-zero or non-finite normal, xy pair or ray, |dd| < 4e-8 (the
-// reference clamps |dd| < 1e-8), or |theta| > 3.2 -- and the caller then runs
-// nbr_ref_f64 instead.
-__device__ __forceinline__ bool nbr_fast_f64(float mxf, float myf, float mzf, int sx, int sy,
-                                             float xsf, float ysf, float thf, float rxf,
-                                             float ryf, float rzf, const AngmfArgs& a,
-                                             double& ox, double& oy, double& oz) {
-    const double mx = mxf, my = myf, mz = mzf, xs = xsf, ys = ysf, t = thf;
-    const double rx = rxf, ry = ryf, rz = rzf;
-    const double m2 = mx * mx + my * my + mz * mz;
-    const double s = xs * xs + ys * ys;
-    const double r2 = rx * rx + ry * ry + rz * rz;
-    if (!(m2 >= 1e-16 && m2 <= 1e30 && s >= 1e-20 && s <= 1e30 && r2 >= 1e-16 &&
-          r2 <= 1e30 && fabs(t) <= 3.2))
-        return false;
-    const double im = rsq64(m2);
-    const double ux = mx * im, uy = my * im, uz = mz * im;
-    const double tu0 = (sx + 0.5 - a.cu) * a.ifu64;
-    const double tv0 = (sy + 0.5 - a.cv) * a.ifv64;
-    const double g = fma(tu0, ux, fma(tv0, uy, uz));
-    const double du = xs * a.ifu64, dv = ys * a.ifv64;
-    const double q = fma(du, ux, dv * uy);
-    const double dd = fma(rsq64(s), q, g);
-    if (!(fabs(dd) >= 4e-8)) return false;
-    const double Vx = fma(g, du, -q * tu0);
-    const double Vy = fma(g, dv, -q * tv0);
-    const double ia = copysign(rsq64(fma(Vx, Vx, fma(Vy, Vy, q * q))), dd);
-    double st, ct;
-    sincos_small64(t, st, ct);
-    const double S = st * ia;
-    const double vx = fma(fma(Vy, uz, q * uy), S, ux * ct);
-    const double vy = fma(fma(-q, ux, -Vx * uz), S, uy * ct);
-    const double vz = fma(fma(Vx, uy, -Vy * ux), S, uz * ct);
-    const double cs = fma(vx, rx, fma(vy, ry, vz * rz)) * rsq64(r2);
-    const double dc = fmax((double)kRayEpsF - cs, 0.0);
-    const double px = fma(rx, dc, vx), py = fma(ry, dc, vy), pz = fma(rz, dc, vz);
-    const double p2 = fma(px, px, fma(py, py, pz * pz));
-    if (!(p2 >= 1e-20)) return false;
-    const double ip = rsq64(p2);
-    ox = px * ip;
-    oy = py * ip;
-    oz = pz * ip;
-    return true;
-}
-
-// The axis of one neighbour in double for the fp32 path, where fp32 cannot
-// be trusted with it (|dd| near 0: its sign flips the axis; m nearly
-// parallel to N: V = m x N loses its relative precision).  Same reduced form,
-// from the raw inputs.  Writes the unit V (times sign(dd)) to V*, and sets
-// `bad` where |dd| or |V| is so small that the reference's 1e-8 / 1e-12
-// clamps can decide the result.
-__device__ __forceinline__ void precise_axis(float mx, float my, float mz, int sx, int sy,
-                                             float xs, float ys, const AngmfArgs& a,
-                                             float& Vx, float& Vy, float& Vz, bool& bad) {
-    const double tu0 = (sx + 0.5 - a.cu) * a.ifu64;
-    const double tv0 = (sy + 0.5 - a.cv) * a.ifv64;
-    const double du = (double)xs * a.ifu64, dv = (double)ys * a.ifv64;
-    const double g = fma(tu0, (double)mx, fma(tv0, (double)my, (double)mz));
-    const double q = fma(du, (double)mx, dv * (double)my);
-    const double s = fma((double)xs, (double)xs, (double)ys * (double)ys);
-    const double dd = fma(rsq64(fmax(s, 1e-24)), q, g);
-    const double vx = fma(g, du, -q * tu0), vy = fma(g, dv, -q * tv0), vz = -q;
-    const double nn = fma(vx, vx, fma(vy, vy, vz * vz));
-    if (!(fabs(dd) >= 4e-8) || !(nn >= 1e-22 * dd * dd)) {
-        bad = true;
-        return;
-    }
-    const double inv = copysign(rsq64(nn), dd);
-    Vx = (float)(vx * inv);
-    Vy = (float)(vy * inv);
-    Vz = (float)(vz * inv);
-}
+// Flagged pixels recomputed per pass and group (64 / PPR lanes per pixel).
+__host__ __device__ constexpr int recompute_ppr(int K) { return (K <= 8) ? 8 : 4; }
 
 // LDS of the fp32 kernel, in 16-byte units:
 //   smask[16]        u64 flagged-pixel mask per 64-pixel group (8 units)
-//   part[K][64*M]    per-window-row fp32 partial (acc.xyz, sum wi^2 or NaN)
+//   part[K][64*M]    per-window-row partial (acc.xyz, sum wi^2 or NaN), 4 doubles
 //   fixp[M][K][PPR]  per-window-row fp64 partial of a flagged pixel (3 doubles)
 __host__ __device__ inline int lds_units(int K, int M) {
-    const int ppr = (K <= 8) ? 8 : 4;
-    return 8 + K * 64 * M + (M * K * ppr * 3 + 1) / 2;
+    return 8 + 2 * K * 64 * M + (M * K * recompute_ppr(K) * 3 + 1) / 2;
 }
 
-// Occupancy target: k = 5 runs two 10-wave workgroups per CU (the 256x256
-// shape in a single round), which needs 20 waves per CU, i.e. <= 96 VGPRs.
+// Occupancy: a workgroup of n waves starts on a CU only when each of its 4
+// SIMDs has room for ceil(n/4) more waves.  k = 5 runs 10-wave workgroups
+// (3 + 3 + 2 + 2 waves), so two of them per CU -- the 256x256 shape in a
+// single round -- need 6 waves per SIMD, i.e. <= 80 VGPRs.
 template <int K>
-constexpr int kWavesPerEU = (K == 5) ? 5 : 4;
+constexpr int kWavesPerEU = (K == 5) ? 6 : 4;
+
+// TW, TH and M of the fp32 kernel's tile, packed into one kernel argument.
+__host__ __device__ inline unsigned pack_tile(int TW, int TH, int M) {
+    return (unsigned)TW | ((unsigned)TH << 11) | ((unsigned)M << 22);
+}
 
 // One workgroup = M groups of 64 output pixels (a TW x TH tile of one
 // sample) x K waves, wave (ky, group) handling window row ky of one pixel per
@@ -422,33 +340,42 @@ constexpr int kWavesPerEU = (K == 5) ? 5 : 4;
 // rows of neighbouring pixels overlap) and the 4K per-neighbour planes, in the
 // order it consumes them, and accumulates the row's fp32 partial; the K
 // partials meet in LDS.
+//
+// Everything the first loads' addresses depend on comes first in the
+// argument list, as scalars: gfx950 preloads up to 14 dwords of kernel
+// arguments into SGPRs at wave launch (built with
+// -amdgpu-kernarg-preload-count), so a workgroup issues its loads without
+// first waiting for a scalar load of its arguments -- which, once the
+// other workgroups have the memory system saturated, takes microseconds.
 template <int K>
 __global__ __launch_bounds__(64 * K * (16 / K))
-__attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(AngmfArgs a) {
+__attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
+    const float* __restrict__ pred_norm, const float* __restrict__ xy,
+    const float* __restrict__ angle, const float* __restrict__ prob, int nblocks,
+    int tiles_per_img, int tiles_x, int W, int H, unsigned tile, AngmfArgs a) {
     constexpr int P = K / 2, K2 = K * K;
-    constexpr int LPG = (K <= 8) ? 8 : 16;  // lanes per flagged pixel in the recompute
-    constexpr int PPR = 64 / LPG;           // flagged pixels per recompute pass
+    constexpr int PPR = recompute_ppr(K);  // flagged pixels per recompute pass
+    constexpr int LPG = 64 / PPR;          // lanes per flagged pixel in the recompute
     extern __shared__ float4 smem[];
-    const int TW = a.TW, TH = a.TH, M = a.M;
+    const int TW = (int)(tile & 0x7ffu), TH = (int)((tile >> 11) & 0x7ffu), M = (int)(tile >> 22);
     const int npx = 64 * M;
     unsigned long long* smask = reinterpret_cast<unsigned long long*>(smem);
-    float4* part = smem + 8;
+    double4* part = reinterpret_cast<double4*>(smem + 8);
     double* fixp = reinterpret_cast<double*>(part + K * npx);
 
-    const int lb = xcd_remap(blockIdx.x, a.nblocks);
-    const int b = lb / a.tiles_per_img;
-    const int t_in = lb - b * a.tiles_per_img;
-    const int tyi = t_in / a.tiles_x;
+    const int lb = xcd_remap(blockIdx.x, nblocks);
+    const int b = lb / tiles_per_img;
+    const int t_in = lb - b * tiles_per_img;
+    const int tyi = t_in / tiles_x;
     const int ty0 = tyi * TH;
-    const int tx0 = (t_in - tyi * a.tiles_x) * TW;
-    const long long HW = a.HW;
-    const float* pn = a.pn + (size_t)b * 3 * HW;
-    const float* pr = a.pr + (size_t)b * K2 * HW;
-    const float* xyp = a.xy + (size_t)b * 2 * K2 * HW;
-    const float* ap = a.ang + (size_t)b * K2 * HW;
+    const int tx0 = (t_in - tyi * tiles_x) * TW;
+    const long long HW = (long long)H * W;
+    const float* pn = pred_norm + (size_t)b * 3 * HW;
+    const float* pr = prob + (size_t)b * K2 * HW;
+    const float* xyp = xy + (size_t)b * 2 * K2 * HW;
+    const float* ap = angle + (size_t)b * K2 * HW;
     const float* rp = a.ray + (size_t)b * a.ray_bstride;
     float* op = a.out + (size_t)b * 3 * HW;
-    const int W = a.W, H = a.H;
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
@@ -460,15 +387,16 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(Angmf
     const bool valid = (ty < TH) && (y < H) && (x < W);
     const uint32_t pb = valid ? (uint32_t)(y * W + x) * 4u : 0u;
 
-    // ---- phase A: window row ky of this lane's pixel, fp32 -----------------
-    float4 res = make_float4(0.f, 0.f, 0.f, 0.f);
-    if (valid) {
-        const int sy = clampi(y - P + ky, 0, H - 1);
-        const uint32_t rowb = (uint32_t)(sy * W);
-        // loads in consumption order: ray, then per neighbour its source
-        // normal and its 4 planes
-        const float rx = ldf(rp, pb), ry = ldf(rp + HW, pb), rz = ldf(rp + 2 * HW, pb);
-        float mxs[K], mys[K], mzs[K], xs[K], ys[K], th[K], wt[K];
+    // ---- phase A: window row ky of this lane's pixel -----------------------
+    // Every lane runs it (lanes past the tile read clamped, in-bounds
+    // addresses and discard the result).
+    const int sy = clampi(y - P + ky, 0, H - 1);
+    const uint32_t rowb = (uint32_t)(sy * W);
+    // loads in consumption order: ray, then per neighbour its source
+    // normal and its 4 planes
+    const float rxf = ldf(rp, pb), ryf = ldf(rp + HW, pb), rzf = ldf(rp + 2 * HW, pb);
+    float mxs[K], mys[K], mzs[K], xs[K], ys[K], th[K], wt[K];
+    {
         const size_t n0 = (size_t)ky * K;
         const uint32_t pbytes = (uint32_t)HW * 4u;
 #pragma unroll
@@ -482,93 +410,79 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(Angmf
             th[kx] = ldb(plane_rsrc(ap + (n0 + kx) * HW, pbytes), pb);
             wt[kx] = ldb(plane_rsrc(pr + (n0 + kx) * HW, pbytes), pb);
         }
+    }
+    {
+        const double rx = rxf, ry = ryf, rz = rzf;
         // cos(v', r) = v'.r / max(|v'||r|, 1e-8) with |v'| = 1
-        const float ir = 1.0f / fmaxf(sqrtf(fmaf(rx, rx, fmaf(ry, ry, rz * rz))), 1e-8f);
-        const float rsx = rx * ir, rsy = ry * ir, rsz = rz * ir;
+        const double r2 = fma(rx, rx, fma(ry, ry, rz * rz));
+        const double ir = (r2 < 1e-16) ? 1e8 : rsq64(r2);
         // (s + 0.5 - c)/f as the reference forms it: exactly 0 at the principal point
-        const double tv0d = ((double)sy + a.hc_v) * a.ifv64;
-        const float tv0 = (float)tv0d;
-        float acc0 = 0.f, acc1 = 0.f, acc2 = 0.f, q2 = 0.f;
+        const double tv0 = ((double)sy + a.hc_v) * a.ifv64;
+        double acc0 = 0.0, acc1 = 0.0, acc2 = 0.0, qs = 0.0;
         bool bad = false;
 #pragma unroll
         for (int kx = 0; kx < K; ++kx) {
             const int sx = clampi(x - P + kx, 0, W - 1);
-            const double tu0d = ((double)sx + a.hc_u) * a.ifu64;
-            const float tu0 = (float)tu0d;
-            const float mx = mxs[kx], my = mys[kx], mz = mzs[kx];
-            const float xsv = xs[kx], ysv = ys[kx], t = th[kx];
-            // The fast path takes unit source normals (every normal this op
-            // or RayReLU writes is one); others go to the double path.
-            const float m2 = fmaf(mx, mx, fmaf(my, my, mz * mz));
-            // g = P0 . m and q = D . m cancel when the surface is edge-on to
-            // the rays; formed in double (exact products of the fp32 inputs)
-            // they keep their relative precision, and so does V below.
-            const double du64 = (double)xsv * a.ifu64, dv64 = (double)ysv * a.ifv64;
-            const float g = (float)fma(tu0d, (double)mx, fma(tv0d, (double)my, (double)mz));
-            const float q = (float)fma(du64, (double)mx, dv64 * (double)my);
-            const float du = (float)du64, dv = (float)dv64;
-            const float s = fmaf(xsv, xsv, ysv * ysv);
-            const float dd = fmaf(rsq(fmaxf(s, 1e-24f)), q, g);
-            bad |= !(fabsf(m2 - 1.0f) <= 1e-5f) | (s < kMinXY2) | !(fabsf(t) <= 3.2f);
-            // axis = sign(dd) * V/|V|,  V = (g du - q tu0, g dv - q tv0, -q) = m x N
-            float Vx = fmaf(g, du, -q * tu0);
-            float Vy = fmaf(g, dv, -q * tv0);
-            float Vz = -q;
-            float n2 = fmaf(Vx, Vx, fmaf(Vy, Vy, q * q));
-            float sg = dd;
-            if (__builtin_expect(!(fabsf(dd) >= fmaxf(kDdRel * fabsf(g), kDdAbs)), 0)) {
-                precise_axis(mx, my, mz, sx, sy, xsv, ysv, a, Vx, Vy, Vz, bad);
-                n2 = 1.0f;
-                sg = 1.0f;
-            }
-            // 1/|V| with one Newton step: its rounding scales the rotation
-            float ia = rsq(n2);
-            ia = fmaf(0.5f * ia, fmaf(-n2 * ia, ia, 1.0f), ia);
-            ia = copysignf(ia, sg);
-            float st, ct;
-            sincos_small(t, st, ct);
-            const float S = st * ia;
-            // v' = m cos(t) + (V x m) sin(t)/|V|
-            const float vx = fmaf(fmaf(Vy, mz, -Vz * my), S, mx * ct);
-            const float vy = fmaf(fmaf(Vz, mx, -Vx * mz), S, my * ct);
-            const float vz = fmaf(fmaf(Vx, my, -Vy * mx), S, mz * ct);
-            // RayReLU against this pixel's ray
-            const float cs = fmaf(vx, rsx, fmaf(vy, rsy, vz * rsz));
-            const float dc = fmaxf(kRayEpsF - cs, 0.0f);
-            const float px = fmaf(rx, dc, vx);
-            const float py = fmaf(ry, dc, vy);
-            const float pz = fmaf(rz, dc, vz);
-            const float wi = wt[kx] * rsq(fmaf(px, px, fmaf(py, py, pz * pz)));
-            acc0 = fmaf(px, wi, acc0);
-            acc1 = fmaf(py, wi, acc1);
-            acc2 = fmaf(pz, wi, acc2);
-            q2 = fmaf(wi, wi, q2);
+            const double tu0 = ((double)sx + a.hc_u) * a.ifu64;
+            const double mx = mxs[kx], my = mys[kx], mz = mzs[kx];
+            const double xsd = xs[kx], ysd = ys[kx];
+            const float tf = th[kx];
+            // g = P0.m, q = D.m, dd = g + q/|xy| from the raw normal, as the
+            // reference forms dd (its 1e-8 clamp applies to this value)
+            const double du = xsd * a.ifu64, dv = ysd * a.ifv64;
+            const double g = fma(tu0, mx, fma(tv0, my, mz));
+            const double q = fma(du, mx, dv * my);
+            const double s = fma(xsd, xsd, ysd * ysd);
+            const double dd = fma(rsq64_1(s), q, g);
+            const double m2 = fma(mx, mx, fma(my, my, mz * mz));
+            bad |= !(m2 >= kMinM2) | !(s >= kMinXY2) | !(fabsf(tf) <= 3.2f) | !(fabs(dd) >= kDdMin);
+            // axis = sign(dd) V/|V|, V = (g du - q tu0, g dv - q tv0, -q) = m x N;
+            // v' = u cos t + (V x u) sin t/|V| with u = m/|m|
+            const double im = rsq64_1(m2);
+            const double Vx = fma(g, du, -q * tu0), Vy = fma(g, dv, -q * tv0);
+            const double ia = copysign(rsq64_1(fma(Vx, Vx, fma(Vy, Vy, q * q))), dd);
+            double st, ct;
+            sincos_small64((double)tf, st, ct);
+            const double S = st * ia * im, C = ct * im;
+            const double vx = fma(fma(Vy, mz, q * my), S, mx * C);
+            const double vy = fma(fma(-q, mx, -Vx * mz), S, my * C);
+            const double vz = fma(fma(Vx, my, -Vy * mx), S, mz * C);
+            // RayReLU against this pixel's ray, then the weighted unit term
+            const double cs = fma(vx, rx, fma(vy, ry, vz * rz)) * ir;
+            const double dc = fmax((double)kRayEpsF - cs, 0.0);
+            const double px = fma(rx, dc, vx), py = fma(ry, dc, vy), pz = fma(rz, dc, vz);
+            const double wi = (double)wt[kx] * rsq64_1(fma(px, px, fma(py, py, pz * pz)));
+            acc0 = fma(px, wi, acc0);
+            acc1 = fma(py, wi, acc1);
+            acc2 = fma(pz, wi, acc2);
+            qs = fma(wi, wi, qs);
         }
-        res = make_float4(acc0, acc1, acc2, bad ? __builtin_nanf("") : q2);
+        part[ky * npx + j] = make_double4(acc0, acc1, acc2, bad ? __builtin_nan("") : qs);
     }
-    part[ky * npx + j] = res;
     __syncthreads();
 
     // ---- phase B: reduce the K rows, write unflagged pixels ----------------
     if (ky == 0) {
         bool flag = false;
         if (valid) {
-            float4 sm = part[j];
+            double4 sm = part[j];
 #pragma unroll
             for (int rr = 1; rr < K; ++rr) {
-                const float4 t = part[rr * npx + j];
+                const double4 t = part[rr * npx + j];
                 sm.x += t.x;
                 sm.y += t.y;
                 sm.z += t.z;
                 sm.w += t.w;
             }
-            const float a2 = fmaf(sm.x, sm.x, fmaf(sm.y, sm.y, sm.z * sm.z));
-            flag = !(a2 >= kAccRatio2 * sm.w) || !(a2 <= 1e37f);
+            const double a2 = fma(sm.x, sm.x, fma(sm.y, sm.y, sm.z * sm.z));
+            // 1 / max(|acc|, 1e-12) as the reference; a non-finite or
+            // cancelled sum goes to the reference-order recompute
+            flag = !(a2 >= kAccRatio2 * sm.w) || !(a2 <= 1e300);
             if (!flag) {
-                const float inv = rsq(fmaxf(a2, 1e-24f));
-                stf(op, pb, sm.x * inv);
-                stf(op + HW, pb, sm.y * inv);
-                stf(op + 2 * HW, pb, sm.z * inv);
+                const double inv = (a2 < 1e-24) ? 1e12 : rsq64(a2);
+                stf(op, pb, (float)(sm.x * inv));
+                stf(op + HW, pb, (float)(sm.y * inv));
+                stf(op + 2 * HW, pb, (float)(sm.z * inv));
             }
         }
         const unsigned long long m = __ballot(flag);
@@ -576,20 +490,25 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(Angmf
     }
     __syncthreads();
 
-    // ---- phase C: double-precision recompute of flagged pixels -------------
-    // Each wave (group, ky) evaluates row ky of up to PPR flagged pixels of
-    // its group per pass, one neighbour per lane (inputs re-read; the block
-    // has just read them, so from L2); row partials meet in LDS and the
-    // ky == 0 wave writes the pixel.
+    // ---- phase C: reference-order recompute of flagged pixels --------------
     int maxc = 0;
     for (int g = 0; g < M; ++g) {
         const int c = __popcll(uniform64(smask[g]));
         maxc = c > maxc ? c : maxc;
     }
     if (maxc == 0) return;
+    // Phase C forms its per-lane values afresh: shared with phase A they
+    // would stay live across its loads and spill.
+    int tid = threadIdx.x, tw = TW;
+    asm volatile("" : "+v"(tid), "+s"(tw));
     const unsigned long long gmask = uniform64(smask[gi]);
     const int cnt = __popcll(gmask);
-    const int slot = lane / LPG, kxl = lane - slot * LPG;
+    // Each wave (group, ky) evaluates row ky of up to PPR flagged pixels of
+    // its group per pass, one neighbour per lane (inputs re-read; the block
+    // has just read them, so from L2); row partials meet in LDS and the
+    // ky == 0 wave writes the pixel.
+    const int clane = tid & 63;
+    const int slot = clane / LPG, kxl = clane - slot * LPG;
     unsigned long long rest = gmask;
     for (int base = 0; base < maxc; base += PPR) {
         int src = 0, fin_src = 0;
@@ -598,26 +517,25 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(Angmf
             const int bitpos = rest ? __ffsll((long long)rest) - 1 : 0;
             if (rest) rest &= rest - 1;
             if (sidx == slot) src = bitpos;
-            if (sidx == lane) fin_src = bitpos;
+            if (sidx == clane) fin_src = bitpos;
         }
         double p0 = 0.0, p1 = 0.0, p2 = 0.0;
         if ((base + slot) < cnt && kxl < K) {
             const int jj = gi * 64 + src;
-            const int fty = jj / TW, ftx = jj - fty * TW;
+            const int fty = jj / tw, ftx = jj - fty * tw;
             const int fy = ty0 + fty, fx = tx0 + ftx;
-            const int sy = clampi(fy - P + ky, 0, H - 1);
-            const int sx = clampi(fx - P + kxl, 0, W - 1);
+            const int fsy = clampi(fy - P + ky, 0, H - 1);
+            const int fsx = clampi(fx - P + kxl, 0, W - 1);
             const uint32_t fb = (uint32_t)(fy * W + fx) * 4u;
-            const uint32_t sb = (uint32_t)(sy * W + sx) * 4u;
+            const uint32_t sb = (uint32_t)(fsy * W + fsx) * 4u;
             const size_t n = (size_t)ky * K + kxl;
             const float mx = ldf(pn, sb), my = ldf(pn + HW, sb), mz = ldf(pn + 2 * HW, sb);
             const float xsv = ldf(xyp + n * HW, fb), ysv = ldf(xyp + (K2 + n) * HW, fb);
             const float thv = ldf(ap + n * HW, fb), wv = ldf(pr + n * HW, fb);
-            const float rx = ldf(rp, fb), ry = ldf(rp + HW, fb), rz = ldf(rp + 2 * HW, fb);
+            const float frx = ldf(rp, fb), fry = ldf(rp + HW, fb), frz = ldf(rp + 2 * HW, fb);
             double ox, oy, oz;
-            if (!nbr_fast_f64(mx, my, mz, sx, sy, xsv, ysv, thv, rx, ry, rz, a, ox, oy, oz))
-                nbr_ref_f64(mx, my, mz, sx + 0.5, sy + 0.5, xsv, ysv, thv, rx, ry, rz, a.fu,
-                            a.cu, a.fv, a.cv, ox, oy, oz);
+            nbr_ref_f64(mx, my, mz, fsx + 0.5, fsy + 0.5, xsv, ysv, thv, frx, fry, frz, a.fu, a.cu,
+                        a.fv, a.cv, ox, oy, oz);
             const double w = wv;
             p0 = w * ox;
             p1 = w * oy;
@@ -636,17 +554,19 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(Angmf
             f[2] = p2;
         }
         __syncthreads();
-        if (ky == 0 && lane < PPR && base + lane < cnt) {
+        if (ky == 0 && clane < PPR && base + clane < cnt) {
             double a0 = 0.0, a1 = 0.0, a2 = 0.0;
             for (int rr = 0; rr < K; ++rr) {
-                const double* f = fixp + ((gi * K + rr) * PPR + lane) * 3;
+                const double* f = fixp + ((gi * K + rr) * PPR + clane) * 3;
                 a0 += f[0];
                 a1 += f[1];
                 a2 += f[2];
             }
-            const double inv = 1.0 / smax(sqrt(a0 * a0 + a1 * a1 + a2 * a2), 1e-12);
+            // 1 / max(|acc|, 1e-12), with the reference's NaN and Inf results
+            const double n2 = a0 * a0 + a1 * a1 + a2 * a2;
+            const double inv = (n2 < 1e-24) ? 1e12 : (n2 == INFINITY ? 0.0 : rsq64(n2));
             const int jj = gi * 64 + fin_src;
-            const int fty = jj / TW, ftx = jj - fty * TW;
+            const int fty = jj / tw, ftx = jj - fty * tw;
             const uint32_t fb = (uint32_t)((ty0 + fty) * W + tx0 + ftx) * 4u;
             stf(op, fb, (float)(a0 * inv));
             stf(op + HW, fb, (float)(a1 * inv));
@@ -709,7 +629,8 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
     }
     const size_t lds = (size_t)lds_units(K, a.M) * 16;
     hipLaunchKernelGGL(angmf_f32_kernel<K>, dim3((unsigned)a.nblocks), dim3(64 * a.M * K),
-                       lds, s, a);
+                       lds, s, a.pn, a.xy, a.ang, a.pr, a.nblocks, a.tiles_per_img, a.tiles_x,
+                       a.W, a.H, pack_tile(a.TW, a.TH, a.M), a);
     return hipGetLastError();
 }
 
