@@ -47,26 +47,30 @@ namespace {
 // reference does arithmetic in double.
 constexpr float kRayEpsF = 1e-2f;
 
-// Raw xy pairs with |xy|^2 below this, and normals with |m|^2 below kMinM2,
-// go to the reference-order path: the reference's 1e-12 clamps stop
-// normalising them.
+// The fast path takes source normals with | |m|^2 - 1 | <= kUnitM2 (every
+// normal this op or RayReLU writes is one) and raw xy pairs with
+// |xy|^2 >= kMinXY2 (below it the reference's 1e-12 clamp stops normalising);
+// a neighbour outside sends its pixel to the reference-order path.
+constexpr float kUnitM2 = 1e-5f;
 constexpr double kMinXY2 = 1e-20;
-constexpr double kMinM2 = 1e-16;
 
-// The fast path's terms are within about 1e-14 * wi of the reference's
-// (wi = prob / |m'|, each term's weight after RayReLU), and the final
-// normalise divides their sum by |acc|: a pixel with
-// |acc|^2 < kAccRatio2 * sum(wi^2) goes to the reference-order path, so the
-// rest stay within 1e-14 / sqrt(kAccRatio2) = 1e-6.
-constexpr double kAccRatio2 = 1e-16;
+// Each fast-path term is within delta * wi of the reference's (wi = prob/|p|,
+// the term's weight before its final normalise, p the RayReLU'd rotation),
+// delta <= 1.3e-7 measured over 1.6M neighbours (rotation in fp32, RayReLU,
+// normalise and sum in double).  The final normalise divides the sum by
+// |acc|, so a pixel with |acc|^2 < kAccRatio2 * sum(wi^2) goes to the
+// reference-order path and the rest stay within 1.3e-7 / sqrt(kAccRatio2),
+// about 7e-6 per component.
+constexpr double kAccRatio2 = 3.5e-4;
 
 // The reference clamps |dd| < 1e-8 (src/dsine_ops.cpp:120-123), where the
-// reduced axis no longer holds: a neighbour with |dd| below kDdMin sends its
-// pixel to the reference-order path.  The fast path's dd is within about
-// 1e-14 of the reference's, so the sign of every other dd is the reference's,
-// and so is the axis -- including where m is nearly parallel to
+// reduced axis no longer holds.  The fast path's dd is within
+// 5.3e-8 * |q|/|xy| <= 5.3e-8 * |m| / min(|fu|, |fv|) of the reference's; a
+// neighbour with |dd| below dd_min = 1.01e-8 + 1e-7 / min(|fu|, |fv|) sends its
+// pixel to the reference-order path, so the sign of every other dd is the
+// reference's, and so is the axis -- including where m is nearly parallel to
 // N = D x P0 (g and q both small), since dd = g + q/|xy| is small then too.
-constexpr double kDdMin = 1.01e-8;
+constexpr double kDdClamp = 1.01e-8;
 
 // ---------------------------------------------------------------------------
 // Double-precision reference body
@@ -174,10 +178,9 @@ struct AngmfArgs {
     // fp32 kernel: TW x TH output tile per workgroup, M groups of 64 pixels,
     // one wave per (group, window row) -> 64*M*K threads.
     int TW, TH, M, tiles_x, tiles_per_img, nblocks;
-    float ifu, ifv;    // 1/fu, 1/fv
-    float tu_c, tv_c;  // (0.5 - cu)/fu, (0.5 - cv)/fv: source ray tu0 = sx*ifu + tu_c
-    double ifu64, ifv64;
-    double hc_u, hc_v;  // 0.5 - cu, 0.5 - cv
+    double ifu64, ifv64;  // 1/fu, 1/fv
+    double tu_c, tv_c;    // (0.5 - cu)/fu, (0.5 - cv)/fv: source ray tu0 = sx/fu + tu_c
+    double dd_min;        // |dd| below this sends a pixel to the reference-order path
 };
 
 // ---------------------------------------------------------------------------
@@ -281,6 +284,27 @@ __device__ __forceinline__ double rsq64_1(double x) {
     return fma(0.5 * y, fma(-x * y, y, 1.0), y);
 }
 
+// sin and cos of t for |t| <= 3.2 (callers send larger |t| to the
+// reference-order path).  Half-angle polynomials in u = h^2, h = t/2 in
+// [0, 1.6]: Chebyshev fits (computed for this kernel) with
+// sin(h) = h + h^3 S(u) to 8e-9 and cos(h) = 1 + u C(u) to 5e-10; then
+// sin t = 2 sin h cos h and cos t = cos^2 h - sin^2 h.
+__device__ __forceinline__ void sincos_small(float t, float& st, float& ct) {
+    const float h = 0.5f * t, u = h * h;
+    float p = fmaf(u, 2.630318e-06f, -0.00019821344f);
+    p = fmaf(u, p, 0.008333231f);
+    p = fmaf(u, p, -0.16666666f);
+    const float s = fmaf(h * u, p, h);
+    float q = fmaf(u, -2.625131e-07f, 2.4772546e-05f);
+    q = fmaf(u, q, -0.0013888624f);
+    q = fmaf(u, q, 0.041666657f);
+    q = fmaf(u, q, -0.5f);
+    const float c = fmaf(u, q, 1.0f);
+    const float sc = s * c;
+    st = sc + sc;
+    ct = fmaf(c, c, -(s * s));
+}
+
 // sin and cos of t for |t| <= 3.2 in double (callers send larger |t| to the
 // reference-order path).  Half-angle polynomials in u = h^2, h = t/2 in
 // [0, 1.6]: degree-17/16 Chebyshev fits (computed for this kernel) with
@@ -311,15 +335,42 @@ __device__ __forceinline__ void sincos_small64(double t, double& st, double& ct)
     ct = fma(c, c, -(s * s));
 }
 
+// One source-normal halo record: {mx, my, mz, 0} and {g, tu0}, g = P0.m
+// with P0 = (tu0, tv0, 1) the source pixel's ray at depth 1.  The fast path
+// takes | |m|^2 - 1 | <= kUnitM2; a NaN g marks the rest.  h indexes the
+// replicate-padded halo whose record 0 is source pixel (y0, x0).
+__device__ __forceinline__ void stage_halo(float mx, float my, float mz, int h, int hw, int y0,
+                                           int x0, int H, int W, const AngmfArgs& a,
+                                           float4* halo_m, double2* halo_g) {
+    const int hr = h / hw, hc = h - hr * hw;
+    const int sy = clampi(y0 + hr, 0, H - 1), sx = clampi(x0 + hc, 0, W - 1);
+    const double tu0 = fma((double)sx, a.ifu64, a.tu_c);
+    const double tv0 = fma((double)sy, a.ifv64, a.tv_c);
+    const double g = fma(tu0, (double)mx, fma(tv0, (double)my, (double)mz));
+    const float m2 = fmaf(mx, mx, fmaf(my, my, mz * mz));
+    halo_m[h] = make_float4(mx, my, mz, 0.0f);
+    halo_g[h] = make_double2((fabsf(m2 - 1.0f) <= kUnitM2) ? g : __builtin_nan(""), tu0);
+}
+
 // Flagged pixels recomputed per pass and group (64 / PPR lanes per pixel).
 __host__ __device__ constexpr int recompute_ppr(int K) { return (K <= 8) ? 8 : 4; }
+
+// Source-normal halo records of a TW x TH tile.
+__host__ __device__ inline int halo_count(int K, int TW, int TH) {
+    return (TW + 2 * (K / 2)) * (TH + 2 * (K / 2));
+}
+
+// LDS records reserved for the halo: one spare.
+__host__ __device__ inline int halo_slots(int K, int TW, int TH) { return halo_count(K, TW, TH) + 1; }
 
 // LDS of the fp32 kernel, in 16-byte units:
 //   smask[16]        u64 flagged-pixel mask per 64-pixel group (8 units)
 //   part[K][64*M]    per-window-row partial (acc.xyz, sum wi^2 or NaN), 4 doubles
+//   halo_m[nhalo+1]  source normal {mx, my, mz, 0} (+ a spare record)
+//   halo_g[nhalo+1]  {g, tu0} of the same source pixel
 //   fixp[M][K][PPR]  per-window-row fp64 partial of a flagged pixel (3 doubles)
-__host__ __device__ inline int lds_units(int K, int M) {
-    return 8 + 2 * K * 64 * M + (M * K * recompute_ppr(K) * 3 + 1) / 2;
+__host__ __device__ inline int lds_units(int K, int M, int TW, int TH) {
+    return 8 + 2 * K * 64 * M + 2 * halo_slots(K, TW, TH) + (M * K * recompute_ppr(K) * 3 + 1) / 2;
 }
 
 // Occupancy: a workgroup of n waves starts on a CU only when each of its 4
@@ -361,7 +412,9 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
     const int npx = 64 * M;
     unsigned long long* smask = reinterpret_cast<unsigned long long*>(smem);
     double4* part = reinterpret_cast<double4*>(smem + 8);
-    double* fixp = reinterpret_cast<double*>(part + K * npx);
+    float4* halo_m = reinterpret_cast<float4*>(part + K * npx);
+    double2* halo_g = reinterpret_cast<double2*>(halo_m + halo_slots(K, TW, TH));
+    double* fixp = reinterpret_cast<double*>(halo_g + halo_slots(K, TW, TH));
 
     const int lb = xcd_remap(blockIdx.x, nblocks);
     const int b = lb / tiles_per_img;
@@ -387,77 +440,122 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
     const bool valid = (ty < TH) && (y < H) && (x < W);
     const uint32_t pb = valid ? (uint32_t)(y * W + x) * 4u : 0u;
 
+    // ---- staging: the tile's source normals, with what depends on them only
+    // The (TH + 2P) x (TW + 2P) replicate-padded halo of pred_norm, as LDS
+    // records {mx, my, mz} and {g = P0.m, tu0} (P0 = (tu0, tv0, 1) the source
+    // pixel's ray at depth 1), at most two per thread.  Their loads are each
+    // lane's first, so waiting for them waits for nothing else.
+    const int hw = TW + 2 * P, nhalo = hw * (TH + 2 * P);
+    const int nthr = 64 * M * K;
+    float hm[3];
+    {
+        const int h = threadIdx.x;
+        const int hr = h / hw, hc = h - hr * hw;
+        const int hsy = clampi(ty0 - P + hr, 0, H - 1), hsx = clampi(tx0 - P + hc, 0, W - 1);
+        const uint32_t hb = (h < nhalo) ? (uint32_t)(hsy * W + hsx) * 4u : 0u;
+        hm[0] = ldf(pn, hb);
+        hm[1] = ldf(pn + HW, hb);
+        hm[2] = ldf(pn + 2 * HW, hb);
+    }
+    // keep the halo loads ahead of the plane loads in the instruction stream
+    __builtin_amdgcn_sched_barrier(0);
+
     // ---- phase A: window row ky of this lane's pixel -----------------------
-    // Every lane runs it (lanes past the tile read clamped, in-bounds
+    // Every lane runs it (lanes past the tile use clamped, in-bounds
     // addresses and discard the result).
     const int sy = clampi(y - P + ky, 0, H - 1);
-    const uint32_t rowb = (uint32_t)(sy * W);
-    // loads in consumption order: ray, then per neighbour its source
-    // normal and its 4 planes
+    // loads in consumption order: ray, then per neighbour its 4 planes
     const float rxf = ldf(rp, pb), ryf = ldf(rp + HW, pb), rzf = ldf(rp + 2 * HW, pb);
-    float mxs[K], mys[K], mzs[K], xs[K], ys[K], th[K], wt[K];
+    float xs[K], ys[K], th[K], wt[K];
     {
         const size_t n0 = (size_t)ky * K;
         const uint32_t pbytes = (uint32_t)HW * 4u;
 #pragma unroll
         for (int kx = 0; kx < K; ++kx) {
-            const uint32_t sb = (rowb + (uint32_t)clampi(x - P + kx, 0, W - 1)) * 4u;
-            mxs[kx] = ldf(pn, sb);
-            mys[kx] = ldf(pn + HW, sb);
-            mzs[kx] = ldf(pn + 2 * HW, sb);
             xs[kx] = ldb(plane_rsrc(xyp + (n0 + kx) * HW, pbytes), pb);
             ys[kx] = ldb(plane_rsrc(xyp + (K2 + n0 + kx) * HW, pbytes), pb);
             th[kx] = ldb(plane_rsrc(ap + (n0 + kx) * HW, pbytes), pb);
             wt[kx] = ldb(plane_rsrc(pr + (n0 + kx) * HW, pbytes), pb);
         }
     }
+    // Threads past the halo write a spare record: an unconditional use keeps
+    // the compiler from sinking the halo loads behind the plane loads.
+    stage_halo(hm[0], hm[1], hm[2], min((int)threadIdx.x, nhalo), hw, ty0 - P, tx0 - P, H, W, a,
+               halo_m, halo_g);
+    // A second record per thread (narrow tiles at k >= 7 only): loaded here,
+    // behind the plane loads, which it then waits for.
+    if (nhalo > nthr) {
+        const int h = threadIdx.x + nthr;
+        if (h < nhalo) {
+            const int hr = h / hw, hc = h - hr * hw;
+            const uint32_t hb = (uint32_t)(clampi(ty0 - P + hr, 0, H - 1) * W +
+                                           clampi(tx0 - P + hc, 0, W - 1)) * 4u;
+            stage_halo(ldf(pn, hb), ldf(pn + HW, hb), ldf(pn + 2 * HW, hb), h, hw, ty0 - P,
+                       tx0 - P, H, W, a, halo_m, halo_g);
+        }
+    }
+    __syncthreads();
     {
         const double rx = rxf, ry = ryf, rz = rzf;
         // cos(v', r) = v'.r / max(|v'||r|, 1e-8) with |v'| = 1
         const double r2 = fma(rx, rx, fma(ry, ry, rz * rz));
         const double ir = (r2 < 1e-16) ? 1e8 : rsq64(r2);
-        // (s + 0.5 - c)/f as the reference forms it: exactly 0 at the principal point
-        const double tv0 = ((double)sy + a.hc_v) * a.ifv64;
-        double acc0 = 0.0, acc1 = 0.0, acc2 = 0.0, qs = 0.0;
+        // the source pixels' ray row: ((sy + 0.5) - cv) / fv
+        const double tv0 = fma((double)sy, a.ifv64, a.tv_c);
+        // this lane's window row in the halo (lanes past the tile use its last row)
+        const int hrow = ((ty < TH) ? ty : TH - 1) + ky;
+        const int hbase = hrow * hw + tx;
+        double acc0 = 0.0, acc1 = 0.0, acc2 = 0.0;
+        float qs = 0.0f;  // sum of wi^2, for the cancellation test only
         bool bad = false;
 #pragma unroll
         for (int kx = 0; kx < K; ++kx) {
-            const int sx = clampi(x - P + kx, 0, W - 1);
-            const double tu0 = ((double)sx + a.hc_u) * a.ifu64;
-            const double mx = mxs[kx], my = mys[kx], mz = mzs[kx];
+            const float4 hmk = halo_m[hbase + kx];
+            const double2 hgk = halo_g[hbase + kx];
+            const float mx = hmk.x, my = hmk.y, mz = hmk.z;
+            const double g = hgk.x, tu0 = hgk.y;
             const double xsd = xs[kx], ysd = ys[kx];
-            const float tf = th[kx];
-            // g = P0.m, q = D.m, dd = g + q/|xy| from the raw normal, as the
-            // reference forms dd (its 1e-8 clamp applies to this value)
+            const float t = th[kx];
+            // q = D.m and dd = g + q/|xy| in double: exact products of the fp32
+            // inputs keep their relative precision where they cancel (a
+            // surface edge-on to the rays), and so does V below.  dd is formed
+            // from the raw normal as the reference forms it, with the hardware
+            // rsq (error < 5.3e-8 measured; dd_min covers it).
             const double du = xsd * a.ifu64, dv = ysd * a.ifv64;
-            const double g = fma(tu0, mx, fma(tv0, my, mz));
-            const double q = fma(du, mx, dv * my);
+            const double q = fma(du, (double)mx, dv * (double)my);
             const double s = fma(xsd, xsd, ysd * ysd);
-            const double dd = fma(rsq64_1(s), q, g);
-            const double m2 = fma(mx, mx, fma(my, my, mz * mz));
-            bad |= !(m2 >= kMinM2) | !(s >= kMinXY2) | !(fabsf(tf) <= 3.2f) | !(fabs(dd) >= kDdMin);
+            const double dd = fma(__builtin_amdgcn_rsq(s), q, g);
+            bad |= !(s >= kMinXY2) | !(fabsf(t) <= 3.2f) | !(fabs(dd) >= a.dd_min);
             // axis = sign(dd) V/|V|, V = (g du - q tu0, g dv - q tv0, -q) = m x N;
-            // v' = u cos t + (V x u) sin t/|V| with u = m/|m|
-            const double im = rsq64_1(m2);
-            const double Vx = fma(g, du, -q * tu0), Vy = fma(g, dv, -q * tv0);
-            const double ia = copysign(rsq64_1(fma(Vx, Vx, fma(Vy, Vy, q * q))), dd);
-            double st, ct;
-            sincos_small64((double)tf, st, ct);
-            const double S = st * ia * im, C = ct * im;
-            const double vx = fma(fma(Vy, mz, q * my), S, mx * C);
-            const double vy = fma(fma(-q, mx, -Vx * mz), S, my * C);
-            const double vz = fma(fma(Vx, my, -Vy * mx), S, mz * C);
-            // RayReLU against this pixel's ray, then the weighted unit term
-            const double cs = fma(vx, rx, fma(vy, ry, vz * rz)) * ir;
+            // v' = m' cos t + (V x m') sin t/|V|, m' = m/|m| (|m| = 1 to 1e-5:
+            // 1/|m| = 1.5 - m2/2 to 4e-11)
+            const float Vx = (float)fma(g, du, -q * tu0);
+            const float Vy = (float)fma(g, dv, -q * tv0);
+            const float Vz = (float)(-q);
+            const float n2 = fmaf(Vx, Vx, fmaf(Vy, Vy, Vz * Vz));
+            float ia = __builtin_amdgcn_rsqf(n2);
+            ia = fmaf(0.5f * ia, fmaf(-n2 * ia, ia, 1.0f), ia);
+            const float im = fmaf(-0.5f, fmaf(mx, mx, fmaf(my, my, mz * mz)), 1.5f);
+            float st, ct;
+            sincos_small(t, st, ct);
+            const float S = st * copysignf(ia, (float)dd) * im, C = ct * im;
+            const float vx = fmaf(fmaf(Vy, mz, -Vz * my), S, mx * C);
+            const float vy = fmaf(fmaf(Vz, mx, -Vx * mz), S, my * C);
+            const float vz = fmaf(fmaf(Vx, my, -Vy * mx), S, mz * C);
+            // RayReLU, the unit term and its weight in double: p = v' + r dc
+            // cancels where v' faces away from the ray, and the sum can cancel
+            const double vxd = vx, vyd = vy, vzd = vz;
+            const double cs = fma(vxd, rx, fma(vyd, ry, vzd * rz)) * ir;
             const double dc = fmax((double)kRayEpsF - cs, 0.0);
-            const double px = fma(rx, dc, vx), py = fma(ry, dc, vy), pz = fma(rz, dc, vz);
+            const double px = fma(rx, dc, vxd), py = fma(ry, dc, vyd), pz = fma(rz, dc, vzd);
             const double wi = (double)wt[kx] * rsq64_1(fma(px, px, fma(py, py, pz * pz)));
             acc0 = fma(px, wi, acc0);
             acc1 = fma(py, wi, acc1);
             acc2 = fma(pz, wi, acc2);
-            qs = fma(wi, wi, qs);
+            const float wf = (float)wi;
+            qs = fmaf(wf, wf, qs);
         }
-        part[ky * npx + j] = make_double4(acc0, acc1, acc2, bad ? __builtin_nan("") : qs);
+        part[ky * npx + j] = make_double4(acc0, acc1, acc2, bad ? __builtin_nan("") : (double)qs);
     }
     __syncthreads();
 
@@ -627,36 +725,44 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
         hipLaunchKernelGGL(angmf_f64_kernel<K>, dim3((unsigned)grid), dim3(256), 0, s, a);
         return hipGetLastError();
     }
-    const size_t lds = (size_t)lds_units(K, a.M) * 16;
+    const size_t lds = (size_t)lds_units(K, a.M, a.TW, a.TH) * 16;
     hipLaunchKernelGGL(angmf_f32_kernel<K>, dim3((unsigned)a.nblocks), dim3(64 * a.M * K),
                        lds, s, a.pn, a.xy, a.ang, a.pr, a.nblocks, a.tiles_per_img, a.tiles_x,
                        a.W, a.H, pack_tile(a.TW, a.TH, a.M), a);
     return hipGetLastError();
 }
 
-// Tile of the fp32 kernel: wide images take 64 x M tiles (each wave one
-// 256 B row segment per plane); narrow ones full-width tiles of TH rows with
-// the fewest idle lanes.  At most 16 waves (M*K) per workgroup.
+// LDS one workgroup may use.
+constexpr int kMaxLdsBytes = 65536;
+
+// Whether a TW x TH tile of M groups fits the kernel: its LDS, and at most
+// two halo records per thread.
+bool tile_fits(int K, int M, int TW, int TH) {
+    return lds_units(K, M, TW, TH) * 16 <= kMaxLdsBytes && halo_count(K, TW, TH) <= 2 * 64 * M * K;
+}
+
+// Tile of the fp32 kernel: wide images (and rows longer than a workgroup's
+// 64 * M pixels) take 64 x M tiles (each wave one 256 B row segment per
+// plane); narrow ones full-width tiles of TH rows with the fewest idle lanes
+// among those that fit.  At most 16 waves (M*K) per workgroup.
 void choose_tile(AngmfArgs& a, int K) {
     const int mmax = 16 / K;
-    if (a.W > 128) {
-        a.TW = 64;
-        a.M = mmax < 2 ? mmax : 2;
-        a.TH = a.M;
-    } else {
-        double best = -1.0;
-        for (int th = 1; th <= a.H && th <= 64 * mmax; ++th) {
-            const int npx = a.W * th;
-            const int m = (npx + 63) / 64;
-            if (m > mmax) break;
-            const double util = (double)npx / (64.0 * m);
-            if (util >= best) {
-                best = util;
-                a.TH = th;
-                a.M = m;
-            }
+    a.TW = 64;
+    a.M = mmax < 2 ? mmax : 2;
+    a.TH = a.M;
+    if (a.W > 128 || a.W > 64 * mmax) return;
+    double best = -1.0;
+    for (int th = 1; th <= a.H && th <= 64 * mmax; ++th) {
+        const int npx = a.W * th;
+        const int m = (npx + 63) / 64;
+        if (m > mmax) break;
+        const double util = (double)npx / (64.0 * m);
+        if (util >= best && tile_fits(K, m, a.W, th)) {
+            best = util;
+            a.TW = a.W;
+            a.TH = th;
+            a.M = m;
         }
-        a.TW = a.W;
     }
 }
 
@@ -732,15 +838,14 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
     a.fu = fu; a.cu = cu; a.fv = fv; a.cv = cv;
     a.ray_bstride = ray_bstride;
     a.HW = HW; a.B = B; a.H = H; a.W = W;
-    a.ifu = (float)(1.0 / fu);
-    a.ifv = (float)(1.0 / fv);
     a.ifu64 = 1.0 / fu;
     a.ifv64 = 1.0 / fv;
-    a.hc_u = 0.5 - cu;
-    a.hc_v = 0.5 - cv;
-    a.tu_c = (float)((0.5 - cu) / fu);
-    a.tv_c = (float)((0.5 - cv) / fv);
+    a.tu_c = (0.5 - cu) / fu;
+    a.tv_c = (0.5 - cv) / fv;
+    a.dd_min = kDdClamp + 1e-7 / std::fmin(std::fabs(fu), std::fabs(fv));
     choose_tile(a, k);
+    if (!tile_fits(k, a.M, a.TW, a.TH))
+        return fail(BVML_DSINE_ESIZE, "angmf_propagate: no tile fits the kernel's LDS");
     a.tiles_x = (W + a.TW - 1) / a.TW;
     const long long tiles_y = (H + a.TH - 1) / a.TH;
     const long long tpi = (long long)a.tiles_x * tiles_y;

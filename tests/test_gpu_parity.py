@@ -102,15 +102,19 @@ def _random_inputs(rng, B, H, W, k, theta_scale=1.0, per_sample_ray=False):
         "pred_norm": n.astype(np.float32),
         "prob": (1 / (1 + np.exp(-rng.standard_normal((B, K2, HW))))).astype(np.float32),
         "xy": rng.standard_normal((B, 2 * K2, HW)).astype(np.float32),
-        "angle": (rng.uniform(0, np.pi, (B, K2, HW)) * theta_scale).astype(np.float32),
+        "angle": (rng.uniform(-np.pi, np.pi, (B, K2, HW)) * theta_scale).astype(np.float32),
         "ray": ray,
         "intrinsics": (fu, cu, fv, cv),
     }
 
 
+# Tiles: wide (64 x M) above 128 columns or 64 * M pixels; narrow full-width
+# otherwise.  (1, 10, 64, 9) and (1, 5, 128, 7) stage two halo records per
+# thread; (1, 6, 100, 9) is a row longer than one k = 9 workgroup.
 SHAPES = [
     (1, 1, 1, 5), (1, 1, 9, 5), (1, 9, 1, 5), (1, 3, 4, 5), (1, 7, 130, 5),
     (1, 33, 65, 3), (2, 17, 200, 7), (1, 12, 20, 9), (3, 5, 6, 1), (1, 64, 64, 5),
+    (1, 10, 64, 9), (1, 5, 128, 7), (1, 6, 100, 9),
 ]
 
 
