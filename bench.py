@@ -6,10 +6,15 @@ HBM.  To keep the 256 MB Infinity Cache from serving the inputs, each step
 reads a different one of `--sets` input copies (together > 512 MB); the warm
 number (same inputs every step) is reported beside it.
 
+The K timed steps are the K kernel launches of one captured HIP graph,
+replayed once between two HIP events on the replay stream: the kernels run
+back to back, so the region measures the GPU, not Python's launch overhead
+(the same K steps launched eagerly from Python are reported as "eager").
+
 Prints one JSON line (rank 0):
-  value       Mpixel/s over the timed region (host clock, K steps)
+  value       Mpixel/s over the timed region (K steps / event time)
   roofline    HBM roofline of the kernel: algorithmic bytes per launch /
-              average launch duration from HIP events around each launch
+              average launch duration (event time of the region / K)
   cpu_baseline  the CPU oracle (double-precision restatement of the
               reference's CPU twin), one thread, on a bounded sample
 """
@@ -119,11 +124,10 @@ def main() -> int:
     base = dev_set()
     sets = [base] + [{key: t.clone() for key, t in base.items()} for _ in range(nsets - 1)]
     outs = [torch.empty_like(s["pred_norm"]) for s in sets]
-    stream = torch.cuda.current_stream(dev)
-    sptr = stream.cuda_stream
 
     def launch(i: int) -> None:
         s = sets[i]
+        sptr = torch.cuda.current_stream(dev).cuda_stream
         pn = s["pred_norm"]
         for c in range(w.calls):
             dst = outs[i]
@@ -135,28 +139,61 @@ def main() -> int:
                 raise RuntimeError(f"angmf_propagate_f32 failed: {st} {_lib.last_error()}")
             pn = dst
 
-    def timed(rotate: bool, steps: int):
-        starts = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
-        ends = [torch.cuda.Event(enable_timing=True) for _ in range(steps)]
+    def capture(rotate: bool):
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for i in range(args.steps):
+                launch(i % nsets if rotate else 0)
+        return g
+
+    def timed_graph(g):
+        stream = torch.cuda.current_stream(dev)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3  # seconds for args.steps steps
+
+    def timed_eager(steps: int) -> float:
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for i in range(steps):
-            starts[i].record(stream)
-            launch(i % nsets if rotate else 0)
-            ends[i].record(stream)
+            launch(i % nsets)
         torch.cuda.synchronize()
-        wall = time.perf_counter() - t0
-        ev = [s.elapsed_time(e) for s, e in zip(starts, ends)]
-        return wall, float(np.mean(ev)) / w.calls, float(np.median(ev)) / w.calls
+        return time.perf_counter() - t0
 
     for i in range(args.warmup):
         launch(i % nsets)
     torch.cuda.synchronize()
+    g_cold = capture(True)
+    g_warm = capture(False)
+    for _ in range(2):
+        g_cold.replay()
+        g_warm.replay()
+    torch.cuda.synchronize()
+    t_cold = timed_graph(g_cold)
+    t_warm = timed_graph(g_warm)
+    t_eager = timed_eager(args.steps)
 
-    wall, ev_mean_ms, ev_med_ms = timed(True, args.steps)
-    for i in range(args.warmup):
-        launch(0)
-    wall_w, ev_mean_w, ev_med_w = timed(False, args.steps)
+    # same-box copy ceiling: a device copy of one launch's algorithmic bytes
+    n_copy = bytes_per_call // 8
+    src = torch.ones(n_copy, dtype=torch.float32, device=dev)
+    dst_c = torch.empty_like(src)
+    for _ in range(5):
+        dst_c.copy_(src)
+    torch.cuda.synchronize()
+    c0 = torch.cuda.Event(enable_timing=True)
+    c1 = torch.cuda.Event(enable_timing=True)
+    c0.record()
+    for _ in range(20):
+        dst_c.copy_(src)
+    c1.record()
+    torch.cuda.synchronize()
+    copy_gbps = 2 * n_copy * 4 * 20 / (c0.elapsed_time(c1) * 1e-3) / 1e9
+    del src, dst_c
 
     if args.calib:
         n = bytes_per_call // 4
@@ -166,10 +203,11 @@ def main() -> int:
             dst.copy_(src)
         torch.cuda.synchronize()
 
-    ms_per_step = wall * 1e3 / args.steps
-    mpix = B * H * W * w.calls * args.steps / wall / 1e6
-    achieved = bytes_per_call / (ev_mean_ms * 1e-3) / 1e9
-    achieved_w = bytes_per_call / (ev_mean_w * 1e-3) / 1e9
+    launch_s = t_cold / (args.steps * w.calls)
+    ms_per_step = t_cold * 1e3 / args.steps
+    mpix = B * H * W * w.calls * args.steps / t_cold / 1e6
+    achieved = bytes_per_call / launch_s / 1e9
+    achieved_w = bytes_per_call / (t_warm / (args.steps * w.calls)) / 1e9
 
     line = {
         "metric": "Mpixel/s (+ achieved HBM GB/s, % of peak), DSINE propagation 256x256 k=5 fp32",
@@ -198,13 +236,18 @@ def main() -> int:
             "traffic": traffic_from_profile(w),
             "kernel": f"angmf_f32_kernel<{k}>",
             "bytes_per_launch": bytes_per_call,
-            "launch_us_mean": round(ev_mean_ms * 1e3, 3),
-            "launch_us_median": round(ev_med_ms * 1e3, 3),
+            "launch_us_mean": round(launch_s * 1e6, 3),
+            "copy_ceiling_gbps": round(copy_gbps, 1),
         },
         "warm": {
-            "value": round(B * H * W * w.calls * args.steps / wall_w / 1e6, 2),
-            "launch_us_mean": round(ev_mean_w * 1e3, 3),
+            "value": round(B * H * W * w.calls * args.steps / t_warm / 1e6, 2),
+            "launch_us_mean": round(t_warm / (args.steps * w.calls) * 1e6, 3),
             "achieved_gbps": round(achieved_w, 1),
+        },
+        "eager": {
+            "value": round(B * H * W * w.calls * args.steps / t_eager / 1e6, 2),
+            "us_per_step": round(t_eager / args.steps * 1e6, 3),
+            "note": "the same steps launched one by one from Python (host-bound)",
         },
         "gpu": torch.cuda.get_device_name(dev),
     }

@@ -65,7 +65,7 @@ constexpr double kAccRatio2 = 3.5e-4;
 
 // The reference clamps |dd| < 1e-8 (src/dsine_ops.cpp:120-123), where the
 // reduced axis no longer holds.  The fast path's dd is within
-// 5.3e-8 * |q|/|xy| <= 5.3e-8 * |m| / min(|fu|, |fv|) of the reference's; a
+// 1.3e-7 * |q|/|xy| <= 1.3e-7 * |m| / min(|fu|, |fv|) of the reference's; a
 // neighbour with |dd| below dd_min = 1.01e-8 + 1e-7 / min(|fu|, |fv|) sends its
 // pixel to the reference-order path, so the sign of every other dd is the
 // reference's, and so is the axis -- including where m is nearly parallel to
@@ -161,6 +161,13 @@ __device__ __forceinline__ void nbr_ref_f64(double nx, double ny, double nz,
 
 __device__ __forceinline__ int clampi(int v, int lo, int hi) {
     return v < lo ? lo : (v > hi ? hi : v);
+}
+
+// n / d for 0 <= n < 2^22 and 1 <= d given rd = 1/d in fp32 (within 1 ulp):
+// n + 0.5 keeps every quotient at least 0.5/d from an integer, far more than
+// the estimate's error (n/d * 2^-22).
+__device__ __forceinline__ int small_div(int n, float rd) {
+    return (int)(((float)n + 0.5f) * rd);
 }
 
 // Per-launch constants of angmf_propagate.
@@ -335,21 +342,31 @@ __device__ __forceinline__ void sincos_small64(double t, double& st, double& ct)
     ct = fma(c, c, -(s * s));
 }
 
-// One source-normal halo record: {mx, my, mz, 0} and {g, tu0}, g = P0.m
-// with P0 = (tu0, tv0, 1) the source pixel's ray at depth 1.  The fast path
-// takes | |m|^2 - 1 | <= kUnitM2; a NaN g marks the rest.  h indexes the
-// replicate-padded halo whose record 0 is source pixel (y0, x0).
+// The source-normal halo of a tile, in LDS as four arrays of 16-byte records
+// (one per source pixel; consecutive lanes read consecutive records).
+struct Halo {
+    float4* m;    // mx, my, mz, 1/|m| = 1.5 - |m|^2/2
+    double2* gt;  // g = P0.m (NaN unless | |m|^2 - 1 | <= kUnitM2), tu0
+    double2* ab;  // mx/fu, my/fv
+    double2* gu;  // g/fu, g/fv
+};
+
+// One halo record.  P0 = (tu0, tv0, 1) is the source pixel's ray at depth 1;
+// h indexes the replicate-padded halo whose record 0 is source pixel (y0, x0).
 __device__ __forceinline__ void stage_halo(float mx, float my, float mz, int h, int hw, int y0,
                                            int x0, int H, int W, const AngmfArgs& a,
-                                           float4* halo_m, double2* halo_g) {
-    const int hr = h / hw, hc = h - hr * hw;
+                                           const Halo& hl) {
+    const int hr = small_div(h, __builtin_amdgcn_rcpf((float)hw)), hc = h - hr * hw;
     const int sy = clampi(y0 + hr, 0, H - 1), sx = clampi(x0 + hc, 0, W - 1);
     const double tu0 = fma((double)sx, a.ifu64, a.tu_c);
     const double tv0 = fma((double)sy, a.ifv64, a.tv_c);
-    const double g = fma(tu0, (double)mx, fma(tv0, (double)my, (double)mz));
     const float m2 = fmaf(mx, mx, fmaf(my, my, mz * mz));
-    halo_m[h] = make_float4(mx, my, mz, 0.0f);
-    halo_g[h] = make_double2((fabsf(m2 - 1.0f) <= kUnitM2) ? g : __builtin_nan(""), tu0);
+    const double g0 = fma(tu0, (double)mx, fma(tv0, (double)my, (double)mz));
+    const double g = (fabsf(m2 - 1.0f) <= kUnitM2) ? g0 : __builtin_nan("");
+    hl.m[h] = make_float4(mx, my, mz, fmaf(-0.5f, m2, 1.5f));
+    hl.gt[h] = make_double2(g, tu0);
+    hl.ab[h] = make_double2((double)mx * a.ifu64, (double)my * a.ifv64);
+    hl.gu[h] = make_double2(g * a.ifu64, g * a.ifv64);
 }
 
 // Flagged pixels recomputed per pass and group (64 / PPR lanes per pixel).
@@ -360,17 +377,16 @@ __host__ __device__ inline int halo_count(int K, int TW, int TH) {
     return (TW + 2 * (K / 2)) * (TH + 2 * (K / 2));
 }
 
-// LDS records reserved for the halo: one spare.
+// LDS records reserved per halo array: one spare.
 __host__ __device__ inline int halo_slots(int K, int TW, int TH) { return halo_count(K, TW, TH) + 1; }
 
 // LDS of the fp32 kernel, in 16-byte units:
 //   smask[16]        u64 flagged-pixel mask per 64-pixel group (8 units)
 //   part[K][64*M]    per-window-row partial (acc.xyz, sum wi^2 or NaN), 4 doubles
-//   halo_m[nhalo+1]  source normal {mx, my, mz, 0} (+ a spare record)
-//   halo_g[nhalo+1]  {g, tu0} of the same source pixel
+//   halo.m, .gt, .ab, .gu [nhalo + 1]  source-pixel records (+ a spare)
 //   fixp[M][K][PPR]  per-window-row fp64 partial of a flagged pixel (3 doubles)
 __host__ __device__ inline int lds_units(int K, int M, int TW, int TH) {
-    return 8 + 2 * K * 64 * M + 2 * halo_slots(K, TW, TH) + (M * K * recompute_ppr(K) * 3 + 1) / 2;
+    return 8 + 2 * K * 64 * M + 4 * halo_slots(K, TW, TH) + (M * K * recompute_ppr(K) * 3 + 1) / 2;
 }
 
 // Occupancy: a workgroup of n waves starts on a CU only when each of its 4
@@ -412,9 +428,13 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
     const int npx = 64 * M;
     unsigned long long* smask = reinterpret_cast<unsigned long long*>(smem);
     double4* part = reinterpret_cast<double4*>(smem + 8);
-    float4* halo_m = reinterpret_cast<float4*>(part + K * npx);
-    double2* halo_g = reinterpret_cast<double2*>(halo_m + halo_slots(K, TW, TH));
-    double* fixp = reinterpret_cast<double*>(halo_g + halo_slots(K, TW, TH));
+    const int nslot = halo_slots(K, TW, TH);
+    Halo hl;
+    hl.m = reinterpret_cast<float4*>(part + K * npx);
+    hl.gt = reinterpret_cast<double2*>(hl.m + nslot);
+    hl.ab = hl.gt + nslot;
+    hl.gu = hl.ab + nslot;
+    double* fixp = reinterpret_cast<double*>(hl.gu + nslot);
 
     const int lb = xcd_remap(blockIdx.x, nblocks);
     const int b = lb / tiles_per_img;
@@ -435,22 +455,22 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
     const int ky = __builtin_amdgcn_readfirstlane(wave / M);
     const int gi = wave - ky * M;
     const int j = gi * 64 + lane;
-    const int ty = j / TW, tx = j - ty * TW;
+    const float rtw = __builtin_amdgcn_rcpf((float)TW);
+    const int ty = small_div(j, rtw), tx = j - ty * TW;
     const int y = ty0 + ty, x = tx0 + tx;
     const bool valid = (ty < TH) && (y < H) && (x < W);
     const uint32_t pb = valid ? (uint32_t)(y * W + x) * 4u : 0u;
 
     // ---- staging: the tile's source normals, with what depends on them only
-    // The (TH + 2P) x (TW + 2P) replicate-padded halo of pred_norm, as LDS
-    // records {mx, my, mz} and {g = P0.m, tu0} (P0 = (tu0, tv0, 1) the source
-    // pixel's ray at depth 1), at most two per thread.  Their loads are each
-    // lane's first, so waiting for them waits for nothing else.
+    // The (TH + 2P) x (TW + 2P) replicate-padded halo of pred_norm, one LDS
+    // record per source pixel (Halo), at most two per thread.  Their loads are
+    // each lane's first, so waiting for them waits for nothing else.
     const int hw = TW + 2 * P, nhalo = hw * (TH + 2 * P);
     const int nthr = 64 * M * K;
     float hm[3];
     {
         const int h = threadIdx.x;
-        const int hr = h / hw, hc = h - hr * hw;
+        const int hr = small_div(h, __builtin_amdgcn_rcpf((float)hw)), hc = h - hr * hw;
         const int hsy = clampi(ty0 - P + hr, 0, H - 1), hsx = clampi(tx0 - P + hc, 0, W - 1);
         const uint32_t hb = (h < nhalo) ? (uint32_t)(hsy * W + hsx) * 4u : 0u;
         hm[0] = ldf(pn, hb);
@@ -481,7 +501,7 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
     // Threads past the halo write a spare record: an unconditional use keeps
     // the compiler from sinking the halo loads behind the plane loads.
     stage_halo(hm[0], hm[1], hm[2], min((int)threadIdx.x, nhalo), hw, ty0 - P, tx0 - P, H, W, a,
-               halo_m, halo_g);
+               hl);
     // A second record per thread (narrow tiles at k >= 7 only): loaded here,
     // behind the plane loads, which it then waits for.
     if (nhalo > nthr) {
@@ -491,7 +511,7 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
             const uint32_t hb = (uint32_t)(clampi(ty0 - P + hr, 0, H - 1) * W +
                                            clampi(tx0 - P + hc, 0, W - 1)) * 4u;
             stage_halo(ldf(pn, hb), ldf(pn + HW, hb), ldf(pn + 2 * HW, hb), h, hw, ty0 - P,
-                       tx0 - P, H, W, a, halo_m, halo_g);
+                       tx0 - P, H, W, a, hl);
         }
     }
     __syncthreads();
@@ -499,7 +519,7 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
         const double rx = rxf, ry = ryf, rz = rzf;
         // cos(v', r) = v'.r / max(|v'||r|, 1e-8) with |v'| = 1
         const double r2 = fma(rx, rx, fma(ry, ry, rz * rz));
-        const double ir = (r2 < 1e-16) ? 1e8 : rsq64(r2);
+        const double ir = (r2 < 1e-16) ? 1e8 : rsq64_1(r2);
         // the source pixels' ray row: ((sy + 0.5) - cv) / fv
         const double tv0 = fma((double)sy, a.ifv64, a.tv_c);
         // this lane's window row in the halo (lanes past the tile use its last row)
@@ -510,32 +530,29 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
         bool bad = false;
 #pragma unroll
         for (int kx = 0; kx < K; ++kx) {
-            const float4 hmk = halo_m[hbase + kx];
-            const double2 hgk = halo_g[hbase + kx];
-            const float mx = hmk.x, my = hmk.y, mz = hmk.z;
-            const double g = hgk.x, tu0 = hgk.y;
+            const float4 hm = hl.m[hbase + kx];
+            const double2 gt = hl.gt[hbase + kx], ab = hl.ab[hbase + kx], gu = hl.gu[hbase + kx];
+            const float mx = hm.x, my = hm.y, mz = hm.z, im = hm.w;
             const double xsd = xs[kx], ysd = ys[kx];
             const float t = th[kx];
-            // q = D.m and dd = g + q/|xy| in double: exact products of the fp32
-            // inputs keep their relative precision where they cancel (a
-            // surface edge-on to the rays), and so does V below.  dd is formed
-            // from the raw normal as the reference forms it, with the hardware
-            // rsq (error < 5.3e-8 measured; dd_min covers it).
-            const double du = xsd * a.ifu64, dv = ysd * a.ifv64;
-            const double q = fma(du, (double)mx, dv * (double)my);
+            // q = D.m = xs mx/fu + ys my/fv and dd = g + q/|xy| in double: exact
+            // products of the fp32 inputs keep their relative precision where
+            // they cancel (a surface edge-on to the rays), and so does V below.
+            // dd is formed from the raw normal as the reference forms it; its
+            // 1/|xy| comes from the hardware double rsq (relative error
+            // < 5.3e-8 measured), which dd_min covers.
+            const double q = fma(xsd, ab.x, ysd * ab.y);
             const double s = fma(xsd, xsd, ysd * ysd);
-            const double dd = fma(__builtin_amdgcn_rsq(s), q, g);
+            const double dd = fma(__builtin_amdgcn_rsq(s), q, gt.x);
             bad |= !(s >= kMinXY2) | !(fabsf(t) <= 3.2f) | !(fabs(dd) >= a.dd_min);
-            // axis = sign(dd) V/|V|, V = (g du - q tu0, g dv - q tv0, -q) = m x N;
-            // v' = m' cos t + (V x m') sin t/|V|, m' = m/|m| (|m| = 1 to 1e-5:
-            // 1/|m| = 1.5 - m2/2 to 4e-11)
-            const float Vx = (float)fma(g, du, -q * tu0);
-            const float Vy = (float)fma(g, dv, -q * tv0);
+            // axis = sign(dd) V/|V|, V = (g xs/fu - q tu0, g ys/fv - q tv0, -q) = m x N;
+            // v' = m' cos t + (V x m') sin t/|V|, m' = m/|m|
+            const float Vx = (float)fma(gu.x, xsd, -q * gt.y);
+            const float Vy = (float)fma(gu.y, ysd, -q * tv0);
             const float Vz = (float)(-q);
             const float n2 = fmaf(Vx, Vx, fmaf(Vy, Vy, Vz * Vz));
             float ia = __builtin_amdgcn_rsqf(n2);
             ia = fmaf(0.5f * ia, fmaf(-n2 * ia, ia, 1.0f), ia);
-            const float im = fmaf(-0.5f, fmaf(mx, mx, fmaf(my, my, mz * mz)), 1.5f);
             float st, ct;
             sincos_small(t, st, ct);
             const float S = st * copysignf(ia, (float)dd) * im, C = ct * im;
@@ -577,7 +594,7 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
             // cancelled sum goes to the reference-order recompute
             flag = !(a2 >= kAccRatio2 * sm.w) || !(a2 <= 1e300);
             if (!flag) {
-                const double inv = (a2 < 1e-24) ? 1e12 : rsq64(a2);
+                const double inv = (a2 < 1e-24) ? 1e12 : rsq64_1(a2);
                 stf(op, pb, (float)(sm.x * inv));
                 stf(op + HW, pb, (float)(sm.y * inv));
                 stf(op + 2 * HW, pb, (float)(sm.z * inv));
@@ -749,6 +766,7 @@ void choose_tile(AngmfArgs& a, int K) {
     const int mmax = 16 / K;
     a.TW = 64;
     a.M = mmax < 2 ? mmax : 2;
+    if (!tile_fits(K, a.M, 64, a.M)) a.M = 1;
     a.TH = a.M;
     if (a.W > 128 || a.W > 64 * mmax) return;
     double best = -1.0;
