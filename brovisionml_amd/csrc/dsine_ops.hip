@@ -6,28 +6,34 @@
 //   angmf_propagate  fused k x k neighbour rotate + RayReLU + prob-weighted
 //                    sum + renormalise (src/dsine_ops.cpp:78-172)
 //
-// angmf_propagate is HBM-bound (436 B/px at k=5) with a VALU budget of
-// roughly 120 lane-instructions per neighbour at 70 % of 8 TB/s, so the
-// reference's double-precision formulation (about 380 per neighbour) cannot be
-// used as the fast path.  The fast kernel instead
-//   * stages the tile's replicate-padded pred_norm halo in LDS once, as
-//     per-source records: the unit normal m, g = P0.m (P0 = the source pixel's
-//     ray at depth 1), and the products ifu*mx, ifv*my, g*ifu, g*ifv;
-//   * evaluates each neighbour in fp32 with an algebraically reduced axis:
-//     the reference's axis normalize(du + dz*tu, dv + dz*tv, dz) with
-//     dz = num/dd equals sign(dd) * normalize(V) where
-//     V = (g*xs/fu - q*tu0, g*ys/fv - q*tv0, -q), q = xs*mx/fu + ys*my/fv on the
-//     RAW xy pair and tu0, tv0 the source ray -- the xy normalisation and the
-//     quadratic terms cancel exactly, and V.m == 0, so Rodrigues reduces to
-//     m*cos(t) + (V x m)*sin(t)/|V|;
-//   * flags every pixel whose fp32 result could miss the reference by more
-//     than the parity tolerance -- a neighbour with |dd| near 0 (the axis
-//     flips sign there), a near-zero xy pair or normal (the reference's
-//     clamps take over), a non-finite value, or an accumulator that is small
-//     compared with the root-sum-square of its terms (the final normalise
-//     amplifies fp32 rounding by 1/|acc|) -- and recomputes flagged pixels in
-//     double precision in the reference's own operation order, one neighbour
-//     per lane of the wave that owns the pixel, with a wave-wide reduction.
+// angmf_propagate moves 436 B/px at k=5 but also does about 25 neighbour
+// rotations per pixel; at the parity bar (1e-5 per component) the reference's
+// all-double formulation costs more VALU time than the HBM traffic takes, so
+// the fast kernel mixes precisions where the error analysis allows:
+//   * the tile's replicate-padded pred_norm halo is staged in LDS once, one
+//     record per source pixel: m and 1/|m|, g = P0.m (P0 = the source pixel's
+//     ray at depth 1, NaN unless m is a unit normal), tu0 = (0.5 - cu)/fu + x/fu
+//     and the double products mx/fu, my/fv, g/fu, g/fv;
+//   * the rotation axis is algebraically reduced: the reference's
+//     normalize(du + dz*tu, dv + dz*tv, dz) with dz = num/dd equals
+//     sign(dd) * V/|V| with V = (g*xs/fu - q*tu0, g*ys/fv - q*tv0, -q),
+//     q = xs*mx/fu + ys*my/fv on the RAW xy pair -- the xy normalisation and
+//     the quadratic terms cancel exactly, and V.m == 0, so Rodrigues reduces to
+//     m'*cos(t) + (V x m')*sin(t)/|V|;
+//   * q, dd = g + q/|xy| and V are formed in double from the fp32 inputs (they
+//     cancel where a surface is edge-on to the rays); the rotation itself
+//     (|V|, sin, cos, the cross product) runs in fp32; RayReLU, the weight
+//     prob/|p|, the accumulation and the final normalise run in double;
+//   * a pixel goes to a reference-order double recompute (one neighbour per
+//     lane of the wave that owns it, wave-wide reduction) when any neighbour
+//     is outside the reduced form's domain -- |dd| near the reference's 1e-8
+//     clamp, a tiny xy pair, a non-unit source normal, |t| > 3.2, a
+//     non-finite value -- or when |acc|^2 < 3.5e-4 * sum(wi^2), where the
+//     final normalise would amplify the per-term error (<= 1.3e-7 * wi) past
+//     the parity bar.
+// Workgroups are k x (16/k) waves (one window row per wave, a 64-pixel-wide
+// tile per wave group); at k=5 the kernel is held to 80 VGPRs so that two
+// 10-wave workgroups fit each CU and a 256x256 image runs in one round.
 // The double-precision body is also available as its own kernel
 // (BVML_DSINE_FP64), which reproduces the CPU reference to a few ulps.
 
@@ -163,9 +169,10 @@ __device__ __forceinline__ int clampi(int v, int lo, int hi) {
     return v < lo ? lo : (v > hi ? hi : v);
 }
 
-// n / d for 0 <= n < 2^22 and 1 <= d given rd = 1/d in fp32 (within 1 ulp):
-// n + 0.5 keeps every quotient at least 0.5/d from an integer, far more than
-// the estimate's error (n/d * 2^-22).
+// n / d for 0 <= n < 2^21 and 1 <= d given rd = 1/d in fp32 (within 1 ulp):
+// n + 0.5 keeps every quotient at least 0.5/d from an integer, more than the
+// estimate's error (below n/d * 2^-22).  Callers divide thread and halo
+// indices (n < 2^12) by tile widths.
 __device__ __forceinline__ int small_div(int n, float rd) {
     return (int)(((float)n + 0.5f) * rd);
 }
@@ -184,7 +191,7 @@ struct AngmfArgs {
     int B, H, W;
     // fp32 kernel: TW x TH output tile per workgroup, M groups of 64 pixels,
     // one wave per (group, window row) -> 64*M*K threads.
-    int TW, TH, M, tiles_x, tiles_per_img, nblocks;
+    int TW, TH, M, tiles_x, tiles_per_img;
     double ifu64, ifv64;  // 1/fu, 1/fv
     double tu_c, tv_c;    // (0.5 - cu)/fu, (0.5 - cv)/fv: source ray tu0 = sx/fu + tu_c
     double dd_min;        // |dd| below this sends a pixel to the reference-order path
@@ -264,6 +271,28 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t plane_rsrc(const float* plane,
 
 __device__ __forceinline__ float ldb(__amdgpu_buffer_rsrc_t r, uint32_t byte_off) {
     return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, 0, 0));
+}
+
+// Raw buffer load at a per-lane byte offset plus a wave-uniform one (held in
+// an SGPR): one descriptor then serves several planes of a tensor.
+__device__ __forceinline__ float ldbs(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, uint32_t soff) {
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, (int)soff, 0));
+}
+
+// base advanced by plane * plane_bytes bytes (64-bit product of 32-bit factors).
+__device__ __forceinline__ const float* at_plane(const float* base, uint32_t plane,
+                                                 uint32_t plane_bytes) {
+    return reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) +
+                                          (uint64_t)plane * plane_bytes);
+}
+
+// n / d for 0 <= n < 2^31 and 1 <= d < 2^31 from d's magic number
+// mag = floor(2^32 (2^L - d) / d) + 1, L = ceil(log2 d) (Granlund and
+// Montgomery, "Division by invariant integers using multiplication", 1994):
+// (umulhi(n, mag) + n) >> L, whose sum cannot wrap for n < 2^31.
+__device__ __forceinline__ int magic_div(int n, unsigned mag, int L) {
+    return (int)((__umulhi((unsigned)n, mag) + (unsigned)n) >> L);
 }
 
 __device__ __forceinline__ void stf(float* base, uint32_t byte_off, float v) {
@@ -396,14 +425,15 @@ __host__ __device__ inline int lds_units(int K, int M, int TW, int TH) {
 template <int K>
 constexpr int kWavesPerEU = (K == 5) ? 6 : 4;
 
-// TW, TH and M of the fp32 kernel's tile, packed into one kernel argument.
-__host__ __device__ inline unsigned pack_tile(int TW, int TH, int M) {
-    return (unsigned)TW | ((unsigned)TH << 11) | ((unsigned)M << 22);
+// TW (< 2^11), TH (< 2^11) and M (< 2^5) of the fp32 kernel's tile and the
+// shift L (< 2^5) of the tiles_x magic number, packed into one kernel argument.
+__host__ __device__ inline unsigned pack_tile(int TW, int TH, int M, int L) {
+    return (unsigned)TW | ((unsigned)TH << 11) | ((unsigned)M << 22) | ((unsigned)L << 27);
 }
 
-// One workgroup = M groups of 64 output pixels (a TW x TH tile of one
-// sample) x K waves, wave (ky, group) handling window row ky of one pixel per
-// lane.  Each lane loads the row's K source normals (L1/L2 hits: the window
+// One workgroup = M groups of 64 output pixels (a TW x TH tile of sample
+// blockIdx.y) x K waves, wave gi * K + ky handling window row ky of group gi,
+// one pixel per lane.  Each lane loads the row's K source normals (L1/L2 hits: the window
 // rows of neighbouring pixels overlap) and the 4K per-neighbour planes, in the
 // order it consumes them, and accumulates the row's fp32 partial; the K
 // partials meet in LDS.
@@ -414,17 +444,23 @@ __host__ __device__ inline unsigned pack_tile(int TW, int TH, int M) {
 // -amdgpu-kernarg-preload-count), so a workgroup issues its loads without
 // first waiting for a scalar load of its arguments -- which, once the
 // other workgroups have the memory system saturated, takes microseconds.
+// The scalar unit is shared by the CU's 20 waves, so the prologue keeps
+// scalar work short: no runtime integer division (the tile row comes from a
+// host-computed magic number, the window row from a constant divisor) and
+// one buffer descriptor per input tensor, its K planes reached through the
+// scalar offset.
 template <int K>
 __global__ __launch_bounds__(64 * K * (16 / K))
 __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
     const float* __restrict__ pred_norm, const float* __restrict__ xy,
-    const float* __restrict__ angle, const float* __restrict__ prob, int nblocks,
-    int tiles_per_img, int tiles_x, int W, int H, unsigned tile, AngmfArgs a) {
+    const float* __restrict__ angle, const float* __restrict__ prob, int W, int H,
+    unsigned tile, int tiles_per_img, int tiles_x, unsigned tx_magic, AngmfArgs a) {
     constexpr int P = K / 2, K2 = K * K;
     constexpr int PPR = recompute_ppr(K);  // flagged pixels per recompute pass
     constexpr int LPG = 64 / PPR;          // lanes per flagged pixel in the recompute
     extern __shared__ float4 smem[];
-    const int TW = (int)(tile & 0x7ffu), TH = (int)((tile >> 11) & 0x7ffu), M = (int)(tile >> 22);
+    const int TW = (int)(tile & 0x7ffu), TH = (int)((tile >> 11) & 0x7ffu);
+    const int M = (int)((tile >> 22) & 0x1fu), LX = (int)(tile >> 27);
     const int npx = 64 * M;
     unsigned long long* smask = reinterpret_cast<unsigned long long*>(smem);
     double4* part = reinterpret_cast<double4*>(smem + 8);
@@ -436,24 +472,18 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
     hl.gu = hl.ab + nslot;
     double* fixp = reinterpret_cast<double*>(hl.gu + nslot);
 
-    const int lb = xcd_remap(blockIdx.x, nblocks);
-    const int b = lb / tiles_per_img;
-    const int t_in = lb - b * tiles_per_img;
-    const int tyi = t_in / tiles_x;
+    const int b = blockIdx.y;
+    const int lb = xcd_remap(blockIdx.x, tiles_per_img);
+    const int tyi = magic_div(lb, tx_magic, LX);
     const int ty0 = tyi * TH;
-    const int tx0 = (t_in - tyi * tiles_x) * TW;
+    const int tx0 = (lb - tyi * tiles_x) * TW;
     const long long HW = (long long)H * W;
-    const float* pn = pred_norm + (size_t)b * 3 * HW;
-    const float* pr = prob + (size_t)b * K2 * HW;
-    const float* xyp = xy + (size_t)b * 2 * K2 * HW;
-    const float* ap = angle + (size_t)b * K2 * HW;
-    const float* rp = a.ray + (size_t)b * a.ray_bstride;
-    float* op = a.out + (size_t)b * 3 * HW;
+    const uint32_t HW4 = (uint32_t)HW * 4u;  // plane bytes; max(K, 3) * HW4 < 2^32
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int ky = __builtin_amdgcn_readfirstlane(wave / M);
-    const int gi = wave - ky * M;
+    const int gi = wave / K;
+    const int ky = wave - gi * K;
     const int j = gi * 64 + lane;
     const float rtw = __builtin_amdgcn_rcpf((float)TW);
     const int ty = small_div(j, rtw), tx = j - ty * TW;
@@ -467,15 +497,17 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
     // each lane's first, so waiting for them waits for nothing else.
     const int hw = TW + 2 * P, nhalo = hw * (TH + 2 * P);
     const int nthr = 64 * M * K;
+    const float rhw = __builtin_amdgcn_rcpf((float)hw);
+    const __amdgpu_buffer_rsrc_t rpn = plane_rsrc(at_plane(pred_norm, (uint32_t)b * 3u, HW4), 3u * HW4);
     float hm[3];
     {
         const int h = threadIdx.x;
-        const int hr = small_div(h, __builtin_amdgcn_rcpf((float)hw)), hc = h - hr * hw;
+        const int hr = small_div(h, rhw), hc = h - hr * hw;
         const int hsy = clampi(ty0 - P + hr, 0, H - 1), hsx = clampi(tx0 - P + hc, 0, W - 1);
         const uint32_t hb = (h < nhalo) ? (uint32_t)(hsy * W + hsx) * 4u : 0u;
-        hm[0] = ldf(pn, hb);
-        hm[1] = ldf(pn + HW, hb);
-        hm[2] = ldf(pn + 2 * HW, hb);
+        hm[0] = ldbs(rpn, hb, 0u);
+        hm[1] = ldbs(rpn, hb, HW4);
+        hm[2] = ldbs(rpn, hb, 2u * HW4);
     }
     // keep the halo loads ahead of the plane loads in the instruction stream
     __builtin_amdgcn_sched_barrier(0);
@@ -485,17 +517,27 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
     // addresses and discard the result).
     const int sy = clampi(y - P + ky, 0, H - 1);
     // loads in consumption order: ray, then per neighbour its 4 planes
-    const float rxf = ldf(rp, pb), ryf = ldf(rp + HW, pb), rzf = ldf(rp + 2 * HW, pb);
+    const __amdgpu_buffer_rsrc_t rry =
+        plane_rsrc(a.ray + (size_t)b * a.ray_bstride, 3u * HW4);
+    const float rxf = ldbs(rry, pb, 0u), ryf = ldbs(rry, pb, HW4), rzf = ldbs(rry, pb, 2u * HW4);
     float xs[K], ys[K], th[K], wt[K];
     {
-        const size_t n0 = (size_t)ky * K;
-        const uint32_t pbytes = (uint32_t)HW * 4u;
+        // planes (sample b, window row ky, kx) of each input: one descriptor
+        // per tensor at kx = 0, plane kx at scalar offset kx * HW4
+        const uint32_t pxy = (uint32_t)b * (2u * K2) + (uint32_t)(ky * K);
+        const uint32_t pk = (uint32_t)b * K2 + (uint32_t)(ky * K);
+        const uint32_t rows = (uint32_t)K * HW4;
+        const __amdgpu_buffer_rsrc_t rxs = plane_rsrc(at_plane(xy, pxy, HW4), rows);
+        const __amdgpu_buffer_rsrc_t rys = plane_rsrc(at_plane(xy, pxy + K2, HW4), rows);
+        const __amdgpu_buffer_rsrc_t rth = plane_rsrc(at_plane(angle, pk, HW4), rows);
+        const __amdgpu_buffer_rsrc_t rwt = plane_rsrc(at_plane(prob, pk, HW4), rows);
 #pragma unroll
         for (int kx = 0; kx < K; ++kx) {
-            xs[kx] = ldb(plane_rsrc(xyp + (n0 + kx) * HW, pbytes), pb);
-            ys[kx] = ldb(plane_rsrc(xyp + (K2 + n0 + kx) * HW, pbytes), pb);
-            th[kx] = ldb(plane_rsrc(ap + (n0 + kx) * HW, pbytes), pb);
-            wt[kx] = ldb(plane_rsrc(pr + (n0 + kx) * HW, pbytes), pb);
+            const uint32_t so = (uint32_t)kx * HW4;
+            xs[kx] = ldbs(rxs, pb, so);
+            ys[kx] = ldbs(rys, pb, so);
+            th[kx] = ldbs(rth, pb, so);
+            wt[kx] = ldbs(rwt, pb, so);
         }
     }
     // Threads past the halo write a spare record: an unconditional use keeps
@@ -507,11 +549,11 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
     if (nhalo > nthr) {
         const int h = threadIdx.x + nthr;
         if (h < nhalo) {
-            const int hr = h / hw, hc = h - hr * hw;
+            const int hr = small_div(h, rhw), hc = h - hr * hw;
             const uint32_t hb = (uint32_t)(clampi(ty0 - P + hr, 0, H - 1) * W +
                                            clampi(tx0 - P + hc, 0, W - 1)) * 4u;
-            stage_halo(ldf(pn, hb), ldf(pn + HW, hb), ldf(pn + 2 * HW, hb), h, hw, ty0 - P,
-                       tx0 - P, H, W, a, hl);
+            stage_halo(ldbs(rpn, hb, 0u), ldbs(rpn, hb, HW4), ldbs(rpn, hb, 2u * HW4), h, hw,
+                       ty0 - P, tx0 - P, H, W, a, hl);
         }
     }
     __syncthreads();
@@ -595,6 +637,7 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
             flag = !(a2 >= kAccRatio2 * sm.w) || !(a2 <= 1e300);
             if (!flag) {
                 const double inv = (a2 < 1e-24) ? 1e12 : rsq64_1(a2);
+                float* op = a.out + (size_t)b * 3 * HW;
                 stf(op, pb, (float)(sm.x * inv));
                 stf(op + HW, pb, (float)(sm.y * inv));
                 stf(op + 2 * HW, pb, (float)(sm.z * inv));
@@ -618,6 +661,12 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
     asm volatile("" : "+v"(tid), "+s"(tw));
     const unsigned long long gmask = uniform64(smask[gi]);
     const int cnt = __popcll(gmask);
+    const float* pn = pred_norm + (size_t)b * 3 * HW;
+    const float* pr = prob + (size_t)b * K2 * HW;
+    const float* xyp = xy + (size_t)b * 2 * K2 * HW;
+    const float* ap = angle + (size_t)b * K2 * HW;
+    const float* rp = a.ray + (size_t)b * a.ray_bstride;
+    float* op = a.out + (size_t)b * 3 * HW;
     // Each wave (group, ky) evaluates row ky of up to PPR flagged pixels of
     // its group per pass, one neighbour per lane (inputs re-read; the block
     // has just read them, so from L2); row partials meet in LDS and the
@@ -734,6 +783,18 @@ bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
     return a0 < b0 + bbytes && b0 < a0 + abytes;
 }
 
+// Samples per launch of the fp32 kernel (its grid's y extent).
+constexpr int kMaxGridY = 65535;
+
+// Magic number of d (1 <= d < 2^31) for magic_div: L = ceil(log2 d),
+// mag = floor(2^32 (2^L - d) / d) + 1 < 2^32.
+void div_magic(int d, unsigned& mag, int& L) {
+    L = 0;
+    while ((1LL << L) < d) ++L;
+    mag = (unsigned)(((1ULL << 32) * ((1ULL << L) - (unsigned long long)d)) /
+                         (unsigned long long)d + 1);
+}
+
 template <int K>
 hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
     if (fp64) {
@@ -743,10 +804,28 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
         return hipGetLastError();
     }
     const size_t lds = (size_t)lds_units(K, a.M, a.TW, a.TH) * 16;
-    hipLaunchKernelGGL(angmf_f32_kernel<K>, dim3((unsigned)a.nblocks), dim3(64 * a.M * K),
-                       lds, s, a.pn, a.xy, a.ang, a.pr, a.nblocks, a.tiles_per_img, a.tiles_x,
-                       a.W, a.H, pack_tile(a.TW, a.TH, a.M), a);
-    return hipGetLastError();
+    unsigned mag;
+    int L;
+    div_magic(a.tiles_x, mag, L);
+    const unsigned tile = pack_tile(a.TW, a.TH, a.M, L);
+    // one launch per kMaxGridY samples (grid y = sample)
+    for (int b0 = 0; b0 < a.B; b0 += kMaxGridY) {
+        const int nb = (a.B - b0 < kMaxGridY) ? a.B - b0 : kMaxGridY;
+        AngmfArgs c = a;
+        c.pn += (size_t)b0 * 3 * a.HW;
+        c.pr += (size_t)b0 * K * K * a.HW;
+        c.xy += (size_t)b0 * 2 * K * K * a.HW;
+        c.ang += (size_t)b0 * K * K * a.HW;
+        c.ray += (size_t)b0 * a.ray_bstride;
+        c.out += (size_t)b0 * 3 * a.HW;
+        c.B = nb;
+        hipLaunchKernelGGL(angmf_f32_kernel<K>, dim3((unsigned)a.tiles_per_img, (unsigned)nb),
+                           dim3(64 * a.M * K), lds, s, c.pn, c.xy, c.ang, c.pr, a.W, a.H, tile,
+                           a.tiles_per_img, a.tiles_x, mag, c);
+        const hipError_t e = hipGetLastError();
+        if (e != hipSuccess) return e;
+    }
+    return hipSuccess;
 }
 
 // LDS one workgroup may use.
@@ -867,9 +946,7 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
     a.tiles_x = (W + a.TW - 1) / a.TW;
     const long long tiles_y = (H + a.TH - 1) / a.TH;
     const long long tpi = (long long)a.tiles_x * tiles_y;
-    if (tpi * B > INT_MAX) return fail(BVML_DSINE_ESIZE, "angmf_propagate: too many tiles");
-    a.tiles_per_img = (int)tpi;
-    a.nblocks = (int)(tpi * B);
+    a.tiles_per_img = (int)(tpi < INT_MAX ? tpi : INT_MAX);
 
     // The fp32 path assumes intrinsics in the range real cameras produce;
     // anything else runs the double-precision kernel (same results as the
@@ -878,7 +955,13 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
                       std::isfinite(cv) && std::fabs(fu) >= 1e-3 && std::fabs(fu) <= 1e7 &&
                       std::fabs(fv) >= 1e-3 && std::fabs(fv) <= 1e7 &&
                       std::fabs(cu) <= 1e7 && std::fabs(cv) <= 1e7;
-    const bool fp64 = (flags & BVML_DSINE_FP64) || !sane;
+    // The fp32 kernel addresses K planes (and the 3 planes of pred_norm and
+    // ray) from one 32-bit buffer offset, and its grid holds one image's tiles
+    // in x; larger images also run the double-precision kernel.
+    const long long nplanes = k > 3 ? k : 3;
+    const bool fits32 = nplanes * HW * 4 < (1LL << 32) && tpi < (1LL << 31) &&
+                        tpi * 64 * a.M * k < (1LL << 32);
+    const bool fp64 = (flags & BVML_DSINE_FP64) || !sane || !fits32;
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e;
     switch (k) {
