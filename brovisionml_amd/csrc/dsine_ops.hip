@@ -401,6 +401,22 @@ __device__ __forceinline__ void stage_halo(float mx, float my, float mz, int h, 
 // Flagged pixels recomputed per pass and group (64 / PPR lanes per pixel).
 __host__ __device__ constexpr int recompute_ppr(int K) { return (K <= 8) ? 8 : 4; }
 
+// Waves per 64-pixel group: the group's K*K neighbours are split into G
+// near-equal runs of consecutive neighbours (row-major over the window), one
+// run per wave.  Workgroups hold kWgWaves = 8 waves (8/G groups): the SPI
+// places a workgroup of n waves only where every SIMD has ceil(n/4) free
+// slots, and spreads 8 waves exactly 2 per SIMD, so every SIMD carries the
+// same work (10-wave workgroups land 3+3+2+2, and two of them leave one SIMD
+// of most CUs with 6 waves where the average is 5).
+__host__ __device__ constexpr int group_waves(int K) {
+    return K == 1 ? 1 : (K == 3 ? 2 : (K == 9 ? 8 : 4));
+}
+constexpr int kWgWaves = 8;
+
+// Neighbours whose planes a wave loads before the halo staging and its
+// barrier; the rest are loaded after it.
+constexpr int kPreLoads = 2;
+
 // Source-normal halo records of a TW x TH tile.
 __host__ __device__ inline int halo_count(int K, int TW, int TH) {
     return (TW + 2 * (K / 2)) * (TH + 2 * (K / 2));
@@ -411,19 +427,15 @@ __host__ __device__ inline int halo_slots(int K, int TW, int TH) { return halo_c
 
 // LDS of the fp32 kernel, in 16-byte units:
 //   smask[16]        u64 flagged-pixel mask per 64-pixel group (8 units)
-//   part[K][64*M]    per-window-row partial (acc.xyz, sum wi^2 or NaN), 4 doubles
+//   part[G][64*M]    per-wave partial (acc.xyz, sum wi^2 or NaN), 4 doubles
 //   halo.m, .gt, .ab, .gu [nhalo + 1]  source-pixel records (+ a spare)
-//   fixp[M][K][PPR]  per-window-row fp64 partial of a flagged pixel (3 doubles)
+//   tvrow[TH + 2P]   source ray row term tv0 per halo row (doubles)
+//   fixp[M][G][PPR]  per-wave fp64 partial of a flagged pixel (3 doubles)
 __host__ __device__ inline int lds_units(int K, int M, int TW, int TH) {
-    return 8 + 2 * K * 64 * M + 4 * halo_slots(K, TW, TH) + (M * K * recompute_ppr(K) * 3 + 1) / 2;
+    const int G = group_waves(K), nrow = TH + 2 * (K / 2);
+    return 8 + 2 * G * 64 * M + 4 * halo_slots(K, TW, TH) + (nrow + 1) / 2 +
+           (M * G * recompute_ppr(K) * 3 + 1) / 2;
 }
-
-// Occupancy: a workgroup of n waves starts on a CU only when each of its 4
-// SIMDs has room for ceil(n/4) more waves.  k = 5 runs 10-wave workgroups
-// (3 + 3 + 2 + 2 waves), so two of them per CU -- the 256x256 shape in a
-// single round -- need 6 waves per SIMD, i.e. <= 80 VGPRs.
-template <int K>
-constexpr int kWavesPerEU = (K == 5) ? 6 : 4;
 
 // TW (< 2^11), TH (< 2^11) and M (< 2^5) of the fp32 kernel's tile and the
 // shift L (< 2^5) of the tiles_x magic number, packed into one kernel argument.
@@ -432,11 +444,14 @@ __host__ __device__ inline unsigned pack_tile(int TW, int TH, int M, int L) {
 }
 
 // One workgroup = M groups of 64 output pixels (a TW x TH tile of sample
-// blockIdx.y) x K waves, wave gi * K + ky handling window row ky of group gi,
-// one pixel per lane.  Each lane loads the row's K source normals (L1/L2 hits: the window
-// rows of neighbouring pixels overlap) and the 4K per-neighbour planes, in the
-// order it consumes them, and accumulates the row's fp32 partial; the K
-// partials meet in LDS.
+// blockIdx.y) x G waves; wave gi * G + r evaluates one run of the window's
+// neighbours for the 64 pixels of group gi, one pixel per lane.  The runs'
+// roles rotate with gi so the longer run falls on a different SIMD in each
+// group.  Each lane loads its run's 4 planes per neighbour in the order it
+// consumes them; the source normals come from the tile's halo in LDS; the G
+// partials of a pixel meet in LDS.  Two workgroups per CU hold 4 waves per
+// SIMD, so the kernel may use 128 VGPRs and a 256x256 image still runs in
+// one round.
 //
 // Everything the first loads' addresses depend on comes first in the
 // argument list, as scalars: gfx950 preloads up to 14 dwords of kernel
@@ -444,33 +459,38 @@ __host__ __device__ inline unsigned pack_tile(int TW, int TH, int M, int L) {
 // -amdgpu-kernarg-preload-count), so a workgroup issues its loads without
 // first waiting for a scalar load of its arguments -- which, once the
 // other workgroups have the memory system saturated, takes microseconds.
-// The scalar unit is shared by the CU's 20 waves, so the prologue keeps
-// scalar work short: no runtime integer division (the tile row comes from a
-// host-computed magic number, the window row from a constant divisor) and
-// one buffer descriptor per input tensor, its K planes reached through the
+// The scalar unit is shared by the CU's waves, so the prologue keeps scalar
+// work short: no runtime integer division (the tile row comes from a
+// host-computed magic number, the wave's group from a constant divisor) and
+// one buffer descriptor per input tensor, its planes reached through the
 // scalar offset.
 template <int K>
-__global__ __launch_bounds__(64 * K * (16 / K))
-__attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
-    const float* __restrict__ pred_norm, const float* __restrict__ xy,
-    const float* __restrict__ angle, const float* __restrict__ prob, int W, int H,
-    unsigned tile, int tiles_per_img, int tiles_x, unsigned tx_magic, AngmfArgs a) {
+__global__ __launch_bounds__(64 * kWgWaves) __attribute__((amdgpu_waves_per_eu(4)))
+void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restrict__ xy,
+                      const float* __restrict__ angle, const float* __restrict__ prob, int W,
+                      int H, unsigned tile, int tiles_per_img, int tiles_x, unsigned tx_magic,
+                      AngmfArgs a) {
     constexpr int P = K / 2, K2 = K * K;
-    constexpr int PPR = recompute_ppr(K);  // flagged pixels per recompute pass
-    constexpr int LPG = 64 / PPR;          // lanes per flagged pixel in the recompute
+    constexpr int G = group_waves(K);
+    constexpr int RUN = K2 / G, REM = K2 % G;  // run lengths RUN + 1 (REM runs) and RUN
+    constexpr int NR = RUN + (REM ? 1 : 0);    // longest run
+    constexpr int PPR = recompute_ppr(K);      // flagged pixels per recompute pass
+    constexpr int LPG = 64 / PPR;              // lanes per flagged pixel in the recompute
     extern __shared__ float4 smem[];
     const int TW = (int)(tile & 0x7ffu), TH = (int)((tile >> 11) & 0x7ffu);
     const int M = (int)((tile >> 22) & 0x1fu), LX = (int)(tile >> 27);
     const int npx = 64 * M;
+    const int nrow = TH + 2 * P;
     unsigned long long* smask = reinterpret_cast<unsigned long long*>(smem);
     double4* part = reinterpret_cast<double4*>(smem + 8);
     const int nslot = halo_slots(K, TW, TH);
     Halo hl;
-    hl.m = reinterpret_cast<float4*>(part + K * npx);
+    hl.m = reinterpret_cast<float4*>(part + G * npx);
     hl.gt = reinterpret_cast<double2*>(hl.m + nslot);
     hl.ab = hl.gt + nslot;
     hl.gu = hl.ab + nslot;
-    double* fixp = reinterpret_cast<double*>(hl.gu + nslot);
+    double* tvrow = reinterpret_cast<double*>(hl.gu + nslot);
+    double* fixp = tvrow + 2 * ((nrow + 1) / 2);
 
     const int b = blockIdx.y;
     const int lb = xcd_remap(blockIdx.x, tiles_per_img);
@@ -478,12 +498,15 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
     const int ty0 = tyi * TH;
     const int tx0 = (lb - tyi * tiles_x) * TW;
     const long long HW = (long long)H * W;
-    const uint32_t HW4 = (uint32_t)HW * 4u;  // plane bytes; max(K, 3) * HW4 < 2^32
+    const uint32_t HW4 = (uint32_t)HW * 4u;  // plane bytes; max(NR, 3) * HW4 < 2^32
 
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int lane = threadIdx.x & 63;
-    const int gi = wave / K;
-    const int ky = wave - gi * K;
+    const int gi = wave / G;
+    const int r = wave - gi * G;
+    const int role = (r + gi) % G;
+    const int n0 = role * RUN + (role < REM ? role : REM);  // first neighbour of the run
+    const int nrun = RUN + (role < REM ? 1 : 0);
     const int j = gi * 64 + lane;
     const float rtw = __builtin_amdgcn_rcpf((float)TW);
     const int ty = small_div(j, rtw), tx = j - ty * TW;
@@ -495,10 +518,11 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
     // The (TH + 2P) x (TW + 2P) replicate-padded halo of pred_norm, one LDS
     // record per source pixel (Halo), at most two per thread.  Their loads are
     // each lane's first, so waiting for them waits for nothing else.
-    const int hw = TW + 2 * P, nhalo = hw * (TH + 2 * P);
-    const int nthr = 64 * M * K;
+    const int hw = TW + 2 * P, nhalo = hw * nrow;
+    const int nthr = 64 * M * G;
     const float rhw = __builtin_amdgcn_rcpf((float)hw);
-    const __amdgpu_buffer_rsrc_t rpn = plane_rsrc(at_plane(pred_norm, (uint32_t)b * 3u, HW4), 3u * HW4);
+    const __amdgpu_buffer_rsrc_t rpn =
+        plane_rsrc(at_plane(pred_norm, (uint32_t)b * 3u, HW4), 3u * HW4);
     float hm[3];
     {
         const int h = threadIdx.x;
@@ -512,39 +536,40 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
     // keep the halo loads ahead of the plane loads in the instruction stream
     __builtin_amdgcn_sched_barrier(0);
 
-    // ---- phase A: window row ky of this lane's pixel -----------------------
+    // ---- phase A: this wave's run of neighbours for this lane's pixel ------
     // Every lane runs it (lanes past the tile use clamped, in-bounds
     // addresses and discard the result).
-    const int sy = clampi(y - P + ky, 0, H - 1);
-    // loads in consumption order: ray, then per neighbour its 4 planes
-    const __amdgpu_buffer_rsrc_t rry =
-        plane_rsrc(a.ray + (size_t)b * a.ray_bstride, 3u * HW4);
+    // loads in consumption order: ray, then per neighbour its 4 planes; the
+    // planes of the first kPreLoads neighbours go out before the staging,
+    // the rest after its barrier
+    const __amdgpu_buffer_rsrc_t rry = plane_rsrc(a.ray + (size_t)b * a.ray_bstride, 3u * HW4);
     const float rxf = ldbs(rry, pb, 0u), ryf = ldbs(rry, pb, HW4), rzf = ldbs(rry, pb, 2u * HW4);
-    float xs[K], ys[K], th[K], wt[K];
-    {
-        // planes (sample b, window row ky, kx) of each input: one descriptor
-        // per tensor at kx = 0, plane kx at scalar offset kx * HW4
-        const uint32_t pxy = (uint32_t)b * (2u * K2) + (uint32_t)(ky * K);
-        const uint32_t pk = (uint32_t)b * K2 + (uint32_t)(ky * K);
-        const uint32_t rows = (uint32_t)K * HW4;
-        const __amdgpu_buffer_rsrc_t rxs = plane_rsrc(at_plane(xy, pxy, HW4), rows);
-        const __amdgpu_buffer_rsrc_t rys = plane_rsrc(at_plane(xy, pxy + K2, HW4), rows);
-        const __amdgpu_buffer_rsrc_t rth = plane_rsrc(at_plane(angle, pk, HW4), rows);
-        const __amdgpu_buffer_rsrc_t rwt = plane_rsrc(at_plane(prob, pk, HW4), rows);
+    float xs[NR], ys[NR], th[NR], wt[NR];
+    // planes (sample b, neighbour n0 + i) of each input: one descriptor per
+    // tensor at i = 0, plane i at scalar offset i * HW4.  A run one shorter
+    // than NR re-reads its first planes in the last slot, unused.
+    const uint32_t pxy = (uint32_t)b * (2u * K2) + (uint32_t)n0;
+    const uint32_t pk = (uint32_t)b * K2 + (uint32_t)n0;
+    const uint32_t span = (uint32_t)nrun * HW4;
+    const __amdgpu_buffer_rsrc_t rxs = plane_rsrc(at_plane(xy, pxy, HW4), span);
+    const __amdgpu_buffer_rsrc_t rys = plane_rsrc(at_plane(xy, pxy + K2, HW4), span);
+    const __amdgpu_buffer_rsrc_t rth = plane_rsrc(at_plane(angle, pk, HW4), span);
+    const __amdgpu_buffer_rsrc_t rwt = plane_rsrc(at_plane(prob, pk, HW4), span);
+    auto load_planes = [&](int i) {
+        const uint32_t so = (i < NR - 1 || nrun == NR) ? (uint32_t)i * HW4 : 0u;
+        xs[i] = ldbs(rxs, pb, so);
+        ys[i] = ldbs(rys, pb, so);
+        th[i] = ldbs(rth, pb, so);
+        wt[i] = ldbs(rwt, pb, so);
+    };
+    constexpr int PRE = kPreLoads < NR ? kPreLoads : NR;
 #pragma unroll
-        for (int kx = 0; kx < K; ++kx) {
-            const uint32_t so = (uint32_t)kx * HW4;
-            xs[kx] = ldbs(rxs, pb, so);
-            ys[kx] = ldbs(rys, pb, so);
-            th[kx] = ldbs(rth, pb, so);
-            wt[kx] = ldbs(rwt, pb, so);
-        }
-    }
+    for (int i = 0; i < PRE; ++i) load_planes(i);
     // Threads past the halo write a spare record: an unconditional use keeps
     // the compiler from sinking the halo loads behind the plane loads.
     stage_halo(hm[0], hm[1], hm[2], min((int)threadIdx.x, nhalo), hw, ty0 - P, tx0 - P, H, W, a,
                hl);
-    // A second record per thread (narrow tiles at k >= 7 only): loaded here,
+    // A second record per thread (k >= 7, and narrow tiles): loaded here,
     // behind the plane loads, which it then waits for.
     if (nhalo > nthr) {
         const int h = threadIdx.x + nthr;
@@ -556,27 +581,35 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
                        ty0 - P, tx0 - P, H, W, a, hl);
         }
     }
+    // the source pixels' ray row per halo row: ((sy + 0.5) - cv) / fv
+    if ((int)threadIdx.x < nrow)
+        tvrow[threadIdx.x] = fma((double)clampi(ty0 - P + (int)threadIdx.x, 0, H - 1), a.ifv64, a.tv_c);
     __syncthreads();
+#pragma unroll
+    for (int i = PRE; i < NR; ++i) load_planes(i);
     {
         const double rx = rxf, ry = ryf, rz = rzf;
         // cos(v', r) = v'.r / max(|v'||r|, 1e-8) with |v'| = 1
         const double r2 = fma(rx, rx, fma(ry, ry, rz * rz));
         const double ir = (r2 < 1e-16) ? 1e8 : rsq64_1(r2);
-        // the source pixels' ray row: ((sy + 0.5) - cv) / fv
-        const double tv0 = fma((double)sy, a.ifv64, a.tv_c);
-        // this lane's window row in the halo (lanes past the tile use its last row)
-        const int hrow = ((ty < TH) ? ty : TH - 1) + ky;
+        // this lane's window in the halo (lanes past the tile use its last row)
+        const int hrow = (ty < TH) ? ty : TH - 1;
         const int hbase = hrow * hw + tx;
         double acc0 = 0.0, acc1 = 0.0, acc2 = 0.0;
         float qs = 0.0f;  // sum of wi^2, for the cancellation test only
         bool bad = false;
 #pragma unroll
-        for (int kx = 0; kx < K; ++kx) {
-            const float4 hm = hl.m[hbase + kx];
-            const double2 gt = hl.gt[hbase + kx], ab = hl.ab[hbase + kx], gu = hl.gu[hbase + kx];
+        for (int i = 0; i < NR; ++i) {
+            if (i == NR - 1 && nrun != NR) break;
+            const int n = n0 + i;
+            const int ky = n / K, kx = n - ky * K;
+            const int h = hbase + ky * hw + kx;
+            const float4 hm = hl.m[h];
+            const double2 gt = hl.gt[h], ab = hl.ab[h], gu = hl.gu[h];
+            const double tv0 = tvrow[hrow + ky];
             const float mx = hm.x, my = hm.y, mz = hm.z, im = hm.w;
-            const double xsd = xs[kx], ysd = ys[kx];
-            const float t = th[kx];
+            const double xsd = xs[i], ysd = ys[i];
+            const float t = th[i];
             // q = D.m = xs mx/fu + ys my/fv and dd = g + q/|xy| in double: exact
             // products of the fp32 inputs keep their relative precision where
             // they cancel (a surface edge-on to the rays), and so does V below.
@@ -607,24 +640,24 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
             const double cs = fma(vxd, rx, fma(vyd, ry, vzd * rz)) * ir;
             const double dc = fmax((double)kRayEpsF - cs, 0.0);
             const double px = fma(rx, dc, vxd), py = fma(ry, dc, vyd), pz = fma(rz, dc, vzd);
-            const double wi = (double)wt[kx] * rsq64_1(fma(px, px, fma(py, py, pz * pz)));
+            const double wi = (double)wt[i] * rsq64_1(fma(px, px, fma(py, py, pz * pz)));
             acc0 = fma(px, wi, acc0);
             acc1 = fma(py, wi, acc1);
             acc2 = fma(pz, wi, acc2);
             const float wf = (float)wi;
             qs = fmaf(wf, wf, qs);
         }
-        part[ky * npx + j] = make_double4(acc0, acc1, acc2, bad ? __builtin_nan("") : (double)qs);
+        part[r * npx + j] = make_double4(acc0, acc1, acc2, bad ? __builtin_nan("") : (double)qs);
     }
     __syncthreads();
 
-    // ---- phase B: reduce the K rows, write unflagged pixels ----------------
-    if (ky == 0) {
+    // ---- phase B: reduce the G runs, write unflagged pixels ----------------
+    if (r == 0) {
         bool flag = false;
         if (valid) {
             double4 sm = part[j];
 #pragma unroll
-            for (int rr = 1; rr < K; ++rr) {
+            for (int rr = 1; rr < G; ++rr) {
                 const double4 t = part[rr * npx + j];
                 sm.x += t.x;
                 sm.y += t.y;
@@ -667,12 +700,13 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
     const float* ap = angle + (size_t)b * K2 * HW;
     const float* rp = a.ray + (size_t)b * a.ray_bstride;
     float* op = a.out + (size_t)b * 3 * HW;
-    // Each wave (group, ky) evaluates row ky of up to PPR flagged pixels of
-    // its group per pass, one neighbour per lane (inputs re-read; the block
-    // has just read them, so from L2); row partials meet in LDS and the
-    // ky == 0 wave writes the pixel.
+    // Each wave (group, run) evaluates its run's neighbours of up to PPR
+    // flagged pixels of its group per pass, LPG lanes per pixel, one
+    // neighbour per lane at a time (inputs re-read; the block has just read
+    // them, so from L2); run partials meet in LDS and wave r == 0 of the
+    // group writes the pixel.
     const int clane = tid & 63;
-    const int slot = clane / LPG, kxl = clane - slot * LPG;
+    const int slot = clane / LPG, il = clane - slot * LPG;
     unsigned long long rest = gmask;
     for (int base = 0; base < maxc; base += PPR) {
         int src = 0, fin_src = 0;
@@ -684,26 +718,30 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
             if (sidx == clane) fin_src = bitpos;
         }
         double p0 = 0.0, p1 = 0.0, p2 = 0.0;
-        if ((base + slot) < cnt && kxl < K) {
+        if ((base + slot) < cnt) {
             const int jj = gi * 64 + src;
             const int fty = jj / tw, ftx = jj - fty * tw;
             const int fy = ty0 + fty, fx = tx0 + ftx;
-            const int fsy = clampi(fy - P + ky, 0, H - 1);
-            const int fsx = clampi(fx - P + kxl, 0, W - 1);
             const uint32_t fb = (uint32_t)(fy * W + fx) * 4u;
-            const uint32_t sb = (uint32_t)(fsy * W + fsx) * 4u;
-            const size_t n = (size_t)ky * K + kxl;
-            const float mx = ldf(pn, sb), my = ldf(pn + HW, sb), mz = ldf(pn + 2 * HW, sb);
-            const float xsv = ldf(xyp + n * HW, fb), ysv = ldf(xyp + (K2 + n) * HW, fb);
-            const float thv = ldf(ap + n * HW, fb), wv = ldf(pr + n * HW, fb);
-            const float frx = ldf(rp, fb), fry = ldf(rp + HW, fb), frz = ldf(rp + 2 * HW, fb);
-            double ox, oy, oz;
-            nbr_ref_f64(mx, my, mz, fsx + 0.5, fsy + 0.5, xsv, ysv, thv, frx, fry, frz, a.fu, a.cu,
-                        a.fv, a.cv, ox, oy, oz);
-            const double w = wv;
-            p0 = w * ox;
-            p1 = w * oy;
-            p2 = w * oz;
+            for (int i = il; i < nrun; i += LPG) {
+                const int n = n0 + i;
+                const int ky = n / K, kx = n - ky * K;
+                const int fsy = clampi(fy - P + ky, 0, H - 1);
+                const int fsx = clampi(fx - P + kx, 0, W - 1);
+                const uint32_t sb = (uint32_t)(fsy * W + fsx) * 4u;
+                const float mx = ldf(pn, sb), my = ldf(pn + HW, sb), mz = ldf(pn + 2 * HW, sb);
+                const float xsv = ldf(xyp + (size_t)n * HW, fb);
+                const float ysv = ldf(xyp + (size_t)(K2 + n) * HW, fb);
+                const float thv = ldf(ap + (size_t)n * HW, fb), wv = ldf(pr + (size_t)n * HW, fb);
+                const float frx = ldf(rp, fb), fry = ldf(rp + HW, fb), frz = ldf(rp + 2 * HW, fb);
+                double ox, oy, oz;
+                nbr_ref_f64(mx, my, mz, fsx + 0.5, fsy + 0.5, xsv, ysv, thv, frx, fry, frz, a.fu,
+                            a.cu, a.fv, a.cv, ox, oy, oz);
+                const double w = wv;
+                p0 += w * ox;
+                p1 += w * oy;
+                p2 += w * oz;
+            }
         }
 #pragma unroll
         for (int off = LPG / 2; off > 0; off >>= 1) {
@@ -711,17 +749,17 @@ __attribute__((amdgpu_waves_per_eu(kWavesPerEU<K>))) void angmf_f32_kernel(
             p1 += __shfl_xor(p1, off, 64);
             p2 += __shfl_xor(p2, off, 64);
         }
-        if (kxl == 0 && (base + slot) < cnt) {
-            double* f = fixp + ((gi * K + ky) * PPR + slot) * 3;
+        if (il == 0 && (base + slot) < cnt) {
+            double* f = fixp + ((gi * G + r) * PPR + slot) * 3;
             f[0] = p0;
             f[1] = p1;
             f[2] = p2;
         }
         __syncthreads();
-        if (ky == 0 && clane < PPR && base + clane < cnt) {
+        if (r == 0 && clane < PPR && base + clane < cnt) {
             double a0 = 0.0, a1 = 0.0, a2 = 0.0;
-            for (int rr = 0; rr < K; ++rr) {
-                const double* f = fixp + ((gi * K + rr) * PPR + clane) * 3;
+            for (int rr = 0; rr < G; ++rr) {
+                const double* f = fixp + ((gi * G + rr) * PPR + clane) * 3;
                 a0 += f[0];
                 a1 += f[1];
                 a2 += f[2];
@@ -820,7 +858,8 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
         c.out += (size_t)b0 * 3 * a.HW;
         c.B = nb;
         hipLaunchKernelGGL(angmf_f32_kernel<K>, dim3((unsigned)a.tiles_per_img, (unsigned)nb),
-                           dim3(64 * a.M * K), lds, s, c.pn, c.xy, c.ang, c.pr, a.W, a.H, tile,
+                           dim3(64 * a.M * group_waves(K)), lds, s, c.pn, c.xy, c.ang, c.pr, a.W,
+                           a.H, tile,
                            a.tiles_per_img, a.tiles_x, mag, c);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -834,18 +873,19 @@ constexpr int kMaxLdsBytes = 65536;
 // Whether a TW x TH tile of M groups fits the kernel: its LDS, and at most
 // two halo records per thread.
 bool tile_fits(int K, int M, int TW, int TH) {
-    return lds_units(K, M, TW, TH) * 16 <= kMaxLdsBytes && halo_count(K, TW, TH) <= 2 * 64 * M * K;
+    return lds_units(K, M, TW, TH) * 16 <= kMaxLdsBytes &&
+           halo_count(K, TW, TH) <= 2 * 64 * M * group_waves(K);
 }
 
 // Tile of the fp32 kernel: wide images (and rows longer than a workgroup's
 // 64 * M pixels) take 64 x M tiles (each wave one 256 B row segment per
 // plane); narrow ones full-width tiles of TH rows with the fewest idle lanes
-// among those that fit.  At most 16 waves (M*K) per workgroup.
+// among those that fit.  At most kWgWaves waves (M * G) per workgroup.
 void choose_tile(AngmfArgs& a, int K) {
-    const int mmax = 16 / K;
+    const int mmax = kWgWaves / group_waves(K);
     a.TW = 64;
-    a.M = mmax < 2 ? mmax : 2;
-    if (!tile_fits(K, a.M, 64, a.M)) a.M = 1;
+    a.M = mmax;
+    while (a.M > 1 && !tile_fits(K, a.M, 64, a.M)) --a.M;
     a.TH = a.M;
     if (a.W > 128 || a.W > 64 * mmax) return;
     double best = -1.0;
@@ -955,12 +995,14 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
                       std::isfinite(cv) && std::fabs(fu) >= 1e-3 && std::fabs(fu) <= 1e7 &&
                       std::fabs(fv) >= 1e-3 && std::fabs(fv) <= 1e7 &&
                       std::fabs(cu) <= 1e7 && std::fabs(cv) <= 1e7;
-    // The fp32 kernel addresses K planes (and the 3 planes of pred_norm and
-    // ray) from one 32-bit buffer offset, and its grid holds one image's tiles
-    // in x; larger images also run the double-precision kernel.
-    const long long nplanes = k > 3 ? k : 3;
+    // The fp32 kernel addresses a wave's run of neighbour planes (and the 3
+    // planes of pred_norm and ray) from one 32-bit buffer offset, and its grid
+    // holds one image's tiles in x; larger images also run the
+    // double-precision kernel.
+    const long long gw = group_waves(k), nrun = (k * k + gw - 1) / gw;
+    const long long nplanes = nrun > 3 ? nrun : 3;
     const bool fits32 = nplanes * HW * 4 < (1LL << 32) && tpi < (1LL << 31) &&
-                        tpi * 64 * a.M * k < (1LL << 32);
+                        tpi * 64 * a.M * gw < (1LL << 32);
     const bool fp64 = (flags & BVML_DSINE_FP64) || !sane || !fits32;
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e;
