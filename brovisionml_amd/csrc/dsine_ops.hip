@@ -55,10 +55,15 @@ constexpr float kRayEpsF = 1e-2f;
 
 // The fast path takes source normals with | |m|^2 - 1 | <= kUnitM2 (every
 // normal this op or RayReLU writes is one) and raw xy pairs with
-// |xy|^2 >= kMinXY2 (below it the reference's 1e-12 clamp stops normalising);
-// a neighbour outside sends its pixel to the reference-order path.
+// kMinXY2 <= |xy|^2 <= kMaxXY2 in fp32 (below, the reference's 1e-12 clamp
+// stops normalising; above, the fp32 |xy|^2 could overflow); a neighbour
+// outside sends its pixel to the reference-order path.  Both bounds are one
+// unsigned comparison on the float's bits (NaN and negatives fall outside).
 constexpr float kUnitM2 = 1e-5f;
-constexpr double kMinXY2 = 1e-20;
+constexpr float kMinXY2 = 1e-20f;
+constexpr float kMaxXY2 = 1e30f;
+constexpr uint32_t kXY2Lo = __builtin_bit_cast(uint32_t, kMinXY2);
+constexpr uint32_t kXY2Span = __builtin_bit_cast(uint32_t, kMaxXY2) - kXY2Lo;
 
 // Each fast-path term is within delta * wi of the reference's (wi = prob/|p|,
 // the term's weight before its final normalise, p the RayReLU'd rotation),
@@ -70,9 +75,11 @@ constexpr double kMinXY2 = 1e-20;
 constexpr double kAccRatio2 = 3.5e-4;
 
 // The reference clamps |dd| < 1e-8 (src/dsine_ops.cpp:120-123), where the
-// reduced axis no longer holds.  The fast path's dd is within
-// 1.3e-7 * |q|/|xy| <= 1.3e-7 * |m| / min(|fu|, |fv|) of the reference's; a
-// neighbour with |dd| below dd_min = 1.01e-8 + 1e-7 / min(|fu|, |fv|) sends its
+// reduced axis no longer holds.  The fast path's dd = g + q/|xy| takes 1/|xy|
+// from the fp32 |xy|^2 (fma, relative error < 1.2e-7) and the hardware fp32
+// rsq (< 9.4e-8 measured), so it is within 1.6e-7 * |q|/|xy| <=
+// 1.6e-7 * |m| / min(|fu|, |fv|) of the reference's; a neighbour with |dd|
+// below dd_min = 1.01e-8 + 3e-7 / min(|fu|, |fv|) sends its
 // pixel to the reference-order path, so the sign of every other dd is the
 // reference's, and so is the axis -- including where m is nearly parallel to
 // N = D x P0 (g and q both small), since dd = g + q/|xy| is small then too.
@@ -614,12 +621,12 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
             // products of the fp32 inputs keep their relative precision where
             // they cancel (a surface edge-on to the rays), and so does V below.
             // dd is formed from the raw normal as the reference forms it; its
-            // 1/|xy| comes from the hardware double rsq (relative error
-            // < 5.3e-8 measured), which dd_min covers.
+            // 1/|xy| comes from the fp32 |xy|^2 and rsq, which dd_min covers.
             const double q = fma(xsd, ab.x, ysd * ab.y);
-            const double s = fma(xsd, xsd, ysd * ysd);
-            const double dd = fma(__builtin_amdgcn_rsq(s), q, gt.x);
-            bad |= !(s >= kMinXY2) | !(fabsf(t) <= 3.2f) | !(fabs(dd) >= a.dd_min);
+            const float s = fmaf(xs[i], xs[i], ys[i] * ys[i]);
+            const double dd = fma((double)__builtin_amdgcn_rsqf(s), q, gt.x);
+            bad |= (__builtin_bit_cast(uint32_t, s) - kXY2Lo > kXY2Span) | !(fabsf(t) <= 3.2f) |
+                   !(fabs(dd) >= a.dd_min);
             // axis = sign(dd) V/|V|, V = (g xs/fu - q tu0, g ys/fv - q tv0, -q) = m x N;
             // v' = m' cos t + (V x m') sin t/|V|, m' = m/|m|
             const float Vx = (float)fma(gu.x, xsd, -q * gt.y);
@@ -979,7 +986,7 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
     a.ifv64 = 1.0 / fv;
     a.tu_c = (0.5 - cu) / fu;
     a.tv_c = (0.5 - cv) / fv;
-    a.dd_min = kDdClamp + 1e-7 / std::fmin(std::fabs(fu), std::fabs(fv));
+    a.dd_min = kDdClamp + 3e-7 / std::fmin(std::fabs(fu), std::fabs(fv));
     choose_tile(a, k);
     if (!tile_fits(k, a.M, a.TW, a.TH))
         return fail(BVML_DSINE_ESIZE, "angmf_propagate: no tile fits the kernel's LDS");

@@ -143,6 +143,24 @@ def test_angmf_per_sample_ray(cuda):
     assert max_abs <= TOL_ABS and max_deg <= TOL_DEG
 
 
+def test_angmf_xy_magnitudes(cuda):
+    """xy pairs scaled log-uniformly over 1e-12 .. 1e21: |xy|^2 crosses the
+    fast path's fp32 range (1e-20 .. 1e30) at both ends and overflows fp32
+    above ~1.8e19; every pixel must match the oracle either way."""
+    H, W, k = 12, 20, 5
+    say("[gpu] angmf xy magnitudes")
+    rng = np.random.default_rng(17)
+    inp = _random_inputs(rng, 1, H, W, k)
+    scale = 10.0 ** rng.uniform(-12.0, 21.0, size=inp["xy"].shape)
+    inp["xy"] = (inp["xy"].astype(np.float64) * scale).astype(np.float32)
+    got = run_gpu(inp, H, W, cuda)
+    want = run_oracle(inp, H, W, k)
+    max_abs, max_deg, nan_mm = compare(got.reshape(1, 3, -1), want.reshape(1, 3, -1))
+    say(f"    max-abs {max_abs:.3e}  max-angle {max_deg:.3e} deg  nan-mismatch {nan_mm}")
+    assert nan_mm == 0
+    assert max_abs <= TOL_ABS and max_deg <= TOL_DEG
+
+
 def test_angmf_degenerate_inputs(cuda):
     """Zero xy pairs, zero / tiny normals, zero probs, dd == 0 exactly,
     non-finite values: every case the reference's clamps and isfinite guard
