@@ -31,9 +31,10 @@
 //     non-finite value -- or when |acc|^2 < 3.5e-4 * sum(wi^2), where the
 //     final normalise would amplify the per-term error (<= 1.3e-7 * wi) past
 //     the parity bar.
-// Workgroups are k x (16/k) waves (one window row per wave, a 64-pixel-wide
-// tile per wave group); at k=5 the kernel is held to 80 VGPRs so that two
-// 10-wave workgroups fit each CU and a 256x256 image runs in one round.
+// Workgroups are 8 waves: G waves per 64-pixel group, each evaluating one run
+// of the window's neighbours (G = 4 at k=5), so the SPI places 2 waves per
+// SIMD and every SIMD carries the same work; two workgroups per CU run a
+// 256x256 image in one round.
 // The double-precision body is also available as its own kernel
 // (BVML_DSINE_FP64), which reproduces the CPU reference to a few ulps.
 
@@ -197,7 +198,8 @@ struct AngmfArgs {
     long long HW;
     int B, H, W;
     // fp32 kernel: TW x TH output tile per workgroup, M groups of 64 pixels,
-    // one wave per (group, window row) -> 64*M*K threads.
+    // G waves per group (one run of the window's neighbours each) -> 64*M*G
+    // threads.
     int TW, TH, M, tiles_x, tiles_per_img;
     double ifu64, ifv64;  // 1/fu, 1/fv
     double tu_c, tv_c;    // (0.5 - cu)/fu, (0.5 - cv)/fv: source ray tu0 = sx/fu + tu_c
