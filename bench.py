@@ -17,6 +17,8 @@ Prints one JSON line (rank 0):
               average launch duration (event time of the region / K)
   cpu_baseline  the CPU oracle (double-precision restatement of the
               reference's CPU twin), one thread, on a bounded sample
+  cpu_baseline_all_cores  the same oracle with its rows over the host's
+              CPU share (OpenMP), labelled separately
 """
 from __future__ import annotations
 
@@ -44,6 +46,18 @@ def cpu_model() -> str:
     except OSError:
         pass
     return platform.processor() or "unknown"
+
+
+def host_share() -> int:
+    """Host threads this process may use: OMP_NUM_THREADS when the job
+    scheduler sets it, else the CPUs in this process's affinity mask."""
+    env = os.environ.get("OMP_NUM_THREADS", "")
+    if env.isdigit() and int(env) > 0:
+        return int(env)
+    try:
+        return len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        return os.cpu_count() or 1
 
 
 PROFILE = os.path.join(ROOT, "profiles", "angmf_f32_k5_256x256_traffic.json")
@@ -89,6 +103,9 @@ def main() -> int:
     ap.add_argument("--sets", type=int, default=0, help="rotating input sets (0 = auto, > 512 MB)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--ray-from-intrinsics", action="store_true",
+                    help="form each pixel's ray from fu, cu, fv, cv in the kernel "
+                         "(BVML_DSINE_RAY_FROM_INTRINSICS) instead of reading the ray planes")
     ap.add_argument("--calib", action="store_true",
                     help="also run 10 plain device copies of one launch's byte count "
                          "(the reference kernel for the FETCH_SIZE / WRITE_SIZE scale)")
@@ -114,6 +131,10 @@ def main() -> int:
     fu, cu, fv, cv = inp["intrinsics"]
     B, H, W, k = w.B, w.H, w.W, w.k
     bytes_per_call = w.algorithmic_bytes(shared_ray=True) // w.calls
+    flags = _lib.DEFAULT
+    if args.ray_from_intrinsics:
+        flags |= _lib.RAY_FROM_INTRINSICS
+        bytes_per_call -= 3 * w.HW * 4  # the shared ray's 3 planes are not read
     set_bytes = bytes_per_call
     nsets = args.sets or max(2, int(np.ceil(512e6 / set_bytes)))
 
@@ -133,8 +154,8 @@ def main() -> int:
             dst = outs[i]
             st = _lib.angmf_propagate_f32(
                 pn.data_ptr(), s["prob"].data_ptr(), s["xy"].data_ptr(), s["angle"].data_ptr(),
-                s["ray"].data_ptr(), fu, cu, fv, cv, B, H, W, k, 0, dst.data_ptr(),
-                _lib.DEFAULT, sptr)
+                0 if args.ray_from_intrinsics else s["ray"].data_ptr(), fu, cu, fv, cv, B, H, W,
+                k, 0, dst.data_ptr(), flags, sptr)
             if st != 0:
                 raise RuntimeError(f"angmf_propagate_f32 failed: {st} {_lib.last_error()}")
             pn = dst
@@ -227,7 +248,8 @@ def main() -> int:
         "data": "synthetic",
         "config": {
             "workload": w.name, "B": B, "H": H, "W": W, "k": k, "calls_per_step": w.calls,
-            "ray": "shared", "inputs": f"{nsets} rotating HBM-resident copies "
+            "ray": "from-intrinsics" if args.ray_from_intrinsics else "shared",
+            "inputs": f"{nsets} rotating HBM-resident copies "
             f"({nsets * set_bytes / 1e6:.0f} MB > 256 MB Infinity Cache)",
         },
         "roofline": {
@@ -236,7 +258,7 @@ def main() -> int:
             "peak": HBM_PEAK_GBPS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBPS, 4),
-            "traffic": traffic_from_profile(w),
+            "traffic": None if args.ray_from_intrinsics else traffic_from_profile(w),
             "kernel": f"angmf_f32_kernel<{k}>",
             "bytes_per_launch": bytes_per_call,
             "launch_us_mean": round(launch_s * 1e6, 3),
@@ -264,6 +286,15 @@ def main() -> int:
             "cpu": cpu_model(),
             "host_threads": os.cpu_count(),
         }
+        # the same oracle with its rows split over the host's CPU share
+        # (OpenMP); the reference itself is single-threaded
+        nt = host_share()
+        if nt > 1:
+            vn, passes_n, el_n = cpu_baseline(w, inp, args.cpu_seconds / 2, nt)
+            line["cpu_baseline_all_cores"] = {
+                "value": round(vn, 4), "unit": "Mpixel/s", "cores": nt, "kind": "port",
+                "sample": f"{passes_n} passes, {el_n:.1f} s, rows over {nt} OpenMP threads",
+            }
     print(json.dumps(line), flush=True)
     return 0
 

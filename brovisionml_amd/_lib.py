@@ -22,11 +22,13 @@ EPARAM = -7
 
 DEFAULT = 0
 FP64 = 1
+RAY_FROM_INTRINSICS = 2
 
 # Every symbol include/bvml_dsine.h declares.
 EXPORTS = (
     "bvml_dsine_ray_relu_f32",
     "bvml_dsine_angmf_propagate_f32",
+    "bvml_dsine_build_ray8_f32",
     "bvml_dsine_last_error",
     "bvml_dsine_version",
 )
@@ -50,6 +52,8 @@ def load(path: str = LIB) -> ctypes.CDLL:
     lib.bvml_dsine_angmf_propagate_f32.argtypes = [
         vp, vp, vp, vp, vp, d, d, d, d, i, i, i, i, ll, vp, u, vp]
     lib.bvml_dsine_angmf_propagate_f32.restype = i
+    lib.bvml_dsine_build_ray8_f32.argtypes = [vp, d, d, d, d, i, i, vp]
+    lib.bvml_dsine_build_ray8_f32.restype = i
     lib.bvml_dsine_last_error.argtypes = []
     lib.bvml_dsine_last_error.restype = ctypes.c_char_p
     lib.bvml_dsine_version.argtypes = []
@@ -76,3 +80,9 @@ def angmf_propagate_f32(pred_norm: int, prob: int, xy: int, angle: int, ray: int
     return load().bvml_dsine_angmf_propagate_f32(
         pred_norm, prob, xy, angle, ray, fu, cu, fv, cv, B, H, W, k,
         ray_bstride, out, flags, stream)
+
+
+def build_ray8_f32(ray: int, fu: float, cu: float, fv: float, cv: float, H: int, W: int,
+                   stream: int = 0) -> int:
+    """Raw call; `ray` is an integer device address of 3*H*W floats."""
+    return load().bvml_dsine_build_ray8_f32(ray, fu, cu, fv, cv, H, W, stream)

@@ -94,6 +94,21 @@ constexpr double kDdClamp = 1.01e-8;
 // reference CPU path does (fmax would not).
 __device__ __forceinline__ double smax(double a, double b) { return (a < b) ? b : a; }
 
+// The ray of pixel (x, y) as build_ray8 forms it from the grid-scaled
+// intrinsics (src/dsine_decoder.cpp:252-253 and :285-290): ray_x, ray_y in
+// double rounded to float, then [ray_x, ray_y, 1] normalised in double and
+// each channel rounded to float.  IEEE double division and square root, in
+// the host's operation order with contraction off, give the host's bits.
+__device__ __forceinline__ float3 synth_ray(int x, int y, double fu, double cu, double fv,
+                                            double cv) {
+#pragma clang fp contract(off)
+    const double rx = (float)(((x + 0.5) - cu) / fu);
+    const double ry = (float)(((y + 0.5) - cv) / fv);
+    const double rz = 1.0;
+    const double inv = 1.0 / smax(sqrt(rx * rx + ry * ry + rz * rz), 1e-12);
+    return make_float3((float)(rx * inv), (float)(ry * inv), (float)(rz * inv));
+}
+
 // One neighbour's RayReLU'd rotated normal, in the operation order of
 // src/dsine_ops.cpp:110-160 (axis :110-138, axis_angle_to_matrix :31-51,
 // rotate + renormalise :140-148, RayReLU :150-160).  Contraction is off so
@@ -204,6 +219,7 @@ struct AngmfArgs {
     double ifu64, ifv64;  // 1/fu, 1/fv
     double tu_c, tv_c;    // (0.5 - cu)/fu, (0.5 - cv)/fv: source ray tu0 = sx/fu + tu_c
     double dd_min;        // |dd| below this sends a pixel to the reference-order path
+    int synth_ray;        // form rays from the intrinsics (synth_ray), not from `ray`
 };
 
 // ---------------------------------------------------------------------------
@@ -223,10 +239,20 @@ __global__ __launch_bounds__(256) void angmf_f64_kernel(AngmfArgs a) {
     const float* pr = a.pr + (size_t)b * K2 * HW;
     const float* xyp = a.xy + (size_t)b * 2 * K2 * HW;
     const float* ap = a.ang + (size_t)b * K2 * HW;
-    const float* rp = a.ray + (size_t)b * a.ray_bstride;
+    const float* rp = a.synth_ray ? nullptr : a.ray + (size_t)b * a.ray_bstride;
     float* op = a.out + (size_t)b * 3 * HW;
 
-    const double rx = rp[p], ry = rp[HW + p], rz = rp[2 * HW + p];
+    double rx, ry, rz;
+    if (a.synth_ray) {
+        const float3 r = synth_ray(x, y, a.fu, a.cu, a.fv, a.cv);
+        rx = r.x;
+        ry = r.y;
+        rz = r.z;
+    } else {
+        rx = rp[p];
+        ry = rp[HW + p];
+        rz = rp[2 * HW + p];
+    }
     double acc0 = 0.0, acc1 = 0.0, acc2 = 0.0;
     for (int n = 0; n < K2; ++n) {
         const int ky = n / K, kx = n - ky * K;
@@ -440,10 +466,11 @@ __host__ __device__ inline int halo_slots(int K, int TW, int TH) { return halo_c
 //   halo.m, .gt, .ab, .gu [nhalo + 1]  source-pixel records (+ a spare)
 //   tvrow[TH + 2P]   source ray row term tv0 per halo row (doubles)
 //   fixp[M][G][PPR]  per-wave fp64 partial of a flagged pixel (3 doubles)
-__host__ __device__ inline int lds_units(int K, int M, int TW, int TH) {
+//   rayl[64*M]       each tile pixel's ray, when formed from the intrinsics
+__host__ __device__ inline int lds_units(int K, int M, int TW, int TH, bool synth_ray) {
     const int G = group_waves(K), nrow = TH + 2 * (K / 2);
     return 8 + 2 * G * 64 * M + 4 * halo_slots(K, TW, TH) + (nrow + 1) / 2 +
-           (M * G * recompute_ppr(K) * 3 + 1) / 2;
+           (M * G * recompute_ppr(K) * 3 + 1) / 2 + (synth_ray ? 64 * M : 0);
 }
 
 // TW (< 2^11), TH (< 2^11) and M (< 2^5) of the fp32 kernel's tile and the
@@ -473,7 +500,7 @@ __host__ __device__ inline unsigned pack_tile(int TW, int TH, int M, int L) {
 // host-computed magic number, the wave's group from a constant divisor) and
 // one buffer descriptor per input tensor, its planes reached through the
 // scalar offset.
-template <int K>
+template <int K, bool SR>
 __global__ __launch_bounds__(64 * kWgWaves) __attribute__((amdgpu_waves_per_eu(4)))
 void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restrict__ xy,
                       const float* __restrict__ angle, const float* __restrict__ prob, int W,
@@ -500,6 +527,9 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     hl.gu = hl.ab + nslot;
     double* tvrow = reinterpret_cast<double*>(hl.gu + nslot);
     double* fixp = tvrow + 2 * ((nrow + 1) / 2);
+    // (SR) the tile pixels' rays, after fixp (M*G*PPR*3 doubles, rounded up
+    // to 16 bytes)
+    float4* rayl = reinterpret_cast<float4*>(fixp + 2 * ((M * G * PPR * 3 + 1) / 2));
 
     const int b = blockIdx.y;
     const int lb = xcd_remap(blockIdx.x, tiles_per_img);
@@ -551,8 +581,14 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     // loads in consumption order: ray, then per neighbour its 4 planes; the
     // planes of the first kPreLoads neighbours go out before the staging,
     // the rest after its barrier
-    const __amdgpu_buffer_rsrc_t rry = plane_rsrc(a.ray + (size_t)b * a.ray_bstride, 3u * HW4);
-    const float rxf = ldbs(rry, pb, 0u), ryf = ldbs(rry, pb, HW4), rzf = ldbs(rry, pb, 2u * HW4);
+    float rxf, ryf, rzf;
+    if constexpr (!SR) {
+        const __amdgpu_buffer_rsrc_t rry =
+            plane_rsrc(a.ray + (size_t)b * a.ray_bstride, 3u * HW4);
+        rxf = ldbs(rry, pb, 0u);
+        ryf = ldbs(rry, pb, HW4);
+        rzf = ldbs(rry, pb, 2u * HW4);
+    }
     float xs[NR], ys[NR], th[NR], wt[NR];
     // planes (sample b, neighbour n0 + i) of each input: one descriptor per
     // tensor at i = 0, plane i at scalar offset i * HW4.  A run one shorter
@@ -593,7 +629,23 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     // the source pixels' ray row per halo row: ((sy + 0.5) - cv) / fv
     if ((int)threadIdx.x < nrow)
         tvrow[threadIdx.x] = fma((double)clampi(ty0 - P + (int)threadIdx.x, 0, H - 1), a.ifv64, a.tv_c);
+    if constexpr (SR) {
+        // each tile pixel's ray, once (pixels past the image: clamped ones)
+        if ((int)threadIdx.x < npx) {
+            const int t = threadIdx.x;
+            const int rty = small_div(t, rtw), rtx = t - rty * TW;
+            const float3 r = synth_ray(min(tx0 + rtx, W - 1), min(ty0 + rty, H - 1), a.fu, a.cu,
+                                       a.fv, a.cv);
+            rayl[t] = make_float4(r.x, r.y, r.z, 0.0f);
+        }
+    }
     __syncthreads();
+    if constexpr (SR) {
+        const float4 r = rayl[j];
+        rxf = r.x;
+        ryf = r.y;
+        rzf = r.z;
+    }
 #pragma unroll
     for (int i = PRE; i < NR; ++i) load_planes(i);
     {
@@ -707,7 +759,7 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     const float* pr = prob + (size_t)b * K2 * HW;
     const float* xyp = xy + (size_t)b * 2 * K2 * HW;
     const float* ap = angle + (size_t)b * K2 * HW;
-    const float* rp = a.ray + (size_t)b * a.ray_bstride;
+    const float* rp = SR ? nullptr : a.ray + (size_t)b * a.ray_bstride;
     float* op = a.out + (size_t)b * 3 * HW;
     // Each wave (group, run) evaluates its run's neighbours of up to PPR
     // flagged pixels of its group per pass, LPG lanes per pixel, one
@@ -742,7 +794,17 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
                 const float xsv = ldf(xyp + (size_t)n * HW, fb);
                 const float ysv = ldf(xyp + (size_t)(K2 + n) * HW, fb);
                 const float thv = ldf(ap + (size_t)n * HW, fb), wv = ldf(pr + (size_t)n * HW, fb);
-                const float frx = ldf(rp, fb), fry = ldf(rp + HW, fb), frz = ldf(rp + 2 * HW, fb);
+                float frx, fry, frz;
+                if constexpr (SR) {
+                    const float3 r = synth_ray(fx, fy, a.fu, a.cu, a.fv, a.cv);
+                    frx = r.x;
+                    fry = r.y;
+                    frz = r.z;
+                } else {
+                    frx = ldf(rp, fb);
+                    fry = ldf(rp + HW, fb);
+                    frz = ldf(rp + 2 * HW, fb);
+                }
                 double ox, oy, oz;
                 nbr_ref_f64(mx, my, mz, fsx + 0.5, fsy + 0.5, xsv, ysv, thv, frx, fry, frz, a.fu,
                             a.cu, a.fv, a.cv, ox, oy, oz);
@@ -816,6 +878,21 @@ __global__ __launch_bounds__(256) void ray_relu_kernel(float* normal, const floa
 }
 
 // ---------------------------------------------------------------------------
+// build_ray8: the ray map from the intrinsics, one pixel per thread.
+// ---------------------------------------------------------------------------
+__global__ __launch_bounds__(256) void build_ray8_kernel(float* ray, double fu, double cu,
+                                                         double fv, double cv, int H, int W) {
+    const long long HW = (long long)H * W;
+    const long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= HW) return;
+    const int y = (int)(p / W), x = (int)(p - (long long)y * W);
+    const float3 r = synth_ray(x, y, fu, cu, fv, cv);
+    ray[p] = r.x;
+    ray[HW + p] = r.y;
+    ray[2 * HW + p] = r.z;
+}
+
+// ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
 thread_local std::string g_last_error;
@@ -850,7 +927,7 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
         hipLaunchKernelGGL(angmf_f64_kernel<K>, dim3((unsigned)grid), dim3(256), 0, s, a);
         return hipGetLastError();
     }
-    const size_t lds = (size_t)lds_units(K, a.M, a.TW, a.TH) * 16;
+    const size_t lds = (size_t)lds_units(K, a.M, a.TW, a.TH, a.synth_ray != 0) * 16;
     unsigned mag;
     int L;
     div_magic(a.tiles_x, mag, L);
@@ -863,13 +940,16 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
         c.pr += (size_t)b0 * K * K * a.HW;
         c.xy += (size_t)b0 * 2 * K * K * a.HW;
         c.ang += (size_t)b0 * K * K * a.HW;
-        c.ray += (size_t)b0 * a.ray_bstride;
+        if (!a.synth_ray) c.ray += (size_t)b0 * a.ray_bstride;
         c.out += (size_t)b0 * 3 * a.HW;
         c.B = nb;
-        hipLaunchKernelGGL(angmf_f32_kernel<K>, dim3((unsigned)a.tiles_per_img, (unsigned)nb),
-                           dim3(64 * a.M * group_waves(K)), lds, s, c.pn, c.xy, c.ang, c.pr, a.W,
-                           a.H, tile,
-                           a.tiles_per_img, a.tiles_x, mag, c);
+        const dim3 grid((unsigned)a.tiles_per_img, (unsigned)nb), block(64 * a.M * group_waves(K));
+        if (a.synth_ray)
+            hipLaunchKernelGGL((angmf_f32_kernel<K, true>), grid, block, lds, s, c.pn, c.xy, c.ang,
+                               c.pr, a.W, a.H, tile, a.tiles_per_img, a.tiles_x, mag, c);
+        else
+            hipLaunchKernelGGL((angmf_f32_kernel<K, false>), grid, block, lds, s, c.pn, c.xy,
+                               c.ang, c.pr, a.W, a.H, tile, a.tiles_per_img, a.tiles_x, mag, c);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -881,8 +961,8 @@ constexpr int kMaxLdsBytes = 65536;
 
 // Whether a TW x TH tile of M groups fits the kernel: its LDS, and at most
 // two halo records per thread.
-bool tile_fits(int K, int M, int TW, int TH) {
-    return lds_units(K, M, TW, TH) * 16 <= kMaxLdsBytes &&
+bool tile_fits(int K, int M, int TW, int TH, bool synth_ray) {
+    return lds_units(K, M, TW, TH, synth_ray) * 16 <= kMaxLdsBytes &&
            halo_count(K, TW, TH) <= 2 * 64 * M * group_waves(K);
 }
 
@@ -894,7 +974,7 @@ void choose_tile(AngmfArgs& a, int K) {
     const int mmax = kWgWaves / group_waves(K);
     a.TW = 64;
     a.M = mmax;
-    while (a.M > 1 && !tile_fits(K, a.M, 64, a.M)) --a.M;
+    while (a.M > 1 && !tile_fits(K, a.M, 64, a.M, a.synth_ray != 0)) --a.M;
     a.TH = a.M;
     if (a.W > 128 || a.W > 64 * mmax) return;
     double best = -1.0;
@@ -903,7 +983,7 @@ void choose_tile(AngmfArgs& a, int K) {
         const int m = (npx + 63) / 64;
         if (m > mmax) break;
         const double util = (double)npx / (64.0 * m);
-        if (util >= best && tile_fits(K, m, a.W, th)) {
+        if (util >= best && tile_fits(K, m, a.W, th, a.synth_ray != 0)) {
             best = util;
             a.TW = a.W;
             a.TH = th;
@@ -919,6 +999,23 @@ extern "C" {
 const char* bvml_dsine_last_error(void) { return g_last_error.c_str(); }
 
 const char* bvml_dsine_version(void) { return "0.1.0"; }
+
+int bvml_dsine_build_ray8_f32(float* ray, double fu, double cu, double fv, double cv, int H,
+                              int W, void* stream) {
+    if (H < 0 || W < 0) return fail(BVML_DSINE_ESHAPE, "build_ray8: H and W must be >= 0");
+    const long long HW = (long long)H * W;
+    if (HW == 0) return BVML_DSINE_OK;
+    if (!ray) return fail(BVML_DSINE_ENULL, "build_ray8: ray must be non-NULL");
+    if (HW > (long long)INT_MAX * 64)
+        return fail(BVML_DSINE_ESIZE, "build_ray8: H*W too large for one launch");
+    const long long grid = (HW + 255) / 256;
+    hipLaunchKernelGGL(build_ray8_kernel, dim3((unsigned)grid), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), ray, fu, cu, fv, cv, H, W);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return fail((int)e, std::string("build_ray8 launch: ") + hipGetErrorString(e));
+    return BVML_DSINE_OK;
+}
 
 int bvml_dsine_ray_relu_f32(float* normal, const float* ray, int B, int H, int W,
                             long long ray_bstride, void* stream) {
@@ -951,8 +1048,13 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
                                    double fv, double cv, int B, int H, int W,
                                    int k, long long ray_bstride, float* out,
                                    unsigned flags, void* stream) {
-    if (flags & ~BVML_DSINE_FP64)
+    if (flags & ~(BVML_DSINE_FP64 | BVML_DSINE_RAY_FROM_INTRINSICS))
         return fail(BVML_DSINE_EFLAGS, "angmf_propagate: unknown flag bits");
+    const bool synth = (flags & BVML_DSINE_RAY_FROM_INTRINSICS) != 0;
+    if (synth) {
+        ray = nullptr;
+        ray_bstride = 0;
+    }
     if (B < 0 || H < 0 || W < 0)
         return fail(BVML_DSINE_ESHAPE, "angmf_propagate: B, H and W must be >= 0");
     if (ray_bstride < 0)
@@ -961,7 +1063,7 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
         return fail(BVML_DSINE_EK, "angmf_propagate: k must be one of 1, 3, 5, 7, 9");
     const long long HW = (long long)H * W;
     if (B == 0 || HW == 0) return BVML_DSINE_OK;
-    if (!pred_norm || !prob || !xy || !angle || !ray || !out)
+    if (!pred_norm || !prob || !xy || !angle || (!ray && !synth) || !out)
         return fail(BVML_DSINE_ENULL, "angmf_propagate: all tensors must be non-NULL");
     const long long K2 = (long long)k * k;
     const long long total = (long long)B * HW;
@@ -976,7 +1078,7 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
     const size_t ry_b = ((size_t)(B - 1) * ray_bstride + 3 * HW) * f;
     if (overlaps(out, out_b, pred_norm, pn_b) || overlaps(out, out_b, prob, pr_b) ||
         overlaps(out, out_b, xy, xy_b) || overlaps(out, out_b, angle, an_b) ||
-        overlaps(out, out_b, ray, ry_b))
+        (!synth && overlaps(out, out_b, ray, ry_b)))
         return fail(BVML_DSINE_EALIAS, "angmf_propagate: out overlaps an input");
 
     AngmfArgs a{};
@@ -989,8 +1091,9 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
     a.tu_c = (0.5 - cu) / fu;
     a.tv_c = (0.5 - cv) / fv;
     a.dd_min = kDdClamp + 3e-7 / std::fmin(std::fabs(fu), std::fabs(fv));
+    a.synth_ray = synth ? 1 : 0;
     choose_tile(a, k);
-    if (!tile_fits(k, a.M, a.TW, a.TH))
+    if (!tile_fits(k, a.M, a.TW, a.TH, synth))
         return fail(BVML_DSINE_ESIZE, "angmf_propagate: no tile fits the kernel's LDS");
     a.tiles_x = (W + a.TW - 1) / a.TW;
     const long long tiles_y = (H + a.TH - 1) / a.TH;

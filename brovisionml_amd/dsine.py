@@ -87,8 +87,10 @@ def angmf_propagate(pred_norm, prob, xy, angle, ray, fu: float, cu: float,
                     precise: bool = False):
     """Fused AngMF propagate (src/dsine_ops.cpp:78-172).  Returns `out`
     (allocated like pred_norm when None; must not alias any input).
-    precise=True runs the double-precision kernel."""
-    _check_tensors("angmf_propagate", [pred_norm, prob, xy, angle, ray])
+    precise=True runs the double-precision kernel.  ray=None forms each
+    pixel's ray from fu, cu, fv, cv in the kernel, bit-identical to
+    build_ray8 (src/dsine_decoder.cpp:242-293)."""
+    _check_tensors("angmf_propagate", [pred_norm, prob, xy, angle] + ([] if ray is None else [ray]))
     import torch
     HW = H * W
     if out is None:
@@ -111,15 +113,32 @@ def angmf_propagate(pred_norm, prob, xy, angle, ray, fu: float, cu: float,
         _fail("angmf_propagate: prob channel count is not a square")
     if xy.numel() != 2 * K2 * B * HW or angle.numel() != K2 * B * HW:
         _fail("angmf_propagate: xy must hold 2*k*k and angle k*k planes per sample")
-    bstride = _ray_stride("angmf_propagate", ray, B, HW)
+    bstride = 0 if ray is None else _ray_stride("angmf_propagate", ray, B, HW)
     flags = _lib.FP64 if precise else _lib.DEFAULT
+    if ray is None:
+        flags |= _lib.RAY_FROM_INTRINSICS
     with _device(pred_norm):
         st = _lib.angmf_propagate_f32(
             pred_norm.data_ptr(), prob.data_ptr(), xy.data_ptr(), angle.data_ptr(),
-            ray.data_ptr(), float(fu), float(cu), float(fv), float(cv), B, H, W, k,
-            bstride, out.data_ptr(), flags, _stream_of(pred_norm))
+            0 if ray is None else ray.data_ptr(), float(fu), float(cu), float(fv), float(cv),
+            B, H, W, k, bstride, out.data_ptr(), flags, _stream_of(pred_norm))
     _raise_status("angmf_propagate", st)
     return out
+
+
+def build_ray8(fu: float, cu: float, fv: float, cv: float, H: int, W: int, device=None):
+    """The (3, H, W) fp32 ray map of build_ray8 (src/dsine_decoder.cpp:242-293)
+    from the grid-scaled intrinsics, formed on the device."""
+    import torch
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    ray = torch.empty((3, H, W), dtype=torch.float32, device=dev)
+    if H * W == 0:
+        return ray
+    with _device(ray):
+        st = _lib.build_ray8_f32(ray.data_ptr(), float(fu), float(cu), float(fv), float(cv), H, W,
+                                 _stream_of(ray))
+    _raise_status("build_ray8", st)
+    return ray
 
 
 class _device:

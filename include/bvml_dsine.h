@@ -48,6 +48,13 @@ extern "C" {
 /* Run every neighbour in double precision in the reference's operation
  * order (one pixel per lane, no fp32 fast path): the parity anchor. */
 #define BVML_DSINE_FP64 1u
+/* Form each pixel's ray from fu, cu, fv, cv in the kernel, bit-identical to
+ * the reference's build_ray8 (src/dsine_decoder.cpp:242-259, :276-293), which
+ * the refiner builds from the same grid-scaled intrinsics
+ * (src/dsine_refine.cpp:229-237), instead of reading a ray tensor: `ray` may
+ * then be NULL and ray_bstride is ignored.  No counterpart in the reference;
+ * saves the 3 ray planes (12 B/px) and the host-side build. */
+#define BVML_DSINE_RAY_FROM_INTRINSICS 2u
 
 /*
  * RayReLU in place (eps = 1e-2), B samples.
@@ -76,6 +83,19 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
                                    double fv, double cv, int B, int H, int W,
                                    int k, long long ray_bstride, float* out,
                                    unsigned flags, void* stream);
+
+/*
+ * The /8-grid ray map, 3 x H x W fp32 planes, as the reference's build_ray8
+ * (src/dsine_decoder.cpp:276-293, through get_ray_core :242-259) forms it on
+ * the host: ray_x = float(((x + 0.5) - cu) / fu), ray_y likewise with cv, fv,
+ * then [ray_x, ray_y, 1] L2-normalised in double and each channel rounded to
+ * float.  fu, cu, fv, cv are the grid-scaled intrinsics with the +0.5 on the
+ * principal point already applied (src/dsine_refine.cpp:232-237); the result
+ * is bit-identical to the host's.  No counterpart on the reference's device
+ * path (it builds the map on the host and copies it over).
+ */
+int bvml_dsine_build_ray8_f32(float* ray, double fu, double cu, double fv,
+                              double cv, int H, int W, void* stream);
 
 /* Message for the calling thread's last non-zero status ("" if none). */
 const char* bvml_dsine_last_error(void);

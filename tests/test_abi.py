@@ -66,6 +66,24 @@ def test_angmf_rejects(kw, code):
     assert _lib.last_error().startswith("angmf_propagate: ")
 
 
+def test_angmf_ray_from_intrinsics_validation():
+    # with the flag the ray pointer may be NULL; the other checks still apply
+    synth = _lib.RAY_FROM_INTRINSICS
+    assert angmf(flags=synth, ray=0, B=-1) == _lib.ESHAPE
+    assert angmf(flags=synth, ray=0, prob=0) == _lib.ENULL
+    assert angmf(flags=synth | _lib.FP64, ray=0, k=4) == _lib.EK
+    assert angmf(flags=synth, ray=0, out=FAKE) == _lib.EALIAS
+    assert angmf(flags=synth, ray=0, H=0) == _lib.OK
+    assert angmf(flags=0, ray=0) == _lib.ENULL
+
+
+def test_build_ray8_rejects():
+    assert _lib.build_ray8_f32(FAKE, 100.0, 10.0, 100.0, 10.0, -1, 4) == _lib.ESHAPE
+    assert _lib.last_error().startswith("build_ray8: ")
+    assert _lib.build_ray8_f32(0, 100.0, 10.0, 100.0, 10.0, 4, 4) == _lib.ENULL
+    assert _lib.build_ray8_f32(0, 100.0, 10.0, 100.0, 10.0, 0, 4) == _lib.OK
+
+
 def test_empty_shapes_are_no_ops():
     # the reference returns before launching when H*W == 0 (src/dsine_ops.cu:162,179)
     assert angmf(H=0) == _lib.OK
