@@ -1,7 +1,9 @@
 """CPU parity oracle -- TEST INFRASTRUCTURE ONLY.
 
 ctypes binding of oracle/_build/liboracle_dsine.so, the double-precision C
-restatement of brovisionml's CPU twin (src/dsine_ops.cpp:24-172).  Only the
+restatement of brovisionml's CPU twin (src/dsine_ops.cpp:24-172) and of the
+refiner's convex upsample + L2 normalise (src/dsine_refine.cpp:276-282,
+spec include/brovisionml/dsine_refine.h:91-97).  Only the
 tests, the smoke check and the CPU-baseline leg of the benchmark may use it,
 as the checker or the timed CPU reference; the product never does.
 
@@ -58,6 +60,9 @@ class Oracle:
         lib.oracle_angmf_propagate_rows_f32.argtypes = [
             vp, vp, vp, vp, vp, d, d, d, d, i, i, i, i, ll, vp, vp, i, i, i]
         lib.oracle_angmf_propagate_rows_f32.restype = None
+        lib.oracle_convex_upsample_f32.argtypes = [
+            vp, vp, i, i, i, i, i, i, d, vp, i]
+        lib.oracle_convex_upsample_f32.restype = None
         self.lib = lib
 
     def axis_angle_to_matrix(self, v) -> np.ndarray:
@@ -115,6 +120,23 @@ class Oracle:
         return (out, acc) if return_acc else out
 
 
+    def convex_upsample(self, x, mask, H: int, W: int, s: int = 8, normalize: bool = True,
+                        eps: float = 1e-12, nthreads: int = 1) -> np.ndarray:
+        """Convex upsample by s (9-tap softmax mask, replicate padding), then
+        the channel L2-normalise when `normalize`.  x: (B, C, H*W) or
+        (B, C, H, W); mask: (B, 9*s*s, ...).  Returns (B, C, s*H, s*W) float32."""
+        xf, mf = _f32c(x), _f32c(mask)
+        HW = H * W
+        B = mf.size // (9 * s * s * HW)
+        C = xf.size // (B * HW)
+        if C > 16:
+            raise ValueError("oracle convex_upsample: at most 16 channels")
+        out = np.full((B, C, s * H, s * W), np.nan, dtype=np.float32)
+        self.lib.oracle_convex_upsample_f32(_ptr(xf), _ptr(mf), B, C, H, W, s,
+                                            1 if normalize else 0, float(eps), _ptr(out), nthreads)
+        return out
+
+
 _default = None
 
 
@@ -151,3 +173,7 @@ def ray_relu(normal, ray, H, W):
 
 def angmf_propagate(*args, **kwargs):
     return default().angmf_propagate(*args, **kwargs)
+
+
+def convex_upsample(*args, **kwargs):
+    return default().convex_upsample(*args, **kwargs)

@@ -1,5 +1,7 @@
 /*
- * CPU parity oracle for the DSINE AngMF propagate and RayReLU ops.
+ * CPU parity oracle for the DSINE AngMF propagate and RayReLU ops, and for the
+ * convex upsample + channel L2-normalise the refiner applies after each
+ * propagate (src/dsine_refine.cpp:276-282).
  *
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product library links, loads or
  * calls this file; only the tests, the smoke check and the CPU-baseline leg of
@@ -19,7 +21,8 @@
  *   - a batch B of NCHW samples with a ray batch stride (0 = one shared ray);
  *   - a row range [y0, y1) so that tests can check bands of a large image.
  *
- * Parity pins (tests/test_oracle_pins.py): every function here is checked
+ * Parity pins (tests/test_oracle_pins.py, tests/test_oracle_upsample.py):
+ * every function here is checked
  * against closed forms, library routines (scipy Rotation, torch F.unfold /
  * F.normalize / F.cosine_similarity in float64) and brute force; the
  * reference source itself cannot be compiled in this image (it needs the
@@ -274,4 +277,95 @@ void oracle_angmf_propagate_f32(const float *pred_norm, const float *prob,
     oracle_angmf_propagate_rows_f32(pred_norm, prob, xy, angle, ray, fu, cu,
                                     fv, cv, B, H, W, k, ray_bstride, out,
                                     (double *)0, 0, H, 1);
+}
+
+/* ---------------------------------------------------------------------------
+ * Convex upsample by s with a 9-tap softmax mask, then (normalize != 0) the
+ * channel L2-normalise -- the two calls the refiner makes after each
+ * propagate (src/dsine_refine.cpp:276-282: brotensor convex_upsample_forward
+ * and l2_normalize_nchw_forward with eps 1e-12), whose arithmetic the
+ * reference specifies in include/brovisionml/dsine_refine.h:91-97 (DSINE's
+ * upsample_via_mask with replicate padding, then F.normalize):
+ *   mask (B, 9*s*s, H, W) viewed as (9, s, s, H, W): channel n*s*s + ky*s + kx
+ *   w_n = softmax over n of mask[n, ky, kx, y, x]   (exp(m - max) / sum)
+ *   v_c = sum_n w_n * x[c, clamp(y - 1 + n/3), clamp(x - 1 + n%3)]
+ *   out[c, s*y + ky, s*x + kx] = v_c / max(|v|, eps)  (or v_c unnormalised)
+ * in double, rounded to float once.  A NaN anywhere in a softmax makes its
+ * sub-pixel NaN, as torch.softmax does.
+ * -------------------------------------------------------------------------*/
+static void upsample_subpixel(const float *x, const float *mask, int C, int H, int W, int s,
+                              int y, int xx, int ky, int kx, int normalize, double eps,
+                              float *out)
+{
+    const size_t HW = (size_t)H * (size_t)W;
+    const size_t p = (size_t)y * W + xx;
+    const int s2 = s * s;
+    double m[9];
+    int nan = 0;
+    for (int n = 0; n < 9; ++n) {
+#if ORACLE_MUTATION == 8 /* mutation: ky and kx swapped in the mask channel */
+        m[n] = mask[((size_t)n * s2 + (size_t)kx * s + ky) * HW + p];
+#else
+        m[n] = mask[((size_t)n * s2 + (size_t)ky * s + kx) * HW + p];
+#endif
+        nan |= isnan(m[n]);
+    }
+    double mx = m[0];
+    for (int n = 1; n < 9; ++n)
+        if (m[n] > mx) mx = m[n];
+    double e[9], sum = 0.0;
+    for (int n = 0; n < 9; ++n) {
+        e[n] = nan ? NAN : exp(m[n] - mx);
+        sum += e[n];
+    }
+    double v[16];
+    for (int c = 0; c < C; ++c) v[c] = 0.0;
+    for (int n = 0; n < 9; ++n) {
+#if ORACLE_MUTATION == 10 /* mutation: column-major taps */
+        const int dy = n % 3 - 1, dx = n / 3 - 1;
+#else
+        const int dy = n / 3 - 1, dx = n % 3 - 1;
+#endif
+        const int sy = y + dy, sx = xx + dx;
+#if ORACLE_MUTATION == 9 /* mutation: zero padding instead of replicate */
+        const int inside = sy >= 0 && sy < H && sx >= 0 && sx < W;
+        const size_t sp = inside ? (size_t)sy * W + sx : 0;
+#else
+        const int inside = 1;
+        const size_t sp = (size_t)imin(imax(sy, 0), H - 1) * W + imin(imax(sx, 0), W - 1);
+#endif
+        const double w = e[n] / sum;
+        for (int c = 0; c < C; ++c) v[c] += inside ? w * x[(size_t)c * HW + sp] : 0.0;
+    }
+    double inv = 1.0;
+    if (normalize) {
+        double n2 = 0.0;
+        for (int c = 0; c < C; ++c) n2 += v[c] * v[c];
+#if ORACLE_MUTATION == 11 /* mutation: eps inside the square root */
+        inv = 1.0 / sqrt(n2 + eps);
+#else
+        inv = 1.0 / smax(sqrt(n2), eps);
+#endif
+    }
+    const size_t Ws = (size_t)W * s, HWs = HW * (size_t)s2;
+    const size_t q = ((size_t)y * s + ky) * Ws + (size_t)xx * s + kx;
+    for (int c = 0; c < C; ++c) out[(size_t)c * HWs + q] = (float)(v[c] * inv);
+}
+
+/* x: B x C x H x W; mask: B x 9s^2 x H x W; out: B x C x sH x sW; C <= 16. */
+void oracle_convex_upsample_f32(const float *x, const float *mask, int B, int C, int H, int W,
+                                int s, int normalize, double eps, float *out, int nthreads)
+{
+    const size_t HW = (size_t)H * (size_t)W;
+    for (int b = 0; b < B; ++b) {
+        const float *xb = x + (size_t)b * C * HW;
+        const float *mb = mask + (size_t)b * 9 * s * s * HW;
+        float *ob = out + (size_t)b * C * HW * s * s;
+#pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads) if (nthreads > 1)
+        for (int y = 0; y < H; ++y)
+            for (int xx = 0; xx < W; ++xx)
+                for (int ky = 0; ky < s; ++ky)
+                    for (int kx = 0; kx < s; ++kx)
+                        upsample_subpixel(xb, mb, C, H, W, s, y, xx, ky, kx, normalize, eps, ob);
+    }
 }

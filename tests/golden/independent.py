@@ -72,3 +72,23 @@ def refine_step(pred_norm, prob, xy, angle, ray, intr, k: int):
     v = ray_relu(rot, rb, dim=1)
     acc = (prob[:, None] * v).sum(2)
     return F.normalize(acc, dim=1).numpy(), acc.numpy()
+
+
+def convex_upsample(x, mask, s: int = 8, normalize: bool = True, eps: float = 1e-12):
+    """DSINE's upsample_via_mask with replicate padding (the structure
+    include/brovisionml/dsine_refine.h:91-97 specifies), then F.normalize over
+    channels: the mask viewed as (N, 1, 9, s, s, H, W) and softmaxed over the
+    9 taps, the 3x3 replicate-padded unfold of x weighted and summed, the
+    (s, s) sub-cells permuted onto the s-times grid.  float64 torch;
+    x (N, C, H, W), mask (N, 9*s*s, H, W) -> (N, C, s*H, s*W)."""
+    xt = torch.as_tensor(np.asarray(x), dtype=torch.float64)
+    mt = torch.as_tensor(np.asarray(mask), dtype=torch.float64)
+    N, C, H, W = xt.shape
+    w = mt.view(N, 1, 9, s, s, H, W).softmax(dim=2)
+    taps = F.unfold(F.pad(xt, (1, 1, 1, 1), mode="replicate"), [3, 3], padding=0)
+    taps = taps.view(N, C, 9, 1, 1, H, W)
+    up = (w * taps).sum(dim=2)                              # (N, C, s, s, H, W)
+    up = up.permute(0, 1, 4, 2, 5, 3).reshape(N, C, s * H, s * W)
+    if normalize:
+        up = F.normalize(up, dim=1, eps=eps)
+    return up.numpy()

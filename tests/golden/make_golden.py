@@ -84,12 +84,35 @@ def ray_relu_case(seed, H, W):
     return dict(normal=n, ray=ray, H=np.int32(H), W=np.int32(W), expect=want)
 
 
+def upsample_case(seed, B, C, H, W, s, normalize, smooth=False):
+    """Convex-upsample inputs: x a field of C-vectors (unit normals when
+    C == 3), the 9*s*s-channel mask ~ N(0, 2^2)."""
+    rng = np.random.default_rng(seed)
+    if smooth:
+        ys, xs = np.meshgrid(np.linspace(0, 1, H), np.linspace(0, 1, W), indexing="ij")
+        x = np.stack([0.5 * np.sin(3 * xs + ys), 0.4 * np.cos(2 * ys), -np.ones_like(xs)])[None]
+        x = np.repeat(x, B, axis=0)
+    else:
+        x = rng.standard_normal((B, C, H, W))
+    if C == 3:
+        x = x / np.linalg.norm(x, axis=1, keepdims=True)
+    x = x.astype(np.float32)
+    mask = (2.0 * rng.standard_normal((B, 9 * s * s, H, W))).astype(np.float32)
+    want = ind.convex_upsample(x.astype(np.float64), mask.astype(np.float64), s, normalize)
+    return dict(x=x, mask=mask, H=np.int32(H), W=np.int32(W), s=np.int32(s),
+                normalize=np.int32(normalize), expect=want)
+
+
 CASES = {
     "angmf_8x10_k5": lambda: finish(random_case(101, 1, 8, 10, 5, (0.0, np.pi))),
     "angmf_b2_12x16_k3_raystride": lambda: finish(random_case(102, 2, 12, 16, 3, (-1.0, 1.0), True)),
     "angmf_9x13_k7": lambda: finish(random_case(103, 1, 9, 13, 7, (0.0, np.pi / 4))),
     "angmf_smooth_16x20_k5": lambda: finish(smooth_case(104, 16, 20)),
     "ray_relu_12x20": lambda: ray_relu_case(105, 12, 20),
+    "upsample_4x5_s8": lambda: upsample_case(106, 1, 3, 4, 5, 8, True),
+    "upsample_4x6_s4_c2_raw": lambda: upsample_case(107, 1, 2, 4, 6, 4, False),
+    "upsample_smooth_5x6_s8": lambda: upsample_case(108, 1, 3, 5, 6, 8, True, smooth=True),
+    "upsample_b2_3x5_s2_c4": lambda: upsample_case(109, 2, 4, 3, 5, 2, True),
 }
 
 

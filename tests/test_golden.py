@@ -13,10 +13,12 @@ import oracle
 
 HERE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden")
 ANGMF = sorted(glob.glob(os.path.join(HERE, "angmf_*.npz")))
+UPSAMPLE = sorted(glob.glob(os.path.join(HERE, "upsample_*.npz")))
 
 
 def test_fixtures_present():
     assert len(ANGMF) >= 4
+    assert len(UPSAMPLE) >= 4
     assert os.path.exists(os.path.join(HERE, "ray_relu_12x20.npz"))
 
 
@@ -34,3 +36,13 @@ def test_oracle_ray_relu_matches_fixture():
     d = np.load(os.path.join(HERE, "ray_relu_12x20.npz"))
     out = oracle.ray_relu(d["normal"], d["ray"], int(d["H"]), int(d["W"]))
     assert np.abs(out - d["expect"]).max() < 1e-7
+
+
+@pytest.mark.parametrize("path", UPSAMPLE, ids=[os.path.basename(p) for p in UPSAMPLE])
+def test_oracle_upsample_matches_fixture(path):
+    d = np.load(path)
+    out = oracle.convex_upsample(d["x"], d["mask"], int(d["H"]), int(d["W"]), int(d["s"]),
+                                 normalize=bool(d["normalize"]))
+    want = d["expect"]
+    assert out.shape == want.shape
+    assert (np.abs(out - want) / np.maximum(1.0, np.abs(want))).max() < 1.2e-7
