@@ -19,6 +19,7 @@ ESIZE = -4
 EALIAS = -5
 EFLAGS = -6
 EPARAM = -7
+EUNSUP = -8
 
 DEFAULT = 0
 FP64 = 1
@@ -29,6 +30,7 @@ EXPORTS = (
     "bvml_dsine_ray_relu_f32",
     "bvml_dsine_angmf_propagate_f32",
     "bvml_dsine_build_ray8_f32",
+    "bvml_dsine_convex_upsample_f32",
     "bvml_dsine_last_error",
     "bvml_dsine_version",
 )
@@ -54,6 +56,9 @@ def load(path: str = LIB) -> ctypes.CDLL:
     lib.bvml_dsine_angmf_propagate_f32.restype = i
     lib.bvml_dsine_build_ray8_f32.argtypes = [vp, d, d, d, d, i, i, vp]
     lib.bvml_dsine_build_ray8_f32.restype = i
+    lib.bvml_dsine_convex_upsample_f32.argtypes = [vp, vp, i, i, i, i, i, i, ctypes.c_float, vp,
+                                                   u, vp]
+    lib.bvml_dsine_convex_upsample_f32.restype = i
     lib.bvml_dsine_last_error.argtypes = []
     lib.bvml_dsine_last_error.restype = ctypes.c_char_p
     lib.bvml_dsine_version.argtypes = []
@@ -86,3 +91,11 @@ def build_ray8_f32(ray: int, fu: float, cu: float, fv: float, cv: float, H: int,
                    stream: int = 0) -> int:
     """Raw call; `ray` is an integer device address of 3*H*W floats."""
     return load().bvml_dsine_build_ray8_f32(ray, fu, cu, fv, cv, H, W, stream)
+
+
+def convex_upsample_f32(x: int, mask: int, B: int, C: int, H: int, W: int, scale: int,
+                        normalize: bool, eps: float, out: int, flags: int = DEFAULT,
+                        stream: int = 0) -> int:
+    """Raw call; pointers are integer device addresses. Returns the status."""
+    return load().bvml_dsine_convex_upsample_f32(x, mask, B, C, H, W, scale, int(bool(normalize)),
+                                                 eps, out, flags, stream)

@@ -37,6 +37,7 @@ HIP_FLAGS = [
 
 SOURCES = [
     os.path.join(CSRC, "dsine_ops.hip"),   # kernels + C ABI
+    os.path.join(CSRC, "upsample.hip"),    # convex upsample + normalise
     os.path.join(CSRC, "dsine_ops.cpp"),   # C++ drop-in (brovisionml::dsine)
     os.path.join(CSRC, "tensor.cpp"),      # brotensor::Tensor subset
 ]

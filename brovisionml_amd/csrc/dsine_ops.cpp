@@ -5,6 +5,7 @@
 
 #include "brovisionml/dsine_ops.h"
 
+#include <climits>
 #include <stdexcept>
 #include <string>
 
@@ -90,6 +91,45 @@ void angmf_propagate(const Tensor& pred_norm, const Tensor& prob, const Tensor& 
     need_size(angle, 25 * hw, "angmf_propagate", "angle");
     need_size(ray, 3 * hw, "angmf_propagate", "ray");
     detail::angmf_propagate_gpu(pred_norm, prob, xy, angle, ray, fu, cu, fv, cv, H, W, out);
+}
+
+namespace {
+
+void upsample(const Tensor& x, const Tensor& mask, int N, int C, int H, int W, int scale,
+              bool normalize, float eps, Tensor& out, const char* op) {
+    if (x.device != mask.device) fail(std::string(op) + ": x and mask must share a device");
+    if (x.device == Device::CPU)
+        fail(std::string(op) + ": tensors are on the CPU; this library implements the HIP "
+             "device path");
+    if (N < 0 || C < 1 || H < 0 || W < 0 || scale < 1)
+        fail(std::string(op) + ": N, H and W must be >= 0, C and scale >= 1");
+    const std::size_t hw = static_cast<std::size_t>(H) * W;
+    const std::size_t s2 = static_cast<std::size_t>(scale) * scale;
+    need_size(x, static_cast<std::size_t>(N) * C * hw, op, "x");
+    need_size(mask, static_cast<std::size_t>(N) * 9 * s2 * hw, op, "mask");
+    const std::size_t n_out = static_cast<std::size_t>(N) * C * s2 * hw;
+    if (C * s2 * hw > static_cast<std::size_t>(INT_MAX))
+        fail(std::string(op) + ": C*scale^2*H*W exceeds a tensor row");
+    const bool reuse = out.device == Device::HIP && out.rows == N && out.numel() == n_out &&
+                       out.data != nullptr && out.data != x.data && out.data != mask.data;
+    if (!reuse) out = Tensor::zeros_on(Device::HIP, N, static_cast<int>(n_out / (N ? N : 1)));
+    if (n_out == 0) return;
+    const int st = bvml_dsine_convex_upsample_f32(
+        static_cast<const float*>(x.data), static_cast<const float*>(mask.data), N, C, H, W, scale,
+        normalize ? 1 : 0, eps, static_cast<float*>(out.data), BVML_DSINE_DEFAULT, nullptr);
+    if (st != BVML_DSINE_OK) fail_hip((std::string(op) + " launch").c_str(), st);
+}
+
+}  // namespace
+
+void convex_upsample_normalize(const Tensor& x, const Tensor& mask, int N, int C, int H, int W,
+                               int scale, float eps, Tensor& out) {
+    upsample(x, mask, N, C, H, W, scale, true, eps, out, "convex_upsample_normalize");
+}
+
+void convex_upsample(const Tensor& x, const Tensor& mask, int N, int C, int H, int W, int scale,
+                     Tensor& out) {
+    upsample(x, mask, N, C, H, W, scale, false, 0.0f, out, "convex_upsample");
 }
 
 }  // namespace brovisionml::dsine

@@ -47,6 +47,23 @@
 #include <string>
 
 #include "bvml_dsine.h"
+#include "status.h"
+
+namespace bvml {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+    return a0 < b0 + bbytes && b0 < a0 + abytes;
+}
+
+}  // namespace bvml
 
 namespace {
 
@@ -895,17 +912,8 @@ __global__ __launch_bounds__(256) void build_ray8_kernel(float* ray, double fu, 
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
-thread_local std::string g_last_error;
-
-int fail(int code, const std::string& msg) {
-    g_last_error = msg;
-    return code;
-}
-
-bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
-    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
-    return a0 < b0 + bbytes && b0 < a0 + abytes;
-}
+using bvml::fail;
+using bvml::overlaps;
 
 // Samples per launch of the fp32 kernel (its grid's y extent).
 constexpr int kMaxGridY = 65535;
@@ -996,7 +1004,7 @@ void choose_tile(AngmfArgs& a, int K) {
 
 extern "C" {
 
-const char* bvml_dsine_last_error(void) { return g_last_error.c_str(); }
+const char* bvml_dsine_last_error(void) { return bvml::g_last_error.c_str(); }
 
 const char* bvml_dsine_version(void) { return "0.1.0"; }
 

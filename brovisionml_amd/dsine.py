@@ -7,6 +7,12 @@ include/brovisionml/dsine_ops.h:19-54):
   ray_relu(normal, ray, H, W)                    in place
   angmf_propagate(pred_norm, prob, xy, angle, ray, fu, cu, fv, cv, H, W, out)
 
+and the refiner's post-propagate step (src/dsine_refine.cpp:276-282), whose
+reference is brotensor's convex_upsample_forward + l2_normalize_nchw_forward:
+
+  convex_upsample(x, mask, N, C, H, W, scale, out)
+  convex_upsample_normalize(x, mask, N, C, H, W, scale, eps, out)   fused
+
 Tensors are torch tensors on a HIP device (torch is only the allocator and
 stream provider here), fp32, contiguous, in the reference's NCHW layout:
 (1, C*H*W), (C, H, W), or batched (B, C, H, W) / (B, C*H*W).  A batch of B
@@ -124,6 +130,52 @@ def angmf_propagate(pred_norm, prob, xy, angle, ray, fu: float, cu: float,
             B, H, W, k, bstride, out.data_ptr(), flags, _stream_of(pred_norm))
     _raise_status("angmf_propagate", st)
     return out
+
+
+def _upsample(op: str, x, mask, N: int, C: int, H: int, W: int, scale: int, out,
+              normalize: bool, eps: float, precise: bool):
+    _check_tensors(op, [x, mask])
+    import torch
+    if min(N, C, H, W) < 0 or scale < 1:
+        _fail(f"{op}: N, C, H and W must be >= 0 and scale >= 1")
+    HW = H * W
+    if x.numel() != N * C * HW:
+        _fail(f"{op}: x holds {x.numel()} elements, expected N*C*H*W = {N * C * HW}")
+    if mask.numel() != N * 9 * scale * scale * HW:
+        _fail(f"{op}: mask holds {mask.numel()} elements, expected N*9*scale^2*H*W")
+    n_out = N * C * scale * scale * HW
+    if out is None:
+        out = torch.empty((N, C, scale * H, scale * W), dtype=torch.float32, device=x.device)
+    elif out.device != x.device or out.dtype != torch.float32 or not out.is_contiguous() \
+            or out.numel() != n_out:
+        _fail(f"{op}: out must be a contiguous float32 tensor of N*C*(scale*H)*(scale*W) "
+              "elements on x's device")
+    if n_out == 0:
+        return out
+    flags = _lib.FP64 if precise else _lib.DEFAULT
+    with _device(x):
+        st = _lib.convex_upsample_f32(x.data_ptr(), mask.data_ptr(), N, C, H, W, scale,
+                                      normalize, float(eps), out.data_ptr(), flags, _stream_of(x))
+    _raise_status(op, st)
+    return out
+
+
+def convex_upsample(x, mask, N: int, C: int, H: int, W: int, scale: int = 8, out=None, *,
+                    precise: bool = False):
+    """Convex upsample by `scale` with a 9-tap softmax mask: brotensor's
+    convex_upsample_forward as the refiner calls it (src/dsine_refine.cpp:278,
+    arithmetic of include/brovisionml/dsine_refine.h:91-97).  x (N, C, H, W),
+    mask (N, 9*scale^2, H, W); returns out (N, C, scale*H, scale*W)."""
+    return _upsample("convex_upsample", x, mask, N, C, H, W, scale, out, False, 0.0, precise)
+
+
+def convex_upsample_normalize(x, mask, N: int, C: int, H: int, W: int, scale: int = 8,
+                              eps: float = 1e-12, out=None, *, precise: bool = False):
+    """convex_upsample followed by the channel L2-normalise with eps, fused:
+    the pair the refiner runs after each propagate (src/dsine_refine.cpp:276-282,
+    l2_normalize_nchw_forward with eps 1e-12f)."""
+    return _upsample("convex_upsample_normalize", x, mask, N, C, H, W, scale, out, True, eps,
+                     precise)
 
 
 def build_ray8(fu: float, cu: float, fv: float, cv: float, H: int, W: int, device=None):

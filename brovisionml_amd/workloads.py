@@ -163,3 +163,45 @@ def make_inputs(wl: Workload):
     out["ray"] = build_ray8(intr, wl.H, wl.W, 8 * wl.H, 8 * wl.W).reshape(3, wl.HW)
     out["intrinsics"] = (fu, cu, fv, cv)
     return out
+
+
+@dataclass(frozen=True)
+class UpsampleWorkload:
+    """The refiner's post-propagate step (src/dsine_refine.cpp:276-282): the
+    C-channel normal map on the /8 grid upsampled by s with a 9*s*s-channel
+    softmax mask, then L2-normalised."""
+    name: str
+    B: int
+    C: int
+    H: int
+    W: int
+    s: int
+    mask_sigma: float   # mask logits ~ N(0, sigma^2)
+    seed: int
+
+    @property
+    def HW(self) -> int:
+        return self.H * self.W
+
+    def algorithmic_bytes(self) -> int:
+        """x and the mask read once, out written once."""
+        return self.B * self.HW * 4 * (self.C + 9 * self.s * self.s + self.C * self.s * self.s)
+
+
+# the refiner's shape at the 2048x2048 headline image (the 256x256 grid of
+# the propagate workload), and at 480x640
+UPSAMPLE_WORKLOADS = [
+    UpsampleWorkload("dsine-upsample-256x256-s8", 1, 3, 256, 256, 8, 1.0, 2000),
+    UpsampleWorkload("dsine-upsample-60x80-s8", 1, 3, 60, 80, 8, 1.0, 2001),
+]
+
+
+def make_upsample_inputs(wl: UpsampleWorkload):
+    """x (B, C, H, W) unit normals drawn independently per pixel (the case
+    with the most cancellation between neighbours), mask (B, 9*s*s, H, W)."""
+    rng = np.random.default_rng(wl.seed)
+    x = np.stack([_unit_normals(rng, wl.HW, "sphere").reshape(wl.C, wl.H, wl.W)
+                  for _ in range(wl.B)])
+    mask = (wl.mask_sigma * rng.standard_normal((wl.B, 9 * wl.s * wl.s, wl.H, wl.W),
+                                                dtype=np.float32)).astype(np.float32)
+    return np.ascontiguousarray(x), mask

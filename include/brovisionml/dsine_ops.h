@@ -38,6 +38,21 @@ void angmf_propagate(const brotensor::Tensor& pred_norm,
                      int H, int W,
                      brotensor::Tensor& out);
 
+// The refiner's post-propagate step (src/dsine_refine.cpp:276-282), whose
+// reference is two brotensor calls:
+//   convex_upsample_forward(x, mask, N, C, H, W, scale, up)
+//   l2_normalize_nchw_forward(up, N, C, scale*H, scale*W, eps, up)
+// convex_upsample_normalize runs both in one pass; convex_upsample is the first
+// alone.  x (N, C*H*W) with C <= 4, mask (N, 9*scale^2*H*W) with scale <= 16
+// (channel n*scale^2 + ky*scale + kx, tap n = 3*(dy+1) + (dx+1), replicate
+// padding), both fp32 on the HIP device; `out` becomes (N, C*scale^2*H*W)
+// fp32 on the device, reused under the same rule as angmf_propagate's.
+void convex_upsample_normalize(const brotensor::Tensor& x, const brotensor::Tensor& mask,
+                               int N, int C, int H, int W, int scale, float eps,
+                               brotensor::Tensor& out);
+void convex_upsample(const brotensor::Tensor& x, const brotensor::Tensor& mask, int N, int C,
+                     int H, int W, int scale, brotensor::Tensor& out);
+
 namespace detail {
 
 // The launchers the dispatch above calls; they replace

@@ -42,6 +42,7 @@ extern "C" {
 #define BVML_DSINE_EALIAS (-5)    /* out overlaps an input */
 #define BVML_DSINE_EFLAGS (-6)    /* unknown flag bits */
 #define BVML_DSINE_EPARAM (-7)    /* fu/fv zero or non-finite, cu/cv non-finite */
+#define BVML_DSINE_EUNSUP (-8)    /* a size outside what the kernels support */
 
 /* Flag bits for bvml_dsine_angmf_propagate_f32. */
 #define BVML_DSINE_DEFAULT 0u
@@ -96,6 +97,31 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
  */
 int bvml_dsine_build_ray8_f32(float* ray, double fu, double cu, double fv,
                               double cv, int H, int W, void* stream);
+
+/*
+ * Convex upsample by `scale` with a 9-tap softmax mask, fused with the channel
+ * L2-normalise (normalize != 0), B samples.  Replaces the two brotensor calls
+ * the refiner makes after each propagate (src/dsine_refine.cpp:276-282:
+ * convex_upsample_forward(pred_norm, up_mask, N, C, H, W, scale, up), then
+ * l2_normalize_nchw_forward(up, N, C, scale*H, scale*W, 1e-12f, up)); the
+ * arithmetic is the one the reference specifies at
+ * include/brovisionml/dsine_refine.h:91-97 (DSINE's upsample_via_mask with
+ * replicate padding, then F.normalize):
+ *   x    : B x C x H x W
+ *   mask : B x 9*scale^2 x H x W, channel n*scale^2 + ky*scale + kx, tap
+ *          n = 3*(dy+1) + (dx+1) for the neighbour (y+dy, x+dx), clamped
+ *   out  : B x C x (scale*H) x (scale*W); sub-pixel (ky, kx) of (y, x) is
+ *          softmax_n(mask)-weighted sum of the taps, then / max(|v|, eps)
+ * C in 1..4 and scale in 1..16 (BVML_DSINE_EUNSUP otherwise); the refiner
+ * uses C = 3, scale = 8, eps = 1e-12f.  A NaN in a sub-pixel's 9 mask values
+ * makes that sub-pixel NaN.  Within 7.2e-6 per component of the
+ * double-precision result (a bound; typically 1e-7); flags BVML_DSINE_FP64
+ * computes every sub-pixel in double.  `out` is caller-allocated and must not
+ * overlap x or mask.
+ */
+int bvml_dsine_convex_upsample_f32(const float* x, const float* mask, int B, int C, int H,
+                                   int W, int scale, int normalize, float eps, float* out,
+                                   unsigned flags, void* stream);
 
 /* Message for the calling thread's last non-zero status ("" if none). */
 const char* bvml_dsine_last_error(void);

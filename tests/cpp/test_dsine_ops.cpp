@@ -1,10 +1,12 @@
-// Drop-in test of brovisionml::dsine::{ray_relu, angmf_propagate} (the C++
+// Drop-in test of brovisionml::dsine::{ray_relu, angmf_propagate,
+// convex_upsample[_normalize]} (the C++
 // surface of include/brovisionml/dsine_ops.h), in the style of the
 // reference's tests (tests/test_dsine_refine.cpp:48-53: CHECK + failure count).
 //
 //   test_dsine_ops cpu   error behaviour; makes no GPU call
-//   test_dsine_ops gpu   the refiner's call pattern (src/dsine_refine.cpp:241-273:
-//                        ray_relu once, then chained angmf_propagate calls)
+//   test_dsine_ops gpu   the refiner's call pattern (src/dsine_refine.cpp:241-282:
+//                        ray_relu once, then chained angmf_propagate calls, then
+//                        the convex upsample + normalise)
 //                        on a 60x80 grid against the CPU oracle (links
 //                        oracle/_build/liboracle_dsine.so; test-only)
 
@@ -27,6 +29,8 @@ void oracle_angmf_propagate_f32(const float* pred_norm, const float* prob, const
                                 const float* angle, const float* ray, double fu, double cu,
                                 double fv, double cv, int B, int H, int W, int k,
                                 long long ray_bstride, float* out);
+void oracle_convex_upsample_f32(const float* x, const float* mask, int B, int C, int H, int W,
+                                int s, int normalize, double eps, float* out, int nthreads);
 }
 
 using brotensor::Device;
@@ -86,6 +90,18 @@ static void test_errors() {
                       "dsine ops: ", "xy holds"));
     CHECK(throws_with([&] { ops::ray_relu(dn, dr, H + 1, W); }, "dsine ops: ", "normal holds"));
     CHECK(throws_with([&] { ops::ray_relu(dn, dr, -1, W); }, "dsine ops: ", "H and W"));
+    // convex upsample (+ normalise): the same checks
+    Tensor mk = Tensor::mat(1, 576 * HW), dmk = fake_device(1, 576 * HW);
+    CHECK(throws_with([&] { ops::convex_upsample_normalize(n, mk, 1, 3, H, W, 8, 1e-12f, out); },
+                      "dsine ops: ", "CPU"));
+    CHECK(throws_with([&] { ops::convex_upsample(dn, mk, 1, 3, H, W, 8, out); }, "dsine ops: ",
+                      "x and mask must share a device"));
+    CHECK(throws_with([&] { ops::convex_upsample(dn, dmk, 1, 3, H, W, 4, out); }, "dsine ops: ",
+                      "mask holds"));
+    CHECK(throws_with([&] { ops::convex_upsample_normalize(dn, dmk, 1, 2, H, W, 8, 1e-12f, out); },
+                      "dsine ops: ", "x holds"));
+    CHECK(throws_with([&] { ops::convex_upsample(dn, dmk, 1, 3, H, W, 0, out); }, "dsine ops: ",
+                      "scale >= 1"));
 }
 
 // Unit normals, sigmoid probs, raw xy, angles, ray_8 of a 480x640 image
@@ -193,6 +209,31 @@ static void test_refiner_call_pattern() {
     Tensor alias = pred_norm;
     ops::angmf_propagate(pred_norm, prob, xy, angle, ray, in.fu, in.cu, in.fv, in.cv, H, W, alias);
     CHECK(alias.data != pred_norm.data);
+    // up_pred_norm = normalize(convex_upsample(pred_norm, up_mask)) -- the
+    // refiner's step after each propagate (src/dsine_refine.cpp:276-282)
+    std::mt19937 rng(11);
+    std::normal_distribution<double> nd;
+    std::vector<float> mask(576 * H * W);
+    for (auto& v : mask) v = static_cast<float>(nd(rng));
+    std::vector<float> pn_host(3 * H * W), want_up(3 * 64 * H * W);
+    {
+        Tensor h = pred_norm.to(Device::CPU);
+        std::memcpy(pn_host.data(), h.host_f32(), pn_host.size() * sizeof(float));
+    }
+    Tensor up_mask = upload(mask), up;
+    ops::convex_upsample_normalize(pred_norm, up_mask, 1, 3, H, W, 8, 1e-12f, up);
+    CHECK(up.device == Device::HIP && up.rows == 1 && up.cols == 3 * 64 * H * W);
+    oracle_convex_upsample_f32(pn_host.data(), mask.data(), 1, 3, H, W, 8, 1, (double)1e-12f,
+                               want_up.data(), 1);
+    const double eu = max_abs(up, want_up);
+    std::printf("    convex_upsample_normalize max-abs %.3e\n", eu);
+    CHECK(eu <= 1e-5);
+    ops::convex_upsample(pred_norm, up_mask, 1, 3, H, W, 8, up);
+    oracle_convex_upsample_f32(pn_host.data(), mask.data(), 1, 3, H, W, 8, 0, 0.0,
+                               want_up.data(), 1);
+    const double er = max_abs(up, want_up);
+    std::printf("    convex_upsample max-abs %.3e\n", er);
+    CHECK(er <= 1e-6);
     CHECK(hipDeviceSynchronize() == hipSuccess);
 }
 

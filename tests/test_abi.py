@@ -103,6 +103,35 @@ def test_ray_relu_rejects(args, code):
     assert _lib.last_error().startswith("ray_relu: ")
 
 
+def upsample(**kw):
+    # x 1x3x4x4 at FAKE, mask 1x576x4x4 at FAKE + 0x100000, out 1x3x32x32 beyond
+    args = dict(x=FAKE, mask=FAKE + 0x100000, B=1, C=3, H=4, W=4, scale=8, normalize=True,
+                eps=1e-12, out=FAKE + 0x200000, flags=0, stream=0)
+    args.update(kw)
+    return _lib.convex_upsample_f32(**args)
+
+
+@pytest.mark.parametrize("kw,code", [
+    (dict(B=-1), _lib.ESHAPE), (dict(W=-1), _lib.ESHAPE), (dict(C=0), _lib.ESHAPE),
+    (dict(scale=0), _lib.ESHAPE),
+    (dict(C=5), _lib.EUNSUP), (dict(scale=17), _lib.EUNSUP),
+    (dict(x=0), _lib.ENULL), (dict(mask=0), _lib.ENULL), (dict(out=0), _lib.ENULL),
+    (dict(flags=2), _lib.EFLAGS),
+    (dict(out=FAKE + 64), _lib.EALIAS),                 # inside x
+    (dict(out=FAKE + 0x100000 + 0x9000 - 16), _lib.EALIAS),  # last bytes of mask
+    (dict(H=1 << 15, W=1 << 15), _lib.ESIZE),            # 2^30 pixels per sample
+])
+def test_upsample_rejects(kw, code):
+    assert upsample(**kw) == code
+    assert _lib.last_error().startswith("convex_upsample: ")
+
+
+def test_upsample_empty_is_no_op():
+    assert upsample(B=0) == _lib.OK
+    assert upsample(H=0, x=0, mask=0, out=0) == _lib.OK
+    assert upsample(W=0, normalize=False) == _lib.OK
+
+
 def test_cpp_dropin_error_paths():
     assert os.path.exists(CPP_TEST), "build() compiles tests/cpp/test_dsine_ops"
     proc = subprocess.run([CPP_TEST, "cpu"], stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
