@@ -8,29 +8,30 @@
 //
 // angmf_propagate moves 436 B/px at k=5 but also does about 25 neighbour
 // rotations per pixel; at the parity bar (1e-5 per component) the reference's
-// all-double formulation costs more VALU time than the HBM traffic takes, so
-// the fast kernel mixes precisions where the error analysis allows:
+// all-double formulation costs far more VALU time than the HBM traffic takes,
+// so the fast kernel evaluates every neighbour in fp32 where the error
+// analysis allows and recomputes the few pixels where it does not:
 //   * the tile's replicate-padded pred_norm halo is staged in LDS once, one
-//     record per source pixel: m and 1/|m|, g = P0.m (P0 = the source pixel's
-//     ray at depth 1, NaN unless m is a unit normal), tu0 = (0.5 - cu)/fu + x/fu
-//     and the double products mx/fu, my/fv, g/fu, g/fv;
+//     record per source pixel: m' = m/|m|, g = P0.m (P0 = the source pixel's
+//     ray at depth 1, NaN unless m is a unit normal), the double products
+//     mx/fu, my/fv, then g/fu, g/fv, tu0, tv0;
 //   * the rotation axis is algebraically reduced: the reference's
 //     normalize(du + dz*tu, dv + dz*tv, dz) with dz = num/dd equals
 //     sign(dd) * V/|V| with V = (g*xs/fu - q*tu0, g*ys/fv - q*tv0, -q),
 //     q = xs*mx/fu + ys*my/fv on the RAW xy pair -- the xy normalisation and
 //     the quadratic terms cancel exactly, and V.m == 0, so Rodrigues reduces to
 //     m'*cos(t) + (V x m')*sin(t)/|V|;
-//   * q, dd = g + q/|xy| and V are formed in double from the fp32 inputs (they
-//     cancel where a surface is edge-on to the rays); the rotation itself
-//     (|V|, sin, cos, the cross product) runs in fp32; RayReLU, the weight
-//     prob/|p|, the accumulation and the final normalise run in double;
-//   * a pixel goes to a reference-order double recompute (one neighbour per
-//     lane of the wave that owns it, wave-wide reduction) when any neighbour
-//     is outside the reduced form's domain -- |dd| near the reference's 1e-8
-//     clamp, a tiny xy pair, a non-unit source normal, |t| > 3.2, a
-//     non-finite value -- or when |acc|^2 < 3.5e-4 * sum(wi^2), where the
-//     final normalise would amplify the per-term error (<= 1.3e-7 * wi) past
-//     the parity bar.
+//   * tier 1 forms q in double (it cancels where the xy pair is nearly
+//     perpendicular to m) and everything else -- dd, V, sin/cos, the
+//     rotation, RayReLU, the weight prob/|p|, the partial sums -- in fp32;
+//   * a pixel goes to tier 2, the same reduced form in double, when a
+//     neighbour is outside the fp32 form's domain (|dd| near the
+//     reference's 1e-8 clamp, an xy pair out of range, a non-unit source
+//     normal, |t| > 3.2, a non-finite value) or when |acc|^2 < 1.6e-3 *
+//     sum(wi^2), where the final normalise would amplify tier 1's error
+//     past the parity bar; and from there to tier 3, the reference-order
+//     double body, when a neighbour is outside the double form's domain or
+//     the sum still nearly cancels.
 // Workgroups are 8 waves: G waves per 64-pixel group, each evaluating one run
 // of the window's neighbours (G = 4 at k=5), so the SPI places 2 waves per
 // SIMD and every SIMD carries the same work; two workgroups per CU run a
@@ -45,6 +46,7 @@
 #include <cstdint>
 #include <cstdio>
 #include <string>
+#include <type_traits>
 
 #include "bvml_dsine.h"
 #include "status.h"
@@ -75,33 +77,58 @@ constexpr float kRayEpsF = 1e-2f;
 // normal this op or RayReLU writes is one) and raw xy pairs with
 // kMinXY2 <= |xy|^2 <= kMaxXY2 in fp32 (below, the reference's 1e-12 clamp
 // stops normalising; above, the fp32 |xy|^2 could overflow); a neighbour
-// outside sends its pixel to the reference-order path.  Both bounds are one
-// unsigned comparison on the float's bits (NaN and negatives fall outside).
+// outside sends its pixel to the recompute.  Both bounds are one unsigned
+// comparison on the float's bits (NaN and negatives fall outside).
 constexpr float kUnitM2 = 1e-5f;
 constexpr float kMinXY2 = 1e-20f;
 constexpr float kMaxXY2 = 1e30f;
 constexpr uint32_t kXY2Lo = __builtin_bit_cast(uint32_t, kMinXY2);
 constexpr uint32_t kXY2Span = __builtin_bit_cast(uint32_t, kMaxXY2) - kXY2Lo;
+// |V|^2 below this (fp32 underflow territory) also sends the pixel there.
+constexpr float kMinV2 = 1e-30f;
 
-// Each fast-path term is within delta * wi of the reference's (wi = prob/|p|,
-// the term's weight before its final normalise, p the RayReLU'd rotation),
-// delta <= 1.3e-7 measured over 1.6M neighbours (rotation in fp32, RayReLU,
-// normalise and sum in double).  The final normalise divides the sum by
-// |acc|, so a pixel with |acc|^2 < kAccRatio2 * sum(wi^2) goes to the
-// reference-order path and the rest stay within 1.3e-7 / sqrt(kAccRatio2),
-// about 7e-6 per component.
-constexpr double kAccRatio2 = 3.5e-4;
+// Tier 1 error budget.  A pixel's summed error is within delta *
+// sqrt(sum(wi^2)) (wi = prob/|p|, a term's weight before its final
+// normalise, p the RayReLU'd rotation); a CPU emulation of every rounding of
+// tier 1 (q in double, the rest fp32, the hardware rsq at its measured
+// bound) over 1.2M random pixels -- unit normals isotropic or +z-biased,
+// angles up to 3.2, fields of view up to 140 degrees (|P0| <= 4) -- gives
+// delta <= 3.65e-7 (2.94e-7 at the 99.99th percentile).  The final normalise
+// divides the sum by |acc|, so a pixel with |acc|^2 < kAccRatio2 * sum(wi^2)
+// is recomputed and the rest stay within 3.65e-7 / sqrt(kAccRatio2) = 9.1e-6
+// per component (7.4e-6 at the 99.99th percentile).  About 1 random pixel
+// in 40,000 falls below it (none of the 256x256 bench input, whose smallest
+// ratio is 1.95e-3); the refiner's camera-facing normals practically never
+// do.  RayReLU and the sums in double would halve delta for 12 more
+// instructions per neighbour; a recompute pass costs about 2.5 us at the
+// end of its workgroup.
+constexpr double kAccRatio2 = 1.6e-3;
+
+// Tier 2 (the double-precision reduced form of flagged pixels) hands a pixel
+// to the reference-order body when its sum nearly cancels: below
+// kAccRatio2Ref * sum(wi^2), or |acc| near the reference's 1e-12 clamp.
+// Its per-term error is a few 1e-16, so the rest stay within about 1e-7.
+constexpr double kAccRatio2Ref = 1e-16;
+constexpr double kAcc2Floor = 1e-22;
 
 // The reference clamps |dd| < 1e-8 (src/dsine_ops.cpp:120-123), where the
-// reduced axis no longer holds.  The fast path's dd = g + q/|xy| takes 1/|xy|
-// from the fp32 |xy|^2 (fma, relative error < 1.2e-7) and the hardware fp32
-// rsq (< 9.4e-8 measured), so it is within 1.6e-7 * |q|/|xy| <=
-// 1.6e-7 * |m| / min(|fu|, |fv|) of the reference's; a neighbour with |dd|
-// below dd_min = 1.01e-8 + 3e-7 / min(|fu|, |fv|) sends its
-// pixel to the reference-order path, so the sign of every other dd is the
-// reference's, and so is the axis -- including where m is nearly parallel to
-// N = D x P0 (g and q both small), since dd = g + q/|xy| is small then too.
-constexpr double kDdClamp = 1.01e-8;
+// reduced axis no longer holds.  Tier 1 forms dd = g + q/|xy| as
+// fma(q, rsq(|xy|^2), g) in fp32 with g and q rounded from double: it is
+// within 6e-8 |g| + 1.9e-7 |m| / min(|fu|, |fv|) (+ 6e-8 |dd|) of the exact
+// value.  A neighbour with |dd| below
+//   dd_min = 1.02e-8 + 1e-7 * gmax + 3e-7 / min(|fu|, |fv|),
+// gmax the largest |P0| (source ray at depth 1) over the image, sends its
+// pixel to the recompute, so the sign of every other dd is the reference's
+// and so is the axis -- including where m is nearly parallel to N = D x P0
+// (g and q both small), since dd = g + q/|xy| is small then too.  Tier 2's
+// double dd is within 1e-15 of the exact value; it sends a neighbour with
+// |dd| < kDdClampRef to the reference-order body.
+constexpr double kDdClamp = 1.02e-8;
+constexpr double kDdClampRef = 1.0001e-8;
+// The fp32 path assumes |P0| <= kMaxP0 over the image (a diagonal field of
+// view up to about 150 degrees): its |V| stays within fp32 range and its
+// error bound above holds.  Wider views run the double-precision kernel.
+constexpr double kMaxP0 = 4.0;
 
 // ---------------------------------------------------------------------------
 // Double-precision reference body
@@ -129,14 +156,15 @@ __device__ __forceinline__ float3 synth_ray(int x, int y, double fu, double cu, 
 // One neighbour's RayReLU'd rotated normal, in the operation order of
 // src/dsine_ops.cpp:110-160 (axis :110-138, axis_angle_to_matrix :31-51,
 // rotate + renormalise :140-148, RayReLU :150-160).  Contraction is off so
-// the sign-deciding dd is bit-identical to the CPU's.
+// the sign-deciding dd is bit-identical to the CPU's.  pinv is the last
+// normalise's 1/max(|p|, 1e-12).
 __device__ __forceinline__ void nbr_ref_f64(double nx, double ny, double nz,
                                             double pix_x, double pix_y,
                                             double xs, double ys, double theta,
                                             double rx, double ry, double rz,
                                             double fu, double cu, double fv,
                                             double cv, double& ox, double& oy,
-                                            double& oz) {
+                                            double& oz, double& pinv) {
 #pragma clang fp contract(off)
     const double xyinv = 1.0 / smax(sqrt(xs * xs + ys * ys), 1e-12);
     xs *= xyinv;
@@ -203,6 +231,7 @@ __device__ __forceinline__ void nbr_ref_f64(double nx, double ny, double nz,
     ox = mx * minv;
     oy = my * minv;
     oz = mz * minv;
+    pinv = minv;
 }
 
 __device__ __forceinline__ int clampi(int v, int lo, int hi) {
@@ -235,7 +264,7 @@ struct AngmfArgs {
     int TW, TH, M, tiles_x, tiles_per_img;
     double ifu64, ifv64;  // 1/fu, 1/fv
     double tu_c, tv_c;    // (0.5 - cu)/fu, (0.5 - cv)/fv: source ray tu0 = sx/fu + tu_c
-    double dd_min;        // |dd| below this sends a pixel to the reference-order path
+    double dd_min;        // tier 1: |dd| below this sends a pixel to the recompute
     int synth_ray;        // form rays from the intrinsics (synth_ray), not from `ray`
 };
 
@@ -276,11 +305,11 @@ __global__ __launch_bounds__(256) void angmf_f64_kernel(AngmfArgs a) {
         const int sy = clampi(y - P + ky, 0, a.H - 1);
         const int sx = clampi(x - P + kx, 0, a.W - 1);
         const long long sp = (long long)sy * a.W + sx;
-        double mx, my, mz;
+        double mx, my, mz, pinv;
         nbr_ref_f64(pn[sp], pn[HW + sp], pn[2 * HW + sp], sx + 0.5, sy + 0.5,
                     xyp[(size_t)n * HW + p], xyp[(size_t)(K2 + n) * HW + p],
                     ap[(size_t)n * HW + p], rx, ry, rz, a.fu, a.cu, a.fv, a.cv,
-                    mx, my, mz);
+                    mx, my, mz, pinv);
         const double w = pr[(size_t)n * HW + p];
         acc0 += w * mx;
         acc1 += w * my;
@@ -423,31 +452,81 @@ __device__ __forceinline__ void sincos_small64(double t, double& st, double& ct)
     ct = fma(c, c, -(s * s));
 }
 
-// The source-normal halo of a tile, in LDS as four arrays of 16-byte records
-// (one per source pixel; consecutive lanes read consecutive records).
-struct Halo {
-    float4* m;    // mx, my, mz, 1/|m| = 1.5 - |m|^2/2
-    double2* gt;  // g = P0.m (NaN unless | |m|^2 - 1 | <= kUnitM2), tu0
-    double2* ab;  // mx/fu, my/fv
-    double2* gu;  // g/fu, g/fv
+// One neighbour in the double-precision reduced form (tier 2, the recompute
+// of pixels the fp32 tier flags): the axis as sign(dd) V/|V| and Rodrigues as
+// m' cos t + (V x m') sin t/|V| -- the identities the fp32 tier uses -- then
+// RayReLU and the normalise as src/dsine_ops.cpp:150-160 (|v| = 1).  Returns
+// false, leaving the outputs unset, for a neighbour outside the form's
+// domain: a non-unit or non-finite source normal, an xy pair outside
+// [kMinXY2, kMaxXY2], |t| > 3.2, |dd| < kDdClampRef, a degenerate V, or a
+// non-finite prob or ray; the caller then runs the reference-order body.
+// ir = 1/max(|r|, 1e-8); pinv as nbr_ref_f64's.
+__device__ __forceinline__ bool nbr_red_f64(float mxf, float myf, float mzf, int sx, int sy,
+                                            float xsf, float ysf, float tf, float wf, double rx,
+                                            double ry, double rz, double ir, const AngmfArgs& a,
+                                            double& ox, double& oy, double& oz, double& pinv) {
+    const double mx = mxf, my = myf, mz = mzf, xs = xsf, ys = ysf, t = tf;
+    const double m2 = fma(mx, mx, fma(my, my, mz * mz));
+    const double s = fma(xs, xs, ys * ys);
+    if (!(fabs(m2 - 1.0) <= (double)kUnitM2) || !(s >= (double)kMinXY2) ||
+        !(s <= (double)kMaxXY2) || !(fabs(t) <= 3.2) || !isfinite(wf) || !isfinite(rx) ||
+        !isfinite(ry) || !isfinite(rz))
+        return false;
+    const double tu0 = fma((double)sx, a.ifu64, a.tu_c);
+    const double tv0 = fma((double)sy, a.ifv64, a.tv_c);
+    const double g = fma(tu0, mx, fma(tv0, my, mz));
+    const double q = fma(xs * a.ifu64, mx, ys * a.ifv64 * my);
+    const double dd = fma(q, rsq64(s), g);
+    if (!(fabs(dd) >= kDdClampRef)) return false;
+    const double Vx = fma(g * a.ifu64, xs, -q * tu0);
+    const double Vy = fma(g * a.ifv64, ys, -q * tv0);
+    const double Vz = -q;
+    const double n2 = fma(Vx, Vx, fma(Vy, Vy, Vz * Vz));
+    if (!(n2 >= 1e-280)) return false;
+    double st, ct;
+    sincos_small64(t, st, ct);
+    const double im = rsq64(m2);
+    const double S = st * copysign(rsq64(n2), dd) * im, C = ct * im;
+    const double vx = fma(fma(Vy, mz, -Vz * my), S, mx * C);
+    const double vy = fma(fma(Vz, mx, -Vx * mz), S, my * C);
+    const double vz = fma(fma(Vx, my, -Vy * mx), S, mz * C);
+    const double cs = fma(vx, rx, fma(vy, ry, vz * rz)) * ir;
+    const double dcoef = (smax(cs - (double)kRayEpsF, 0.0) + (double)kRayEpsF) - cs;
+    const double px = fma(rx, dcoef, vx), py = fma(ry, dcoef, vy), pz = fma(rz, dcoef, vz);
+    const double p2 = fma(px, px, fma(py, py, pz * pz));
+    pinv = (p2 < 1e-24) ? 1e12 : rsq64(p2);
+    ox = px * pinv;
+    oy = py * pinv;
+    oz = pz * pinv;
+    return true;
+}
+
+// The source-normal halo of a tile in LDS: one 48-byte record per source
+// pixel of the tile's replicate-padded window, read with one address per
+// neighbour and immediate offsets.
+struct alignas(16) HaloRec {
+    float4 m;    // m' = m/|m| (1/|m| as 1.5 - |m|^2/2), g = P0.m (NaN unless m is a unit normal)
+    double2 ab;  // mx/fu, my/fv: q = xs mx/fu + ys my/fv is formed in double, since it
+                 // cancels where the xy pair is nearly perpendicular to m
+    float4 gt;   // g/fu, g/fv, tu0, tv0; P0 = (tu0, tv0, 1) is the source pixel's ray
 };
 
-// One halo record.  P0 = (tu0, tv0, 1) is the source pixel's ray at depth 1;
-// h indexes the replicate-padded halo whose record 0 is source pixel (y0, x0).
+// The record of halo slot h, whose slot 0 is source pixel (y0, x0).
 __device__ __forceinline__ void stage_halo(float mx, float my, float mz, int h, int hw, int y0,
                                            int x0, int H, int W, const AngmfArgs& a,
-                                           const Halo& hl) {
+                                           HaloRec* hl) {
     const int hr = small_div(h, __builtin_amdgcn_rcpf((float)hw)), hc = h - hr * hw;
     const int sy = clampi(y0 + hr, 0, H - 1), sx = clampi(x0 + hc, 0, W - 1);
     const double tu0 = fma((double)sx, a.ifu64, a.tu_c);
     const double tv0 = fma((double)sy, a.ifv64, a.tv_c);
     const float m2 = fmaf(mx, mx, fmaf(my, my, mz * mz));
+    const float im = fmaf(-0.5f, m2, 1.5f);
     const double g0 = fma(tu0, (double)mx, fma(tv0, (double)my, (double)mz));
     const double g = (fabsf(m2 - 1.0f) <= kUnitM2) ? g0 : __builtin_nan("");
-    hl.m[h] = make_float4(mx, my, mz, fmaf(-0.5f, m2, 1.5f));
-    hl.gt[h] = make_double2(g, tu0);
-    hl.ab[h] = make_double2((double)mx * a.ifu64, (double)my * a.ifv64);
-    hl.gu[h] = make_double2(g * a.ifu64, g * a.ifv64);
+    HaloRec& rec = hl[h];
+    rec.m = make_float4(mx * im, my * im, mz * im, (float)g);
+    rec.ab = make_double2((double)mx * a.ifu64, (double)my * a.ifv64);
+    rec.gt = make_float4((float)(g * a.ifu64), (float)(g * a.ifv64), (float)tu0, (float)tv0);
 }
 
 // Flagged pixels recomputed per pass and group (64 / PPR lanes per pixel).
@@ -474,20 +553,21 @@ __host__ __device__ inline int halo_count(int K, int TW, int TH) {
     return (TW + 2 * (K / 2)) * (TH + 2 * (K / 2));
 }
 
-// LDS records reserved per halo array: one spare.
+// LDS records reserved for the halo: one spare.
 __host__ __device__ inline int halo_slots(int K, int TW, int TH) { return halo_count(K, TW, TH) + 1; }
 
 // LDS of the fp32 kernel, in 16-byte units:
-//   smask[16]        u64 flagged-pixel mask per 64-pixel group (8 units)
-//   part[G][64*M]    per-wave partial (acc.xyz, sum wi^2 or NaN), 4 doubles
-//   halo.m, .gt, .ab, .gu [nhalo + 1]  source-pixel records (+ a spare)
-//   tvrow[TH + 2P]   source ray row term tv0 per halo row (doubles)
-//   fixp[M][G][PPR]  per-wave fp64 partial of a flagged pixel (3 doubles)
-//   rayl[64*M]       each tile pixel's ray, when formed from the intrinsics
+//   smask[16]          u64 per 64-pixel group (8 units): [0, 8) the pixels
+//                      tier 1 flags, [8, 16) those tier 2 hands to tier 3
+//   part[G][64*M]      per-wave fp32 partial (acc.xyz, sum wi^2 or NaN)
+//   halo[nhalo + 1]    source-pixel records (HaloRec, 3 units) + a spare
+//   fixp[M][G][PPR]    per-wave double partial of a recomputed pixel
+//                      (acc.xyz, sum wi^2: 2 units)
+//   rayl[64*M]         each tile pixel's ray, when formed from the intrinsics
 __host__ __device__ inline int lds_units(int K, int M, int TW, int TH, bool synth_ray) {
-    const int G = group_waves(K), nrow = TH + 2 * (K / 2);
-    return 8 + 2 * G * 64 * M + 4 * halo_slots(K, TW, TH) + (nrow + 1) / 2 +
-           (M * G * recompute_ppr(K) * 3 + 1) / 2 + (synth_ray ? 64 * M : 0);
+    const int G = group_waves(K);
+    return 8 + G * 64 * M + 3 * halo_slots(K, TW, TH) + 2 * M * G * recompute_ppr(K) +
+           (synth_ray ? 64 * M : 0);
 }
 
 // TW (< 2^11), TH (< 2^11) and M (< 2^5) of the fp32 kernel's tile and the
@@ -505,6 +585,20 @@ __host__ __device__ inline unsigned pack_tile(int TW, int TH, int M, int L) {
 // partials of a pixel meet in LDS.  Two workgroups per CU hold 4 waves per
 // SIMD, so the kernel may use 128 VGPRs and a 256x256 image still runs in
 // one round.
+//
+// Three tiers of arithmetic:
+//   1. every pixel (this wave's run, one neighbour per iteration):
+//      q = xs mx/fu + ys my/fv in double, rounded once; dd, V, |V|, sin/cos,
+//      the rotation, RayReLU, the weight prob/|p| and the partial sums in
+//      fp32.  A pixel is flagged when a neighbour leaves
+//      the domain (xy range, |t| > 3.2, |dd| < dd_min, a non-unit source
+//      normal, |V|^2 < kMinV2, anything non-finite) or when |acc|^2 <
+//      kAccRatio2 * sum(wi^2);
+//   2. flagged pixels, the same reduced form in double (nbr_red_f64), one
+//      neighbour per lane; a pixel with a neighbour outside the double
+//      form's domain, or whose double sum still nearly cancels, goes on to
+//   3. the reference-order body (nbr_ref_f64) for all its neighbours.
+// On the 256x256 bench input no pixel reaches tier 2.
 //
 // Everything the first loads' addresses depend on comes first in the
 // argument list, as scalars: gfx950 preloads up to 14 dwords of kernel
@@ -535,18 +629,12 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     const int npx = 64 * M;
     const int nrow = TH + 2 * P;
     unsigned long long* smask = reinterpret_cast<unsigned long long*>(smem);
-    double4* part = reinterpret_cast<double4*>(smem + 8);
+    float4* part = smem + 8;
     const int nslot = halo_slots(K, TW, TH);
-    Halo hl;
-    hl.m = reinterpret_cast<float4*>(part + G * npx);
-    hl.gt = reinterpret_cast<double2*>(hl.m + nslot);
-    hl.ab = hl.gt + nslot;
-    hl.gu = hl.ab + nslot;
-    double* tvrow = reinterpret_cast<double*>(hl.gu + nslot);
-    double* fixp = tvrow + 2 * ((nrow + 1) / 2);
-    // (SR) the tile pixels' rays, after fixp (M*G*PPR*3 doubles, rounded up
-    // to 16 bytes)
-    float4* rayl = reinterpret_cast<float4*>(fixp + 2 * ((M * G * PPR * 3 + 1) / 2));
+    HaloRec* hl = reinterpret_cast<HaloRec*>(part + G * npx);
+    double* fixp = reinterpret_cast<double*>(hl + nslot);
+    // (SR) the tile pixels' rays, after fixp
+    float4* rayl = reinterpret_cast<float4*>(fixp + M * G * PPR * 4);
 
     const int b = blockIdx.y;
     const int lb = xcd_remap(blockIdx.x, tiles_per_img);
@@ -572,8 +660,8 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
 
     // ---- staging: the tile's source normals, with what depends on them only
     // The (TH + 2P) x (TW + 2P) replicate-padded halo of pred_norm, one LDS
-    // record per source pixel (Halo), at most two per thread.  Their loads are
-    // each lane's first, so waiting for them waits for nothing else.
+    // record per source pixel (HaloRec), at most two per thread.  Their loads
+    // are each lane's first, so waiting for them waits for nothing else.
     const int hw = TW + 2 * P, nhalo = hw * nrow;
     const int nthr = 64 * M * G;
     const float rhw = __builtin_amdgcn_rcpf((float)hw);
@@ -643,9 +731,7 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
                        ty0 - P, tx0 - P, H, W, a, hl);
         }
     }
-    // the source pixels' ray row per halo row: ((sy + 0.5) - cv) / fv
-    if ((int)threadIdx.x < nrow)
-        tvrow[threadIdx.x] = fma((double)clampi(ty0 - P + (int)threadIdx.x, 0, H - 1), a.ifv64, a.tv_c);
+    if ((int)threadIdx.x < 8) smask[8 + threadIdx.x] = 0ull;
     if constexpr (SR) {
         // each tile pixel's ray, once (pixels past the image: clamped ones)
         if ((int)threadIdx.x < npx) {
@@ -666,14 +752,15 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
 #pragma unroll
     for (int i = PRE; i < NR; ++i) load_planes(i);
     {
-        const double rx = rxf, ry = ryf, rz = rzf;
         // cos(v', r) = v'.r / max(|v'||r|, 1e-8) with |v'| = 1
-        const double r2 = fma(rx, rx, fma(ry, ry, rz * rz));
-        const double ir = (r2 < 1e-16) ? 1e8 : rsq64_1(r2);
+        const float r2 = fmaf(rxf, rxf, fmaf(ryf, ryf, rzf * rzf));
+        const float ir = (r2 < 1e-16f) ? 1e8f : __builtin_amdgcn_rsqf(r2);
+        const float rhx = rxf * ir, rhy = ryf * ir, rhz = rzf * ir;
+        const float dd_min = (float)a.dd_min;
         // this lane's window in the halo (lanes past the tile use its last row)
         const int hrow = (ty < TH) ? ty : TH - 1;
-        const int hbase = hrow * hw + tx;
-        double acc0 = 0.0, acc1 = 0.0, acc2 = 0.0;
+        const char* hbase = reinterpret_cast<const char*>(hl + hrow * hw + tx);
+        float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f;
         float qs = 0.0f;  // sum of wi^2, for the cancellation test only
         bool bad = false;
 #pragma unroll
@@ -681,51 +768,46 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
             if (i == NR - 1 && nrun != NR) break;
             const int n = n0 + i;
             const int ky = n / K, kx = n - ky * K;
-            const int h = hbase + ky * hw + kx;
-            const float4 hm = hl.m[h];
-            const double2 gt = hl.gt[h], ab = hl.ab[h], gu = hl.gu[h];
-            const double tv0 = tvrow[hrow + ky];
-            const float mx = hm.x, my = hm.y, mz = hm.z, im = hm.w;
-            const double xsd = xs[i], ysd = ys[i];
-            const float t = th[i];
-            // q = D.m = xs mx/fu + ys my/fv and dd = g + q/|xy| in double: exact
-            // products of the fp32 inputs keep their relative precision where
-            // they cancel (a surface edge-on to the rays), and so does V below.
-            // dd is formed from the raw normal as the reference forms it; its
-            // 1/|xy| comes from the fp32 |xy|^2 and rsq, which dd_min covers.
-            const double q = fma(xsd, ab.x, ysd * ab.y);
-            const float s = fmaf(xs[i], xs[i], ys[i] * ys[i]);
-            const double dd = fma((double)__builtin_amdgcn_rsqf(s), q, gt.x);
-            bad |= (__builtin_bit_cast(uint32_t, s) - kXY2Lo > kXY2Span) | !(fabsf(t) <= 3.2f) |
-                   !(fabs(dd) >= a.dd_min);
+            const HaloRec& rec = *reinterpret_cast<const HaloRec*>(
+                hbase + (ky * hw + kx) * (int)sizeof(HaloRec));
+            const float4 hm = rec.m, gt = rec.gt;
+            const double2 ab = rec.ab;
+            const float xv = xs[i], yv = ys[i], t = th[i];
+            // q in double (exact products, one rounding), the rest fp32;
+            // dd = g + q/|xy| is formed from the raw normal as the reference
+            // forms it, with 1/|xy| from the fp32 |xy|^2 and rsq (dd_min
+            // covers their error)
+            const float q = (float)fma((double)xv, ab.x, (double)yv * ab.y);
+            const float s = fmaf(xv, xv, yv * yv);
+            const float dd = fmaf(q, __builtin_amdgcn_rsqf(s), hm.w);
             // axis = sign(dd) V/|V|, V = (g xs/fu - q tu0, g ys/fv - q tv0, -q) = m x N;
-            // v' = m' cos t + (V x m') sin t/|V|, m' = m/|m|
-            const float Vx = (float)fma(gu.x, xsd, -q * gt.y);
-            const float Vy = (float)fma(gu.y, ysd, -q * tv0);
-            const float Vz = (float)(-q);
-            const float n2 = fmaf(Vx, Vx, fmaf(Vy, Vy, Vz * Vz));
-            float ia = __builtin_amdgcn_rsqf(n2);
-            ia = fmaf(0.5f * ia, fmaf(-n2 * ia, ia, 1.0f), ia);
+            // v' = m' cos t + (V x m') sin t/|V|
+            const float Vx = fmaf(gt.x, xv, -q * gt.z);
+            const float Vy = fmaf(gt.y, yv, -q * gt.w);
+            const float n2 = fmaf(Vx, Vx, fmaf(Vy, Vy, q * q));
+            bad |= (__builtin_bit_cast(uint32_t, s) - kXY2Lo > kXY2Span) | !(fabsf(t) <= 3.2f) |
+                   !(fabsf(dd) >= dd_min) | !(n2 >= kMinV2);
             float st, ct;
             sincos_small(t, st, ct);
-            const float S = st * copysignf(ia, (float)dd) * im, C = ct * im;
-            const float vx = fmaf(fmaf(Vy, mz, -Vz * my), S, mx * C);
-            const float vy = fmaf(fmaf(Vz, mx, -Vx * mz), S, my * C);
-            const float vz = fmaf(fmaf(Vx, my, -Vy * mx), S, mz * C);
-            // RayReLU, the unit term and its weight in double: p = v' + r dc
-            // cancels where v' faces away from the ray, and the sum can cancel
-            const double vxd = vx, vyd = vy, vzd = vz;
-            const double cs = fma(vxd, rx, fma(vyd, ry, vzd * rz)) * ir;
-            const double dc = fmax((double)kRayEpsF - cs, 0.0);
-            const double px = fma(rx, dc, vxd), py = fma(ry, dc, vyd), pz = fma(rz, dc, vzd);
-            const double wi = (double)wt[i] * rsq64_1(fma(px, px, fma(py, py, pz * pz)));
-            acc0 = fma(px, wi, acc0);
-            acc1 = fma(py, wi, acc1);
-            acc2 = fma(pz, wi, acc2);
-            const float wf = (float)wi;
-            qs = fmaf(wf, wf, qs);
+            const float S = st * copysignf(__builtin_amdgcn_rsqf(n2), dd);
+            // V x m' with Vz = -q
+            const float cx = fmaf(Vy, hm.z, q * hm.y);
+            const float cy = -fmaf(q, hm.x, Vx * hm.z);
+            const float cz = fmaf(Vx, hm.y, -Vy * hm.x);
+            const float vx = fmaf(cx, S, hm.x * ct);
+            const float vy = fmaf(cy, S, hm.y * ct);
+            const float vz = fmaf(cz, S, hm.z * ct);
+            // RayReLU: p = v' + r max(eps - cos, 0), then the weight prob/|p|
+            const float cs = fmaf(vx, rhx, fmaf(vy, rhy, vz * rhz));
+            const float dc = fmaxf(kRayEpsF - cs, 0.0f);
+            const float px = fmaf(rxf, dc, vx), py = fmaf(ryf, dc, vy), pz = fmaf(rzf, dc, vz);
+            const float wi = wt[i] * __builtin_amdgcn_rsqf(fmaf(px, px, fmaf(py, py, pz * pz)));
+            acc0 = fmaf(px, wi, acc0);
+            acc1 = fmaf(py, wi, acc1);
+            acc2 = fmaf(pz, wi, acc2);
+            qs = fmaf(wi, wi, qs);
         }
-        part[r * npx + j] = make_double4(acc0, acc1, acc2, bad ? __builtin_nan("") : (double)qs);
+        part[r * npx + j] = make_float4(acc0, acc1, acc2, bad ? __builtin_nanf("") : qs);
     }
     __syncthreads();
 
@@ -733,25 +815,25 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     if (r == 0) {
         bool flag = false;
         if (valid) {
-            double4 sm = part[j];
+            double s0 = 0.0, s1 = 0.0, s2 = 0.0, sw = 0.0;
 #pragma unroll
-            for (int rr = 1; rr < G; ++rr) {
-                const double4 t = part[rr * npx + j];
-                sm.x += t.x;
-                sm.y += t.y;
-                sm.z += t.z;
-                sm.w += t.w;
+            for (int rr = 0; rr < G; ++rr) {
+                const float4 t = part[rr * npx + j];
+                s0 += t.x;
+                s1 += t.y;
+                s2 += t.z;
+                sw += t.w;
             }
-            const double a2 = fma(sm.x, sm.x, fma(sm.y, sm.y, sm.z * sm.z));
+            const double a2 = fma(s0, s0, fma(s1, s1, s2 * s2));
             // 1 / max(|acc|, 1e-12) as the reference; a non-finite or
-            // cancelled sum goes to the reference-order recompute
-            flag = !(a2 >= kAccRatio2 * sm.w) || !(a2 <= 1e300);
+            // cancelled sum goes to the recompute
+            flag = !(a2 >= kAccRatio2 * sw) || !(a2 <= 1e300);
             if (!flag) {
                 const double inv = (a2 < 1e-24) ? 1e12 : rsq64_1(a2);
                 float* op = a.out + (size_t)b * 3 * HW;
-                stf(op, pb, (float)(sm.x * inv));
-                stf(op + HW, pb, (float)(sm.y * inv));
-                stf(op + 2 * HW, pb, (float)(sm.z * inv));
+                stf(op, pb, (float)(s0 * inv));
+                stf(op + HW, pb, (float)(s1 * inv));
+                stf(op + 2 * HW, pb, (float)(s2 * inv));
             }
         }
         const unsigned long long m = __ballot(flag);
@@ -759,19 +841,15 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     }
     __syncthreads();
 
-    // ---- phase C: reference-order recompute of flagged pixels --------------
+    // ---- phase C: recompute flagged pixels (tier 2, then tier 3) -----------
     int maxc = 0;
     for (int g = 0; g < M; ++g) {
         const int c = __popcll(uniform64(smask[g]));
         maxc = c > maxc ? c : maxc;
     }
     if (maxc == 0) return;
-    // Phase C forms its per-lane values afresh: shared with phase A they
-    // would stay live across its loads and spill.
     int tid = threadIdx.x, tw = TW;
     asm volatile("" : "+v"(tid), "+s"(tw));
-    const unsigned long long gmask = uniform64(smask[gi]);
-    const int cnt = __popcll(gmask);
     const float* pn = pred_norm + (size_t)b * 3 * HW;
     const float* pr = prob + (size_t)b * K2 * HW;
     const float* xyp = xy + (size_t)b * 2 * K2 * HW;
@@ -779,91 +857,132 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     const float* rp = SR ? nullptr : a.ray + (size_t)b * a.ray_bstride;
     float* op = a.out + (size_t)b * 3 * HW;
     // Each wave (group, run) evaluates its run's neighbours of up to PPR
-    // flagged pixels of its group per pass, LPG lanes per pixel, one
-    // neighbour per lane at a time (inputs re-read; the block has just read
-    // them, so from L2); run partials meet in LDS and wave r == 0 of the
-    // group writes the pixel.
+    // pixels of its group per pass, LPG lanes per pixel, one neighbour per
+    // lane at a time; run partials meet in LDS and wave r == 0 of the group
+    // writes the pixel -- or, in tier 2, hands it to tier 3.  Inputs are
+    // re-read (the block has just read them, so from L2).  Pass counts come
+    // from LDS after a barrier, so every wave of the block runs the same
+    // barriers.
     const int clane = tid & 63;
     const int slot = clane / LPG, il = clane - slot * LPG;
-    unsigned long long rest = gmask;
-    for (int base = 0; base < maxc; base += PPR) {
-        int src = 0, fin_src = 0;
-#pragma unroll
-        for (int sidx = 0; sidx < PPR; ++sidx) {
-            const int bitpos = rest ? __ffsll((long long)rest) - 1 : 0;
-            if (rest) rest &= rest - 1;
-            if (sidx == slot) src = bitpos;
-            if (sidx == clane) fin_src = bitpos;
+    // One tier over the pixels of mask slot `mo` of smask; TIER is 2 or 3.
+    auto recompute = [&](auto tier_tag, int mo) {
+        constexpr int TIER = decltype(tier_tag)::value;
+        int maxt = 0;
+        for (int g = 0; g < M; ++g) {
+            const int c = __popcll(uniform64(smask[mo + g]));
+            maxt = c > maxt ? c : maxt;
         }
-        double p0 = 0.0, p1 = 0.0, p2 = 0.0;
-        if ((base + slot) < cnt) {
+        const unsigned long long gmask = uniform64(smask[mo + gi]);
+        const int cnt = __popcll(gmask);
+        unsigned long long rest = gmask;
+        for (int base = 0; base < maxt; base += PPR) {
+            int src = 0, fin_src = 0;
+#pragma unroll
+            for (int sidx = 0; sidx < PPR; ++sidx) {
+                const int bitpos = rest ? __ffsll((long long)rest) - 1 : 0;
+                if (rest) rest &= rest - 1;
+                if (sidx == slot) src = bitpos;
+                if (sidx == clane) fin_src = bitpos;
+            }
+            const bool act = (base + slot) < cnt;
             const int jj = gi * 64 + src;
             const int fty = jj / tw, ftx = jj - fty * tw;
             const int fy = ty0 + fty, fx = tx0 + ftx;
             const uint32_t fb = (uint32_t)(fy * W + fx) * 4u;
-            for (int i = il; i < nrun; i += LPG) {
-                const int n = n0 + i;
-                const int ky = n / K, kx = n - ky * K;
-                const int fsy = clampi(fy - P + ky, 0, H - 1);
-                const int fsx = clampi(fx - P + kx, 0, W - 1);
-                const uint32_t sb = (uint32_t)(fsy * W + fsx) * 4u;
-                const float mx = ldf(pn, sb), my = ldf(pn + HW, sb), mz = ldf(pn + 2 * HW, sb);
-                const float xsv = ldf(xyp + (size_t)n * HW, fb);
-                const float ysv = ldf(xyp + (size_t)(K2 + n) * HW, fb);
-                const float thv = ldf(ap + (size_t)n * HW, fb), wv = ldf(pr + (size_t)n * HW, fb);
+            double p0 = 0.0, p1 = 0.0, p2 = 0.0, q2 = 0.0;
+            if (act) {
                 float frx, fry, frz;
                 if constexpr (SR) {
-                    const float3 r = synth_ray(fx, fy, a.fu, a.cu, a.fv, a.cv);
-                    frx = r.x;
-                    fry = r.y;
-                    frz = r.z;
+                    const float3 rr3 = synth_ray(fx, fy, a.fu, a.cu, a.fv, a.cv);
+                    frx = rr3.x;
+                    fry = rr3.y;
+                    frz = rr3.z;
                 } else {
                     frx = ldf(rp, fb);
                     fry = ldf(rp + HW, fb);
                     frz = ldf(rp + 2 * HW, fb);
                 }
-                double ox, oy, oz;
-                nbr_ref_f64(mx, my, mz, fsx + 0.5, fsy + 0.5, xsv, ysv, thv, frx, fry, frz, a.fu,
-                            a.cu, a.fv, a.cv, ox, oy, oz);
-                const double w = wv;
-                p0 += w * ox;
-                p1 += w * oy;
-                p2 += w * oz;
+                for (int i = il; i < nrun; i += LPG) {
+                    const int n = n0 + i;
+                    const int ky = n / K, kx = n - ky * K;
+                    const int fsy = clampi(fy - P + ky, 0, H - 1);
+                    const int fsx = clampi(fx - P + kx, 0, W - 1);
+                    const uint32_t sb = (uint32_t)(fsy * W + fsx) * 4u;
+                    const float mx = ldf(pn, sb), my = ldf(pn + HW, sb), mz = ldf(pn + 2 * HW, sb);
+                    const float xsv = ldf(xyp + (size_t)n * HW, fb);
+                    const float ysv = ldf(xyp + (size_t)(K2 + n) * HW, fb);
+                    const float thv = ldf(ap + (size_t)n * HW, fb), wv = ldf(pr + (size_t)n * HW, fb);
+                    double ox, oy, oz, pinv;
+                    if constexpr (TIER == 2) {
+                        const double rxd = frx, ryd = fry, rzd = frz;
+                        const double ird =
+                            1.0 / smax(sqrt(fma(rxd, rxd, fma(ryd, ryd, rzd * rzd))), 1e-8);
+                        // outside the reduced form's domain: the pixel goes to tier 3
+                        if (!nbr_red_f64(mx, my, mz, fsx, fsy, xsv, ysv, thv, wv, rxd, ryd, rzd,
+                                         ird, a, ox, oy, oz, pinv)) {
+                            q2 = __builtin_nan("");
+                            continue;
+                        }
+                    } else {
+                        nbr_ref_f64(mx, my, mz, fsx + 0.5, fsy + 0.5, xsv, ysv, thv, frx, fry, frz,
+                                    a.fu, a.cu, a.fv, a.cv, ox, oy, oz, pinv);
+                    }
+                    const double w = wv;
+                    p0 += w * ox;
+                    p1 += w * oy;
+                    p2 += w * oz;
+                    const double wi = w * pinv;
+                    q2 = fma(wi, wi, q2);
+                }
             }
-        }
 #pragma unroll
-        for (int off = LPG / 2; off > 0; off >>= 1) {
-            p0 += __shfl_xor(p0, off, 64);
-            p1 += __shfl_xor(p1, off, 64);
-            p2 += __shfl_xor(p2, off, 64);
-        }
-        if (il == 0 && (base + slot) < cnt) {
-            double* f = fixp + ((gi * G + r) * PPR + slot) * 3;
-            f[0] = p0;
-            f[1] = p1;
-            f[2] = p2;
-        }
-        __syncthreads();
-        if (r == 0 && clane < PPR && base + clane < cnt) {
-            double a0 = 0.0, a1 = 0.0, a2 = 0.0;
-            for (int rr = 0; rr < G; ++rr) {
-                const double* f = fixp + ((gi * G + rr) * PPR + clane) * 3;
-                a0 += f[0];
-                a1 += f[1];
-                a2 += f[2];
+            for (int off = LPG / 2; off > 0; off >>= 1) {
+                p0 += __shfl_xor(p0, off, 64);
+                p1 += __shfl_xor(p1, off, 64);
+                p2 += __shfl_xor(p2, off, 64);
+                q2 += __shfl_xor(q2, off, 64);
             }
-            // 1 / max(|acc|, 1e-12), with the reference's NaN and Inf results
-            const double n2 = a0 * a0 + a1 * a1 + a2 * a2;
-            const double inv = (n2 < 1e-24) ? 1e12 : (n2 == INFINITY ? 0.0 : rsq64(n2));
-            const int jj = gi * 64 + fin_src;
-            const int fty = jj / tw, ftx = jj - fty * tw;
-            const uint32_t fb = (uint32_t)((ty0 + fty) * W + tx0 + ftx) * 4u;
-            stf(op, fb, (float)(a0 * inv));
-            stf(op + HW, fb, (float)(a1 * inv));
-            stf(op + 2 * HW, fb, (float)(a2 * inv));
+            if (il == 0 && act) {
+                double* f = fixp + ((gi * G + r) * PPR + slot) * 4;
+                f[0] = p0;
+                f[1] = p1;
+                f[2] = p2;
+                f[3] = q2;
+            }
+            __syncthreads();
+            if (r == 0 && clane < PPR && base + clane < cnt) {
+                double a0 = 0.0, a1 = 0.0, a2 = 0.0, aq = 0.0;
+                for (int rr = 0; rr < G; ++rr) {
+                    const double* f = fixp + ((gi * G + rr) * PPR + clane) * 4;
+                    a0 += f[0];
+                    a1 += f[1];
+                    a2 += f[2];
+                    aq += f[3];
+                }
+                const double n2 = a0 * a0 + a1 * a1 + a2 * a2;
+                // tier 2 hands on a pixel with a neighbour outside its domain
+                // (aq NaN) or a sum that nearly cancels
+                if (TIER == 2 &&
+                    (!(n2 >= kAccRatio2Ref * aq) || !(n2 >= kAcc2Floor) || !(n2 <= 1e300))) {
+                    atomicOr(&smask[8 + gi], 1ull << fin_src);
+                } else {
+                    // 1 / max(|acc|, 1e-12), with the reference's NaN and Inf results
+                    const double inv =
+                        (n2 < 1e-24) ? 1e12 : (n2 == INFINITY ? 0.0 : rsq64(n2));
+                    const int jw = gi * 64 + fin_src;
+                    const int wty = jw / tw, wtx = jw - wty * tw;
+                    const uint32_t wb = (uint32_t)((ty0 + wty) * W + tx0 + wtx) * 4u;
+                    stf(op, wb, (float)(a0 * inv));
+                    stf(op + HW, wb, (float)(a1 * inv));
+                    stf(op + 2 * HW, wb, (float)(a2 * inv));
+                }
+            }
+            __syncthreads();
         }
-        __syncthreads();
-    }
+    };
+    recompute(std::integral_constant<int, 2>{}, 0);
+    recompute(std::integral_constant<int, 3>{}, 8);
 }
 
 // ---------------------------------------------------------------------------
@@ -1098,7 +1217,16 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
     a.ifv64 = 1.0 / fv;
     a.tu_c = (0.5 - cu) / fu;
     a.tv_c = (0.5 - cv) / fv;
-    a.dd_min = kDdClamp + 3e-7 / std::fmin(std::fabs(fu), std::fabs(fv));
+    // gmax: the largest |P0| over the image's pixel centres (at a corner),
+    // times the largest |m| the fast path accepts
+    double gmax = 0.0;
+    for (const int cy : {0, H - 1})
+        for (const int cx : {0, W - 1}) {
+            const double tu = (cx + 0.5 - cu) / fu, tv = (cy + 0.5 - cv) / fv;
+            gmax = std::fmax(gmax, std::sqrt(1.0 + tu * tu + tv * tv));
+        }
+    gmax *= std::sqrt(1.0 + (double)kUnitM2);
+    a.dd_min = kDdClamp + 1e-7 * gmax + 3e-7 / std::fmin(std::fabs(fu), std::fabs(fv));
     a.synth_ray = synth ? 1 : 0;
     choose_tile(a, k);
     if (!tile_fits(k, a.M, a.TW, a.TH, synth))
@@ -1114,7 +1242,7 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
     const bool sane = std::isfinite(fu) && std::isfinite(fv) && std::isfinite(cu) &&
                       std::isfinite(cv) && std::fabs(fu) >= 1e-3 && std::fabs(fu) <= 1e7 &&
                       std::fabs(fv) >= 1e-3 && std::fabs(fv) <= 1e7 &&
-                      std::fabs(cu) <= 1e7 && std::fabs(cv) <= 1e7;
+                      std::fabs(cu) <= 1e7 && std::fabs(cv) <= 1e7 && gmax <= kMaxP0;
     // The fp32 kernel addresses a wave's run of neighbour planes (and the 3
     // planes of pred_norm and ray) from one 32-bit buffer offset, and its grid
     // holds one image's tiles in x; larger images also run the
