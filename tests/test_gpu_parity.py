@@ -231,6 +231,77 @@ def test_angmf_large_angles_and_cancellation(cuda):
     assert max_abs <= TOL_ABS and max_deg <= TOL_DEG
 
 
+def _cancel_count(inp, H, W, k, thresh):
+    """Pixels whose prob-weighted sum nearly cancels: |acc|^2 < thresh *
+    sum(prob^2), acc from the independent restatement.  sum(wi^2) >= sum(prob^2),
+    so each of them is below the fast path's own |acc|^2 / sum(wi^2) test."""
+    from tests.golden import independent as ind
+    B = inp["pred_norm"].shape[0]
+    shp = lambda a, c: np.asarray(a).reshape(-1, c, H, W)
+    _, acc = ind.refine_step(shp(inp["pred_norm"], 3), shp(inp["prob"], k * k),
+                             shp(inp["xy"], 2 * k * k), shp(inp["angle"], k * k),
+                             shp(inp["ray"], 3), inp["intrinsics"], k)
+    a2 = (acc ** 2).sum(axis=1)
+    p2 = (shp(inp["prob"], k * k).astype(np.float64) ** 2).sum(axis=1)
+    return int((a2 < thresh * p2).sum())
+
+
+@pytest.mark.parametrize("far_angles", [False, True])
+def test_angmf_recompute_tiers(cuda, far_angles):
+    """Sums that nearly cancel, by construction: normals +-x alternating
+    column by column, prob 1 on two horizontally adjacent slots (opposite
+    normals) and 0 elsewhere, small angles.  Near the principal column both
+    terms are RayReLU-clamped to ~ +-x + eps*r, so |acc|^2 / sum(wi^2) ~ 2e-4:
+    tier 1 flags those pixels and tier 2 (the reduced form in double)
+    recomputes them.  With far_angles a zero-prob slot of every pixel gets an
+    angle of 5 rad, outside tier 2's domain, so every flagged pixel goes on
+    to tier 3 (the reference-order body)."""
+    H, W, k = 24, 64, 5
+    K2 = k * k
+    say(f"[gpu] angmf recompute tiers far_angles={far_angles}")
+    rng = np.random.default_rng(21 + far_angles)
+    inp = _random_inputs(rng, 1, H, W, k)
+    pn = np.zeros((3, H, W), np.float32)
+    pn[0] = 1.0
+    pn[:, :, 1::2] *= -1
+    inp["pred_norm"] = pn.reshape(1, 3, H * W)
+    prob = np.zeros((1, K2, H * W), np.float32)
+    prob[0, 2 * k + 2] = 0.8      # the pixel itself
+    prob[0, 2 * k + 3] = 0.8      # its right-hand neighbour: the opposite normal
+    inp["prob"] = prob
+    inp["angle"] = rng.normal(0.0, 1e-3, inp["angle"].shape).astype(np.float32)
+    if far_angles:
+        inp["angle"][0, 0] = 5.0  # slot 0 has prob 0
+    n_cancel = _cancel_count(inp, H, W, k, 1.6e-3)
+    say(f"    pixels below the fast path's cancellation threshold: >= {n_cancel}")
+    assert n_cancel >= 2 * H
+    got = run_gpu(inp, H, W, cuda)
+    want = run_oracle(inp, H, W, k)
+    max_abs, max_deg, nan_mm = compare(got.reshape(1, 3, -1), want.reshape(1, 3, -1))
+    say(f"    max-abs {max_abs:.3e}  max-angle {max_deg:.3e} deg")
+    assert nan_mm == 0
+    assert max_abs <= TOL_ABS and max_deg <= TOL_DEG
+
+
+@pytest.mark.parametrize("fov", [100.0, 140.0, 170.0])
+def test_angmf_wide_fields_of_view(cuda, fov):
+    """The fp32 path's error bound holds up to |P0| = 4 over the image (about
+    150 degrees diagonally); a 170-degree view runs the double kernel."""
+    H, W, k = 40, 40, 5
+    say(f"[gpu] angmf field of view {fov}")
+    rng = np.random.default_rng(int(fov))
+    inp = _random_inputs(rng, 1, H, W, k)
+    intr = wl.intrins_from_fov(8 * H, 8 * W, fov)
+    inp["intrinsics"] = wl.scaled_intrinsics(intr, H, W, 8 * H, 8 * W)
+    inp["ray"] = wl.build_ray8(intr, H, W, 8 * H, 8 * W).reshape(3, H * W)
+    got = run_gpu(inp, H, W, cuda)
+    want = run_oracle(inp, H, W, k)
+    max_abs, max_deg, nan_mm = compare(got.reshape(1, 3, -1), want.reshape(1, 3, -1))
+    say(f"    max-abs {max_abs:.3e}  max-angle {max_deg:.3e} deg")
+    assert nan_mm == 0
+    assert max_abs <= TOL_ABS and max_deg <= TOL_DEG
+
+
 def test_angmf_odd_intrinsics_use_fp64(cuda):
     """Intrinsics outside the fp32 path's range run the double kernel."""
     H, W, k = 9, 11, 3
