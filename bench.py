@@ -228,6 +228,16 @@ def bench_angmf(args, dev) -> dict:
     if args.ray_from_intrinsics:
         flags |= _lib.RAY_FROM_INTRINSICS
         bytes_per_call -= 3 * w.HW * 4  # the shared ray's 3 planes are not read
+    cpu_inp = inp  # the CPU leg always runs the op on activated planes
+    if args.logits:
+        # the heads' raw logits: the prob planes' logits and the angle
+        # planes' logits of angle / pi, so the activations give back the
+        # workload's own planes
+        flags |= _lib.LOGITS
+        inp = dict(inp)
+        for key, scale in (("prob", 1.0), ("angle", np.pi)):
+            q = np.clip(inp[key].astype(np.float64) / scale, 1e-6, 1 - 1e-6)
+            inp[key] = np.log(q / (1.0 - q)).astype(np.float32)
     nsets = args.sets or max(2, int(np.ceil(512e6 / bytes_per_call)))
 
     base = {key: torch.from_numpy(np.ascontiguousarray(inp[key])).to(dev)
@@ -263,6 +273,7 @@ def bench_angmf(args, dev) -> dict:
         {
             "workload": w.name, "B": B, "H": H, "W": W, "k": k, "calls_per_step": w.calls,
             "ray": "from-intrinsics" if args.ray_from_intrinsics else "shared",
+            "prob_angle": "logits, activated in the kernel" if args.logits else "activated",
             "inputs": f"{nsets} rotating HBM-resident copies "
                       f"({nsets * bytes_per_call / 1e6:.0f} MB > 256 MB Infinity Cache)",
         })
@@ -282,11 +293,42 @@ def bench_angmf(args, dev) -> dict:
     }
     line["gpu"] = torch.cuda.get_device_name(dev)
 
+    if args.logits:
+        # the unfused step for comparison: the refiner's two activation
+        # passes (here torch's sigmoid kernels) over the same rotating
+        # logits, then the op on the activated planes
+        acts = [(torch.empty_like(s_["prob"]), torch.empty_like(s_["angle"])) for s_ in sets]
+        kpi = float(np.float32(np.pi))
+
+        def launch_unfused(i: int) -> None:
+            s_ = sets[i]
+            ap_, aa_ = acts[i]
+            torch.sigmoid(s_["prob"], out=ap_)
+            torch.sigmoid(s_["angle"], out=aa_)
+            aa_.mul_(kpi)
+            sptr = torch.cuda.current_stream(dev).cuda_stream
+            st = _lib.angmf_propagate_f32(
+                s_["pred_norm"].data_ptr(), ap_.data_ptr(), s_["xy"].data_ptr(), aa_.data_ptr(),
+                0 if args.ray_from_intrinsics else s_["ray"].data_ptr(), fu, cu, fv, cv, B, H,
+                W, k, 0, outs[i].data_ptr(), flags & ~_lib.LOGITS, sptr)
+            if st != 0:
+                raise RuntimeError(f"angmf_propagate_f32 failed: {st} {_lib.last_error()}")
+
+        tu = Timer(dev, launch_unfused, nsets, args.steps, args.warmup, bytes_per_call)
+        g_u = tu.capture(True)
+        g_u.replay()
+        t_unfused = tu.timed_graph(g_u)
+        line["unfused"] = {
+            "us_per_step": round(t_unfused / args.steps * 1e6, 3),
+            "note": "torch sigmoid on the prob logits, sigmoid and * pi on the angle logits, "
+                    "then the op on the activated planes; same rotating inputs, one graph",
+        }
+
     if not args.no_cpu:
         def cpu_pass(nt):
             return lambda: oracle.angmf_propagate(
-                inp["pred_norm"], inp["prob"], inp["xy"], inp["angle"], inp["ray"],
-                inp["intrinsics"], H, W, k, nthreads=nt)
+                cpu_inp["pred_norm"], cpu_inp["prob"], cpu_inp["xy"], cpu_inp["angle"],
+                cpu_inp["ray"], cpu_inp["intrinsics"], H, W, k, nthreads=nt)
 
         passes, el = timed_cpu(cpu_pass(1), args.cpu_seconds)
         line["cpu_baseline"] = {
@@ -412,6 +454,9 @@ def main() -> int:
     ap.add_argument("--ray-from-intrinsics", action="store_true",
                     help="angmf: form each pixel's ray from fu, cu, fv, cv in the kernel "
                          "(BVML_DSINE_RAY_FROM_INTRINSICS) instead of reading the ray planes")
+    ap.add_argument("--logits", action="store_true",
+                    help="angmf: prob and angle hold the heads' raw logits and the kernel applies "
+                         "the activations (BVML_DSINE_LOGITS); also times the unfused step")
     ap.add_argument("--precise", action="store_true",
                     help="upsample: the double-precision kernel (BVML_DSINE_FP64)")
     ap.add_argument("--calib", action="store_true",

@@ -24,6 +24,7 @@ EUNSUP = -8
 DEFAULT = 0
 FP64 = 1
 RAY_FROM_INTRINSICS = 2
+LOGITS = 4
 
 # Every symbol include/bvml_dsine.h declares.
 EXPORTS = (

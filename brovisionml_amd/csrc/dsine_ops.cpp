@@ -43,9 +43,11 @@ void ray_relu_gpu(Tensor& normal, const Tensor& ray, int H, int W) {
     if (st != BVML_DSINE_OK) fail_hip("ray_relu launch", st);
 }
 
-void angmf_propagate_gpu(const Tensor& pred_norm, const Tensor& prob, const Tensor& xy,
-                         const Tensor& angle, const Tensor& ray, double fu, double cu,
-                         double fv, double cv, int H, int W, Tensor& out) {
+namespace {
+
+void angmf_launch(const Tensor& pred_norm, const Tensor& prob, const Tensor& xy,
+                  const Tensor& angle, const Tensor& ray, double fu, double cu, double fv,
+                  double cv, int H, int W, Tensor& out, unsigned flags) {
     const std::size_t n3 = static_cast<std::size_t>(3) * H * W;
     const bool reuse = out.device == Device::HIP && out.rows == 1 && out.numel() == n3 &&
                        out.data != nullptr && out.data != pred_norm.data &&
@@ -56,8 +58,17 @@ void angmf_propagate_gpu(const Tensor& pred_norm, const Tensor& prob, const Tens
         static_cast<const float*>(pred_norm.data), static_cast<const float*>(prob.data),
         static_cast<const float*>(xy.data), static_cast<const float*>(angle.data),
         static_cast<const float*>(ray.data), fu, cu, fv, cv, 1, H, W, 5, 0,
-        static_cast<float*>(out.data), BVML_DSINE_DEFAULT, nullptr);
+        static_cast<float*>(out.data), flags, nullptr);
     if (st != BVML_DSINE_OK) fail_hip("angmf_propagate launch", st);
+}
+
+}  // namespace
+
+void angmf_propagate_gpu(const Tensor& pred_norm, const Tensor& prob, const Tensor& xy,
+                         const Tensor& angle, const Tensor& ray, double fu, double cu,
+                         double fv, double cv, int H, int W, Tensor& out) {
+    angmf_launch(pred_norm, prob, xy, angle, ray, fu, cu, fv, cv, H, W, out,
+                 BVML_DSINE_DEFAULT);
 }
 
 }  // namespace detail
@@ -74,23 +85,41 @@ void ray_relu(Tensor& normal, const Tensor& ray, int H, int W) {
     detail::ray_relu_gpu(normal, ray, H, W);
 }
 
+namespace {
+
+void angmf_check(const Tensor& pred_norm, const Tensor& prob, const Tensor& xy,
+                 const Tensor& angle, const Tensor& ray, int H, int W, const char* op) {
+    const Device dev = pred_norm.device;
+    if (prob.device != dev || xy.device != dev || angle.device != dev || ray.device != dev)
+        fail(std::string(op) + ": all inputs must share a device");
+    if (dev == Device::CPU)
+        fail(std::string(op) + ": tensors are on the CPU; this library implements the HIP "
+             "device path");
+    if (H < 0 || W < 0) fail(std::string(op) + ": H and W must be >= 0");
+    const std::size_t hw = static_cast<std::size_t>(H) * W;
+    need_size(pred_norm, 3 * hw, op, "pred_norm");
+    need_size(prob, 25 * hw, op, "prob");
+    need_size(xy, 50 * hw, op, "xy");
+    need_size(angle, 25 * hw, op, "angle");
+    need_size(ray, 3 * hw, op, "ray");
+}
+
+}  // namespace
+
 void angmf_propagate(const Tensor& pred_norm, const Tensor& prob, const Tensor& xy,
                      const Tensor& angle, const Tensor& ray, double fu, double cu,
                      double fv, double cv, int H, int W, Tensor& out) {
-    const Device dev = pred_norm.device;
-    if (prob.device != dev || xy.device != dev || angle.device != dev || ray.device != dev)
-        fail("angmf_propagate: all inputs must share a device");
-    if (dev == Device::CPU)
-        fail("angmf_propagate: tensors are on the CPU; this library implements the HIP "
-             "device path");
-    if (H < 0 || W < 0) fail("angmf_propagate: H and W must be >= 0");
-    const std::size_t hw = static_cast<std::size_t>(H) * W;
-    need_size(pred_norm, 3 * hw, "angmf_propagate", "pred_norm");
-    need_size(prob, 25 * hw, "angmf_propagate", "prob");
-    need_size(xy, 50 * hw, "angmf_propagate", "xy");
-    need_size(angle, 25 * hw, "angmf_propagate", "angle");
-    need_size(ray, 3 * hw, "angmf_propagate", "ray");
+    angmf_check(pred_norm, prob, xy, angle, ray, H, W, "angmf_propagate");
     detail::angmf_propagate_gpu(pred_norm, prob, xy, angle, ray, fu, cu, fv, cv, H, W, out);
+}
+
+void angmf_propagate_logits(const Tensor& pred_norm, const Tensor& prob_logits,
+                            const Tensor& xy, const Tensor& angle_logits, const Tensor& ray,
+                            double fu, double cu, double fv, double cv, int H, int W,
+                            Tensor& out) {
+    angmf_check(pred_norm, prob_logits, xy, angle_logits, ray, H, W, "angmf_propagate_logits");
+    detail::angmf_launch(pred_norm, prob_logits, xy, angle_logits, ray, fu, cu, fv, cv, H, W,
+                         out, BVML_DSINE_LOGITS);
 }
 
 namespace {

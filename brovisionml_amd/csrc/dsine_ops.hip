@@ -104,6 +104,17 @@ constexpr float kMinV2 = 1e-30f;
 // end of its workgroup.
 constexpr double kAccRatio2 = 1.6e-3;
 
+// With BVML_DSINE_LOGITS, prob and angle hold the heads' raw logits and the
+// kernel applies the refiner's activations (src/dsine_refine.cpp:262-267):
+// prob = sigmoid(L), angle = sigmoid(L) * kPiF, kPiF the float pi of
+// src/dsine_refine.cpp:26.  Tier 1 forms them in fp32 (the angle's sigmoid
+// within 4 ulps or 3e-8 of the correctly rounded float; the weight as
+// rsq(|p|^2 (1 + exp(-L))^2)); the same emulation then gives delta <= 4.7e-7,
+// so such launches recompute below kAccRatio2Logits, which keeps the bound
+// at 8.9e-6.  Tiers 2 and 3 use the correctly rounded floats (sigmoid_ref).
+constexpr float kPiF = 3.14159265358979323846f;
+constexpr double kAccRatio2Logits = 2.8e-3;
+
 // Tier 2 (the double-precision reduced form of flagged pixels) hands a pixel
 // to the reference-order body when its sum nearly cancels: below
 // kAccRatio2Ref * sum(wi^2), or |acc| near the reference's 1e-12 clamp.
@@ -137,6 +148,14 @@ constexpr double kMaxP0 = 4.0;
 // std::max(a, b) == (a < b) ? b : a -- returns a when a is NaN, as the
 // reference CPU path does (fmax would not).
 __device__ __forceinline__ double smax(double a, double b) { return (a < b) ? b : a; }
+
+// The activations the refiner applies to the prob and angle heads
+// (src/dsine_refine.cpp:262-267), as correctly rounded floats: sigmoid in
+// double, rounded once; the angle's product with the float pi in float.
+__device__ __forceinline__ float sigmoid_ref(float x) {
+    return (float)(1.0 / (1.0 + exp(-(double)x)));
+}
+__device__ __forceinline__ float angle_ref(float x) { return sigmoid_ref(x) * kPiF; }
 
 // The ray of pixel (x, y) as build_ray8 forms it from the grid-scaled
 // intrinsics (src/dsine_decoder.cpp:252-253 and :285-290): ray_x, ray_y in
@@ -266,6 +285,8 @@ struct AngmfArgs {
     double tu_c, tv_c;    // (0.5 - cu)/fu, (0.5 - cv)/fv: source ray tu0 = sx/fu + tu_c
     double dd_min;        // tier 1: |dd| below this sends a pixel to the recompute
     int synth_ray;        // form rays from the intrinsics (synth_ray), not from `ray`
+    int logits;           // prob and angle are logits (BVML_DSINE_LOGITS)
+    double acc_ratio2;    // tier 1's cancellation threshold for this launch
 };
 
 // ---------------------------------------------------------------------------
@@ -306,11 +327,12 @@ __global__ __launch_bounds__(256) void angmf_f64_kernel(AngmfArgs a) {
         const int sx = clampi(x - P + kx, 0, a.W - 1);
         const long long sp = (long long)sy * a.W + sx;
         double mx, my, mz, pinv;
+        const float th = ap[(size_t)n * HW + p], wp = pr[(size_t)n * HW + p];
         nbr_ref_f64(pn[sp], pn[HW + sp], pn[2 * HW + sp], sx + 0.5, sy + 0.5,
                     xyp[(size_t)n * HW + p], xyp[(size_t)(K2 + n) * HW + p],
-                    ap[(size_t)n * HW + p], rx, ry, rz, a.fu, a.cu, a.fv, a.cv,
+                    a.logits ? angle_ref(th) : th, rx, ry, rz, a.fu, a.cu, a.fv, a.cv,
                     mx, my, mz, pinv);
-        const double w = pr[(size_t)n * HW + p];
+        const double w = a.logits ? sigmoid_ref(wp) : wp;
         acc0 += w * mx;
         acc1 += w * my;
         acc2 += w * mz;
@@ -399,6 +421,26 @@ __device__ __forceinline__ double rsq64(double x) {
 __device__ __forceinline__ double rsq64_1(double x) {
     const double y = __builtin_amdgcn_rsq(x);
     return fma(0.5 * y, fma(-x * y, y, 1.0), y);
+}
+
+// 1 + exp(-x) in fp32 from the hardware exp2: the rounding of t = -x log2(e)
+// changes exp(-x) by 6e-8 |x| relatively, and sigmoid = 1/(1 + exp(-x)) by
+// sigmoid (1 - sigmoid) 6e-8 |x| <= 1.3e-8 absolutely, below its own
+// rounding.  +inf below x = -88.7, NaN for NaN.
+__device__ __forceinline__ float one_plus_exp_neg(float x) {
+    constexpr float kL2E = 1.44269502f;  // log2(e) rounded to float
+    return 1.0f + __builtin_amdgcn_exp2f(-x * kL2E);
+}
+
+// sigmoid(x) in fp32, within 4 ulps or 3e-8: 1/(1 + exp(-x)) from the hardware
+// rcp and one Newton step.  Below x = -87 (sigmoid under 2e-38, a denormal
+// or 0 as a float) it returns 0, so -inf gives exactly 0 as the reference's
+// sigmoid does; NaN stays NaN.
+__device__ __forceinline__ float sigmoid_f32(float x) {
+    const bool tiny = x < -87.0f;
+    const float d = one_plus_exp_neg(tiny ? 0.0f : x);
+    const float r = __builtin_amdgcn_rcpf(d);
+    return tiny ? 0.0f : fmaf(r, fmaf(-d, r, 1.0f), r);
 }
 
 // sin and cos of t for |t| <= 3.2 (callers send larger |t| to the
@@ -611,7 +653,7 @@ __host__ __device__ inline unsigned pack_tile(int TW, int TH, int M, int L) {
 // host-computed magic number, the wave's group from a constant divisor) and
 // one buffer descriptor per input tensor, its planes reached through the
 // scalar offset.
-template <int K, bool SR>
+template <int K, bool SR, bool LG>
 __global__ __launch_bounds__(64 * kWgWaves) __attribute__((amdgpu_waves_per_eu(4)))
 void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restrict__ xy,
                       const float* __restrict__ angle, const float* __restrict__ prob, int W,
@@ -772,7 +814,8 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
                 hbase + (ky * hw + kx) * (int)sizeof(HaloRec));
             const float4 hm = rec.m, gt = rec.gt;
             const double2 ab = rec.ab;
-            const float xv = xs[i], yv = ys[i], t = th[i];
+            const float xv = xs[i], yv = ys[i];
+            const float t = LG ? sigmoid_f32(th[i]) * kPiF : th[i];
             // q in double (exact products, one rounding), the rest fp32;
             // dd = g + q/|xy| is formed from the raw normal as the reference
             // forms it, with 1/|xy| from the fp32 |xy|^2 and rsq (dd_min
@@ -801,7 +844,16 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
             const float cs = fmaf(vx, rhx, fmaf(vy, rhy, vz * rhz));
             const float dc = fmaxf(kRayEpsF - cs, 0.0f);
             const float px = fmaf(rxf, dc, vx), py = fmaf(ryf, dc, vy), pz = fmaf(rzf, dc, vz);
-            const float wi = wt[i] * __builtin_amdgcn_rsqf(fmaf(px, px, fmaf(py, py, pz * pz)));
+            // wi = prob / |p|; with logits prob = 1/d, d = 1 + exp(-L), and
+            // wi = rsq(|p|^2 d^2) (d = inf: exactly 0)
+            const float p2 = fmaf(px, px, fmaf(py, py, pz * pz));
+            float wi;
+            if constexpr (LG) {
+                const float d = one_plus_exp_neg(wt[i]);
+                wi = __builtin_amdgcn_rsqf(p2 * d * d);
+            } else {
+                wi = wt[i] * __builtin_amdgcn_rsqf(p2);
+            }
             acc0 = fmaf(px, wi, acc0);
             acc1 = fmaf(py, wi, acc1);
             acc2 = fmaf(pz, wi, acc2);
@@ -827,7 +879,7 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
             const double a2 = fma(s0, s0, fma(s1, s1, s2 * s2));
             // 1 / max(|acc|, 1e-12) as the reference; a non-finite or
             // cancelled sum goes to the recompute
-            flag = !(a2 >= kAccRatio2 * sw) || !(a2 <= 1e300);
+            flag = !(a2 >= a.acc_ratio2 * sw) || !(a2 <= 1e300);
             if (!flag) {
                 const double inv = (a2 < 1e-24) ? 1e12 : rsq64_1(a2);
                 float* op = a.out + (size_t)b * 3 * HW;
@@ -912,7 +964,11 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
                     const float mx = ldf(pn, sb), my = ldf(pn + HW, sb), mz = ldf(pn + 2 * HW, sb);
                     const float xsv = ldf(xyp + (size_t)n * HW, fb);
                     const float ysv = ldf(xyp + (size_t)(K2 + n) * HW, fb);
-                    const float thv = ldf(ap + (size_t)n * HW, fb), wv = ldf(pr + (size_t)n * HW, fb);
+                    float thv = ldf(ap + (size_t)n * HW, fb), wv = ldf(pr + (size_t)n * HW, fb);
+                    if constexpr (LG) {
+                        thv = angle_ref(thv);
+                        wv = sigmoid_ref(wv);
+                    }
                     double ox, oy, oz, pinv;
                     if constexpr (TIER == 2) {
                         const double rxd = frx, ryd = fry, rzd = frz;
@@ -1071,12 +1127,12 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
         c.out += (size_t)b0 * 3 * a.HW;
         c.B = nb;
         const dim3 grid((unsigned)a.tiles_per_img, (unsigned)nb), block(64 * a.M * group_waves(K));
-        if (a.synth_ray)
-            hipLaunchKernelGGL((angmf_f32_kernel<K, true>), grid, block, lds, s, c.pn, c.xy, c.ang,
-                               c.pr, a.W, a.H, tile, a.tiles_per_img, a.tiles_x, mag, c);
-        else
-            hipLaunchKernelGGL((angmf_f32_kernel<K, false>), grid, block, lds, s, c.pn, c.xy,
-                               c.ang, c.pr, a.W, a.H, tile, a.tiles_per_img, a.tiles_x, mag, c);
+        auto kern = a.synth_ray ? (a.logits ? angmf_f32_kernel<K, true, true>
+                                            : angmf_f32_kernel<K, true, false>)
+                                : (a.logits ? angmf_f32_kernel<K, false, true>
+                                            : angmf_f32_kernel<K, false, false>);
+        hipLaunchKernelGGL(kern, grid, block, lds, s, c.pn, c.xy, c.ang, c.pr, a.W, a.H, tile,
+                           a.tiles_per_img, a.tiles_x, mag, c);
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
     }
@@ -1175,7 +1231,7 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
                                    double fv, double cv, int B, int H, int W,
                                    int k, long long ray_bstride, float* out,
                                    unsigned flags, void* stream) {
-    if (flags & ~(BVML_DSINE_FP64 | BVML_DSINE_RAY_FROM_INTRINSICS))
+    if (flags & ~(BVML_DSINE_FP64 | BVML_DSINE_RAY_FROM_INTRINSICS | BVML_DSINE_LOGITS))
         return fail(BVML_DSINE_EFLAGS, "angmf_propagate: unknown flag bits");
     const bool synth = (flags & BVML_DSINE_RAY_FROM_INTRINSICS) != 0;
     if (synth) {
@@ -1228,6 +1284,8 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
     gmax *= std::sqrt(1.0 + (double)kUnitM2);
     a.dd_min = kDdClamp + 1e-7 * gmax + 3e-7 / std::fmin(std::fabs(fu), std::fabs(fv));
     a.synth_ray = synth ? 1 : 0;
+    a.logits = (flags & BVML_DSINE_LOGITS) ? 1 : 0;
+    a.acc_ratio2 = a.logits ? kAccRatio2Logits : kAccRatio2;
     choose_tile(a, k);
     if (!tile_fits(k, a.M, a.TW, a.TH, synth))
         return fail(BVML_DSINE_ESIZE, "angmf_propagate: no tile fits the kernel's LDS");

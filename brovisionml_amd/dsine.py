@@ -90,12 +90,14 @@ def ray_relu(normal, ray, H: int, W: int) -> None:
 
 def angmf_propagate(pred_norm, prob, xy, angle, ray, fu: float, cu: float,
                     fv: float, cv: float, H: int, W: int, out=None, *,
-                    precise: bool = False):
+                    precise: bool = False, logits: bool = False):
     """Fused AngMF propagate (src/dsine_ops.cpp:78-172).  Returns `out`
     (allocated like pred_norm when None; must not alias any input).
     precise=True runs the double-precision kernel.  ray=None forms each
     pixel's ray from fu, cu, fv, cv in the kernel, bit-identical to
-    build_ray8 (src/dsine_decoder.cpp:242-293)."""
+    build_ray8 (src/dsine_decoder.cpp:242-293).  logits=True takes prob and
+    angle as the heads' raw logits and applies the refiner's activations
+    (src/dsine_refine.cpp:262-267: sigmoid, and sigmoid * pi) in the kernel."""
     _check_tensors("angmf_propagate", [pred_norm, prob, xy, angle] + ([] if ray is None else [ray]))
     import torch
     HW = H * W
@@ -123,6 +125,8 @@ def angmf_propagate(pred_norm, prob, xy, angle, ray, fu: float, cu: float,
     flags = _lib.FP64 if precise else _lib.DEFAULT
     if ray is None:
         flags |= _lib.RAY_FROM_INTRINSICS
+    if logits:
+        flags |= _lib.LOGITS
     with _device(pred_norm):
         st = _lib.angmf_propagate_f32(
             pred_norm.data_ptr(), prob.data_ptr(), xy.data_ptr(), angle.data_ptr(),

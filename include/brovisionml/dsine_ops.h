@@ -38,6 +38,21 @@ void angmf_propagate(const brotensor::Tensor& pred_norm,
                      int H, int W,
                      brotensor::Tensor& out);
 
+// angmf_propagate on the prob and angle heads' raw logits: the kernel applies
+// the activations the refiner applies before each propagate
+// (src/dsine_refine.cpp:262-267: sigmoid, and sigmoid * kPi), so the two
+// elementwise passes over them disappear.  No counterpart in the reference;
+// the result matches angmf_propagate given the correctly rounded float
+// activations, to the same tolerance.
+void angmf_propagate_logits(const brotensor::Tensor& pred_norm,
+                            const brotensor::Tensor& prob_logits,
+                            const brotensor::Tensor& xy,
+                            const brotensor::Tensor& angle_logits,
+                            const brotensor::Tensor& ray,
+                            double fu, double cu, double fv, double cv,
+                            int H, int W,
+                            brotensor::Tensor& out);
+
 // The refiner's post-propagate step (src/dsine_refine.cpp:276-282), whose
 // reference is two brotensor calls:
 //   convex_upsample_forward(x, mask, N, C, H, W, scale, up)

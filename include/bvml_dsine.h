@@ -56,6 +56,15 @@ extern "C" {
  * then be NULL and ray_bstride is ignored.  No counterpart in the reference;
  * saves the 3 ray planes (12 B/px) and the host-side build. */
 #define BVML_DSINE_RAY_FROM_INTRINSICS 2u
+/* `prob` and `angle` hold the prob and angle heads' raw logits, and the
+ * kernel applies the activations the refiner applies to them before each
+ * propagate (src/dsine_refine.cpp:262-267: apply_sigmoid(prob);
+ * apply_sigmoid(angle); scale_inplace(angle, kPi) with the float kPi of
+ * src/dsine_refine.cpp:26): prob = sigmoid(L), angle = sigmoid(L) * kPi.
+ * Results match the op given the correctly rounded float activations, to the
+ * same bar.  No counterpart in the reference; saves the two elementwise
+ * passes over 2 k^2 planes (read and write) per refiner iteration. */
+#define BVML_DSINE_LOGITS 4u
 
 /*
  * RayReLU in place (eps = 1e-2), B samples.

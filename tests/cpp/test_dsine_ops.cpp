@@ -1,4 +1,4 @@
-// Drop-in test of brovisionml::dsine::{ray_relu, angmf_propagate,
+// Drop-in test of brovisionml::dsine::{ray_relu, angmf_propagate[_logits],
 // convex_upsample[_normalize]} (the C++
 // surface of include/brovisionml/dsine_ops.h), in the style of the
 // reference's tests (tests/test_dsine_refine.cpp:48-53: CHECK + failure count).
@@ -209,10 +209,34 @@ static void test_refiner_call_pattern() {
     Tensor alias = pred_norm;
     ops::angmf_propagate(pred_norm, prob, xy, angle, ray, in.fu, in.cu, in.fv, in.cv, H, W, alias);
     CHECK(alias.data != pred_norm.data);
-    // up_pred_norm = normalize(convex_upsample(pred_norm, up_mask)) -- the
-    // refiner's step after each propagate (src/dsine_refine.cpp:276-282)
+    // the same step on the heads' raw logits: the kernel applies sigmoid and
+    // sigmoid * pi (src/dsine_refine.cpp:262-267); the oracle takes the
+    // correctly rounded float activations
     std::mt19937 rng(11);
     std::normal_distribution<double> nd;
+    {
+        const float kPi = 3.14159265358979323846f;
+        std::vector<float> lp(in.prob.size()), la(in.angle.size());
+        std::vector<float> sp(lp.size()), ang(la.size());
+        for (std::size_t i = 0; i < lp.size(); ++i) {
+            lp[i] = static_cast<float>(2.0 * nd(rng));
+            la[i] = static_cast<float>(2.0 * nd(rng));
+            sp[i] = static_cast<float>(1.0 / (1.0 + std::exp(-static_cast<double>(lp[i]))));
+            ang[i] = static_cast<float>(1.0 / (1.0 + std::exp(-static_cast<double>(la[i])))) * kPi;
+        }
+        Tensor dlp = upload(lp), dla = upload(la), lout;
+        ops::angmf_propagate_logits(pred_norm, dlp, xy, dla, ray, in.fu, in.cu, in.fv, in.cv, H,
+                                    W, lout);
+        CHECK(lout.device == Device::HIP && lout.rows == 1 && lout.cols == 3 * H * W);
+        oracle_angmf_propagate_f32(want_n.data(), sp.data(), in.xy.data(), ang.data(),
+                                   in.ray.data(), in.fu, in.cu, in.fv, in.cv, 1, H, W, 5, 0,
+                                   want_out.data());
+        const double el = max_abs(lout, want_out);
+        std::printf("    angmf_propagate_logits max-abs %.3e\n", el);
+        CHECK(el <= 1e-5);
+    }
+    // up_pred_norm = normalize(convex_upsample(pred_norm, up_mask)) -- the
+    // refiner's step after each propagate (src/dsine_refine.cpp:276-282)
     std::vector<float> mask(576 * H * W);
     for (auto& v : mask) v = static_cast<float>(nd(rng));
     std::vector<float> pn_host(3 * H * W), want_up(3 * 64 * H * W);

@@ -56,7 +56,7 @@ def angmf(**kw):
     (dict(B=-1), _lib.ESHAPE), (dict(H=-2), _lib.ESHAPE), (dict(ray_bstride=-3), _lib.ESHAPE),
     (dict(k=4), _lib.EK), (dict(k=11), _lib.EK), (dict(k=0), _lib.EK),
     (dict(prob=0), _lib.ENULL), (dict(out=0), _lib.ENULL),
-    (dict(flags=4), _lib.EFLAGS),
+    (dict(flags=8), _lib.EFLAGS),
     (dict(out=FAKE), _lib.EALIAS),                  # out == pred_norm
     (dict(out=FAKE + 0x200000 + 64), _lib.EALIAS),  # inside xy
     (dict(H=1 << 16, W=1 << 14), _lib.ESIZE),       # plane of 2^30 pixels

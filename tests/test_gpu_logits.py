@@ -1,0 +1,114 @@
+"""GPU parity of BVML_DSINE_LOGITS: angmf_propagate on the prob and angle
+heads' raw logits, the kernel applying the refiner's activations
+(src/dsine_refine.cpp:262-267: apply_sigmoid(prob); apply_sigmoid(angle);
+scale_inplace(angle, kPi), kPi the float pi of src/dsine_refine.cpp:26).
+
+The expected output is the oracle's on the correctly rounded float
+activations: sigmoid in double rounded once to float, the angle the float
+product of that with float(pi).  Same bar as the plain op."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from brovisionml_amd import dsine, workloads as wl
+from tests._util import TOL_ABS, TOL_DEG, compare, to_dev
+
+pytestmark = pytest.mark.gpu
+
+F32_PI = np.float32(3.14159265358979323846)
+
+
+def say(msg: str) -> None:
+    print(msg, flush=True)
+
+
+def activate(prob_logits, angle_logits):
+    """The refiner's activations as correctly rounded floats."""
+    with np.errstate(over="ignore"):
+        sp = (1.0 / (1.0 + np.exp(-np.asarray(prob_logits, np.float64)))).astype(np.float32)
+        sa = (1.0 / (1.0 + np.exp(-np.asarray(angle_logits, np.float64)))).astype(np.float32)
+    ang = (sa.astype(np.float64) * np.float64(F32_PI)).astype(np.float32)
+    return sp, ang
+
+
+def logit(p):
+    p = np.asarray(p, np.float64)
+    return np.log(p / (1.0 - p))
+
+
+def run(inp, lp, la, H, W, k, device, precise=False):
+    import torch
+    t = {key: to_dev(inp[key], device) for key in ("pred_norm", "xy", "ray")}
+    fu, cu, fv, cv = inp["intrinsics"]
+    out = dsine.angmf_propagate(t["pred_norm"], to_dev(lp, device), t["xy"], to_dev(la, device),
+                                t["ray"], fu, cu, fv, cv, H, W, precise=precise, logits=True)
+    torch.cuda.synchronize()
+    got = out.cpu().numpy()
+    sp, ang = activate(lp, la)
+    want = oracle.angmf_propagate(inp["pred_norm"], sp, inp["xy"], ang, inp["ray"],
+                                  inp["intrinsics"], H, W, k, nthreads=16)
+    return got, want
+
+
+@pytest.mark.parametrize("idx", [0, 2, 3])
+@pytest.mark.parametrize("precise", [False, True])
+def test_logits_workload(cuda, idx, precise):
+    """The workloads' prob and angle planes turned back into logits (the
+    angle planes through angle / pi), so the activated inputs are the
+    workloads' own up to rounding."""
+    w = wl.WORKLOADS[idx]
+    say(f"[gpu] angmf logits {w.name} precise={precise}")
+    inp = wl.make_inputs(w)
+    lp = logit(np.clip(inp["prob"], 1e-6, 1 - 1e-6)).astype(np.float32)
+    la = logit(np.clip(inp["angle"] / np.pi, 1e-6, 1 - 1e-6)).astype(np.float32)
+    got, want = run(inp, lp, la, w.H, w.W, w.k, cuda, precise)
+    max_abs, max_deg, nan_mm = compare(got.reshape(w.B, 3, -1), want.reshape(w.B, 3, -1))
+    say(f"    max-abs {max_abs:.3e}  max-angle {max_deg:.3e} deg")
+    assert nan_mm == 0
+    assert max_abs <= (2.5e-7 if precise else TOL_ABS) and max_deg <= TOL_DEG
+
+
+@pytest.mark.parametrize("scale", [0.3, 3.0, 30.0])
+def test_logits_scales(cuda, scale):
+    """Random logits N(0, scale^2): from nearly-constant activations to
+    saturated ones (sigmoid at 0 and 1, angles at 0 and pi)."""
+    H, W, k = 40, 56, 5
+    say(f"[gpu] angmf logits scale {scale}")
+    rng = np.random.default_rng(int(scale * 10))
+    w = wl.Workload(0, "logits", 1, H, W, k, 1, "normal:0.1", "sphere", 7)
+    inp = wl.make_inputs(w)
+    lp = (rng.standard_normal(inp["prob"].shape) * scale).astype(np.float32)
+    la = (rng.standard_normal(inp["angle"].shape) * scale).astype(np.float32)
+    got, want = run(inp, lp, la, H, W, k, cuda)
+    max_abs, max_deg, nan_mm = compare(got.reshape(1, 3, -1), want.reshape(1, 3, -1))
+    say(f"    max-abs {max_abs:.3e}  max-angle {max_deg:.3e} deg")
+    assert nan_mm == 0
+    assert max_abs <= TOL_ABS and max_deg <= TOL_DEG
+
+
+def test_logits_special_values(cuda):
+    """+-inf, NaN and extreme logits: sigmoid exactly 0 or 1 (a zero weight, a
+    zero or pi angle), NaN propagating as the activated planes would."""
+    H, W, k = 12, 16, 5
+    say("[gpu] angmf logits special values")
+    rng = np.random.default_rng(33)
+    w = wl.Workload(0, "logits-special", 1, H, W, k, 1, "normal:0.1", "sphere", 8)
+    inp = wl.make_inputs(w)
+    lp = rng.standard_normal(inp["prob"].shape).astype(np.float32)
+    la = rng.standard_normal(inp["angle"].shape).astype(np.float32)
+    vals = np.array([np.inf, -np.inf, 100.0, -100.0, 87.5, -87.5, -200.0, 1e30, -1e30],
+                    np.float32)
+    for i, v in enumerate(vals):
+        lp[0, i, 10 + i] = v
+        la[0, (i + 3) % 25, 40 + i] = v
+    lp[0, :, 60] = -np.inf          # every weight 0: output exactly 0
+    lp[0, 5, 70] = np.nan           # NaN output
+    la[0, 6, 80] = np.nan           # NaN output
+    got, want = run(inp, lp, la, H, W, k, cuda)
+    max_abs, max_deg, nan_mm = compare(got.reshape(1, 3, -1), want.reshape(1, 3, -1))
+    say(f"    max-abs {max_abs:.3e}  max-angle {max_deg:.3e} deg  nan-mismatch {nan_mm}")
+    assert nan_mm == 0
+    assert max_abs <= TOL_ABS and max_deg <= TOL_DEG
+    assert np.all(got.reshape(3, -1)[:, 60] == 0)

@@ -46,8 +46,42 @@ def sincos(t):
     return sc + sc, fma(c, c, -(s * s))
 
 
-def tier1(pred_norm, prob, xy, angle, ray, intr, H, W, k, rng):
-    """One sample: (B=1) planes as the op takes them.  Returns the pixel
+K_PI = f32(3.14159265358979323846)
+L2E = f32(1.44269502)
+
+
+def exp2(x, rng):
+    """The hardware exp2 (v_exp_f32), at its measured relative error bound."""
+    y = np.exp2(np.asarray(x, f32).astype(f64))
+    with np.errstate(over="ignore"):
+        return (y * (1.0 + rng.choice([-8.5e-8, 8.5e-8], size=y.shape))).astype(f32)
+
+
+def rcp(x, rng):
+    y = 1.0 / np.asarray(x, f32).astype(f64)
+    return (y * (1.0 + rng.choice([-RSQ_REL, RSQ_REL], size=y.shape))).astype(f32)
+
+
+def one_plus_exp_neg(x, rng):
+    """1 + exp(-x) from the hardware exp2 of the rounded -x log2(e)."""
+    with np.errstate(over="ignore"):
+        return f32(1.0) + exp2(-np.asarray(x, f32) * L2E, rng)
+
+
+def sigmoid(x, rng):
+    """sigmoid_f32: 1/(1 + exp(-x)) from the hardware rcp and one Newton
+    step; 0 below x = -87."""
+    x = np.asarray(x, f32)
+    tiny = x < f32(-87.0)
+    d = one_plus_exp_neg(np.where(tiny, f32(0.0), x), rng)
+    r = rcp(d, rng)
+    return np.where(tiny, f32(0.0), fma(r, fma(-d, r, f32(1.0)), r))
+
+
+def tier1(pred_norm, prob, xy, angle, ray, intr, H, W, k, rng, logits=False):
+    """One sample: (B=1) planes as the op takes them (with logits, prob and
+    angle hold the heads' raw logits and the kernel applies sigmoid and
+    sigmoid * pi itself).  Returns the pixel
     outputs (3, HW) float64 (normalised in double, as phase B does), |acc|^2
     and sum(wi^2) per pixel.  Runs of the window split as the kernel splits
     them (k = 5: 7, 6, 6, 6), each run's sums in fp32."""
@@ -90,6 +124,8 @@ def tier1(pred_norm, prob, xy, angle, ray, intr, H, W, k, rng):
             ys = np.asarray(xy[K2 + n], f32)
             t = np.asarray(angle[n], f32)
             w = np.asarray(prob[n], f32)
+            if logits:
+                t = sigmoid(t, rng) * K_PI
             q = (xs.astype(f64) * (mx.astype(f64) * ifu)
                  + ys.astype(f64) * (my.astype(f64) * ifv)).astype(f32)
             s = fma(xs, xs, ys * ys)
@@ -108,7 +144,13 @@ def tier1(pred_norm, prob, xy, angle, ray, intr, H, W, k, rng):
             cs = fma(vx, rhx, fma(vy, rhy, vz * rhz))
             dc = np.maximum(EPS - cs, f32(0))
             px, py, pz = fma(rx, dc, vx), fma(ry, dc, vy), fma(rz, dc, vz)
-            wi = w * rsq(fma(px, px, fma(py, py, pz * pz)), rng)
+            p2 = fma(px, px, fma(py, py, pz * pz))
+            if logits:
+                d = one_plus_exp_neg(w, rng)
+                with np.errstate(over="ignore"):
+                    wi = rsq(p2 * d * d, rng)
+            else:
+                wi = w * rsq(p2, rng)
             pa = np.stack([fma(px, wi, pa[0]), fma(py, wi, pa[1]), fma(pz, wi, pa[2])])
             pq = fma(wi, wi, pq)
         acc += pa.astype(f64)
