@@ -580,9 +580,12 @@ __host__ __device__ constexpr int recompute_ppr(int K) { return (K <= 8) ? 8 : 4
 // places a workgroup of n waves only where every SIMD has ceil(n/4) free
 // slots, and spreads 8 waves exactly 2 per SIMD, so every SIMD carries the
 // same work (10-wave workgroups land 3+3+2+2, and two of them leave one SIMD
-// of most CUs with 6 waves where the average is 5).
+// of most CUs with 6 waves where the average is 5).  Runs stay at 7
+// neighbours or fewer (k = 7, 9: 8 waves): a wave buffers its run's planes in
+// registers, and runs of 12-13 (k = 7 with 4 waves) spill them to scratch
+// (311 us against 204 us at 4 x 512 x 512).
 __host__ __device__ constexpr int group_waves(int K) {
-    return K == 1 ? 1 : (K == 3 ? 2 : (K == 9 ? 8 : 4));
+    return K == 1 ? 1 : (K == 3 ? 2 : (K >= 7 ? 8 : 4));
 }
 constexpr int kWgWaves = 8;
 
