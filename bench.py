@@ -440,12 +440,82 @@ def bench_upsample(args, dev) -> dict:
     return line
 
 
+def bench_refiner(args, dev) -> dict:
+    """The whole NRN refiner forward (brovisionml_amd/refiner.py: 5 iterations
+    of ConvGRU + heads on MIOpen, the package's propagate with fused
+    activations and its upsample + normalise) at a 256x256 grid (a 2048x2048
+    image), synthetic weights and decoder outputs, one forward per step,
+    captured in one graph.  The CPU leg is its restatement in oracle/refiner.py
+    (float64 convolutions, the C oracle's ops) on a 24x32 grid."""
+    import torch
+    from brovisionml_amd import refiner as rf, workloads as wl
+
+    H = W = 256 if args.workload is None or args.workload == 0 else 64
+    rng = np.random.default_rng(0)
+    normal = rng.standard_normal((1, 3, H, W))
+    normal[:, 2] = np.abs(normal[:, 2]) + 0.5
+    normal = (normal / np.linalg.norm(normal, axis=1, keepdims=True)).astype(np.float32)
+    feature = rng.standard_normal((1, 64, H, W)).astype(np.float32)
+    hidden = rng.uniform(-1, 1, (1, 64, H, W)).astype(np.float32)
+    model = rf.Refiner(rf.random_weights(0), dev)
+    dec = rf.DecoderOutput(*(torch.from_numpy(a).to(dev) for a in (normal, feature, hidden)))
+    intr = wl.intrins_from_fov(8 * H, 8 * W, 60.0)
+    cond = model.conditioning(intr, H, W, 8 * H, 8 * W)
+    for _ in range(3):
+        model.forward(dec, intr, 8 * H, 8 * W, cond=cond)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(args.steps):
+            model.forward(dec, intr, 8 * H, 8 * W, cond=cond)
+    g.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream(dev)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    g.replay()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    t = e0.elapsed_time(e1) * 1e-3
+    opx = 64 * H * W * args.steps
+    line = base_line(args, f"output Mpixel/s, DSINE NRN refiner forward (5 iterations), {H}x{W} "
+                           f"grid -> {8 * H}x{8 * W} fp32", opx / t / 1e6, "Mpixel/s",
+                     t * 1e3 / args.steps,
+                     {"workload": f"dsine-refiner-{H}x{W}", "H": H, "W": W, "iterations": 5,
+                      "weights": "synthetic (uniform +-1/sqrt(fan_in))",
+                      "convolutions": "torch F.conv2d (MIOpen), fp32"})
+    line["gpu"] = torch.cuda.get_device_name(dev)
+    if not args.no_cpu:
+        import oracle.refiner as oref
+        h2, w2 = 24, 32
+        intr2 = wl.intrins_from_fov(8 * h2, 8 * w2, 60.0)
+        fuv2 = wl.scaled_intrinsics(intr2, h2, w2, 8 * h2, 8 * w2)
+        ray2 = wl.build_ray8(intr2, h2, w2, 8 * h2, 8 * w2).reshape(3, h2, w2)
+        uv2 = rf.uv_map(intr2, h2, w2, 8 * h2, 8 * w2)
+        w0 = rf.random_weights(0)
+        n2, f2, hd2 = normal[0, :, :h2, :w2], feature[0, :, :h2, :w2], hidden[0, :, :h2, :w2]
+        n2 = (n2 / np.linalg.norm(n2, axis=0)).astype(np.float32)
+        nthr = torch.get_num_threads()
+        torch.set_num_threads(1)
+        passes, el = timed_cpu(lambda: oref.refine_forward(w0, n2, f2, hd2, intr2, fuv2, ray2,
+                                                           uv2), args.cpu_seconds)
+        torch.set_num_threads(nthr)
+        line["cpu_baseline"] = {
+            "value": round(passes * 64 * h2 * w2 / el / 1e6, 4), "unit": "Mpixel/s", "cores": 1,
+            "kind": "port",
+            "sample": f"{passes} forwards of a {h2}x{w2} grid, {el:.1f} s: float64 torch "
+                      "convolutions and the C oracle's ops, one thread",
+            "cpu": cpu_model(),
+        }
+    return line
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--op", choices=("angmf", "upsample"), default="angmf")
+    ap.add_argument("--op", choices=("angmf", "upsample", "refiner"), default="angmf")
     ap.add_argument("--workload", type=int, default=None,
                     help="index into the op's workloads (default: angmf 2, upsample 0)")
     ap.add_argument("--sets", type=int, default=0, help="rotating input sets (0 = auto, > 512 MB)")
@@ -463,7 +533,7 @@ def main() -> int:
                     help="also run 10 plain device copies of one launch's byte count "
                          "(the reference kernel for the FETCH_SIZE / WRITE_SIZE scale)")
     args = ap.parse_args()
-    if args.workload is None:
+    if args.workload is None and args.op != "refiner":
         args.workload = 2 if args.op == "angmf" else 0
 
     if args.gpus != 1:
@@ -480,7 +550,8 @@ def main() -> int:
         return 1
     dev = torch.device("cuda:0")
     _lib.load()
-    line = bench_angmf(args, dev) if args.op == "angmf" else bench_upsample(args, dev)
+    line = {"angmf": bench_angmf, "upsample": bench_upsample,
+            "refiner": bench_refiner}[args.op](args, dev)
     print(json.dumps(line), flush=True)
     return 0
 

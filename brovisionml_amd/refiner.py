@@ -1,0 +1,199 @@
+"""DSINE NRN refiner on the HIP device: the 5-iteration loop of brovisionml's
+Refiner::forward (src/dsine_refine.cpp:212-294; the spec comment at
+include/brovisionml/dsine_refine.h:1-111), driving this package's kernels.
+
+Per iteration (src/dsine_refine.cpp:255-287):
+  h_new     = ConvGRU(h, feat_map)                 convz/convr/convq 5x5, 130 -> 64
+  hin       = cat(h_new, uv_8)                      66 channels
+  prob, xy, angle = the three heads on hin          (25, 50, 25 channels)
+  pred_norm = angmf_propagate(pred_norm, sigmoid(prob), xy, sigmoid(angle)*pi, ray_8)
+  up        = normalize(convex_upsample(pred_norm, up_prob_head(hin)))
+  h         = h_new
+after pred_norm = RayReLU(decoder.normal, ray_8) and feat_map = cat(decoder.feature,
+uv_8).  The result is the last iteration's up-sampled normals, cropped to the
+unpadded image.
+
+What runs where:
+  * RayReLU, the propagate and the convex upsample + normalise are the
+    package's gfx950 kernels (C ABI in include/bvml_dsine.h); the propagate
+    takes the heads' raw logits and applies the activations itself
+    (BVML_DSINE_LOGITS), so the two activation passes of :262-267 are gone;
+    the upsample fuses convex_upsample_forward and l2_normalize_nchw_forward
+    (:278-282); the ray map comes from bvml_dsine_build_ray8_f32 on the device.
+  * The ConvGRU and the heads are plain convolutions (the reference's
+    brotensor conv2d_forward, :94-101): torch's F.conv2d, i.e. MIOpen on ROCm,
+    in fp32 with their elementwise gates; they are not this package's hot path.
+
+Weights are the checkpoint's top-level tensors gru.conv{z,r,q}.{weight,bias}
+and {prob,xy,angle,up_prob}_head.{0,2,4}.{weight,bias} (:161-180), loaded
+from a safetensors file or drawn at random for synthetic runs (no checkpoint
+ships in this environment).
+"""
+from __future__ import annotations
+
+import math
+from dataclasses import dataclass
+
+import numpy as np
+
+from . import dsine, workloads
+
+K_UP = 8            # downsample_ratio (src/dsine_refine.cpp:24)
+N_ITER = 5          # num_iter_test (:25)
+PS = 5              # the propagate's window (:24 of src/dsine_ops.cpp)
+K_PI = float(np.float32(3.14159265358979323846))  # the float kPi (:26)
+HEAD_OUT = {"prob_head": PS * PS, "xy_head": 2 * PS * PS, "angle_head": PS * PS,
+            "up_prob_head": 9 * K_UP * K_UP}
+
+
+@dataclass
+class DecoderOutput:
+    """The decoder's /8-grid maps (include/brovisionml/dsine_decoder.h:96-102):
+    normal (1, 3, h8, w8) unit normals, feature (1, 64, h8, w8), hidden
+    (1, 64, h8, w8); fp32 tensors on the device."""
+    normal: object
+    feature: object
+    hidden: object
+
+
+@dataclass(frozen=True)
+class Crop:
+    """The part of DsineTransform the refiner uses
+    (include/brovisionml/dsine_preprocess.h:48-57): the unpadded size and the
+    top/left padding."""
+    orig_h: int
+    orig_w: int
+    pad_t: int = 0
+    pad_l: int = 0
+
+
+def weight_shapes(hidden: int = 64, feature: int = 64) -> dict:
+    """Checkpoint tensor name -> shape (OIHW weights, (C_out,) biases)."""
+    inp = feature + 2          # feat_map = cat(feature, uv_8)
+    shapes = {}
+    for g in ("convz", "convr", "convq"):
+        shapes[f"gru.{g}.weight"] = (hidden, hidden + inp, 5, 5)
+        shapes[f"gru.{g}.bias"] = (hidden,)
+    for head, out in HEAD_OUT.items():
+        for idx, (ci, co, k) in zip((0, 2, 4), ((hidden + 2, 64, 3), (64, 64, 1), (64, out, 1))):
+            shapes[f"{head}.{idx}.weight"] = (co, ci, k, k)
+            shapes[f"{head}.{idx}.bias"] = (co,)
+    return shapes
+
+
+def random_weights(seed: int, hidden: int = 64, feature: int = 64) -> dict:
+    """Synthetic weights: uniform(-1/sqrt(fan_in), 1/sqrt(fan_in)) for each
+    convolution's weight and bias (torch's default initialisation bound), as
+    float32 numpy arrays."""
+    rng = np.random.default_rng(seed)
+    shapes = weight_shapes(hidden, feature)
+    out = {}
+    for name, shape in shapes.items():
+        conv = name.rsplit(".", 1)[0]
+        bound = 1.0 / math.sqrt(math.prod(shapes[conv + ".weight"][1:]))
+        out[name] = rng.uniform(-bound, bound, shape).astype(np.float32)
+    return out
+
+
+def load_safetensors(path: str) -> dict:
+    """The checkpoint's refiner tensors as float32 numpy arrays, weights
+    reshaped to OIHW (the reference stores (C_out, C_in*k*k) as well)."""
+    from safetensors.numpy import load_file
+    raw = load_file(path)
+    shapes = weight_shapes()
+    out = {}
+    for name, shape in shapes.items():
+        if name not in raw:
+            raise RuntimeError(f"dsine::Refiner: missing tensor '{name}'")
+        out[name] = np.asarray(raw[name], np.float32).reshape(shape)
+    return out
+
+
+def uv_map(intr: workloads.Intrinsics, H: int, W: int, orig_h: int, orig_w: int):
+    """build_uv (src/dsine_decoder.cpp:242-274): ray_x, ray_y on the (H, W)
+    grid, double arithmetic rounded to float; (2, H, W) float32 numpy."""
+    fu, cu, fv, cv = workloads.scaled_intrinsics(intr, H, W, orig_h, orig_w)
+    x = np.arange(W, dtype=np.float64)
+    y = np.arange(H, dtype=np.float64)
+    rx = (((x + 0.5) - cu) / fu).astype(np.float32)
+    ry = (((y + 0.5) - cv) / fv).astype(np.float32)
+    return np.stack([np.broadcast_to(rx, (H, W)), np.broadcast_to(ry[:, None], (H, W))])
+
+
+class Refiner:
+    """Refiner::forward on the device.  `weights` as weight_shapes() names
+    them (numpy or torch); hidden / feature are the checkpoint's widths."""
+
+    def __init__(self, weights: dict, device, hidden: int = 64, feature: int = 64):
+        import torch
+        self.device = torch.device(device)
+        self.hidden, self.feature = hidden, feature
+        shapes = weight_shapes(hidden, feature)
+        self.w = {}
+        for name, shape in shapes.items():
+            t = torch.as_tensor(np.asarray(weights[name], np.float32)).reshape(shape)
+            self.w[name] = t.to(self.device).contiguous()
+
+    def _conv(self, x, name: str, pad: int):
+        import torch.nn.functional as F
+        return F.conv2d(x, self.w[name + ".weight"], self.w[name + ".bias"], padding=pad)
+
+    def _gru(self, h, x):
+        """submodules.ConvGRU (src/dsine_refine.cpp:138-159)."""
+        import torch
+        hx = torch.cat([h, x], dim=1)
+        z = torch.sigmoid(self._conv(hx, "gru.convz", 2))
+        r = torch.sigmoid(self._conv(hx, "gru.convr", 2))
+        q = torch.tanh(self._conv(torch.cat([r * h, x], dim=1), "gru.convq", 2))
+        return (1 - z) * h + z * q
+
+    def _head(self, name: str, x):
+        """get_prediction_head (src/dsine_refine.cpp:119-127)."""
+        import torch
+        h = torch.relu(self._conv(x, name + ".0", 1))
+        h = torch.relu(self._conv(h, name + ".2", 0))
+        return self._conv(h, name + ".4", 0)
+
+    def conditioning(self, intr: workloads.Intrinsics, H: int, W: int, orig_h: int, orig_w: int):
+        """(ray_8, uv_8, (fu, cu, fv, cv)) on the device for an (H, W) grid: the
+        ray map from bvml_dsine_build_ray8_f32, the uv map from build_uv."""
+        import torch
+        fuv = workloads.scaled_intrinsics(intr, H, W, orig_h, orig_w)
+        ray8 = dsine.build_ray8(*fuv, H, W, device=self.device)
+        uv8 = torch.from_numpy(np.ascontiguousarray(uv_map(intr, H, W, orig_h, orig_w)))
+        return ray8, uv8.to(self.device)[None], fuv
+
+    def forward(self, dec: DecoderOutput, intr: workloads.Intrinsics, orig_h: int, orig_w: int,
+                crop: Crop | None = None, trace: list | None = None, cond=None):
+        """The refined normals (1, 3, h, w) at the unpadded resolution
+        (crop.orig_h x crop.orig_w; the whole 8*h8 x 8*w8 map without crop).
+        trace, when given, receives each iteration's (pred_norm, up) pair;
+        cond, when given, is conditioning()'s result for these intrinsics (so
+        the call does no host-to-device copy and can be captured in a graph)."""
+        import torch
+        _, _, H, W = dec.normal.shape
+        ray8, uv8, (fu, cu, fv, cv) = (cond if cond is not None
+                                       else self.conditioning(intr, H, W, orig_h, orig_w))
+        pred_norm = dec.normal.contiguous().clone()
+        dsine.ray_relu(pred_norm, ray8, H, W)
+        feat_map = torch.cat([dec.feature, uv8], dim=1)
+        h = dec.hidden
+        up = None
+        for _ in range(N_ITER):
+            h_new = self._gru(h, feat_map)
+            hin = torch.cat([h_new, uv8], dim=1)
+            prob = self._head("prob_head", hin).contiguous()
+            xy = self._head("xy_head", hin).contiguous()
+            angle = self._head("angle_head", hin).contiguous()
+            pred_norm = dsine.angmf_propagate(pred_norm, prob, xy, angle, ray8, fu, cu, fv, cv,
+                                              H, W, logits=True)
+            up_mask = self._head("up_prob_head", hin).contiguous()
+            up = dsine.convex_upsample_normalize(pred_norm, up_mask, 1, 3, H, W, K_UP,
+                                                 float(np.float32(1e-12)))
+            if trace is not None:
+                trace.append((pred_norm, up))
+            h = h_new
+        if crop is None:
+            return up
+        return up[:, :, crop.pad_t:crop.pad_t + crop.orig_h,
+                  crop.pad_l:crop.pad_l + crop.orig_w].contiguous()

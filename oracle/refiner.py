@@ -1,0 +1,74 @@
+"""CPU restatement of the DSINE NRN refiner loop -- TEST INFRASTRUCTURE ONLY.
+
+Refiner::forward (src/dsine_refine.cpp:212-294) on the CPU: the ConvGRU and
+the four heads as float64 torch convolutions (the reference's brotensor
+conv2d_forward, :94-101, in higher precision), each head's output rounded to
+float as the reference's fp32 tensors are; the activations of :262-267 as
+correctly rounded floats; RayReLU, angmf_propagate and the convex upsample +
+normalise from this directory's C oracle.  The checker for
+brovisionml_amd/refiner.py; the product never imports it.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+from . import angmf_propagate, convex_upsample, ray_relu
+
+K_UP, N_ITER, PS = 8, 5, 5
+K_PI32 = np.float32(3.14159265358979323846)   # src/dsine_refine.cpp:26
+
+
+def _sigmoid_f32(x):
+    return (1.0 / (1.0 + np.exp(-np.asarray(x, np.float64)))).astype(np.float32)
+
+
+def refine_forward(weights, normal, feature, hidden, intr, fuv, ray8, uv8, trace=None,
+                   nthreads: int = 1):
+    """weights: name -> OIHW / (C,) float32 arrays; normal (3, H, W), feature
+    and hidden (C, H, W) float32; intr unused beyond fuv = (fu, cu, fv, cv);
+    ray8 (3, H, W) and uv8 (2, H, W) float32 as build_ray8 / build_uv give
+    them.  Returns the last up-sampled map (3, 8H, 8W) float32; trace, when
+    given, receives each iteration's (pred_norm, up)."""
+    import torch
+    import torch.nn.functional as F
+
+    del intr
+    _, H, W = normal.shape
+    t64 = lambda a: torch.as_tensor(np.asarray(a, np.float64))[None]
+    w = {k: torch.as_tensor(np.asarray(v, np.float64)) for k, v in weights.items()}
+
+    def conv(x, name, pad):
+        return F.conv2d(x, w[name + ".weight"], w[name + ".bias"], padding=pad)
+
+    def head(name, x):
+        h = torch.relu(conv(x, name + ".0", 1))
+        h = torch.relu(conv(h, name + ".2", 0))
+        return conv(h, name + ".4", 0)[0].numpy().astype(np.float32)
+
+    uv = t64(uv8)
+    pred = ray_relu(np.asarray(normal, np.float32).reshape(3, -1), ray8.reshape(3, -1), H, W)
+    feat_map = torch.cat([t64(feature), uv], dim=1)
+    h = t64(hidden)
+    up = None
+    for _ in range(N_ITER):
+        hx = torch.cat([h, feat_map], dim=1)
+        z = torch.sigmoid(conv(hx, "gru.convz", 2))
+        r = torch.sigmoid(conv(hx, "gru.convr", 2))
+        q = torch.tanh(conv(torch.cat([r * h, feat_map], dim=1), "gru.convq", 2))
+        h_new = (1 - z) * h + z * q
+        hin = torch.cat([h_new, uv], dim=1)
+        prob = _sigmoid_f32(head("prob_head", hin))
+        xy = head("xy_head", hin)
+        angle = (_sigmoid_f32(head("angle_head", hin)).astype(np.float64)
+                 * np.float64(K_PI32)).astype(np.float32)
+        pred = angmf_propagate(pred.reshape(1, 3, -1), prob.reshape(1, PS * PS, -1),
+                               xy.reshape(1, 2 * PS * PS, -1), angle.reshape(1, PS * PS, -1),
+                               ray8.reshape(3, -1), fuv, H, W, PS, nthreads=nthreads)
+        pred = pred.reshape(3, -1)
+        mask = head("up_prob_head", hin)
+        up = convex_upsample(pred.reshape(1, 3, H, W), mask[None], H, W, K_UP, normalize=True,
+                             eps=float(np.float32(1e-12)), nthreads=nthreads)[0]
+        if trace is not None:
+            trace.append((pred.reshape(3, H, W).copy(), up))
+        h = h_new
+    return up
