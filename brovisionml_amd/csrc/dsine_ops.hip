@@ -448,19 +448,23 @@ __device__ __forceinline__ float sigmoid_f32(float x) {
 // [0, 1.6]: Chebyshev fits (computed for this kernel) with
 // sin(h) = h + h^3 S(u) to 8e-9 and cos(h) = 1 + u C(u) to 5e-10; then
 // sin t = 2 sin h cos h and cos t = cos^2 h - sin^2 h.
+// Evaluated in v = t^2 = 4u with the coefficients of S and C scaled by powers
+// of 4, which forms 2 sin h directly: every intermediate is the u-form's
+// times a power of two, so the results are bit-identical to evaluating in u
+// and two instructions shorter.
 __device__ __forceinline__ void sincos_small(float t, float& st, float& ct) {
-    const float h = 0.5f * t, u = h * h;
-    float p = fmaf(u, 2.630318e-06f, -0.00019821344f);
-    p = fmaf(u, p, 0.008333231f);
-    p = fmaf(u, p, -0.16666666f);
-    const float s = fmaf(h * u, p, h);
-    float q = fmaf(u, -2.625131e-07f, 2.4772546e-05f);
-    q = fmaf(u, q, -0.0013888624f);
-    q = fmaf(u, q, 0.041666657f);
-    q = fmaf(u, q, -0.5f);
-    const float c = fmaf(u, q, 1.0f);
-    const float sc = s * c;
-    st = sc + sc;
+    const float v = t * t;
+    float p = fmaf(v, 2.630318e-06f * 0x1p-8f, -0.00019821344f * 0x1p-6f);
+    p = fmaf(v, p, 0.008333231f * 0x1p-4f);
+    p = fmaf(v, p, -0.16666666f * 0x1p-2f);
+    const float s2 = fmaf(t * v, p, t);  // 2 sin h
+    float q = fmaf(v, -2.625131e-07f * 0x1p-10f, 2.4772546e-05f * 0x1p-8f);
+    q = fmaf(v, q, -0.0013888624f * 0x1p-6f);
+    q = fmaf(v, q, 0.041666657f * 0x1p-4f);
+    q = fmaf(v, q, -0.5f * 0x1p-2f);
+    const float c = fmaf(v, q, 1.0f);  // cos h
+    st = s2 * c;
+    const float s = 0.5f * s2;
     ct = fmaf(c, c, -(s * s));
 }
 
@@ -543,6 +547,11 @@ __device__ __forceinline__ bool nbr_red_f64(float mxf, float myf, float mzf, int
     return true;
 }
 
+// LDS-space (address space 3) views of the halo records: 32-bit addresses
+typedef __attribute__((address_space(3))) const char lds_byte;
+typedef float lds_f4 __attribute__((ext_vector_type(4)));
+typedef double lds_d2 __attribute__((ext_vector_type(2)));
+
 // The source-normal halo of a tile in LDS: one 48-byte record per source
 // pixel of the tile's replicate-padded window, read with one address per
 // neighbour and immediate offsets.
@@ -590,8 +599,9 @@ __host__ __device__ constexpr int group_waves(int K) {
 constexpr int kWgWaves = 8;
 
 // Neighbours whose planes a wave loads before the halo staging and its
-// barrier; the rest are loaded after it.
-constexpr int kPreLoads = 2;
+// barrier; the rest are loaded after it.  One measured best on a 256 x 256
+// k = 5 call (8.6 us, against 8.8 us with two and 8.9 us with none).
+constexpr int kPreLoads = 1;
 
 // Source-normal halo records of a TW x TH tile.
 __host__ __device__ inline int halo_count(int K, int TW, int TH) {
@@ -730,7 +740,13 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     // addresses and discard the result).
     // loads in consumption order: ray, then per neighbour its 4 planes; the
     // planes of the first kPreLoads neighbours go out before the staging,
-    // the rest after its barrier
+    // the rest after its barrier.  Vector loads complete in issue order, so
+    // the neighbour loop below consumes them one neighbour at a time: a
+    // scheduling barrier after each neighbour's loads keeps them in that
+    // order, and the loop's register fences keep the compiler from hoisting
+    // one neighbour's arithmetic ahead of the previous one's, which would
+    // wait for late data before using early data (8.6 us against 9.3 us on
+    // a 256 x 256 k = 5 call with cold inputs).
     float rxf, ryf, rzf;
     if constexpr (!SR) {
         const __amdgpu_buffer_rsrc_t rry =
@@ -759,7 +775,10 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     };
     constexpr int PRE = kPreLoads < NR ? kPreLoads : NR;
 #pragma unroll
-    for (int i = 0; i < PRE; ++i) load_planes(i);
+    for (int i = 0; i < PRE; ++i) {
+        load_planes(i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     // Threads past the halo write a spare record: an unconditional use keeps
     // the compiler from sinking the halo loads behind the plane loads.
     stage_halo(hm[0], hm[1], hm[2], min((int)threadIdx.x, nhalo), hw, ty0 - P, tx0 - P, H, W, a,
@@ -795,7 +814,10 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
         rzf = r.z;
     }
 #pragma unroll
-    for (int i = PRE; i < NR; ++i) load_planes(i);
+    for (int i = PRE; i < NR; ++i) {
+        load_planes(i);
+        __builtin_amdgcn_sched_barrier(0);
+    }
     {
         // cos(v', r) = v'.r / max(|v'||r|, 1e-8) with |v'| = 1
         const float r2 = fmaf(rxf, rxf, fmaf(ryf, ryf, rzf * rzf));
@@ -804,19 +826,36 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
         const float dd_min = (float)a.dd_min;
         // this lane's window in the halo (lanes past the tile use its last row)
         const int hrow = (ty < TH) ? ty : TH - 1;
-        const char* hbase = reinterpret_cast<const char*>(hl + hrow * hw + tx);
+        // (an LDS-space pointer: 32-bit record addresses)
+        const lds_byte* hbase = (const lds_byte*)reinterpret_cast<const char*>(hl + hrow * hw + tx);
         float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f;
         float qs = 0.0f;  // sum of wi^2, for the cancellation test only
-        bool bad = false;
+        // the fp32 form's domain over the run, as running extremes: bits of
+        // |xy|^2 above kMinXY2, |t|, |dd| and |V|^2.  A NaN drops out of a
+        // min or max but not out of the sums: every NaN these would see
+        // reaches acc (through q, V, sin/cos or the weight), which phase B
+        // flags.
+        uint32_t smax = 0u;
+        float tmax = 0.0f, ddmin = __builtin_inff(), n2min = __builtin_inff();
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
+            // this neighbour's planes: the fence makes the wait for them the
+            // first use (and keeps the last slot's loads out of its branch)
+            asm volatile("" : "+v"(xs[i]), "+v"(ys[i]), "+v"(th[i]), "+v"(wt[i]));
             if (i == NR - 1 && nrun != NR) break;
             const int n = n0 + i;
             const int ky = n / K, kx = n - ky * K;
-            const HaloRec& rec = *reinterpret_cast<const HaloRec*>(
-                hbase + (ky * hw + kx) * (int)sizeof(HaloRec));
-            const float4 hm = rec.m, gt = rec.gt;
-            const double2 ab = rec.ab;
+            // the record offset in a scalar register, added once (the compiler
+            // would otherwise fold it into a 64-bit multiply-add per neighbour)
+            int roff = (ky * hw + kx) * (int)sizeof(HaloRec);
+            asm("" : "+s"(roff));
+            const lds_byte* rb = hbase + roff;
+            const lds_f4 hm4 = *(const __attribute__((address_space(3))) lds_f4*)rb;
+            const lds_d2 ab2 = *(const __attribute__((address_space(3))) lds_d2*)(rb + 16);
+            const lds_f4 gt4 = *(const __attribute__((address_space(3))) lds_f4*)(rb + 32);
+            const float4 hm = make_float4(hm4.x, hm4.y, hm4.z, hm4.w);
+            const float4 gt = make_float4(gt4.x, gt4.y, gt4.z, gt4.w);
+            const double2 ab = make_double2(ab2.x, ab2.y);
             const float xv = xs[i], yv = ys[i];
             const float t = LG ? sigmoid_f32(th[i]) * kPiF : th[i];
             // q in double (exact products, one rounding), the rest fp32;
@@ -831,8 +870,10 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
             const float Vx = fmaf(gt.x, xv, -q * gt.z);
             const float Vy = fmaf(gt.y, yv, -q * gt.w);
             const float n2 = fmaf(Vx, Vx, fmaf(Vy, Vy, q * q));
-            bad |= (__builtin_bit_cast(uint32_t, s) - kXY2Lo > kXY2Span) | !(fabsf(t) <= 3.2f) |
-                   !(fabsf(dd) >= dd_min) | !(n2 >= kMinV2);
+            smax = max(smax, __builtin_bit_cast(uint32_t, s) - kXY2Lo);
+            tmax = fmaxf(tmax, fabsf(t));
+            ddmin = fminf(ddmin, fabsf(dd));
+            n2min = fminf(n2min, n2);
             float st, ct;
             sincos_small(t, st, ct);
             const float S = st * copysignf(__builtin_amdgcn_rsqf(n2), dd);
@@ -861,7 +902,11 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
             acc1 = fmaf(py, wi, acc1);
             acc2 = fmaf(pz, wi, acc2);
             qs = fmaf(wi, wi, qs);
+            // this neighbour done before the next one's data are waited for
+            asm volatile("" : "+v"(acc0), "+v"(acc1), "+v"(acc2), "+v"(qs));
         }
+        const bool bad = (smax > kXY2Span) | !(tmax <= 3.2f) | !(ddmin >= dd_min) |
+                         !(n2min >= kMinV2);
         part[r * npx + j] = make_float4(acc0, acc1, acc2, bad ? __builtin_nanf("") : qs);
     }
     __syncthreads();
