@@ -451,7 +451,7 @@ __device__ __forceinline__ float sigmoid_f32(float x) {
 // Evaluated in v = t^2 = 4u with the coefficients of S and C scaled by powers
 // of 4, which forms 2 sin h directly: every intermediate is the u-form's
 // times a power of two, so the results are bit-identical to evaluating in u
-// and two instructions shorter.
+// and one instruction shorter.
 __device__ __forceinline__ void sincos_small(float t, float& st, float& ct) {
     const float v = t * t;
     float p = fmaf(v, 2.630318e-06f * 0x1p-8f, -0.00019821344f * 0x1p-6f);
