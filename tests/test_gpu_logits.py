@@ -112,3 +112,31 @@ def test_logits_special_values(cuda):
     assert nan_mm == 0
     assert max_abs <= TOL_ABS and max_deg <= TOL_DEG
     assert np.all(got.reshape(3, -1)[:, 60] == 0)
+
+
+@pytest.mark.parametrize("B,H,W,k", [(2, 9, 13, 1), (1, 33, 65, 3), (1, 20, 140, 5),
+                                     (2, 17, 70, 7), (1, 12, 20, 9), (1, 6, 100, 9)])
+def test_logits_window_sizes(cuda, B, H, W, k):
+    """Every window size's logits kernel (the workloads above are all k = 5):
+    random logits N(0, 2^2) for prob and angle, so the activated angles
+    span (0, pi), on narrow and wide tiles."""
+    say(f"[gpu] angmf logits shape B={B} H={H} W={W} k={k}")
+    rng = np.random.default_rng(700 + B * 1000 + H * 10 + W + k)
+    HW, K2 = H * W, k * k
+    n = rng.standard_normal((B, 3, HW))
+    n /= np.linalg.norm(n, axis=1, keepdims=True)
+    intr = wl.intrins_from_fov(8 * H, 8 * W, 60.0)
+    fuv = wl.scaled_intrinsics(intr, H, W, 8 * H, 8 * W)
+    inp = {
+        "pred_norm": n.astype(np.float32),
+        "xy": rng.standard_normal((B, 2 * K2, HW)).astype(np.float32),
+        "ray": wl.build_ray8(intr, H, W, 8 * H, 8 * W).reshape(3, HW),
+        "intrinsics": fuv,
+    }
+    lp = (2.0 * rng.standard_normal((B, K2, HW))).astype(np.float32)
+    la = (2.0 * rng.standard_normal((B, K2, HW))).astype(np.float32)
+    got, want = run(inp, lp, la, H, W, k, cuda)
+    max_abs, max_deg, nan_mm = compare(got.reshape(B, 3, -1), want.reshape(B, 3, -1))
+    say(f"    max-abs {max_abs:.3e}  max-angle {max_deg:.3e} deg")
+    assert nan_mm == 0
+    assert max_abs <= TOL_ABS and max_deg <= TOL_DEG
