@@ -114,14 +114,8 @@ def test_logits_special_values(cuda):
     assert np.all(got.reshape(3, -1)[:, 60] == 0)
 
 
-@pytest.mark.parametrize("B,H,W,k", [(2, 9, 13, 1), (1, 33, 65, 3), (1, 20, 140, 5),
-                                     (2, 17, 70, 7), (1, 12, 20, 9), (1, 6, 100, 9)])
-def test_logits_window_sizes(cuda, B, H, W, k):
-    """Every window size's logits kernel (the workloads above are all k = 5):
-    random logits N(0, 2^2) for prob and angle, so the activated angles
-    span (0, pi), on narrow and wide tiles."""
-    say(f"[gpu] angmf logits shape B={B} H={H} W={W} k={k}")
-    rng = np.random.default_rng(700 + B * 1000 + H * 10 + W + k)
+def _random_logit_inputs(seed, B, H, W, k):
+    rng = np.random.default_rng(seed + B * 1000 + H * 10 + W + k)
     HW, K2 = H * W, k * k
     n = rng.standard_normal((B, 3, HW))
     n /= np.linalg.norm(n, axis=1, keepdims=True)
@@ -135,8 +129,42 @@ def test_logits_window_sizes(cuda, B, H, W, k):
     }
     lp = (2.0 * rng.standard_normal((B, K2, HW))).astype(np.float32)
     la = (2.0 * rng.standard_normal((B, K2, HW))).astype(np.float32)
+    return inp, lp, la
+
+
+@pytest.mark.parametrize("B,H,W,k", [(2, 9, 13, 1), (1, 33, 65, 3), (1, 20, 140, 5),
+                                     (2, 17, 70, 7), (1, 12, 20, 9), (1, 6, 100, 9)])
+def test_logits_window_sizes(cuda, B, H, W, k):
+    """Every window size's logits kernel (the workloads above are all k = 5):
+    random logits N(0, 2^2) for prob and angle, so the activated angles
+    span (0, pi), on narrow and wide tiles."""
+    say(f"[gpu] angmf logits shape B={B} H={H} W={W} k={k}")
+    inp, lp, la = _random_logit_inputs(700, B, H, W, k)
     got, want = run(inp, lp, la, H, W, k, cuda)
     max_abs, max_deg, nan_mm = compare(got.reshape(B, 3, -1), want.reshape(B, 3, -1))
     say(f"    max-abs {max_abs:.3e}  max-angle {max_deg:.3e} deg")
     assert nan_mm == 0
     assert max_abs <= TOL_ABS and max_deg <= TOL_DEG
+
+
+@pytest.mark.parametrize("B,H,W,k", [(1, 20, 200, 5), (2, 9, 13, 7)])
+@pytest.mark.parametrize("precise", [False, True])
+def test_logits_ray_from_intrinsics(cuda, B, H, W, k, precise):
+    """Logits with the ray formed in the kernel (BVML_DSINE_LOGITS |
+    BVML_DSINE_RAY_FROM_INTRINSICS): bit-identical to the same call on
+    build_ray8's planes, which the oracle checks."""
+    import torch
+    say(f"[gpu] angmf logits, ray from intrinsics B={B} {H}x{W} k={k} precise={precise}")
+    inp, lp, la = _random_logit_inputs(900, B, H, W, k)
+    got, want = run(inp, lp, la, H, W, k, cuda, precise)
+    fu, cu, fv, cv = inp["intrinsics"]
+    synth = dsine.angmf_propagate(to_dev(inp["pred_norm"], cuda), to_dev(lp, cuda),
+                                  to_dev(inp["xy"], cuda), to_dev(la, cuda), None,
+                                  fu, cu, fv, cv, H, W, precise=precise, logits=True)
+    torch.cuda.synchronize()
+    synth = synth.cpu().numpy()
+    assert np.array_equal(got.view(np.uint32), synth.view(np.uint32))
+    max_abs, max_deg, nan_mm = compare(got.reshape(B, 3, -1), want.reshape(B, 3, -1))
+    say(f"    max-abs {max_abs:.3e}  max-angle {max_deg:.3e} deg")
+    assert nan_mm == 0
+    assert max_abs <= (2.5e-7 if precise else TOL_ABS) and max_deg <= TOL_DEG
