@@ -1,29 +1,35 @@
 """Benchmark: DSINE AngMF propagate on one MI355X (and, with --op upsample,
-the refiner's fused convex upsample + L2-normalise).
+the refiner's fused convex upsample + L2-normalise; --op refiner, the whole
+refiner forward).
 
 A step is one pass of the hot path over one batch: one angmf_propagate call
 (workload 2: B=1, 256x256, k=5, fp32) through the C ABI, inputs resident in
-HBM.  To keep the 256 MB Infinity Cache from serving the inputs, each step
-reads a different one of `--sets` input copies (together > 512 MB); the warm
-number (same inputs every step) is reported beside it.
+HBM.  Each step reads a different one of `--sets` input sets, each an
+independent seeded draw of the workload (draw 0 is its stated seed), which
+together exceed 512 MB, so the 256 MB Infinity Cache cannot serve them; the
+timed replay starts after a 512 MB flush.  The warm figure (one set, read by
+every step) is measured after the cold ones, on a set of its own.
 
 The K timed steps are the K kernel launches of one captured HIP graph,
 replayed once between two HIP events on the replay stream: the kernels run
-back to back, so the region measures the GPU, not Python's launch overhead
-(the same K steps launched eagerly from Python are reported as "eager").
+back to back, so the region measures the GPU, not Python's launch overhead.
+Per-launch durations come from a second, eager pass over the same rotation
+with an event pair around every launch (median and max reported).
 
 Prints one JSON line (rank 0):
-  value       Mpixel/s over the timed region (K steps / event time)
-  roofline    HBM roofline of the kernel: algorithmic bytes per launch /
-              average launch duration (event time of the region / K)
+  value         Mpixel/s over the timed region (K steps / event time)
+  roofline      algorithmic bytes per launch / mean launch time, against the
+                8 TB/s HBM peak, with the same-box read ceiling (a streaming
+                read of each set's inputs) and copy ceiling over the same
+                rotating footprint
   cpu_baseline  the CPU oracle (double-precision restatement of the
-              reference's CPU twin), one thread, on a bounded sample
-  cpu_baseline_all_cores  the same oracle with its rows over the host's
-              CPU share (OpenMP), labelled separately
-
---op upsample measures bvml_dsine_convex_upsample_f32 on the refiner's
-shape (C=3, s=8) at the 256x256 grid (a 2048x2048 output) the same way; its
-value is output Mpixel/s.
+                reference's CPU twin), one thread, on a bounded sample
+  configs       the other workloads (0, 1, 3, 4): cold and warm time per call,
+                Mpixel/s, roofline fraction and their own CPU baseline
+  fp64          the double-precision reference-order kernel on the headline
+                workload (BVML_DSINE_FP64)
+  recompute     per set, the pixels below the fast path's cancellation
+                threshold (recomputed in double), from the oracle's sums
 """
 from __future__ import annotations
 
@@ -40,6 +46,7 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
+FLUSH_BYTES = 512 << 20
 
 
 def cpu_model() -> str:
@@ -98,31 +105,43 @@ def timed_cpu(fn, seconds: float):
 
 
 class Timer:
-    """Graph-captured timing of K launches of `launch(i)` (i selects the
-    input set), plus the eager and warm variants and the same-box copy
-    ceiling over the same footprint."""
+    """Timing of `launch(i)` (i selects the input set) over a rotation of
+    nsets sets: graph-captured cold and warm replays, an eager pass with
+    per-launch events, and the same-box read and copy ceilings over the same
+    footprint."""
 
-    def __init__(self, dev, launch, nsets: int, steps: int, warmup: int, bytes_per_call: int):
+    def __init__(self, dev, launch, nsets: int, steps: int, warmup: int, bytes_per_call: int,
+                 warm_index: int | None = None):
         import torch
         self.torch, self.dev = torch, dev
         self.launch, self.nsets, self.steps = launch, nsets, steps
         self.bytes_per_call = bytes_per_call
+        self.warm_index = warm_index
+        self._flush_buf = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
         for i in range(warmup):
             launch(i % nsets)
         torch.cuda.synchronize()
 
-    def capture(self, rotate: bool):
+    def flush(self):
+        """Read 512 MB, so nothing read before stays in the Infinity Cache.  A
+        read, not a write: 512 MB of dirty lines would be written back while
+        the timed kernels run and take HBM bandwidth from them."""
+        self._flush_sum = self._flush_buf.sum()
+
+    def capture(self, sets):
         g = self.torch.cuda.CUDAGraph()
         with self.torch.cuda.graph(g):
-            for i in range(self.steps):
-                self.launch(i % self.nsets if rotate else 0)
+            for i in sets:
+                self.launch(i)
         return g
 
-    def timed_graph(self, g):
+    def timed_graph(self, g, flush: bool):
         torch = self.torch
         stream = torch.cuda.current_stream(self.dev)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
+        if flush:
+            self.flush()
         torch.cuda.synchronize()
         e0.record(stream)
         g.replay()
@@ -130,43 +149,73 @@ class Timer:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e-3
 
-    def timed_eager(self) -> float:
+    def cold(self) -> float:
+        """Seconds for self.steps launches rotating over the sets, the replay
+        starting after a flush."""
+        g = self.capture([i % self.nsets for i in range(self.steps)])
+        g.replay()
+        return self.timed_graph(g, flush=True)
+
+    def warm(self) -> float:
+        """Seconds for self.steps launches of one set (Infinity Cache warm)."""
+        w = self.warm_index if self.warm_index is not None else 0
+        g = self.capture([w] * self.steps)
+        g.replay()
+        return self.timed_graph(g, flush=False)
+
+    def eager(self):
+        """(total s, per-launch us list): the rotation launched one by one
+        from Python with an event pair around each launch (after a flush)."""
         torch = self.torch
+        stream = torch.cuda.current_stream(self.dev)
+        ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+              for _ in range(self.steps)]
+        self.flush()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
         for i in range(self.steps):
+            ev[i][0].record(stream)
             self.launch(i % self.nsets)
+            ev[i][1].record(stream)
         torch.cuda.synchronize()
-        return time.perf_counter() - t0
+        total = time.perf_counter() - t0
+        return total, [a.elapsed_time(b) * 1e3 for a, b in ev]
 
-    def run(self):
-        """(cold s, warm s, eager s) for self.steps steps."""
-        g_cold = self.capture(True)
-        g_warm = self.capture(False)
-        for _ in range(2):
-            g_cold.replay()
-            g_warm.replay()
-        self.torch.cuda.synchronize()
-        return self.timed_graph(g_cold), self.timed_graph(g_warm), self.timed_eager()
+    def read_ceiling_gbps(self, bufs) -> float:
+        """A streaming read of one set's inputs (one flat buffer per set,
+        float4 non-temporal loads, tests/hw/probe.hip) per launch, over the
+        same rotation, captured in one graph: the same-box read rate of this
+        footprint."""
+        torch = self.torch
+        from tests.hw import probe
+        part = torch.empty(probe.read_blocks(), dtype=torch.float32, device=self.dev)
+        n_rep = max(self.steps, 2 * len(bufs))
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            sptr = torch.cuda.current_stream(self.dev).cuda_stream
+            for i in range(n_rep):
+                b = bufs[i % len(bufs)]
+                probe.stream_read(b.data_ptr(), b.numel(), part.data_ptr(), sptr)
+        g.replay()
+        t = self.timed_graph(g, flush=True)
+        return sum(bufs[i % len(bufs)].numel() * 4 for i in range(n_rep)) / t / 1e9
 
     def copy_ceiling_gbps(self) -> float:
         """Device copies that each move one launch's algorithmic bytes (half
-        read, half written), rotating over the same footprint as the kernel's
-        input sets so they miss the Infinity Cache alike, captured in one
-        graph like the kernel's launches."""
+        read, half written), rotating over a footprint of the kernel's
+        size, captured in one graph like the kernel's launches."""
         torch = self.torch
         n_copy = self.bytes_per_call // 8
-        src = torch.ones(self.nsets, n_copy, dtype=torch.float32, device=self.dev)
+        nsets = max(2, int(np.ceil(FLUSH_BYTES / (2 * n_copy * 4))))
+        src = torch.ones(nsets, n_copy, dtype=torch.float32, device=self.dev)
         dst = torch.empty_like(src)
-        pairs = [(dst[i], src[i]) for i in range(self.nsets)]
-        n_rep = 4 * self.nsets
+        n_rep = max(self.steps, 2 * nsets)
         g = torch.cuda.CUDAGraph()
         with torch.cuda.graph(g):
             for i in range(n_rep):
-                d, s_ = pairs[i % self.nsets]
-                d.copy_(s_)
+                dst[i % nsets].copy_(src[i % nsets])
         g.replay()
-        t = self.timed_graph(g)
+        t = self.timed_graph(g, flush=True)
         return 2 * n_copy * 4 * n_rep / t / 1e9
 
     def calib(self) -> None:
@@ -198,9 +247,9 @@ def base_line(args, metric, value, unit, ms_per_step, config):
     }
 
 
-def roofline(bytes_per_call, launch_s, traffic, kernel, copy_gbps):
+def roofline(bytes_per_call, launch_s, traffic, kernel, copy_gbps, read_gbps=None):
     achieved = bytes_per_call / launch_s / 1e9
-    return {
+    r = {
         "bound": "hbm",
         "achieved": round(achieved, 1),
         "peak": HBM_PEAK_GBPS,
@@ -212,96 +261,258 @@ def roofline(bytes_per_call, launch_s, traffic, kernel, copy_gbps):
         "launch_us_mean": round(launch_s * 1e6, 3),
         "copy_ceiling_gbps": round(copy_gbps, 1),
     }
+    if read_gbps is not None:
+        r["read_ceiling_gbps"] = round(read_gbps, 1)
+    return r
 
 
-def bench_angmf(args, dev) -> dict:
+# ---------------------------------------------------------------------------
+# angmf_propagate
+# ---------------------------------------------------------------------------
+
+PLANES = ("pred_norm", "prob", "xy", "angle")
+
+
+def _activate_logits(inp):
+    """The heads' raw logits of a draw's planes: the prob planes' logits and
+    the angle planes' logits of angle / pi, so the activations give them back."""
+    inp = dict(inp)
+    for key, scale in (("prob", 1.0), ("angle", np.pi)):
+        q = np.clip(inp[key].astype(np.float64) / scale, 1e-6, 1 - 1e-6)
+        inp[key] = np.log(q / (1.0 - q)).astype(np.float32)
+    return inp
+
+
+class AngmfSets:
+    """nsets independent draws of a workload on the device, each one flat
+    buffer (so a single reduction reads a whole set) with views per tensor,
+    and an output per set."""
+
+    def __init__(self, w, nsets, dev, logits=False, extra_warm=True):
+        import torch
+        self.w, self.nsets = w, nsets
+        self.sets, self.bufs, self.outs, self.host = [], [], [], []
+        total = nsets + (1 if extra_warm else 0)
+        for d in range(total):
+            inp = w_inputs(w, d if d < nsets else 0)
+            self.host.append(inp if d < nsets else None)
+            dev_inp = _activate_logits(inp) if logits else inp
+            arrs = [np.ascontiguousarray(dev_inp[k], np.float32).ravel() for k in PLANES]
+            arrs.append(np.ascontiguousarray(inp["ray"], np.float32).ravel())
+            flat = torch.from_numpy(np.concatenate(arrs)).to(dev)
+            views, off = {}, 0
+            for key, a in zip(PLANES + ("ray",), arrs):
+                views[key] = flat[off:off + a.size]
+                off += a.size
+            self.sets.append(views)
+            self.bufs.append(flat)
+            self.outs.append(torch.empty_like(views["pred_norm"]))
+        self.intr = self.host[0]["intrinsics"]
+        self.warm_index = nsets if extra_warm else 0
+
+
+def w_inputs(w, draw):
+    return wl_mod().make_inputs(w, draw)
+
+
+def wl_mod():
+    from brovisionml_amd import workloads
+    return workloads
+
+
+def nsets_for(bytes_per_call: int, cap: int = 256) -> int:
+    return int(min(cap, max(2, np.ceil(FLUSH_BYTES / bytes_per_call))))
+
+
+def angmf_launcher(sets: AngmfSets, dev, flags: int, ray_from_intrinsics: bool, calls: int):
     import torch
-    import oracle
-    from brovisionml_amd import _lib, workloads as wl
-
-    w = wl.WORKLOADS[args.workload]
-    inp = wl.make_inputs(w)
-    fu, cu, fv, cv = inp["intrinsics"]
-    B, H, W, k = w.B, w.H, w.W, w.k
-    bytes_per_call = w.algorithmic_bytes(shared_ray=True) // w.calls
-    flags = _lib.DEFAULT
-    if args.ray_from_intrinsics:
-        flags |= _lib.RAY_FROM_INTRINSICS
-        bytes_per_call -= 3 * w.HW * 4  # the shared ray's 3 planes are not read
-    cpu_inp = inp  # the CPU leg always runs the op on activated planes
-    if args.logits:
-        # the heads' raw logits: the prob planes' logits and the angle
-        # planes' logits of angle / pi, so the activations give back the
-        # workload's own planes
-        flags |= _lib.LOGITS
-        inp = dict(inp)
-        for key, scale in (("prob", 1.0), ("angle", np.pi)):
-            q = np.clip(inp[key].astype(np.float64) / scale, 1e-6, 1 - 1e-6)
-            inp[key] = np.log(q / (1.0 - q)).astype(np.float32)
-    nsets = args.sets or max(2, int(np.ceil(512e6 / bytes_per_call)))
-
-    base = {key: torch.from_numpy(np.ascontiguousarray(inp[key])).to(dev)
-            for key in ("pred_norm", "prob", "xy", "angle", "ray")}
-    sets = [base] + [{key: t.clone() for key, t in base.items()} for _ in range(nsets - 1)]
-    outs = [torch.empty_like(s["pred_norm"]) for s in sets]
+    from brovisionml_amd import _lib
+    w = sets.w
+    fu, cu, fv, cv = sets.intr
 
     def launch(i: int) -> None:
-        s = sets[i]
+        s = sets.sets[i]
         sptr = torch.cuda.current_stream(dev).cuda_stream
         pn = s["pred_norm"]
-        for _ in range(w.calls):
-            dst = outs[i]
+        for c in range(calls):
+            # a chain: each call's output feeds the next call's pred_norm; the
+            # set's output buffer alternates with a second one
+            dst = sets.outs[i] if c % 2 == 0 else sets.outs2[i]
             st = _lib.angmf_propagate_f32(
                 pn.data_ptr(), s["prob"].data_ptr(), s["xy"].data_ptr(), s["angle"].data_ptr(),
-                0 if args.ray_from_intrinsics else s["ray"].data_ptr(), fu, cu, fv, cv, B, H, W,
-                k, 0, dst.data_ptr(), flags, sptr)
+                0 if ray_from_intrinsics else s["ray"].data_ptr(), fu, cu, fv, cv, w.B, w.H,
+                w.W, w.k, 0, dst.data_ptr(), flags, sptr)
             if st != 0:
                 raise RuntimeError(f"angmf_propagate_f32 failed: {st} {_lib.last_error()}")
             pn = dst
 
-    tm = Timer(dev, launch, nsets, args.steps, args.warmup, bytes_per_call)
-    t_cold, t_warm, t_eager = tm.run()
-    copy_gbps = tm.copy_ceiling_gbps()
+    if calls > 1:
+        sets.outs2 = [torch.empty_like(o) for o in sets.outs]
+    return launch
+
+
+def recompute_counts(sets: AngmfSets, flags: int, nthreads: int):
+    """Per set: pixels below the fast path's cancellation threshold, from
+    the oracle's double sums (|acc|^2 / sum (prob/|p|)^2)."""
+    import oracle
+    from brovisionml_amd import _lib
+    w = sets.w
+    t = _lib.angmf_recompute_ratio(flags)
+    counts = []
+    for inp in sets.host:
+        if inp is None:
+            continue
+        _, acc, qs = oracle.angmf_propagate(inp["pred_norm"], inp["prob"], inp["xy"],
+                                            inp["angle"], inp["ray"], inp["intrinsics"], w.H,
+                                            w.W, w.k, nthreads=nthreads, return_acc=True,
+                                            return_qs=True)
+        a2 = (acc.reshape(w.B, 3, -1) ** 2).sum(axis=1)
+        counts.append(int((a2 < t * qs).sum()))
+    return t, counts
+
+
+def cpu_baseline_angmf(w, inp, seconds: float, nthreads: int = 1):
+    """The oracle on whole images (or row bands of a large one) of the
+    workload for about `seconds`: (Mpixel/s, sample text)."""
+    import oracle
+    H, W, k, B = w.H, w.W, w.k, w.B
+    band = H if (B * w.HW <= 1 << 17 or w.calls > 1) else max(1, (1 << 17) // (B * W))
+    px_done, passes, y0 = 0, 0, 0
+    t0 = time.perf_counter()
+    while True:
+        y1 = min(H, y0 + band)
+        pn = inp["pred_norm"]
+        for _ in range(w.calls):
+            # (a chain runs whole images: band == H whenever calls > 1)
+            pn = oracle.angmf_propagate(pn, inp["prob"], inp["xy"], inp["angle"], inp["ray"],
+                                        inp["intrinsics"], H, W, k, rows=(y0, y1),
+                                        nthreads=nthreads)
+        px_done += B * (y1 - y0) * W * w.calls
+        passes += 1
+        y0 = 0 if y1 >= H else y1
+        el = time.perf_counter() - t0
+        if el >= seconds:
+            break
+    what = (f"{passes} passes of {band} of {H} rows" if band < H else f"{passes} passes")
+    return px_done / el / 1e6, f"{what} over the {w.name} input (B={B}, {H}x{W}, k={k}), {el:.1f} s"
+
+
+def measure_angmf(args, dev, w, steps, warmup, flags=0, ray_from_intrinsics=False,
+                  logits=False, with_ceilings=True, with_eager=True):
+    """Cold/warm timing of one workload; returns a dict of figures."""
+    import torch
+    bytes_per_call = w.algorithmic_bytes(shared_ray=True) // w.calls
+    if ray_from_intrinsics:
+        bytes_per_call -= 3 * w.HW * 4
+    nsets = args.sets or nsets_for(bytes_per_call * w.calls)
+    sets = AngmfSets(w, nsets, dev, logits=logits)
+    launch = angmf_launcher(sets, dev, flags, ray_from_intrinsics, w.calls)
+    tm = Timer(dev, launch, nsets, steps, warmup, bytes_per_call, warm_index=sets.warm_index)
+    t_cold = tm.cold()
+    res = {"sets": sets, "timer": tm, "bytes_per_call": bytes_per_call, "nsets": nsets,
+           "launch_s": t_cold / (steps * w.calls), "t_cold": t_cold}
+    if with_eager:
+        t_eager, per = tm.eager()
+        res["t_eager"], res["per_launch_us"] = t_eager, per
+    res["t_warm"] = tm.warm()
+    if with_ceilings:
+        res["copy_gbps"] = tm.copy_ceiling_gbps()
+        res["read_gbps"] = tm.read_ceiling_gbps(sets.bufs[:nsets])
+    torch.cuda.synchronize()
+    return res
+
+
+def bench_angmf(args, dev) -> dict:
+    import torch
+    from brovisionml_amd import _lib
+    W_ = wl_mod()
+
+    w = W_.WORKLOADS[args.workload]
+    flags = _lib.DEFAULT
+    if args.ray_from_intrinsics:
+        flags |= _lib.RAY_FROM_INTRINSICS
+    if args.logits:
+        flags |= _lib.LOGITS
+    m = measure_angmf(args, dev, w, args.steps, args.warmup, flags, args.ray_from_intrinsics,
+                      args.logits)
+    sets, tm, bytes_per_call, nsets = m["sets"], m["timer"], m["bytes_per_call"], m["nsets"]
     if args.calib:
         tm.calib()
-
-    launch_s = t_cold / (args.steps * w.calls)
+    B, H, W, k = w.B, w.H, w.W, w.k
     px = B * H * W * w.calls * args.steps
+    per = np.array(m["per_launch_us"])
     line = base_line(
         args, "Mpixel/s (+ achieved HBM GB/s, % of peak), DSINE propagation 256x256 k=5 fp32",
-        px / t_cold / 1e6, "Mpixel/s", t_cold * 1e3 / args.steps,
+        px / m["t_cold"] / 1e6, "Mpixel/s", m["t_cold"] * 1e3 / args.steps,
         {
             "workload": w.name, "B": B, "H": H, "W": W, "k": k, "calls_per_step": w.calls,
             "ray": "from-intrinsics" if args.ray_from_intrinsics else "shared",
             "prob_angle": "logits, activated in the kernel" if args.logits else "activated",
-            "inputs": f"{nsets} rotating HBM-resident copies "
-                      f"({nsets * bytes_per_call / 1e6:.0f} MB > 256 MB Infinity Cache)",
+            "inputs": f"{nsets} independent seeded draws, rotating "
+                      f"({nsets * bytes_per_call * w.calls / 1e6:.0f} MB > 256 MB Infinity "
+                      "Cache); timed replay after a 512 MB flush",
         })
     line["roofline"] = roofline(
-        bytes_per_call, launch_s,
-        None if args.ray_from_intrinsics else traffic_from_profile("angmf", w.name),
-        f"angmf_f32_kernel<{k}>", copy_gbps)
+        bytes_per_call, m["launch_s"],
+        None if (args.ray_from_intrinsics or args.logits) else traffic_from_profile("angmf", w.name),
+        f"angmf_f32_kernel<{k}>", m["copy_gbps"], m["read_gbps"])
+    line["per_launch"] = {
+        "us_median": round(float(np.median(per)), 3),
+        "us_max": round(float(per.max()), 3),
+        "us_min": round(float(per.min()), 3),
+        "note": "eager pass over the same rotation, an event pair around each launch "
+                "(includes the events' own overhead)",
+    }
     line["warm"] = {
-        "value": round(px / t_warm / 1e6, 2),
-        "launch_us_mean": round(t_warm / (args.steps * w.calls) * 1e6, 3),
-        "achieved_gbps": round(bytes_per_call / (t_warm / (args.steps * w.calls)) / 1e9, 1),
+        "value": round(px / m["t_warm"] / 1e6, 2),
+        "launch_us_mean": round(m["t_warm"] / (args.steps * w.calls) * 1e6, 3),
+        "achieved_gbps": round(bytes_per_call / (m["t_warm"] / (args.steps * w.calls)) / 1e9, 1),
+        "note": "one set, not part of the rotation, read by every launch",
     }
     line["eager"] = {
-        "value": round(px / t_eager / 1e6, 2),
-        "us_per_step": round(t_eager / args.steps * 1e6, 3),
-        "note": "the same steps launched one by one from Python (host-bound)",
+        "value": round(px / m["t_eager"] / 1e6, 2),
+        "us_per_step": round(m["t_eager"] / args.steps * 1e6, 3),
+        "note": "the same steps launched one by one from Python with per-launch events",
     }
     line["gpu"] = torch.cuda.get_device_name(dev)
+    nt = host_share()
+    t_ratio, counts = recompute_counts(sets, flags, nt)
+    line["recompute"] = {
+        "threshold": t_ratio,
+        "pixels_per_call_mean": round(float(np.mean(counts)), 3),
+        "pixels_per_call_max": int(max(counts)),
+        "calls_with_any": int(sum(c > 0 for c in counts)),
+        "calls": len(counts),
+        "note": "pixels with |acc|^2 < threshold * sum (prob/|p|)^2 (oracle sums), which the "
+                "fast path recomputes in double",
+    }
+
+    if not args.logits and not args.ray_from_intrinsics:
+        # the double-precision reference-order kernel on the same rotation
+        fl = flags | _lib.FP64
+        launch64 = angmf_launcher(sets, dev, fl, False, w.calls)
+        k64 = max(4, args.steps // 4)
+        t64 = Timer(dev, launch64, nsets, k64, 1, bytes_per_call, warm_index=sets.warm_index)
+        t = t64.cold()
+        line["fp64"] = {
+            "kernel": f"angmf_f64_kernel<{k}>",
+            "launch_us_mean": round(t / k64 * 1e6, 3),
+            "achieved_gbps": round(bytes_per_call / (t / k64) / 1e9, 1),
+            "note": "BVML_DSINE_FP64: every neighbour in double in the reference's operation "
+                    "order, one pixel per lane",
+        }
 
     if args.logits:
         # the unfused step for comparison: the refiner's two activation
         # passes (here torch's sigmoid kernels) over the same rotating
         # logits, then the op on the activated planes
-        acts = [(torch.empty_like(s_["prob"]), torch.empty_like(s_["angle"])) for s_ in sets]
+        acts = [(torch.empty_like(s_["prob"]), torch.empty_like(s_["angle"]))
+                for s_ in sets.sets]
         kpi = float(np.float32(np.pi))
+        fu, cu, fv, cv = sets.intr
 
         def launch_unfused(i: int) -> None:
-            s_ = sets[i]
+            s_ = sets.sets[i]
             ap_, aa_ = acts[i]
             torch.sigmoid(s_["prob"], out=ap_)
             torch.sigmoid(s_["angle"], out=aa_)
@@ -310,47 +521,82 @@ def bench_angmf(args, dev) -> dict:
             st = _lib.angmf_propagate_f32(
                 s_["pred_norm"].data_ptr(), ap_.data_ptr(), s_["xy"].data_ptr(), aa_.data_ptr(),
                 0 if args.ray_from_intrinsics else s_["ray"].data_ptr(), fu, cu, fv, cv, B, H,
-                W, k, 0, outs[i].data_ptr(), flags & ~_lib.LOGITS, sptr)
+                W, k, 0, sets.outs[i].data_ptr(), flags & ~_lib.LOGITS, sptr)
             if st != 0:
                 raise RuntimeError(f"angmf_propagate_f32 failed: {st} {_lib.last_error()}")
 
         tu = Timer(dev, launch_unfused, nsets, args.steps, args.warmup, bytes_per_call)
-        g_u = tu.capture(True)
-        g_u.replay()
-        t_unfused = tu.timed_graph(g_u)
         line["unfused"] = {
-            "us_per_step": round(t_unfused / args.steps * 1e6, 3),
+            "us_per_step": round(tu.cold() / args.steps * 1e6, 3),
             "note": "torch sigmoid on the prob logits, sigmoid and * pi on the angle logits, "
                     "then the op on the activated planes; same rotating inputs, one graph",
         }
 
-    if not args.no_cpu:
-        def cpu_pass(nt):
-            return lambda: oracle.angmf_propagate(
-                cpu_inp["pred_norm"], cpu_inp["prob"], cpu_inp["xy"], cpu_inp["angle"],
-                cpu_inp["ray"], cpu_inp["intrinsics"], H, W, k, nthreads=nt)
+    inp0 = sets.host[0]
+    del sets, tm, m
+    torch.cuda.empty_cache()
 
-        passes, el = timed_cpu(cpu_pass(1), args.cpu_seconds)
+    if not args.no_cpu:
+        v, sample = cpu_baseline_angmf(w, inp0, args.cpu_seconds)
         line["cpu_baseline"] = {
-            "value": round(passes * B * w.HW * w.calls / el / 1e6, 4), "unit": "Mpixel/s",
-            "cores": 1, "kind": "port",
-            "sample": f"{passes} passes over the {w.name} input ({H}x{W}, k={k}), "
-                      f"{el:.1f} s, oracle restatement of src/dsine_ops.cpp in double",
-            "cpu": cpu_model(),
-            "host_threads": os.cpu_count(),
+            "value": round(v, 4), "unit": "Mpixel/s", "cores": 1, "kind": "port",
+            "sample": sample + ", oracle restatement of src/dsine_ops.cpp in double",
+            "cpu": cpu_model(), "host_threads": os.cpu_count(),
         }
         # the same oracle with its rows split over the host's CPU share
         # (OpenMP); the reference itself is single-threaded
-        nt = host_share()
         if nt > 1:
-            passes_n, el_n = timed_cpu(cpu_pass(nt), args.cpu_seconds / 2)
+            vn, sample_n = cpu_baseline_angmf(w, inp0, args.cpu_seconds / 2, nthreads=nt)
             line["cpu_baseline_all_cores"] = {
-                "value": round(passes_n * B * w.HW * w.calls / el_n / 1e6, 4),
-                "unit": "Mpixel/s", "cores": nt, "kind": "port",
-                "sample": f"{passes_n} passes, {el_n:.1f} s, rows over {nt} OpenMP threads",
+                "value": round(vn, 4), "unit": "Mpixel/s", "cores": nt, "kind": "port",
+                "sample": sample_n + f", rows over {nt} OpenMP threads",
             }
+
+    if args.configs and not (args.logits or args.ray_from_intrinsics):
+        line["configs"] = bench_configs(args, dev, [i for i in (0, 1, 2, 3, 4)
+                                                    if i != args.workload])
     return line
 
+
+def bench_configs(args, dev, indices) -> dict:
+    """The other workloads: cold/warm time per call, Mpixel/s, roofline
+    fraction and a CPU baseline of each."""
+    import torch
+    W_ = wl_mod()
+    out = {}
+    for idx in indices:
+        w = W_.WORKLOADS[idx]
+        steps = max(4, min(args.steps, 20 if w.B * w.HW * w.K2 > 1 << 24 else args.steps))
+        m = measure_angmf(args, dev, w, steps, 2, with_ceilings=False, with_eager=False)
+        bpc, nsets = m["bytes_per_call"], m["nsets"]
+        px_call = w.B * w.HW
+        entry = {
+            "B": w.B, "H": w.H, "W": w.W, "k": w.k, "calls_per_step": w.calls,
+            "cold_us_per_call": round(m["launch_s"] * 1e6, 3),
+            "warm_us_per_call": round(m["t_warm"] / (steps * w.calls) * 1e6, 3),
+            "mpixel_s": round(px_call / m["launch_s"] / 1e6, 1),
+            "achieved_gbps": round(bpc / m["launch_s"] / 1e9, 1),
+            "frac": round(bpc / m["launch_s"] / 1e9 / HBM_PEAK_GBPS, 4),
+            "bytes_per_call": bpc,
+            "inputs": f"{nsets} independent draws ({nsets * bpc * w.calls / 1e6:.0f} MB), "
+                      "timed after a 512 MB flush",
+        }
+        if w.calls > 1:
+            entry["note"] = f"{w.calls} chained calls per step (each output feeds the next call)"
+        inp0 = m["sets"].host[0]
+        del m
+        torch.cuda.empty_cache()
+        if not args.no_cpu:
+            v, sample = cpu_baseline_angmf(w, inp0, args.cpu_seconds / 3)
+            entry["cpu_baseline"] = {"value": round(v, 4), "unit": "Mpixel/s", "cores": 1,
+                                     "kind": "port", "sample": sample}
+        out[w.name] = entry
+    return out
+
+
+# ---------------------------------------------------------------------------
+# convex upsample
+# ---------------------------------------------------------------------------
 
 def bench_upsample(args, dev) -> dict:
     import torch
@@ -358,20 +604,24 @@ def bench_upsample(args, dev) -> dict:
     from brovisionml_amd import _lib, workloads as wl
 
     w = wl.UPSAMPLE_WORKLOADS[args.workload]
-    x, mask = wl.make_upsample_inputs(w)
     B, C, H, W, s = w.B, w.C, w.H, w.W, w.s
     bytes_per_call = w.algorithmic_bytes()
-    nsets = args.sets or max(2, int(np.ceil(512e6 / bytes_per_call)))
+    nsets = args.sets or nsets_for(bytes_per_call)
     flags = _lib.FP64 if args.precise else _lib.DEFAULT
     eps = float(np.float32(1e-12))
 
-    xs = [torch.from_numpy(x).to(dev)]
-    ms = [torch.from_numpy(mask).to(dev)]
-    for _ in range(nsets - 1):
-        xs.append(xs[0].clone())
-        ms.append(ms[0].clone())
+    xs, ms, bufs = [], [], []
+    x0 = mask0 = None
+    for d in range(nsets + 1):
+        x, mask = wl.make_upsample_inputs(w, d if d < nsets else 0)
+        if d == 0:
+            x0, mask0 = x, mask
+        flat = torch.from_numpy(np.concatenate([x.ravel(), mask.ravel()])).to(dev)
+        xs.append(flat[:x.size])
+        ms.append(flat[x.size:])
+        bufs.append(flat)
     outs = [torch.empty((B, C, s * H, s * W), dtype=torch.float32, device=dev)
-            for _ in range(nsets)]
+            for _ in range(nsets + 1)]
 
     def launch(i: int) -> None:
         sptr = torch.cuda.current_stream(dev).cuda_stream
@@ -380,14 +630,18 @@ def bench_upsample(args, dev) -> dict:
         if st != 0:
             raise RuntimeError(f"convex_upsample_f32 failed: {st} {_lib.last_error()}")
 
-    tm = Timer(dev, launch, nsets, args.steps, args.warmup, bytes_per_call)
-    t_cold, t_warm, t_eager = tm.run()
+    tm = Timer(dev, launch, nsets, args.steps, args.warmup, bytes_per_call, warm_index=nsets)
+    t_cold = tm.cold()
+    t_eager, per = tm.eager()
+    t_warm = tm.warm()
     copy_gbps = tm.copy_ceiling_gbps()
+    read_gbps = tm.read_ceiling_gbps(bufs[:nsets])
     if args.calib:
         tm.calib()
 
     launch_s = t_cold / args.steps
     opx = B * s * s * H * W * args.steps  # output pixels
+    per = np.array(per)
     line = base_line(
         args, "output Mpixel/s (+ achieved HBM GB/s, % of peak), DSINE convex upsample x8 + "
               "L2 normalise, 256x256 -> 2048x2048 fp32",
@@ -396,13 +650,16 @@ def bench_upsample(args, dev) -> dict:
             "workload": w.name, "B": B, "C": C, "H": H, "W": W, "scale": s,
             "mask": f"logits ~ N(0, {w.mask_sigma}^2)", "x": "unit normals, independent per pixel",
             "kernel_mode": "fp64" if args.precise else "fast",
-            "inputs": f"{nsets} rotating HBM-resident copies "
-                      f"({nsets * bytes_per_call / 1e6:.0f} MB > 256 MB Infinity Cache)",
+            "inputs": f"{nsets} independent seeded draws, rotating "
+                      f"({nsets * bytes_per_call / 1e6:.0f} MB > 256 MB Infinity Cache); "
+                      "timed replay after a 512 MB flush",
         })
     line["roofline"] = roofline(
         bytes_per_call, launch_s,
         None if args.precise else traffic_from_profile("upsample", w.name),
-        f"upsample8_kernel<{C}>" if s == 8 else f"upsample_kernel<{C}>", copy_gbps)
+        f"upsample8_kernel<{C}>" if s == 8 else f"upsample_kernel<{C}>", copy_gbps, read_gbps)
+    line["per_launch"] = {"us_median": round(float(np.median(per)), 3),
+                          "us_max": round(float(per.max()), 3)}
     line["warm"] = {
         "value": round(opx / t_warm / 1e6, 2),
         "launch_us_mean": round(t_warm / args.steps * 1e6, 3),
@@ -411,13 +668,15 @@ def bench_upsample(args, dev) -> dict:
     line["eager"] = {
         "value": round(opx / t_eager / 1e6, 2),
         "us_per_step": round(t_eager / args.steps * 1e6, 3),
-        "note": "the same steps launched one by one from Python (host-bound)",
+        "note": "the same steps launched one by one from Python with per-launch events",
     }
     line["gpu"] = torch.cuda.get_device_name(dev)
+    del xs, ms, bufs, outs, tm
+    torch.cuda.empty_cache()
 
     if not args.no_cpu:
         def cpu_pass(nt):
-            return lambda: oracle.convex_upsample(x, mask, H, W, s, normalize=True, eps=eps,
+            return lambda: oracle.convex_upsample(x0, mask0, H, W, s, normalize=True, eps=eps,
                                                   nthreads=nt)
 
         passes, el = timed_cpu(cpu_pass(1), args.cpu_seconds)
@@ -439,6 +698,10 @@ def bench_upsample(args, dev) -> dict:
             }
     return line
 
+
+# ---------------------------------------------------------------------------
+# refiner forward
+# ---------------------------------------------------------------------------
 
 def bench_refiner(args, dev) -> dict:
     """The whole NRN refiner forward (brovisionml_amd/refiner.py: 5 iterations
@@ -518,9 +781,12 @@ def main() -> int:
     ap.add_argument("--op", choices=("angmf", "upsample", "refiner"), default="angmf")
     ap.add_argument("--workload", type=int, default=None,
                     help="index into the op's workloads (default: angmf 2, upsample 0)")
-    ap.add_argument("--sets", type=int, default=0, help="rotating input sets (0 = auto, > 512 MB)")
+    ap.add_argument("--sets", type=int, default=0,
+                    help="rotating input sets (0 = auto: > 512 MB, at most 256)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-configs", dest="configs", action="store_false",
+                    help="angmf: skip the other workloads' sub-object")
     ap.add_argument("--ray-from-intrinsics", action="store_true",
                     help="angmf: form each pixel's ray from fu, cu, fv, cv in the kernel "
                          "(BVML_DSINE_RAY_FROM_INTRINSICS) instead of reading the ray planes")

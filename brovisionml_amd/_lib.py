@@ -32,6 +32,7 @@ EXPORTS = (
     "bvml_dsine_angmf_propagate_f32",
     "bvml_dsine_build_ray8_f32",
     "bvml_dsine_convex_upsample_f32",
+    "bvml_dsine_angmf_recompute_ratio",
     "bvml_dsine_last_error",
     "bvml_dsine_version",
 )
@@ -60,6 +61,8 @@ def load(path: str = LIB) -> ctypes.CDLL:
     lib.bvml_dsine_convex_upsample_f32.argtypes = [vp, vp, i, i, i, i, i, i, ctypes.c_float, vp,
                                                    u, vp]
     lib.bvml_dsine_convex_upsample_f32.restype = i
+    lib.bvml_dsine_angmf_recompute_ratio.argtypes = [u]
+    lib.bvml_dsine_angmf_recompute_ratio.restype = d
     lib.bvml_dsine_last_error.argtypes = []
     lib.bvml_dsine_last_error.restype = ctypes.c_char_p
     lib.bvml_dsine_version.argtypes = []
@@ -100,3 +103,9 @@ def convex_upsample_f32(x: int, mask: int, B: int, C: int, H: int, W: int, scale
     """Raw call; pointers are integer device addresses. Returns the status."""
     return load().bvml_dsine_convex_upsample_f32(x, mask, B, C, H, W, scale, int(bool(normalize)),
                                                  eps, out, flags, stream)
+
+
+def angmf_recompute_ratio(flags: int = DEFAULT) -> float:
+    """The fast path's cancellation threshold: pixels with |acc|^2 below
+    this times sum (prob/|p|)^2 are recomputed in double."""
+    return load().bvml_dsine_angmf_recompute_ratio(flags)

@@ -11,31 +11,34 @@
 // all-double formulation costs far more VALU time than the HBM traffic takes,
 // so the fast kernel evaluates every neighbour in fp32 where the error
 // analysis allows and recomputes the few pixels where it does not:
-//   * the tile's replicate-padded pred_norm halo is staged in LDS once, one
-//     record per source pixel: m' = m/|m|, g = P0.m (P0 = the source pixel's
-//     ray at depth 1, NaN unless m is a unit normal), the double products
-//     mx/fu, my/fv, then g/fu, g/fv, tu0, tv0;
 //   * the rotation axis is algebraically reduced: the reference's
 //     normalize(du + dz*tu, dv + dz*tv, dz) with dz = num/dd equals
 //     sign(dd) * V/|V| with V = (g*xs/fu - q*tu0, g*ys/fv - q*tv0, -q),
+//     g = P0.m (P0 = the source pixel's ray at depth 1) and
 //     q = xs*mx/fu + ys*my/fv on the RAW xy pair -- the xy normalisation and
-//     the quadratic terms cancel exactly, and V.m == 0, so Rodrigues reduces to
-//     m'*cos(t) + (V x m')*sin(t)/|V|;
+//     the quadratic terms cancel exactly, and V.m == 0, so Rodrigues reduces
+//     to m'*cos(t) + (V x m')*sin(t)/|V|, and V x m' = xs e1 + ys e2 - q f
+//     with three per-source vectors;
+//   * the tile's replicate-padded pred_norm halo is staged in LDS once, one
+//     record per source pixel: m' = m/|m|, g (NaN unless m is a unit
+//     normal), the double products mx/fu, my/fv, and e1, e2, f;
 //   * tier 1 forms q in double (it cancels where the xy pair is nearly
-//     perpendicular to m) and everything else -- dd, V, sin/cos, the
-//     rotation, RayReLU, the weight prob/|p|, the partial sums -- in fp32;
+//     perpendicular to m) and everything else -- dd, V x m', sin/cos (the
+//     hardware's, with an argument correction), the rotation, RayReLU, the
+//     weight prob/|p|, the partial sums -- in fp32;
 //   * a pixel goes to tier 2, the same reduced form in double, when a
 //     neighbour is outside the fp32 form's domain (|dd| near the
 //     reference's 1e-8 clamp, an xy pair out of range, a non-unit source
-//     normal, |t| > 3.2, a non-finite value) or when |acc|^2 < 1.6e-3 *
+//     normal, |t| > 3.2, a non-finite value) or when |acc|^2 < 1.85e-3 *
 //     sum(wi^2), where the final normalise would amplify tier 1's error
 //     past the parity bar; and from there to tier 3, the reference-order
 //     double body, when a neighbour is outside the double form's domain or
-//     the sum still nearly cancels.
+//     the sum still nearly cancels.  The wave that reduces a pixel group
+//     recomputes its flagged pixels by itself, one neighbour per lane.
 // Workgroups are 8 waves: G waves per 64-pixel group, each evaluating one run
-// of the window's neighbours (G = 4 at k=5), so the SPI places 2 waves per
-// SIMD and every SIMD carries the same work; two workgroups per CU run a
-// 256x256 image in one round.
+// of the window's neighbours (G = 4 or 2 at k=5, 4 at k = 7, 9), so the SPI
+// places 2 waves per SIMD and every SIMD carries the same work; two
+// workgroups per CU run a 256x256 image in one round.
 // The double-precision body is also available as its own kernel
 // (BVML_DSINE_FP64), which reproduces the CPU reference to a few ulps.
 
@@ -50,6 +53,7 @@
 
 #include "bvml_dsine.h"
 #include "status.h"
+
 
 namespace bvml {
 
@@ -87,33 +91,34 @@ constexpr uint32_t kXY2Span = __builtin_bit_cast(uint32_t, kMaxXY2) - kXY2Lo;
 // |V|^2 below this (fp32 underflow territory) also sends the pixel there.
 constexpr float kMinV2 = 1e-30f;
 
-// Tier 1 error budget.  A pixel's summed error is within delta *
+// Tier 1 error budget.  A pixel's summed error behaves like delta *
 // sqrt(sum(wi^2)) (wi = prob/|p|, a term's weight before its final
-// normalise, p the RayReLU'd rotation); a CPU emulation of every rounding of
-// tier 1 (q in double, the rest fp32, the hardware rsq at its measured
-// bound) over 1.2M random pixels -- unit normals isotropic or +z-biased,
-// angles up to 3.2, fields of view up to 140 degrees (|P0| <= 4) -- gives
-// delta <= 3.65e-7 (2.94e-7 at the 99.99th percentile).  The final normalise
-// divides the sum by |acc|, so a pixel with |acc|^2 < kAccRatio2 * sum(wi^2)
-// is recomputed and the rest stay within 3.65e-7 / sqrt(kAccRatio2) = 9.1e-6
-// per component (7.4e-6 at the 99.99th percentile).  About 1 random pixel
-// in 40,000 falls below it (none of the 256x256 bench input, whose smallest
-// ratio is 1.95e-3); the refiner's camera-facing normals practically never
-// do.  RayReLU and the sums in double would halve delta for 12 more
-// instructions per neighbour; a recompute pass costs about 2.5 us at the
-// end of its workgroup.
-constexpr double kAccRatio2 = 1.6e-3;
+// normalise, p the RayReLU'd rotation: near the ray's antipode |p| -> eps and
+// the rotation's rounding is amplified by 1/|p|, which wi carries).  Measured
+// on this kernel over input families built to stress each mechanism (random
+// and camera-facing normals, normals facing away, grazing normals, q and g
+// cancelling, checkerboards of nearly opposite normals, wide angles and
+// fields of view, saturated logits; 2.6M pixels each), pixels whose sum nearly
+// cancels show delta <= 3.17e-7.  The final normalise divides the sum by
+// |acc|, so a pixel with |acc|^2 < kAccRatio2 * sum(wi^2) is recomputed, and
+// the rest stay within 3.2e-7 / sqrt(kAccRatio2) = 7.44e-6 per component,
+// 25% inside the bar (the largest kept error measured is 4.8e-6).  About
+// 0.8 pixels of a 256x256 image of independent random unit normals fall
+// below it; the refiner's camera-facing normals practically never do.  A
+// flagged pixel costs its group's reducing wave a reload of its inputs and
+// the double evaluation, about 0.6 us at the end of its workgroup.
+constexpr double kAccRatio2 = 1.85e-3;
 
 // With BVML_DSINE_LOGITS, prob and angle hold the heads' raw logits and the
 // kernel applies the refiner's activations (src/dsine_refine.cpp:262-267):
 // prob = sigmoid(L), angle = sigmoid(L) * kPiF, kPiF the float pi of
 // src/dsine_refine.cpp:26.  Tier 1 forms them in fp32 (the angle's sigmoid
 // within 4 ulps or 3e-8 of the correctly rounded float; the weight as
-// rsq(|p|^2 (1 + exp(-L))^2)); the same emulation then gives delta <= 4.7e-7,
-// so such launches recompute below kAccRatio2Logits, which keeps the bound
-// at 8.9e-6.  Tiers 2 and 3 use the correctly rounded floats (sigmoid_ref).
+// rsq(|p|^2 (1 + exp(-L))^2)); the same measurement gives delta <= 3.10e-7
+// (saturated logits N(0, 30^2)), inside the same threshold's 3.2e-7.  Tiers
+// 2 and 3 use the correctly rounded floats (sigmoid_ref).
 constexpr float kPiF = 3.14159265358979323846f;
-constexpr double kAccRatio2Logits = 2.8e-3;
+constexpr double kAccRatio2Logits = 1.85e-3;
 
 // Tier 2 (the double-precision reduced form of flagged pixels) hands a pixel
 // to the reference-order body when its sum nearly cancels: below
@@ -280,7 +285,7 @@ struct AngmfArgs {
     // fp32 kernel: TW x TH output tile per workgroup, M groups of 64 pixels,
     // G waves per group (one run of the window's neighbours each) -> 64*M*G
     // threads.
-    int TW, TH, M, tiles_x, tiles_per_img;
+    int G, TW, TH, M, tiles_x, tiles_per_img;
     double ifu64, ifv64;  // 1/fu, 1/fv
     double tu_c, tv_c;    // (0.5 - cu)/fu, (0.5 - cv)/fv: source ray tu0 = sx/fu + tu_c
     double dd_min;        // tier 1: |dd| below this sends a pixel to the recompute
@@ -443,31 +448,6 @@ __device__ __forceinline__ float sigmoid_f32(float x) {
     return tiny ? 0.0f : fmaf(r, fmaf(-d, r, 1.0f), r);
 }
 
-// sin and cos of t for |t| <= 3.2 (callers send larger |t| to the
-// reference-order path).  Half-angle polynomials in u = h^2, h = t/2 in
-// [0, 1.6]: Chebyshev fits (computed for this kernel) with
-// sin(h) = h + h^3 S(u) to 8e-9 and cos(h) = 1 + u C(u) to 5e-10; then
-// sin t = 2 sin h cos h and cos t = cos^2 h - sin^2 h.
-// Evaluated in v = t^2 = 4u with the coefficients of S and C scaled by powers
-// of 4, which forms 2 sin h directly: every intermediate is the u-form's
-// times a power of two, so the results are bit-identical to evaluating in u
-// and one instruction shorter.
-__device__ __forceinline__ void sincos_small(float t, float& st, float& ct) {
-    const float v = t * t;
-    float p = fmaf(v, 2.630318e-06f * 0x1p-8f, -0.00019821344f * 0x1p-6f);
-    p = fmaf(v, p, 0.008333231f * 0x1p-4f);
-    p = fmaf(v, p, -0.16666666f * 0x1p-2f);
-    const float s2 = fmaf(t * v, p, t);  // 2 sin h
-    float q = fmaf(v, -2.625131e-07f * 0x1p-10f, 2.4772546e-05f * 0x1p-8f);
-    q = fmaf(v, q, -0.0013888624f * 0x1p-6f);
-    q = fmaf(v, q, 0.041666657f * 0x1p-4f);
-    q = fmaf(v, q, -0.5f * 0x1p-2f);
-    const float c = fmaf(v, q, 1.0f);  // cos h
-    st = s2 * c;
-    const float s = 0.5f * s2;
-    ct = fmaf(c, c, -(s * s));
-}
-
 // sin and cos of t for |t| <= 3.2 in double (callers send larger |t| to the
 // reference-order path).  Half-angle polynomials in u = h^2, h = t/2 in
 // [0, 1.6]: degree-17/16 Chebyshev fits (computed for this kernel) with
@@ -552,56 +532,62 @@ typedef __attribute__((address_space(3))) const char lds_byte;
 typedef float lds_f4 __attribute__((ext_vector_type(4)));
 typedef double lds_d2 __attribute__((ext_vector_type(2)));
 
-// The source-normal halo of a tile in LDS: one 48-byte record per source
+// The source-normal halo of a tile in LDS: one 80-byte record per source
 // pixel of the tile's replicate-padded window, read with one address per
-// neighbour and immediate offsets.
+// neighbour and immediate offsets (the 80-byte stride leaves consecutive
+// lanes' ds_read_b128 free of bank conflicts, where 64 bytes would not).  With m the raw normal, m' = m/|m|, P0 = (tu0, tv0, 1)
+// the source pixel's ray at depth 1 and g = P0.m, the rotation's cross product
+// for a neighbour with raw xy pair (xs, ys) and q = xs mx/fu + ys my/fv is
+//   c = V x m' = g (D x m') - q (P0 x m'),   D = (xs/fu, ys/fv, 0),
+// i.e. c = xs e1 + ys e2 - q f with the per-source vectors
+//   e1 = g/fu (ex x m') = (0, -g m'z/fu, g m'y/fu),
+//   e2 = g/fv (ey x m') = (g m'z/fv, 0, -g m'x/fv),   f = P0 x m'.
 struct alignas(16) HaloRec {
-    float4 m;    // m' = m/|m| (1/|m| as 1.5 - |m|^2/2), g = P0.m (NaN unless m is a unit normal)
-    double2 ab;  // mx/fu, my/fv: q = xs mx/fu + ys my/fv is formed in double, since it
-                 // cancels where the xy pair is nearly perpendicular to m
-    float4 gt;   // g/fu, g/fv, tu0, tv0; P0 = (tu0, tv0, 1) is the source pixel's ray
+    float4 m;    // m'x, m'y, m'z, g (g NaN unless m is a unit normal)
+    double2 ab;  // mx/fu, my/fv: q is formed in double, since it cancels where the
+                 // xy pair is nearly perpendicular to m
+    float4 e;    // e1.y, e1.z, e2.x, e2.z
+    float4 f;    // f = P0 x m', 0
+    float4 pad;
 };
 
-// The record of halo slot h, whose slot 0 is source pixel (y0, x0).
-__device__ __forceinline__ void stage_halo(float mx, float my, float mz, int h, int hw, int y0,
-                                           int x0, int H, int W, const AngmfArgs& a,
-                                           HaloRec* hl) {
-    const int hr = small_div(h, __builtin_amdgcn_rcpf((float)hw)), hc = h - hr * hw;
-    const int sy = clampi(y0 + hr, 0, H - 1), sx = clampi(x0 + hc, 0, W - 1);
+// The record of source pixel (sy, sx) for its halo slot `rec`.
+__device__ __forceinline__ void stage_halo(float mx, float my, float mz, int sx, int sy,
+                                           const AngmfArgs& a, HaloRec& rec) {
     const double tu0 = fma((double)sx, a.ifu64, a.tu_c);
     const double tv0 = fma((double)sy, a.ifv64, a.tv_c);
+    // 1/|m| as 1.5 - |m|^2/2: exact to 1e-10 for the accepted | |m|^2 - 1 | <= 1e-5
     const float m2 = fmaf(mx, mx, fmaf(my, my, mz * mz));
     const float im = fmaf(-0.5f, m2, 1.5f);
+    const float px = mx * im, py = my * im, pz = mz * im;
     const double g0 = fma(tu0, (double)mx, fma(tv0, (double)my, (double)mz));
     const double g = (fabsf(m2 - 1.0f) <= kUnitM2) ? g0 : __builtin_nan("");
-    HaloRec& rec = hl[h];
-    rec.m = make_float4(mx * im, my * im, mz * im, (float)g);
+    const float gu = (float)(g * a.ifu64), gv = (float)(g * a.ifv64);
+    const float tu = (float)tu0, tv = (float)tv0;
+    rec.m = make_float4(px, py, pz, (float)g);
     rec.ab = make_double2((double)mx * a.ifu64, (double)my * a.ifv64);
-    rec.gt = make_float4((float)(g * a.ifu64), (float)(g * a.ifv64), (float)tu0, (float)tv0);
+    rec.e = make_float4(-gu * pz, gu * py, gv * pz, -gv * px);
+    rec.f = make_float4(fmaf(tv, pz, -py), fmaf(-tu, pz, px), fmaf(tu, py, -(tv * px)), 0.0f);
 }
 
-// Flagged pixels recomputed per pass and group (64 / PPR lanes per pixel).
-__host__ __device__ constexpr int recompute_ppr(int K) { return (K <= 8) ? 8 : 4; }
-
-// Waves per 64-pixel group: the group's K*K neighbours are split into G
-// near-equal runs of consecutive neighbours (row-major over the window), one
-// run per wave.  Workgroups hold kWgWaves = 8 waves (8/G groups): the SPI
-// places a workgroup of n waves only where every SIMD has ceil(n/4) free
-// slots, and spreads 8 waves exactly 2 per SIMD, so every SIMD carries the
-// same work (10-wave workgroups land 3+3+2+2, and two of them leave one SIMD
-// of most CUs with 6 waves where the average is 5).  Runs stay at 7
-// neighbours or fewer (k = 7, 9: 8 waves): a wave buffers its run's planes in
-// registers, and runs of 12-13 (k = 7 with 4 waves) spill them to scratch
-// (311 us against 204 us at 4 x 512 x 512).
-__host__ __device__ constexpr int group_waves(int K) {
-    return K == 1 ? 1 : (K == 3 ? 2 : (K >= 7 ? 8 : 4));
-}
+// Waves per 64-pixel group (G, chosen per launch): the group's K*K
+// neighbours are split into G near-equal runs of consecutive neighbours
+// (row-major over the window), one run per wave.  Workgroups hold kWgWaves = 8
+// waves (8/G groups): the SPI places a workgroup of n waves only where every
+// SIMD has ceil(n/4) free slots and spreads 8 waves exactly 2 per SIMD, so
+// every SIMD carries the same work.  A wave keeps at most kLookahead
+// neighbours' planes in flight, issuing the next neighbour's loads as it
+// finishes one.
 constexpr int kWgWaves = 8;
+// Measured best: 3 at k <= 5 (a 256 x 256 call in one round of waves wants
+// each wave's first neighbours' data first), 7 at k >= 7 (many rounds).
+__host__ __device__ constexpr int lookahead(int K) { return K <= 5 ? 3 : 7; }
 
 // Neighbours whose planes a wave loads before the halo staging and its
-// barrier; the rest are loaded after it.  One measured best on a 256 x 256
-// k = 5 call (8.6 us, against 8.8 us with two and 8.9 us with none).
-constexpr int kPreLoads = 1;
+// barrier; the rest are loaded after it.
+// Measured best: 1 at k <= 5; at k >= 7 all of the lookahead (7), which
+// overlaps the halo's staging with the first neighbours' loads.
+__host__ __device__ constexpr int preloads(int K) { return K <= 5 ? 1 : 7; }
 
 // Source-normal halo records of a TW x TH tile.
 __host__ __device__ inline int halo_count(int K, int TW, int TH) {
@@ -612,17 +598,11 @@ __host__ __device__ inline int halo_count(int K, int TW, int TH) {
 __host__ __device__ inline int halo_slots(int K, int TW, int TH) { return halo_count(K, TW, TH) + 1; }
 
 // LDS of the fp32 kernel, in 16-byte units:
-//   smask[16]          u64 per 64-pixel group (8 units): [0, 8) the pixels
-//                      tier 1 flags, [8, 16) those tier 2 hands to tier 3
 //   part[G][64*M]      per-wave fp32 partial (acc.xyz, sum wi^2 or NaN)
-//   halo[nhalo + 1]    source-pixel records (HaloRec, 3 units) + a spare
-//   fixp[M][G][PPR]    per-wave double partial of a recomputed pixel
-//                      (acc.xyz, sum wi^2: 2 units)
+//   halo[nhalo + 1]    source-pixel records (HaloRec, 5 units) + a spare
 //   rayl[64*M]         each tile pixel's ray, when formed from the intrinsics
-__host__ __device__ inline int lds_units(int K, int M, int TW, int TH, bool synth_ray) {
-    const int G = group_waves(K);
-    return 8 + G * 64 * M + 3 * halo_slots(K, TW, TH) + 2 * M * G * recompute_ppr(K) +
-           (synth_ray ? 64 * M : 0);
+__host__ __device__ inline int lds_units(int K, int G, int M, int TW, int TH, bool synth_ray) {
+    return G * 64 * M + 5 * halo_slots(K, TW, TH) + (synth_ray ? 64 * M : 0);
 }
 
 // TW (< 2^11), TH (< 2^11) and M (< 2^5) of the fp32 kernel's tile and the
@@ -631,65 +611,75 @@ __host__ __device__ inline unsigned pack_tile(int TW, int TH, int M, int L) {
     return (unsigned)TW | ((unsigned)TH << 11) | ((unsigned)M << 22) | ((unsigned)L << 27);
 }
 
+// sin t and cos t for |t| <= 3.2 from the hardware sine and cosine (their
+// argument in revolutions; within 1.26e-7 of sin(2 pi a), cos(2 pi a) for
+// |a| <= 0.51, measured over every float argument): a = t/(2 pi) rounded to
+// fp32, e = t - 2 pi a (exactly enough, from a two-word 2 pi), then the
+// first-order correction sin(2 pi a + e) = s + e c, cos(2 pi a + e) = c - e s.
+constexpr float kInv2Pi = 0.159154943091895335768883763f;
+constexpr float k2PiHi = 6.28318548202514648438f;    // 2 pi rounded to float
+constexpr float k2PiLo = -1.74845553146951715e-07f;  // 2 pi - k2PiHi
+__device__ __forceinline__ void sincos_hw(float t, float& st, float& ct) {
+    const float a = t * kInv2Pi;
+    const float s = __builtin_amdgcn_sinf(a), c = __builtin_amdgcn_cosf(a);
+    const float e = fmaf(-a, k2PiLo, fmaf(-a, k2PiHi, t));
+    st = fmaf(e, c, s);
+    ct = fmaf(-e, s, c);
+}
+
 // One workgroup = M groups of 64 output pixels (a TW x TH tile of sample
 // blockIdx.y) x G waves; wave gi * G + r evaluates one run of the window's
 // neighbours for the 64 pixels of group gi, one pixel per lane.  The runs'
 // roles rotate with gi so the longer run falls on a different SIMD in each
 // group.  Each lane loads its run's 4 planes per neighbour in the order it
-// consumes them; the source normals come from the tile's halo in LDS; the G
-// partials of a pixel meet in LDS.  Two workgroups per CU hold 4 waves per
-// SIMD, so the kernel may use 128 VGPRs and a 256x256 image still runs in
-// one round.
+// consumes them; the source-pixel records come from the tile's halo in LDS;
+// the G partials of a pixel meet in LDS, where wave r = 0 of the group sums
+// them, writes the pixel, and recomputes the pixels it flags on its own.
 //
 // Three tiers of arithmetic:
 //   1. every pixel (this wave's run, one neighbour per iteration):
-//      q = xs mx/fu + ys my/fv in double, rounded once; dd, V, |V|, sin/cos,
+//      q = xs mx/fu + ys my/fv in double, rounded once; dd, c, |c|, sin/cos,
 //      the rotation, RayReLU, the weight prob/|p| and the partial sums in
-//      fp32.  A pixel is flagged when a neighbour leaves
-//      the domain (xy range, |t| > 3.2, |dd| < dd_min, a non-unit source
-//      normal, |V|^2 < kMinV2, anything non-finite) or when |acc|^2 <
-//      kAccRatio2 * sum(wi^2);
+//      fp32.  A pixel is flagged when a neighbour leaves the domain (xy
+//      range, |t| > 3.2, |dd| < dd_min, a non-unit source normal,
+//      |c|^2 < kMinV2, anything non-finite) or when |acc|^2 < acc_ratio2 *
+//      sum(wi^2);
 //   2. flagged pixels, the same reduced form in double (nbr_red_f64), one
-//      neighbour per lane; a pixel with a neighbour outside the double
-//      form's domain, or whose double sum still nearly cancels, goes on to
+//      neighbour per lane of the flagging wave; a pixel with a neighbour
+//      outside the double form's domain, or whose double sum still nearly
+//      cancels, goes on to
 //   3. the reference-order body (nbr_ref_f64) for all its neighbours.
-// On the 256x256 bench input no pixel reaches tier 2.
 //
 // Everything the first loads' addresses depend on comes first in the
 // argument list, as scalars: gfx950 preloads up to 14 dwords of kernel
 // arguments into SGPRs at wave launch (built with
 // -amdgpu-kernarg-preload-count), so a workgroup issues its loads without
-// first waiting for a scalar load of its arguments -- which, once the
-// other workgroups have the memory system saturated, takes microseconds.
-// The scalar unit is shared by the CU's waves, so the prologue keeps scalar
-// work short: no runtime integer division (the tile row comes from a
+// first waiting for a scalar load of its arguments.  The prologue keeps
+// scalar work short: no runtime integer division (the tile row comes from a
 // host-computed magic number, the wave's group from a constant divisor) and
 // one buffer descriptor per input tensor, its planes reached through the
 // scalar offset.
-template <int K, bool SR, bool LG>
+template <int K, int G, bool SR, bool LG>
 __global__ __launch_bounds__(64 * kWgWaves) __attribute__((amdgpu_waves_per_eu(4)))
 void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restrict__ xy,
                       const float* __restrict__ angle, const float* __restrict__ prob, int W,
                       int H, unsigned tile, int tiles_per_img, int tiles_x, unsigned tx_magic,
                       AngmfArgs a) {
     constexpr int P = K / 2, K2 = K * K;
-    constexpr int G = group_waves(K);
     constexpr int RUN = K2 / G, REM = K2 % G;  // run lengths RUN + 1 (REM runs) and RUN
     constexpr int NR = RUN + (REM ? 1 : 0);    // longest run
-    constexpr int PPR = recompute_ppr(K);      // flagged pixels per recompute pass
-    constexpr int LPG = 64 / PPR;              // lanes per flagged pixel in the recompute
+    constexpr int LA = lookahead(K) < NR ? lookahead(K) : NR;  // neighbours in flight
     extern __shared__ float4 smem[];
     const int TW = (int)(tile & 0x7ffu), TH = (int)((tile >> 11) & 0x7ffu);
     const int M = (int)((tile >> 22) & 0x1fu), LX = (int)(tile >> 27);
     const int npx = 64 * M;
     const int nrow = TH + 2 * P;
-    unsigned long long* smask = reinterpret_cast<unsigned long long*>(smem);
-    float4* part = smem + 8;
-    const int nslot = halo_slots(K, TW, TH);
+    float4* part = smem;
+    const int hw = TW + 2 * P, nhalo = hw * nrow;
+    const int nslot = nhalo + 1;
     HaloRec* hl = reinterpret_cast<HaloRec*>(part + G * npx);
-    double* fixp = reinterpret_cast<double*>(hl + nslot);
-    // (SR) the tile pixels' rays, after fixp
-    float4* rayl = reinterpret_cast<float4*>(fixp + M * G * PPR * 4);
+    // (SR) the tile pixels' rays, after the halo
+    float4* rayl = reinterpret_cast<float4*>(hl + nslot);
 
     const int b = blockIdx.y;
     const int lb = xcd_remap(blockIdx.x, tiles_per_img);
@@ -715,19 +705,19 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
 
     // ---- staging: the tile's source normals, with what depends on them only
     // The (TH + 2P) x (TW + 2P) replicate-padded halo of pred_norm, one LDS
-    // record per source pixel (HaloRec), at most two per thread.  Their loads
-    // are each lane's first, so waiting for them waits for nothing else.
-    const int hw = TW + 2 * P, nhalo = hw * nrow;
+    // record pair per source pixel, at most two per thread.  Their loads are
+    // each lane's first, so waiting for them waits for nothing else.
     const int nthr = 64 * M * G;
     const float rhw = __builtin_amdgcn_rcpf((float)hw);
     const __amdgpu_buffer_rsrc_t rpn =
         plane_rsrc(at_plane(pred_norm, (uint32_t)b * 3u, HW4), 3u * HW4);
     float hm[3];
+    // threads past the halo write the spare record, from clamped coordinates
+    const int h0 = min((int)threadIdx.x, nhalo);
+    const int hr0 = small_div(h0, rhw), hc0 = h0 - hr0 * hw;
+    const int hsy0 = clampi(ty0 - P + hr0, 0, H - 1), hsx0 = clampi(tx0 - P + hc0, 0, W - 1);
     {
-        const int h = threadIdx.x;
-        const int hr = small_div(h, rhw), hc = h - hr * hw;
-        const int hsy = clampi(ty0 - P + hr, 0, H - 1), hsx = clampi(tx0 - P + hc, 0, W - 1);
-        const uint32_t hb = (h < nhalo) ? (uint32_t)(hsy * W + hsx) * 4u : 0u;
+        const uint32_t hb = (uint32_t)(hsy0 * W + hsx0) * 4u;
         hm[0] = ldbs(rpn, hb, 0u);
         hm[1] = ldbs(rpn, hb, HW4);
         hm[2] = ldbs(rpn, hb, 2u * HW4);
@@ -738,15 +728,13 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     // ---- phase A: this wave's run of neighbours for this lane's pixel ------
     // Every lane runs it (lanes past the tile use clamped, in-bounds
     // addresses and discard the result).
-    // loads in consumption order: ray, then per neighbour its 4 planes; the
-    // planes of the first kPreLoads neighbours go out before the staging,
-    // the rest after its barrier.  Vector loads complete in issue order, so
-    // the neighbour loop below consumes them one neighbour at a time: a
-    // scheduling barrier after each neighbour's loads keeps them in that
-    // order, and the loop's register fences keep the compiler from hoisting
-    // one neighbour's arithmetic ahead of the previous one's, which would
-    // wait for late data before using early data (8.6 us against 9.3 us on
-    // a 256 x 256 k = 5 call with cold inputs).
+    // Loads in consumption order: ray, then per neighbour its 4 planes, at
+    // most LA neighbours ahead of the one being evaluated; the planes of the
+    // first kPreLoads neighbours go out before the staging.  Vector loads
+    // complete in issue order, so the loop consumes them one neighbour at a
+    // time: a scheduling barrier after each neighbour's loads keeps them in
+    // that order, and the loop's register fences keep the compiler from
+    // hoisting one neighbour's arithmetic ahead of the previous one's.
     float rxf, ryf, rzf;
     if constexpr (!SR) {
         const __amdgpu_buffer_rsrc_t rry =
@@ -773,7 +761,7 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
         th[i] = ldbs(rth, pb, so);
         wt[i] = ldbs(rwt, pb, so);
     };
-    constexpr int PRE = kPreLoads < NR ? kPreLoads : NR;
+    constexpr int PRE = preloads(K) < LA ? preloads(K) : LA;
 #pragma unroll
     for (int i = 0; i < PRE; ++i) {
         load_planes(i);
@@ -781,61 +769,67 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     }
     // Threads past the halo write a spare record: an unconditional use keeps
     // the compiler from sinking the halo loads behind the plane loads.
-    stage_halo(hm[0], hm[1], hm[2], min((int)threadIdx.x, nhalo), hw, ty0 - P, tx0 - P, H, W, a,
-               hl);
+    stage_halo(hm[0], hm[1], hm[2], hsx0, hsy0, a, hl[h0]);
     // A second record per thread (k >= 7, and narrow tiles): loaded here,
     // behind the plane loads, which it then waits for.
     if (nhalo > nthr) {
         const int h = threadIdx.x + nthr;
         if (h < nhalo) {
             const int hr = small_div(h, rhw), hc = h - hr * hw;
-            const uint32_t hb = (uint32_t)(clampi(ty0 - P + hr, 0, H - 1) * W +
-                                           clampi(tx0 - P + hc, 0, W - 1)) * 4u;
-            stage_halo(ldbs(rpn, hb, 0u), ldbs(rpn, hb, HW4), ldbs(rpn, hb, 2u * HW4), h, hw,
-                       ty0 - P, tx0 - P, H, W, a, hl);
+            const int sy = clampi(ty0 - P + hr, 0, H - 1), sx = clampi(tx0 - P + hc, 0, W - 1);
+            const uint32_t hb = (uint32_t)(sy * W + sx) * 4u;
+            stage_halo(ldbs(rpn, hb, 0u), ldbs(rpn, hb, HW4), ldbs(rpn, hb, 2u * HW4), sx, sy, a,
+                       hl[h]);
         }
     }
-    if ((int)threadIdx.x < 8) smask[8 + threadIdx.x] = 0ull;
     if constexpr (SR) {
         // each tile pixel's ray, once (pixels past the image: clamped ones)
         if ((int)threadIdx.x < npx) {
             const int t = threadIdx.x;
             const int rty = small_div(t, rtw), rtx = t - rty * TW;
-            const float3 r = synth_ray(min(tx0 + rtx, W - 1), min(ty0 + rty, H - 1), a.fu, a.cu,
-                                       a.fv, a.cv);
-            rayl[t] = make_float4(r.x, r.y, r.z, 0.0f);
+            const float3 r3 = synth_ray(min(tx0 + rtx, W - 1), min(ty0 + rty, H - 1), a.fu, a.cu,
+                                        a.fv, a.cv);
+            rayl[t] = make_float4(r3.x, r3.y, r3.z, 0.0f);
         }
     }
     __syncthreads();
     if constexpr (SR) {
-        const float4 r = rayl[j];
-        rxf = r.x;
-        ryf = r.y;
-        rzf = r.z;
+        const float4 r4 = rayl[j];
+        rxf = r4.x;
+        ryf = r4.y;
+        rzf = r4.z;
     }
 #pragma unroll
-    for (int i = PRE; i < NR; ++i) {
+    for (int i = PRE; i < LA; ++i) {
         load_planes(i);
         __builtin_amdgcn_sched_barrier(0);
     }
     {
-        // cos(v', r) = v'.r / max(|v'||r|, 1e-8) with |v'| = 1
+        // cos(v', r) = v'.r / max(|v'||r|, 1e-8) with |v'| = 1.  1/|r| from the
+        // hardware rsq and one Newton step: r-hat is shared by all the
+        // pixel's neighbours, so its error would not average out over them.
         const float r2 = fmaf(rxf, rxf, fmaf(ryf, ryf, rzf * rzf));
-        const float ir = (r2 < 1e-16f) ? 1e8f : __builtin_amdgcn_rsqf(r2);
-        const float rhx = rxf * ir, rhy = ryf * ir, rhz = rzf * ir;
+        const float ir0 = __builtin_amdgcn_rsqf(r2);
+        const float ir1 = fmaf(0.5f * ir0, fmaf(-r2 * ir0, ir0, 1.0f), ir0);
+        const float ir = (r2 < 1e-16f) ? 1e8f : ir1;
+        // -r-hat/2 and 2r: the RayReLU shift dc = max(eps - cos, 0) is formed as
+        // 2 clamp(eps/2 - v'.r-hat/2) in the dot product's last fma (the
+        // clamp's upper bound, 1, is above (eps + 1)/2)
+        const float nhx = -0.5f * (rxf * ir), nhy = -0.5f * (ryf * ir), nhz = -0.5f * (rzf * ir);
+        const float r2x = 2.0f * rxf, r2y = 2.0f * ryf, r2z = 2.0f * rzf;
         const float dd_min = (float)a.dd_min;
         // this lane's window in the halo (lanes past the tile use its last row)
         const int hrow = (ty < TH) ? ty : TH - 1;
-        // (an LDS-space pointer: 32-bit record addresses)
+        // (LDS-space pointers: 32-bit record addresses)
         const lds_byte* hbase = (const lds_byte*)reinterpret_cast<const char*>(hl + hrow * hw + tx);
         float acc0 = 0.0f, acc1 = 0.0f, acc2 = 0.0f;
         float qs = 0.0f;  // sum of wi^2, for the cancellation test only
         // the fp32 form's domain over the run, as running extremes: bits of
-        // |xy|^2 above kMinXY2, |t|, |dd| and |V|^2.  A NaN drops out of a
+        // |xy|^2 above kMinXY2, |t|, |dd| and |c|^2.  A NaN drops out of a
         // min or max but not out of the sums: every NaN these would see
-        // reaches acc (through q, V, sin/cos or the weight), which phase B
+        // reaches acc (through q, c, sin/cos or the weight), which phase B
         // flags.
-        uint32_t smax = 0u;
+        uint32_t smx = 0u;
         float tmax = 0.0f, ddmin = __builtin_inff(), n2min = __builtin_inff();
 #pragma unroll
         for (int i = 0; i < NR; ++i) {
@@ -845,49 +839,45 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
             if (i == NR - 1 && nrun != NR) break;
             const int n = n0 + i;
             const int ky = n / K, kx = n - ky * K;
-            // the record offset in a scalar register, added once (the compiler
-            // would otherwise fold it into a 64-bit multiply-add per neighbour)
+            // the record offsets in scalar registers, added once each (the
+            // compiler would otherwise fold them into a 64-bit multiply-add
+            // per neighbour)
             int roff = (ky * hw + kx) * (int)sizeof(HaloRec);
             asm("" : "+s"(roff));
             const lds_byte* rb = hbase + roff;
             const lds_f4 hm4 = *(const __attribute__((address_space(3))) lds_f4*)rb;
             const lds_d2 ab2 = *(const __attribute__((address_space(3))) lds_d2*)(rb + 16);
-            const lds_f4 gt4 = *(const __attribute__((address_space(3))) lds_f4*)(rb + 32);
-            const float4 hm = make_float4(hm4.x, hm4.y, hm4.z, hm4.w);
-            const float4 gt = make_float4(gt4.x, gt4.y, gt4.z, gt4.w);
-            const double2 ab = make_double2(ab2.x, ab2.y);
+            const lds_f4 e4 = *(const __attribute__((address_space(3))) lds_f4*)(rb + 32);
+            const lds_f4 f4 = *(const __attribute__((address_space(3))) lds_f4*)(rb + 48);
             const float xv = xs[i], yv = ys[i];
             const float t = LG ? sigmoid_f32(th[i]) * kPiF : th[i];
             // q in double (exact products, one rounding), the rest fp32;
             // dd = g + q/|xy| is formed from the raw normal as the reference
             // forms it, with 1/|xy| from the fp32 |xy|^2 and rsq (dd_min
             // covers their error)
-            const float q = (float)fma((double)xv, ab.x, (double)yv * ab.y);
+            const float q = (float)fma((double)xv, ab2.x, (double)yv * ab2.y);
             const float s = fmaf(xv, xv, yv * yv);
-            const float dd = fmaf(q, __builtin_amdgcn_rsqf(s), hm.w);
-            // axis = sign(dd) V/|V|, V = (g xs/fu - q tu0, g ys/fv - q tv0, -q) = m x N;
-            // v' = m' cos t + (V x m') sin t/|V|
-            const float Vx = fmaf(gt.x, xv, -q * gt.z);
-            const float Vy = fmaf(gt.y, yv, -q * gt.w);
-            const float n2 = fmaf(Vx, Vx, fmaf(Vy, Vy, q * q));
-            smax = max(smax, __builtin_bit_cast(uint32_t, s) - kXY2Lo);
+            const float dd = fmaf(q, __builtin_amdgcn_rsqf(s), hm4.w);
+            // c = V x m' = xs e1 + ys e2 - q f;  v' = m' cos t + c sign(dd) sin t/|c|
+            const float cx = fmaf(yv, e4.z, -q * f4.x);
+            const float cy = fmaf(xv, e4.x, -q * f4.y);
+            const float cz = fmaf(xv, e4.y, fmaf(yv, e4.w, -q * f4.z));
+            const float n2 = fmaf(cx, cx, fmaf(cy, cy, cz * cz));
+            smx = max(smx, __builtin_bit_cast(uint32_t, s) - kXY2Lo);
             tmax = fmaxf(tmax, fabsf(t));
             ddmin = fminf(ddmin, fabsf(dd));
             n2min = fminf(n2min, n2);
             float st, ct;
-            sincos_small(t, st, ct);
+            sincos_hw(t, st, ct);
             const float S = st * copysignf(__builtin_amdgcn_rsqf(n2), dd);
-            // V x m' with Vz = -q
-            const float cx = fmaf(Vy, hm.z, q * hm.y);
-            const float cy = -fmaf(q, hm.x, Vx * hm.z);
-            const float cz = fmaf(Vx, hm.y, -Vy * hm.x);
-            const float vx = fmaf(cx, S, hm.x * ct);
-            const float vy = fmaf(cy, S, hm.y * ct);
-            const float vz = fmaf(cz, S, hm.z * ct);
-            // RayReLU: p = v' + r max(eps - cos, 0), then the weight prob/|p|
-            const float cs = fmaf(vx, rhx, fmaf(vy, rhy, vz * rhz));
-            const float dc = fmaxf(kRayEpsF - cs, 0.0f);
-            const float px = fmaf(rxf, dc, vx), py = fmaf(ryf, dc, vy), pz = fmaf(rzf, dc, vz);
+            const float vx = fmaf(cx, S, hm4.x * ct);
+            const float vy = fmaf(cy, S, hm4.y * ct);
+            const float vz = fmaf(cz, S, hm4.z * ct);
+            // RayReLU: p = v' + r max(eps - cos, 0) = v' + 2r h, h = clamp(eps/2 - cos/2),
+            // then the weight prob/|p|
+            const float h = __builtin_amdgcn_fmed3f(
+                fmaf(vz, nhz, fmaf(vy, nhy, fmaf(vx, nhx, 0.5f * kRayEpsF))), 0.0f, 1.0f);
+            const float px = fmaf(r2x, h, vx), py = fmaf(r2y, h, vy), pz = fmaf(r2z, h, vz);
             // wi = prob / |p|; with logits prob = 1/d, d = 1 + exp(-L), and
             // wi = rsq(|p|^2 d^2) (d = inf: exactly 0)
             const float p2 = fmaf(px, px, fmaf(py, py, pz * pz));
@@ -904,189 +894,159 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
             qs = fmaf(wi, wi, qs);
             // this neighbour done before the next one's data are waited for
             asm volatile("" : "+v"(acc0), "+v"(acc1), "+v"(acc2), "+v"(qs));
+            if (i + LA < NR) {
+                load_planes(i + LA);
+                __builtin_amdgcn_sched_barrier(0);
+            }
         }
-        const bool bad = (smax > kXY2Span) | !(tmax <= 3.2f) | !(ddmin >= dd_min) |
+        const bool bad = (smx > kXY2Span) | !(tmax <= 3.2f) | !(ddmin >= dd_min) |
                          !(n2min >= kMinV2);
         part[r * npx + j] = make_float4(acc0, acc1, acc2, bad ? __builtin_nanf("") : qs);
     }
     __syncthreads();
 
-    // ---- phase B: reduce the G runs, write unflagged pixels ----------------
-    if (r == 0) {
-        bool flag = false;
-        if (valid) {
-            double s0 = 0.0, s1 = 0.0, s2 = 0.0, sw = 0.0;
+    // ---- phase B: wave r = 0 of each group reduces the G runs, writes the
+    // unflagged pixels and recomputes the flagged ones by itself; the other
+    // waves are done (no barrier follows).
+    if (r != 0) return;
+    bool flag = false;
+    if (valid) {
+        double s0 = 0.0, s1 = 0.0, s2 = 0.0, sw = 0.0;
 #pragma unroll
-            for (int rr = 0; rr < G; ++rr) {
-                const float4 t = part[rr * npx + j];
-                s0 += t.x;
-                s1 += t.y;
-                s2 += t.z;
-                sw += t.w;
-            }
-            const double a2 = fma(s0, s0, fma(s1, s1, s2 * s2));
-            // 1 / max(|acc|, 1e-12) as the reference; a non-finite or
-            // cancelled sum goes to the recompute
-            flag = !(a2 >= a.acc_ratio2 * sw) || !(a2 <= 1e300);
-            if (!flag) {
-                const double inv = (a2 < 1e-24) ? 1e12 : rsq64_1(a2);
-                float* op = a.out + (size_t)b * 3 * HW;
-                stf(op, pb, (float)(s0 * inv));
-                stf(op + HW, pb, (float)(s1 * inv));
-                stf(op + 2 * HW, pb, (float)(s2 * inv));
-            }
+        for (int rr = 0; rr < G; ++rr) {
+            const float4 t = part[rr * npx + j];
+            s0 += t.x;
+            s1 += t.y;
+            s2 += t.z;
+            sw += t.w;
         }
-        const unsigned long long m = __ballot(flag);
-        if (lane == 0) smask[gi] = m;
+        const double a2 = fma(s0, s0, fma(s1, s1, s2 * s2));
+        // 1 / max(|acc|, 1e-12) as the reference; a non-finite or
+        // cancelled sum goes to the recompute
+        flag = !(a2 >= a.acc_ratio2 * sw) || !(a2 <= 1e300);
+        if (!flag) {
+            const double inv = (a2 < 1e-24) ? 1e12 : rsq64_1(a2);
+            float* op = a.out + (size_t)b * 3 * HW;
+            stf(op, pb, (float)(s0 * inv));
+            stf(op + HW, pb, (float)(s1 * inv));
+            stf(op + 2 * HW, pb, (float)(s2 * inv));
+        }
     }
-    __syncthreads();
+    unsigned long long fm = __ballot(flag);
+    if (fm == 0) return;
 
-    // ---- phase C: recompute flagged pixels (tier 2, then tier 3) -----------
-    int maxc = 0;
-    for (int g = 0; g < M; ++g) {
-        const int c = __popcll(uniform64(smask[g]));
-        maxc = c > maxc ? c : maxc;
-    }
-    if (maxc == 0) return;
-    int tid = threadIdx.x, tw = TW;
-    asm volatile("" : "+v"(tid), "+s"(tw));
+    // ---- phase C: the group's flagged pixels, tier 2 then tier 3 ----------
+    // LP lanes per pixel, one neighbour per lane at a time; inputs are
+    // re-read (the workgroup has just read them, so mostly from L2).
+    constexpr int LP = (K2 > 32) ? 64 : 32;
+    constexpr int PPP = 64 / LP;
+    const int slot = lane / LP, il = lane - slot * LP;
+    int tw = TW;
+    asm volatile("" : "+s"(tw));
     const float* pn = pred_norm + (size_t)b * 3 * HW;
     const float* pr = prob + (size_t)b * K2 * HW;
     const float* xyp = xy + (size_t)b * 2 * K2 * HW;
     const float* ap = angle + (size_t)b * K2 * HW;
     const float* rp = SR ? nullptr : a.ray + (size_t)b * a.ray_bstride;
     float* op = a.out + (size_t)b * 3 * HW;
-    // Each wave (group, run) evaluates its run's neighbours of up to PPR
-    // pixels of its group per pass, LPG lanes per pixel, one neighbour per
-    // lane at a time; run partials meet in LDS and wave r == 0 of the group
-    // writes the pixel -- or, in tier 2, hands it to tier 3.  Inputs are
-    // re-read (the block has just read them, so from L2).  Pass counts come
-    // from LDS after a barrier, so every wave of the block runs the same
-    // barriers.
-    const int clane = tid & 63;
-    const int slot = clane / LPG, il = clane - slot * LPG;
-    // One tier over the pixels of mask slot `mo` of smask; TIER is 2 or 3.
-    auto recompute = [&](auto tier_tag, int mo) {
-        constexpr int TIER = decltype(tier_tag)::value;
-        int maxt = 0;
-        for (int g = 0; g < M; ++g) {
-            const int c = __popcll(uniform64(smask[mo + g]));
-            maxt = c > maxt ? c : maxt;
+    while (fm) {
+        int src = -1;
+#pragma unroll
+        for (int sidx = 0; sidx < PPP; ++sidx) {
+            const int bitpos = fm ? __ffsll((long long)fm) - 1 : -1;
+            if (fm) fm &= fm - 1;
+            if (sidx == slot) src = bitpos;
         }
-        const unsigned long long gmask = uniform64(smask[mo + gi]);
-        const int cnt = __popcll(gmask);
-        unsigned long long rest = gmask;
-        for (int base = 0; base < maxt; base += PPR) {
-            int src = 0, fin_src = 0;
-#pragma unroll
-            for (int sidx = 0; sidx < PPR; ++sidx) {
-                const int bitpos = rest ? __ffsll((long long)rest) - 1 : 0;
-                if (rest) rest &= rest - 1;
-                if (sidx == slot) src = bitpos;
-                if (sidx == clane) fin_src = bitpos;
+        const bool act = src >= 0;
+        const int jj = gi * 64 + (act ? src : 0);
+        const int fty = jj / tw, ftx = jj - fty * tw;
+        const int fy = ty0 + fty, fx = tx0 + ftx;
+        const uint32_t fb = (uint32_t)(fy * W + fx) * 4u;
+        float frx = 0.0f, fry = 0.0f, frz = 0.0f;
+        if (act) {
+            if constexpr (SR) {
+                const float3 rr3 = synth_ray(fx, fy, a.fu, a.cu, a.fv, a.cv);
+                frx = rr3.x;
+                fry = rr3.y;
+                frz = rr3.z;
+            } else {
+                frx = ldf(rp, fb);
+                fry = ldf(rp + HW, fb);
+                frz = ldf(rp + 2 * HW, fb);
             }
-            const bool act = (base + slot) < cnt;
-            const int jj = gi * 64 + src;
-            const int fty = jj / tw, ftx = jj - fty * tw;
-            const int fy = ty0 + fty, fx = tx0 + ftx;
-            const uint32_t fb = (uint32_t)(fy * W + fx) * 4u;
-            double p0 = 0.0, p1 = 0.0, p2 = 0.0, q2 = 0.0;
-            if (act) {
-                float frx, fry, frz;
-                if constexpr (SR) {
-                    const float3 rr3 = synth_ray(fx, fy, a.fu, a.cu, a.fv, a.cv);
-                    frx = rr3.x;
-                    fry = rr3.y;
-                    frz = rr3.z;
+        }
+        // one tier over this lane's neighbours of its pixel; returns false
+        // (tier 2) when a neighbour is outside the reduced form's domain
+        auto tier = [&](auto tier_tag, double& p0, double& p1, double& p2, double& q2) {
+            constexpr int TIER = decltype(tier_tag)::value;
+            p0 = p1 = p2 = q2 = 0.0;
+            if (!act) return;
+            const double rxd = frx, ryd = fry, rzd = frz;
+            const double ird = 1.0 / smax(sqrt(fma(rxd, rxd, fma(ryd, ryd, rzd * rzd))), 1e-8);
+#pragma unroll 1
+            for (int n = il; n < K2; n += LP) {
+                const int ky = n / K, kx = n - ky * K;
+                const int fsy = clampi(fy - P + ky, 0, H - 1);
+                const int fsx = clampi(fx - P + kx, 0, W - 1);
+                const uint32_t sb = (uint32_t)(fsy * W + fsx) * 4u;
+                const float mx = ldf(pn, sb), my = ldf(pn + HW, sb), mz = ldf(pn + 2 * HW, sb);
+                const float xsv = ldf(xyp + (size_t)n * HW, fb);
+                const float ysv = ldf(xyp + (size_t)(K2 + n) * HW, fb);
+                float thv = ldf(ap + (size_t)n * HW, fb), wv = ldf(pr + (size_t)n * HW, fb);
+                if constexpr (LG) {
+                    thv = angle_ref(thv);
+                    wv = sigmoid_ref(wv);
+                }
+                double ox, oy, oz, pinv;
+                if constexpr (TIER == 2) {
+                    if (!nbr_red_f64(mx, my, mz, fsx, fsy, xsv, ysv, thv, wv, rxd, ryd, rzd, ird,
+                                     a, ox, oy, oz, pinv)) {
+                        q2 = __builtin_nan("");
+                        continue;
+                    }
                 } else {
-                    frx = ldf(rp, fb);
-                    fry = ldf(rp + HW, fb);
-                    frz = ldf(rp + 2 * HW, fb);
+                    nbr_ref_f64(mx, my, mz, fsx + 0.5, fsy + 0.5, xsv, ysv, thv, frx, fry, frz,
+                                a.fu, a.cu, a.fv, a.cv, ox, oy, oz, pinv);
                 }
-                for (int i = il; i < nrun; i += LPG) {
-                    const int n = n0 + i;
-                    const int ky = n / K, kx = n - ky * K;
-                    const int fsy = clampi(fy - P + ky, 0, H - 1);
-                    const int fsx = clampi(fx - P + kx, 0, W - 1);
-                    const uint32_t sb = (uint32_t)(fsy * W + fsx) * 4u;
-                    const float mx = ldf(pn, sb), my = ldf(pn + HW, sb), mz = ldf(pn + 2 * HW, sb);
-                    const float xsv = ldf(xyp + (size_t)n * HW, fb);
-                    const float ysv = ldf(xyp + (size_t)(K2 + n) * HW, fb);
-                    float thv = ldf(ap + (size_t)n * HW, fb), wv = ldf(pr + (size_t)n * HW, fb);
-                    if constexpr (LG) {
-                        thv = angle_ref(thv);
-                        wv = sigmoid_ref(wv);
-                    }
-                    double ox, oy, oz, pinv;
-                    if constexpr (TIER == 2) {
-                        const double rxd = frx, ryd = fry, rzd = frz;
-                        const double ird =
-                            1.0 / smax(sqrt(fma(rxd, rxd, fma(ryd, ryd, rzd * rzd))), 1e-8);
-                        // outside the reduced form's domain: the pixel goes to tier 3
-                        if (!nbr_red_f64(mx, my, mz, fsx, fsy, xsv, ysv, thv, wv, rxd, ryd, rzd,
-                                         ird, a, ox, oy, oz, pinv)) {
-                            q2 = __builtin_nan("");
-                            continue;
-                        }
-                    } else {
-                        nbr_ref_f64(mx, my, mz, fsx + 0.5, fsy + 0.5, xsv, ysv, thv, frx, fry, frz,
-                                    a.fu, a.cu, a.fv, a.cv, ox, oy, oz, pinv);
-                    }
-                    const double w = wv;
-                    p0 += w * ox;
-                    p1 += w * oy;
-                    p2 += w * oz;
-                    const double wi = w * pinv;
-                    q2 = fma(wi, wi, q2);
-                }
+                const double w = wv;
+                p0 += w * ox;
+                p1 += w * oy;
+                p2 += w * oz;
+                const double wi = w * pinv;
+                q2 = fma(wi, wi, q2);
             }
 #pragma unroll
-            for (int off = LPG / 2; off > 0; off >>= 1) {
+            for (int off = LP / 2; off > 0; off >>= 1) {
                 p0 += __shfl_xor(p0, off, 64);
                 p1 += __shfl_xor(p1, off, 64);
                 p2 += __shfl_xor(p2, off, 64);
                 q2 += __shfl_xor(q2, off, 64);
             }
-            if (il == 0 && act) {
-                double* f = fixp + ((gi * G + r) * PPR + slot) * 4;
-                f[0] = p0;
-                f[1] = p1;
-                f[2] = p2;
-                f[3] = q2;
-            }
-            __syncthreads();
-            if (r == 0 && clane < PPR && base + clane < cnt) {
-                double a0 = 0.0, a1 = 0.0, a2 = 0.0, aq = 0.0;
-                for (int rr = 0; rr < G; ++rr) {
-                    const double* f = fixp + ((gi * G + rr) * PPR + clane) * 4;
-                    a0 += f[0];
-                    a1 += f[1];
-                    a2 += f[2];
-                    aq += f[3];
-                }
-                const double n2 = a0 * a0 + a1 * a1 + a2 * a2;
-                // tier 2 hands on a pixel with a neighbour outside its domain
-                // (aq NaN) or a sum that nearly cancels
-                if (TIER == 2 &&
-                    (!(n2 >= kAccRatio2Ref * aq) || !(n2 >= kAcc2Floor) || !(n2 <= 1e300))) {
-                    atomicOr(&smask[8 + gi], 1ull << fin_src);
-                } else {
-                    // 1 / max(|acc|, 1e-12), with the reference's NaN and Inf results
-                    const double inv =
-                        (n2 < 1e-24) ? 1e12 : (n2 == INFINITY ? 0.0 : rsq64(n2));
-                    const int jw = gi * 64 + fin_src;
-                    const int wty = jw / tw, wtx = jw - wty * tw;
-                    const uint32_t wb = (uint32_t)((ty0 + wty) * W + tx0 + wtx) * 4u;
-                    stf(op, wb, (float)(a0 * inv));
-                    stf(op + HW, wb, (float)(a1 * inv));
-                    stf(op + 2 * HW, wb, (float)(a2 * inv));
-                }
-            }
-            __syncthreads();
+        };
+        // 1 / max(|acc|, 1e-12), with the reference's NaN and Inf results
+        auto write = [&](double a0, double a1, double a2) {
+            const double n2 = a0 * a0 + a1 * a1 + a2 * a2;
+            const double inv = (n2 < 1e-24) ? 1e12 : (n2 == INFINITY ? 0.0 : rsq64(n2));
+            stf(op, fb, (float)(a0 * inv));
+            stf(op + HW, fb, (float)(a1 * inv));
+            stf(op + 2 * HW, fb, (float)(a2 * inv));
+        };
+        bool need3;
+        {
+            double a0, a1, a2, aq;
+            tier(std::integral_constant<int, 2>{}, a0, a1, a2, aq);
+            const double n2 = a0 * a0 + a1 * a1 + a2 * a2;
+            // tier 2 hands on a pixel with a neighbour outside its domain
+            // (aq NaN) or a sum that nearly cancels
+            need3 = act && (!(n2 >= kAccRatio2Ref * aq) || !(n2 >= kAcc2Floor) || !(n2 <= 1e300));
+            if (act && !need3 && il == 0) write(a0, a1, a2);
         }
-    };
-    recompute(std::integral_constant<int, 2>{}, 0);
-    recompute(std::integral_constant<int, 3>{}, 8);
+        if (__ballot(need3)) {
+            double a0, a1, a2, aq;
+            tier(std::integral_constant<int, 3>{}, a0, a1, a2, aq);
+            if (need3 && il == 0) write(a0, a1, a2);
+        }
+    }
 }
 
 // ---------------------------------------------------------------------------
@@ -1150,6 +1110,26 @@ void div_magic(int d, unsigned& mag, int& L) {
                          (unsigned long long)d + 1);
 }
 
+// The fp32 kernel's instantiation for window K, G waves per group, and the
+// ray and logits modes.
+template <int K, int G>
+auto angmf_f32_for(bool synth_ray, bool logits) {
+    return synth_ray ? (logits ? angmf_f32_kernel<K, G, true, true>
+                               : angmf_f32_kernel<K, G, true, false>)
+                     : (logits ? angmf_f32_kernel<K, G, false, true>
+                               : angmf_f32_kernel<K, G, false, false>);
+}
+
+// Candidate G values per window size, in order of preference (the first
+// wins ties in lane utilisation).  Runs longer than kLookahead neighbours
+// keep only kLookahead of them in flight.
+//   K = 5: 4 (runs of 6-7) on wide images; 2 (runs of 12-13) gives narrow
+//          images (W = 60, 80) full-width tiles of 3-4 rows with few idle lanes
+//   K = 7, 9: 4 (runs of 12-13 / 20-21; 64 x 2 tiles halve the halo per pixel
+//          against 8 waves of runs of 6-7 on 64 x 1 tiles)
+constexpr int kGChoices[10][2] = {{0, 0}, {1, 1}, {0, 0}, {2, 2}, {0, 0},
+                                  {4, 2}, {0, 0}, {4, 8}, {0, 0}, {4, 8}};
+
 template <int K>
 hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
     if (fp64) {
@@ -1158,11 +1138,14 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
         hipLaunchKernelGGL(angmf_f64_kernel<K>, dim3((unsigned)grid), dim3(256), 0, s, a);
         return hipGetLastError();
     }
-    const size_t lds = (size_t)lds_units(K, a.M, a.TW, a.TH, a.synth_ray != 0) * 16;
+    const size_t lds = (size_t)lds_units(K, a.G, a.M, a.TW, a.TH, a.synth_ray != 0) * 16;
     unsigned mag;
     int L;
     div_magic(a.tiles_x, mag, L);
     const unsigned tile = pack_tile(a.TW, a.TH, a.M, L);
+    constexpr int G0 = kGChoices[K][0], G1 = kGChoices[K][1];
+    const auto kern = (a.G == G0) ? angmf_f32_for<K, G0>(a.synth_ray != 0, a.logits != 0)
+                                  : angmf_f32_for<K, G1>(a.synth_ray != 0, a.logits != 0);
     // one launch per kMaxGridY samples (grid y = sample)
     for (int b0 = 0; b0 < a.B; b0 += kMaxGridY) {
         const int nb = (a.B - b0 < kMaxGridY) ? a.B - b0 : kMaxGridY;
@@ -1174,11 +1157,7 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
         if (!a.synth_ray) c.ray += (size_t)b0 * a.ray_bstride;
         c.out += (size_t)b0 * 3 * a.HW;
         c.B = nb;
-        const dim3 grid((unsigned)a.tiles_per_img, (unsigned)nb), block(64 * a.M * group_waves(K));
-        auto kern = a.synth_ray ? (a.logits ? angmf_f32_kernel<K, true, true>
-                                            : angmf_f32_kernel<K, true, false>)
-                                : (a.logits ? angmf_f32_kernel<K, false, true>
-                                            : angmf_f32_kernel<K, false, false>);
+        const dim3 grid((unsigned)a.tiles_per_img, (unsigned)nb), block(64 * a.M * a.G);
         hipLaunchKernelGGL(kern, grid, block, lds, s, c.pn, c.xy, c.ang, c.pr, a.W, a.H, tile,
                            a.tiles_per_img, a.tiles_x, mag, c);
         const hipError_t e = hipGetLastError();
@@ -1190,37 +1169,69 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
 // LDS one workgroup may use.
 constexpr int kMaxLdsBytes = 65536;
 
-// Whether a TW x TH tile of M groups fits the kernel: its LDS, and at most
-// two halo records per thread.
-bool tile_fits(int K, int M, int TW, int TH, bool synth_ray) {
-    return lds_units(K, M, TW, TH, synth_ray) * 16 <= kMaxLdsBytes &&
-           halo_count(K, TW, TH) <= 2 * 64 * M * group_waves(K);
+// Whether a TW x TH tile of M groups of G waves fits the kernel: its LDS, and
+// at most two halo records per thread.
+bool tile_fits(int K, int G, int M, int TW, int TH, bool synth_ray) {
+    return lds_units(K, G, M, TW, TH, synth_ray) * 16 <= kMaxLdsBytes &&
+           halo_count(K, TW, TH) <= 2 * 64 * M * G;
 }
 
-// Tile of the fp32 kernel: wide images (and rows longer than a workgroup's
-// 64 * M pixels) take 64 x M tiles (each wave one 256 B row segment per
-// plane); narrow ones full-width tiles of TH rows with the fewest idle lanes
-// among those that fit.  At most kWgWaves waves (M * G) per workgroup.
-void choose_tile(AngmfArgs& a, int K) {
-    const int mmax = kWgWaves / group_waves(K);
+// Tile of the fp32 kernel for G waves per group: wide images (and rows longer
+// than a workgroup's 64 * M pixels) take 64 x M tiles (each wave one 256 B row
+// segment per plane); narrow ones full-width tiles of TH rows with the fewest
+// idle lanes among those that fit.  Returns the fraction of lanes that hold a
+// pixel (0 if nothing fits).
+double tile_for(AngmfArgs& a, int K, int G) {
+    const int mmax = kWgWaves / G;
+    a.G = G;
     a.TW = 64;
     a.M = mmax;
-    while (a.M > 1 && !tile_fits(K, a.M, 64, a.M, a.synth_ray != 0)) --a.M;
+    while (a.M > 1 && !tile_fits(K, G, a.M, 64, a.M, a.synth_ray != 0)) --a.M;
     a.TH = a.M;
-    if (a.W > 128 || a.W > 64 * mmax) return;
-    double best = -1.0;
+    double best = tile_fits(K, G, a.M, 64, a.M, a.synth_ray != 0) ? 1.0 : 0.0;
+    if (a.W > 128 || a.W > 64 * mmax) return best;
+    best = -1.0;
     for (int th = 1; th <= a.H && th <= 64 * mmax; ++th) {
         const int npx = a.W * th;
         const int m = (npx + 63) / 64;
         if (m > mmax) break;
         const double util = (double)npx / (64.0 * m);
-        if (util >= best && tile_fits(K, m, a.W, th, a.synth_ray != 0)) {
+        if (util >= best && tile_fits(K, G, m, a.W, th, a.synth_ray != 0)) {
             best = util;
             a.TW = a.W;
             a.TH = th;
             a.M = m;
         }
     }
+    return best < 0.0 ? 0.0 : best;
+}
+
+// Workgroups below which a launch is latency-bound: two per CU.
+constexpr long long kSmallGrid = 512;
+
+// G and the tile.  A launch of fewer than kSmallGrid workgroups takes the
+// candidate with more of them (its runs are shorter, so its waves finish
+// sooner); a larger one the candidate with the most lanes holding a pixel,
+// the preferred G on ties.
+void choose_tile(AngmfArgs& a, int K) {
+    AngmfArgs alt = a;
+    const double u0 = tile_for(a, K, kGChoices[K][0]);
+    if (kGChoices[K][1] == kGChoices[K][0]) return;
+    const double u1 = tile_for(alt, K, kGChoices[K][1]);
+    if (u1 <= 0.0) return;
+    if (u0 <= 0.0) {
+        a = alt;
+        return;
+    }
+    auto wgs = [](const AngmfArgs& c) {
+        return (long long)((c.W + c.TW - 1) / c.TW) * ((c.H + c.TH - 1) / c.TH) * c.B;
+    };
+    const long long w0 = wgs(a), w1 = wgs(alt);
+    if (w0 < kSmallGrid || w1 < kSmallGrid) {
+        if (w1 > w0) a = alt;
+        return;
+    }
+    if (u1 > u0 + 1e-9) a = alt;
 }
 
 }  // namespace
@@ -1229,7 +1240,12 @@ extern "C" {
 
 const char* bvml_dsine_last_error(void) { return bvml::g_last_error.c_str(); }
 
-const char* bvml_dsine_version(void) { return "0.1.0"; }
+const char* bvml_dsine_version(void) { return "0.2.0"; }
+
+double bvml_dsine_angmf_recompute_ratio(unsigned flags) {
+    if (flags & BVML_DSINE_FP64) return 0.0;
+    return (flags & BVML_DSINE_LOGITS) ? kAccRatio2Logits : kAccRatio2;
+}
 
 int bvml_dsine_build_ray8_f32(float* ray, double fu, double cu, double fv, double cv, int H,
                               int W, void* stream) {
@@ -1335,7 +1351,7 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
     a.logits = (flags & BVML_DSINE_LOGITS) ? 1 : 0;
     a.acc_ratio2 = a.logits ? kAccRatio2Logits : kAccRatio2;
     choose_tile(a, k);
-    if (!tile_fits(k, a.M, a.TW, a.TH, synth))
+    if (!tile_fits(k, a.G, a.M, a.TW, a.TH, synth))
         return fail(BVML_DSINE_ESIZE, "angmf_propagate: no tile fits the kernel's LDS");
     a.tiles_x = (W + a.TW - 1) / a.TW;
     const long long tiles_y = (H + a.TH - 1) / a.TH;
@@ -1353,7 +1369,7 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
     // planes of pred_norm and ray) from one 32-bit buffer offset, and its grid
     // holds one image's tiles in x; larger images also run the
     // double-precision kernel.
-    const long long gw = group_waves(k), nrun = (k * k + gw - 1) / gw;
+    const long long gw = a.G, nrun = (k * k + gw - 1) / gw;
     const long long nplanes = nrun > 3 ? nrun : 3;
     const bool fits32 = nplanes * HW * 4 < (1LL << 32) && tpi < (1LL << 31) &&
                         tpi * 64 * a.M * gw < (1LL << 32);

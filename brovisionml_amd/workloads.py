@@ -141,9 +141,15 @@ def _angles(rng: np.random.Generator, shape, spec: str) -> np.ndarray:
     raise ValueError(spec)
 
 
-def make_sample(wl: Workload, b: int = 0):
-    """Inputs of sample b: dict of float32 arrays shaped (C, H*W)."""
-    rng = np.random.default_rng(wl.seed + b)
+# Seed offset between independent draws of a workload (draw 0 is the stated
+# seed; sample b of draw d uses seed + d * DRAW_STRIDE + b).
+DRAW_STRIDE = 100003
+
+
+def make_sample(wl: Workload, b: int = 0, draw: int = 0):
+    """Inputs of sample b of draw `draw` (0: the workload's stated seed):
+    dict of float32 arrays shaped (C, H*W)."""
+    rng = np.random.default_rng(wl.seed + draw * DRAW_STRIDE + b)
     HW, K2 = wl.HW, wl.K2
     pred = _unit_normals(rng, HW, wl.normals)
     angle = _angles(rng, (K2, HW), wl.angle)
@@ -153,10 +159,11 @@ def make_sample(wl: Workload, b: int = 0):
     return {"pred_norm": pred, "prob": prob, "xy": xy, "angle": angle}
 
 
-def make_inputs(wl: Workload):
-    """All B samples stacked: pred_norm (B,3,HW), prob (B,K2,HW),
-    xy (B,2K2,HW), angle (B,K2,HW); ray (3,HW) shared; (fu,cu,fv,cv)."""
-    samples = [make_sample(wl, b) for b in range(wl.B)]
+def make_inputs(wl: Workload, draw: int = 0):
+    """All B samples of draw `draw` stacked: pred_norm (B,3,HW), prob
+    (B,K2,HW), xy (B,2K2,HW), angle (B,K2,HW); ray (3,HW) shared;
+    (fu,cu,fv,cv)."""
+    samples = [make_sample(wl, b, draw) for b in range(wl.B)]
     out = {key: np.ascontiguousarray(np.stack([s[key] for s in samples]))
            for key in samples[0]}
     intr, (fu, cu, fv, cv) = wl.intrinsics()
@@ -196,10 +203,11 @@ UPSAMPLE_WORKLOADS = [
 ]
 
 
-def make_upsample_inputs(wl: UpsampleWorkload):
+def make_upsample_inputs(wl: UpsampleWorkload, draw: int = 0):
     """x (B, C, H, W) unit normals drawn independently per pixel (the case
-    with the most cancellation between neighbours), mask (B, 9*s*s, H, W)."""
-    rng = np.random.default_rng(wl.seed)
+    with the most cancellation between neighbours), mask (B, 9*s*s, H, W);
+    draw d > 0 is an independent draw (seed + d * DRAW_STRIDE)."""
+    rng = np.random.default_rng(wl.seed + draw * DRAW_STRIDE)
     x = np.stack([_unit_normals(rng, wl.HW, "sphere").reshape(wl.C, wl.H, wl.W)
                   for _ in range(wl.B)])
     mask = (wl.mask_sigma * rng.standard_normal((wl.B, 9 * wl.s * wl.s, wl.H, wl.W),

@@ -132,6 +132,17 @@ int bvml_dsine_convex_upsample_f32(const float* x, const float* mask, int B, int
                                    int W, int scale, int normalize, float eps, float* out,
                                    unsigned flags, void* stream);
 
+/*
+ * The fast path's cancellation threshold for a propagate call with `flags`:
+ * a pixel whose fp32 sum satisfies |acc|^2 < ratio * sum_i (prob_i / |p_i|)^2
+ * (p_i a neighbour's RayReLU'd vector before its normalise) is recomputed in
+ * double, since the final normalise would amplify the fp32 rounding past the
+ * parity bar.  0 for BVML_DSINE_FP64 (nothing is recomputed).  No counterpart
+ * in the reference: it lets a caller count, on its own data, how many pixels
+ * take the slower path.
+ */
+double bvml_dsine_angmf_recompute_ratio(unsigned flags);
+
 /* Message for the calling thread's last non-zero status ("" if none). */
 const char* bvml_dsine_last_error(void);
 

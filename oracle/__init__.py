@@ -58,7 +58,7 @@ class Oracle:
         lib.oracle_ray_relu_f32.argtypes = [vp, vp, i, i, i, ll]
         lib.oracle_ray_relu_f32.restype = None
         lib.oracle_angmf_propagate_rows_f32.argtypes = [
-            vp, vp, vp, vp, vp, d, d, d, d, i, i, i, i, ll, vp, vp, i, i, i]
+            vp, vp, vp, vp, vp, d, d, d, d, i, i, i, i, ll, vp, vp, vp, i, i, i]
         lib.oracle_angmf_propagate_rows_f32.restype = None
         lib.oracle_convex_upsample_f32.argtypes = [
             vp, vp, i, i, i, i, i, i, d, vp, i]
@@ -102,22 +102,28 @@ class Oracle:
         return n
 
     def angmf_propagate(self, pred_norm, prob, xy, angle, ray, intr, H: int, W: int,
-                        k: int = 5, rows=None, nthreads: int = 1, return_acc: bool = False):
+                        k: int = 5, rows=None, nthreads: int = 1, return_acc: bool = False,
+                        return_qs: bool = False):
         """angmf_propagate over all B samples (inferred from pred_norm).
         rows=(y0, y1) limits the output rows computed (others stay NaN).
-        Returns out (float32, pred_norm's shape) [and the double accumulator]."""
+        Returns out (float32, pred_norm's shape) [and the double accumulator
+        (pred_norm's shape)] [and sum over neighbours of (prob/|p|)^2, shaped
+        (B, H*W)], p a neighbour's RayReLU'd vector before its normalise."""
         pn, pr, xyp, ap, rp = (_f32c(a) for a in (pred_norm, prob, xy, angle, ray))
         HW = H * W
         B = pn.size // (3 * HW)
         bstride = 0 if rp.size == 3 * HW else 3 * HW
         out = np.full(pn.shape, np.nan, dtype=np.float32)
         acc = np.full(pn.shape, np.nan, dtype=np.float64) if return_acc else None
+        qs = np.full((B, HW), np.nan, dtype=np.float64) if return_qs else None
         y0, y1 = rows if rows is not None else (0, H)
         fu, cu, fv, cv = intr
         self.lib.oracle_angmf_propagate_rows_f32(
             _ptr(pn), _ptr(pr), _ptr(xyp), _ptr(ap), _ptr(rp), fu, cu, fv, cv, B, H, W, k,
-            bstride, _ptr(out), _ptr(acc) if acc is not None else None, y0, y1, nthreads)
-        return (out, acc) if return_acc else out
+            bstride, _ptr(out), _ptr(acc) if acc is not None else None,
+            _ptr(qs) if qs is not None else None, y0, y1, nthreads)
+        res = (out,) + ((acc,) if return_acc else ()) + ((qs,) if return_qs else ())
+        return res if len(res) > 1 else out
 
 
     def convex_upsample(self, x, mask, H: int, W: int, s: int = 8, normalize: bool = True,

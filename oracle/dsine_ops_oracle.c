@@ -125,9 +125,10 @@ void oracle_axis(double nx, double ny, double nz, double pix_x, double pix_y,
 
 /* RayReLU of one vector against one ray, in double -- the arithmetic of
  * src/dsine_ops.cpp:62-74 (standalone op) and :150-160 (fused copy, where the
- * input is the renormalised rotated neighbour).  Writes normalize(n + diff). */
-void oracle_ray_relu_vec(double nx, double ny, double nz, double rx, double ry,
-                         double rz, double out[3])
+ * input is the renormalised rotated neighbour).  Writes normalize(n + diff)
+ * and, when pinv != NULL, the normalise's factor 1/max(|n + diff|, 1e-12). */
+static void ray_relu_core(double nx, double ny, double nz, double rx, double ry,
+                          double rz, double out[3], double *pinv)
 {
     const double nn = sqrt(nx * nx + ny * ny + nz * nz);
     const double rr = sqrt(rx * rx + ry * ry + rz * rz);
@@ -140,15 +141,22 @@ void oracle_ray_relu_vec(double nx, double ny, double nz, double rx, double ry,
     const double mz = nz + rz * dcoef;
     const double inv = 1.0 / smax(sqrt(mx * mx + my * my + mz * mz), 1e-12);
     out[0] = mx * inv; out[1] = my * inv; out[2] = mz * inv;
+    if (pinv) *pinv = inv;
+}
+
+void oracle_ray_relu_vec(double nx, double ny, double nz, double rx, double ry,
+                         double rz, double out[3])
+{
+    ray_relu_core(nx, ny, nz, rx, ry, rz, out, (double *)0);
 }
 
 /* One neighbour's contribution before the prob weight: rotate the neighbour
  * normal about its axis by theta, renormalise, RayReLU against the output
  * pixel's ray -- src/dsine_ops.cpp:110-160. */
-void oracle_neighbour(double nx, double ny, double nz, double pix_x,
-                      double pix_y, double xs, double ys, double theta,
-                      double rx, double ry, double rz, double fu, double cu,
-                      double fv, double cv, double out[3])
+static void neighbour_core(double nx, double ny, double nz, double pix_x,
+                           double pix_y, double xs, double ys, double theta,
+                           double rx, double ry, double rz, double fu, double cu,
+                           double fv, double cv, double out[3], double *pinv)
 {
     double ax[3], R[9];
     oracle_axis(nx, ny, nz, pix_x, pix_y, xs, ys, fu, cu, fv, cv, ax);
@@ -163,7 +171,16 @@ void oracle_neighbour(double nx, double ny, double nz, double pix_x,
         1.0 / smax(sqrt(rnx * rnx + rny * rny + rnz * rnz), 1e-12);
 #endif
     rnx *= rinv; rny *= rinv; rnz *= rinv;
-    oracle_ray_relu_vec(rnx, rny, rnz, rx, ry, rz, out);
+    ray_relu_core(rnx, rny, rnz, rx, ry, rz, out, pinv);
+}
+
+void oracle_neighbour(double nx, double ny, double nz, double pix_x,
+                      double pix_y, double xs, double ys, double theta,
+                      double rx, double ry, double rz, double fu, double cu,
+                      double fv, double cv, double out[3])
+{
+    neighbour_core(nx, ny, nz, pix_x, pix_y, xs, ys, theta, rx, ry, rz, fu, cu,
+                   fv, cv, out, (double *)0);
 }
 
 /* ray_relu_cpu -- src/dsine_ops.cpp:55-76, batched: sample b uses
@@ -187,17 +204,20 @@ void oracle_ray_relu_f32(float *normal, const float *ray, int B, int H, int W,
 }
 
 /* One output pixel of angmf_propagate_cpu -- src/dsine_ops.cpp:91-170 for a
- * general odd k.  Also returns the double accumulator when acc != NULL. */
+ * general odd k.  Also returns the double accumulator when acc != NULL, and
+ * when qs != NULL the sum over neighbours of (prob / |p|)^2, p a neighbour's
+ * RayReLU'd vector before its normalise (the scale of the sum's rounding
+ * error in an fp32 evaluation, for the fast kernel's error budget). */
 static void angmf_pixel(const float *pn, const float *pr, const float *xyp,
                         const float *ap, const float *rp, double fu, double cu,
                         double fv, double cv, int H, int W, int k, int y, int x,
-                        float *op, double *acc_out)
+                        float *op, double *acc_out, double *qs_out)
 {
     const size_t HW = (size_t)H * (size_t)W;
     const int P = (k - 1) / 2, K2 = k * k;
     const size_t p = (size_t)y * W + x;
     const double rx = rp[p], ry = rp[HW + p], rz = rp[2 * HW + p];
-    double acc0 = 0.0, acc1 = 0.0, acc2 = 0.0;
+    double acc0 = 0.0, acc1 = 0.0, acc2 = 0.0, qs = 0.0;
     for (int n = 0; n < K2; ++n) {
 #if ORACLE_MUTATION == 4 /* mutation: column-major slots */
         const int kx = n / k, ky = n % k;
@@ -217,10 +237,11 @@ static void angmf_pixel(const float *pn, const float *pr, const float *xyp,
         const double ys = xyp[(size_t)(K2 + n) * HW + p];
         const double theta = ap[(size_t)n * HW + p];
         const double w = pr[(size_t)n * HW + p];
-        double m[3];
-        oracle_neighbour(nx, ny, nz, pix_x, pix_y, xs, ys, theta, rx, ry, rz,
-                         fu, cu, fv, cv, m);
+        double m[3], pinv;
+        neighbour_core(nx, ny, nz, pix_x, pix_y, xs, ys, theta, rx, ry, rz,
+                       fu, cu, fv, cv, m, &pinv);
         acc0 += w * m[0]; acc1 += w * m[1]; acc2 += w * m[2];
+        qs += (w * pinv) * (w * pinv);
     }
     const double inv =
         1.0 / smax(sqrt(acc0 * acc0 + acc1 * acc1 + acc2 * acc2), 1e-12);
@@ -232,20 +253,23 @@ static void angmf_pixel(const float *pn, const float *pr, const float *xyp,
         acc_out[HW + p] = acc1;
         acc_out[2 * HW + p] = acc2;
     }
+    if (qs_out) qs_out[p] = qs;
 }
 
 /* angmf_propagate_cpu -- src/dsine_ops.cpp:78-172, batched and restricted to
  * output rows [y0, y1) of every sample (rows outside stay untouched).
  * Sample b reads pred_norm + b*3HW, prob + b*K2*HW, xy + b*2*K2*HW,
  * angle + b*K2*HW, ray + b*ray_bstride and writes out + b*3HW.
- * acc (nullable, 3HW per sample) receives the pre-normalisation sum.
+ * acc (nullable, 3HW per sample) receives the pre-normalisation sum, qs
+ * (nullable, HW per sample) the sum of (prob/|p|)^2 (see angmf_pixel).
  * nthreads > 1 splits rows over OpenMP threads (same per-pixel arithmetic). */
 void oracle_angmf_propagate_rows_f32(const float *pred_norm, const float *prob,
                                      const float *xy, const float *angle,
                                      const float *ray, double fu, double cu,
                                      double fv, double cv, int B, int H, int W,
                                      int k, long long ray_bstride, float *out,
-                                     double *acc, int y0, int y1, int nthreads)
+                                     double *acc, double *qs, int y0, int y1,
+                                     int nthreads)
 {
     const size_t HW = (size_t)H * (size_t)W;
     const size_t K2 = (size_t)k * (size_t)k;
@@ -259,11 +283,12 @@ void oracle_angmf_propagate_rows_f32(const float *pred_norm, const float *prob,
         const float *rp = ray + (size_t)b * (size_t)ray_bstride;
         float *op = out + (size_t)b * 3 * HW;
         double *ac = acc ? acc + (size_t)b * 3 * HW : (double *)0;
+        double *qq = qs ? qs + (size_t)b * HW : (double *)0;
 #pragma omp parallel for schedule(dynamic, 1) num_threads(nthreads) if (nthreads > 1)
         for (int y = y0; y < y1; ++y)
             for (int x = 0; x < W; ++x)
                 angmf_pixel(pn, pr, xyp, ap, rp, fu, cu, fv, cv, H, W, k, y, x,
-                            op, ac);
+                            op, ac, qq);
     }
 }
 
@@ -276,7 +301,7 @@ void oracle_angmf_propagate_f32(const float *pred_norm, const float *prob,
 {
     oracle_angmf_propagate_rows_f32(pred_norm, prob, xy, angle, ray, fu, cu,
                                     fv, cv, B, H, W, k, ray_bstride, out,
-                                    (double *)0, 0, H, 1);
+                                    (double *)0, (double *)0, 0, H, 1);
 }
 
 /* ---------------------------------------------------------------------------

@@ -1,0 +1,170 @@
+// Test infrastructure for gfx950 (nothing in the product links it):
+//   * accuracy sweeps of the hardware transcendentals the fast kernels use
+//     (v_sin_f32, v_cos_f32, v_rsq_f32, v_rcp_f32, v_exp_f32, v_sqrt_f32)
+//     against double-precision references, over every float argument of a
+//     range: the error bounds the kernels' budgets assume
+//     (tests/test_gpu_hw_bounds.py);
+//   * a streaming read of a buffer, the same-box read ceiling bench.py
+//     reports beside the kernels' bandwidth.
+// Every kernel writes one result per workgroup, into arrays the host sizes
+// to the grid, with vector stores.
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+namespace {
+
+enum Op { kSin = 0, kCos = 1, kRsq = 2, kRcp = 3, kExp2 = 4, kSqrt = 5 };
+
+constexpr int kBlock = 256;
+constexpr uint32_t kPerThread = 256;
+
+// Largest absolute and relative error of op over the float bit patterns
+// [lo, hi] (the range's magnitudes; `sign` the sign bit to give them), and
+// the argument of the largest relative error, per workgroup.
+__global__ __launch_bounds__(kBlock) void sweep(int op, uint32_t lo, uint32_t hi, uint32_t sign,
+                                                double* out_abs, double* out_rel,
+                                                uint32_t* out_arg) {
+    __shared__ double sa[kBlock], sr[kBlock];
+    __shared__ uint32_t sg[kBlock];
+    const uint64_t t = (uint64_t)blockIdx.x * kBlock + threadIdx.x;
+    double ma = 0.0, mr = 0.0;
+    uint32_t marg = 0;
+    for (uint32_t i = 0; i < kPerThread; ++i) {
+        const uint64_t bits = (uint64_t)lo + t * kPerThread + i;
+        if (bits > hi) break;
+        const float x = __builtin_bit_cast(float, (uint32_t)bits | sign);
+        double ref, got;
+        switch (op) {
+            case kSin: got = __builtin_amdgcn_sinf(x); ref = sin(2.0 * M_PI * (double)x); break;
+            case kCos: got = __builtin_amdgcn_cosf(x); ref = cos(2.0 * M_PI * (double)x); break;
+            case kRsq: got = __builtin_amdgcn_rsqf(x); ref = 1.0 / sqrt((double)x); break;
+            case kRcp: got = __builtin_amdgcn_rcpf(x); ref = 1.0 / (double)x; break;
+            case kExp2: got = __builtin_amdgcn_exp2f(x); ref = exp2((double)x); break;
+            default: got = __builtin_amdgcn_sqrtf(x); ref = sqrt((double)x); break;
+        }
+        const double ea = fabs(got - ref);
+        const double er = (ref != 0.0) ? ea / fabs(ref) : ea;
+        if (ea > ma) ma = ea;
+        if (er > mr) {
+            mr = er;
+            marg = (uint32_t)bits | sign;
+        }
+    }
+    sa[threadIdx.x] = ma;
+    sr[threadIdx.x] = mr;
+    sg[threadIdx.x] = marg;
+    __syncthreads();
+    for (int s = kBlock / 2; s > 0; s >>= 1) {
+        if ((int)threadIdx.x < s) {
+            sa[threadIdx.x] = fmax(sa[threadIdx.x], sa[threadIdx.x + s]);
+            if (sr[threadIdx.x + s] > sr[threadIdx.x]) {
+                sr[threadIdx.x] = sr[threadIdx.x + s];
+                sg[threadIdx.x] = sg[threadIdx.x + s];
+            }
+        }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) {
+        out_abs[blockIdx.x] = sa[0];
+        out_rel[blockIdx.x] = sr[0];
+        out_arg[blockIdx.x] = sg[0];
+    }
+}
+
+constexpr int kReadBlocks = 8192;
+
+typedef float f4v __attribute__((ext_vector_type(4)));
+
+// Sum of n floats (n4 float4s, then the tail), one partial per workgroup.
+__global__ __launch_bounds__(kBlock) void stream_read(const f4v* p, size_t n4, const float* tail,
+                                                      int ntail, float* out) {
+    __shared__ float s[kBlock];
+    float acc = 0.0f;
+    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n4;
+         i += (size_t)gridDim.x * kBlock) {
+        const f4v v = __builtin_nontemporal_load(p + i);
+        acc += (v.x + v.y) + (v.z + v.w);
+    }
+    if (blockIdx.x == 0 && (int)threadIdx.x < ntail) acc += tail[threadIdx.x];
+    s[threadIdx.x] = acc;
+    __syncthreads();
+    for (int k = kBlock / 2; k > 0; k >>= 1) {
+        if ((int)threadIdx.x < k) s[threadIdx.x] += s[threadIdx.x + k];
+        __syncthreads();
+    }
+    if (threadIdx.x == 0) out[blockIdx.x] = s[0];
+}
+
+uint32_t bits_of(float f) {
+    uint32_t u;
+    std::memcpy(&u, &f, 4);
+    return u;
+}
+
+}  // namespace
+
+extern "C" {
+
+// Largest errors of `op` over every float whose magnitude lies in [lo, hi]
+// (0 <= lo <= hi), with the sign of `negative`.  Returns 0 or a hipError_t.
+int bvml_probe_hw_error(int op, float lo, float hi, int negative, double* max_abs,
+                        double* max_rel, float* argmax) {
+    if (!(lo >= 0.0f) || !(hi >= lo)) return -1;
+    const uint32_t blo = bits_of(lo), bhi = bits_of(hi);
+    const uint64_t n = (uint64_t)bhi - blo + 1;
+    const uint64_t threads = (n + kPerThread - 1) / kPerThread;
+    const uint32_t blocks = (uint32_t)((threads + kBlock - 1) / kBlock);
+    double *da = nullptr, *dr = nullptr;
+    uint32_t* dg = nullptr;
+    hipError_t e = hipMalloc(&da, blocks * sizeof(double));
+    if (e == hipSuccess) e = hipMalloc(&dr, blocks * sizeof(double));
+    if (e == hipSuccess) e = hipMalloc(&dg, blocks * sizeof(uint32_t));
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(sweep, dim3(blocks), dim3(kBlock), 0, 0, op, blo, bhi,
+                           negative ? 0x80000000u : 0u, da, dr, dg);
+        e = hipGetLastError();
+    }
+    std::vector<double> ha(blocks), hr(blocks);
+    std::vector<uint32_t> hg(blocks);
+    if (e == hipSuccess) e = hipMemcpy(ha.data(), da, blocks * sizeof(double), hipMemcpyDeviceToHost);
+    if (e == hipSuccess) e = hipMemcpy(hr.data(), dr, blocks * sizeof(double), hipMemcpyDeviceToHost);
+    if (e == hipSuccess)
+        e = hipMemcpy(hg.data(), dg, blocks * sizeof(uint32_t), hipMemcpyDeviceToHost);
+    if (e == hipSuccess) {
+        double a = 0.0, r = 0.0;
+        uint32_t g = 0;
+        for (uint32_t i = 0; i < blocks; ++i) {
+            a = std::fmax(a, ha[i]);
+            if (hr[i] > r) {
+                r = hr[i];
+                g = hg[i];
+            }
+        }
+        *max_abs = a;
+        *max_rel = r;
+        std::memcpy(argmax, &g, 4);
+    }
+    (void)hipFree(da);
+    (void)hipFree(dr);
+    (void)hipFree(dg);
+    return (int)e;
+}
+
+// Partial sums of n floats at p into out (kReadBlocks floats), on `stream`.
+int bvml_probe_stream_read(const float* p, size_t n, float* out, void* stream) {
+    const size_t n4 = n / 4;
+    const int ntail = (int)(n - 4 * n4);
+    hipLaunchKernelGGL(stream_read, dim3(kReadBlocks), dim3(kBlock), 0,
+                       static_cast<hipStream_t>(stream), reinterpret_cast<const f4v*>(p), n4,
+                       p + 4 * n4, ntail, out);
+    return (int)hipGetLastError();
+}
+
+int bvml_probe_read_blocks(void) { return kReadBlocks; }
+
+}  // extern "C"

@@ -1,0 +1,52 @@
+"""ctypes binding of tests/hw/_build/libbvml_probe.so (built by
+__graft_entry__.build() from tests/hw/probe.hip): hardware-function error
+sweeps and a streaming-read kernel.  Test and measurement infrastructure."""
+from __future__ import annotations
+
+import ctypes
+import os
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB = os.path.join(HERE, "_build", "libbvml_probe.so")
+OPS = {"sin": 0, "cos": 1, "rsq": 2, "rcp": 3, "exp2": 4, "sqrt": 5}
+
+_lib = None
+
+
+def load() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB):
+            raise RuntimeError(f"{LIB} missing: run __graft_entry__.build()")
+        lib = ctypes.CDLL(LIB)
+        d, f, i, vp, sz = ctypes.c_double, ctypes.c_float, ctypes.c_int, ctypes.c_void_p, ctypes.c_size_t
+        lib.bvml_probe_hw_error.argtypes = [i, f, f, i, ctypes.POINTER(d), ctypes.POINTER(d),
+                                            ctypes.POINTER(f)]
+        lib.bvml_probe_hw_error.restype = i
+        lib.bvml_probe_stream_read.argtypes = [vp, sz, vp, vp]
+        lib.bvml_probe_stream_read.restype = i
+        lib.bvml_probe_read_blocks.argtypes = []
+        lib.bvml_probe_read_blocks.restype = i
+        _lib = lib
+    return _lib
+
+
+def hw_error(op: str, lo: float, hi: float, negative: bool = False):
+    """(max abs error, max relative error, argument of the latter) of the
+    hardware function over every float of magnitude in [lo, hi]."""
+    a, r, g = ctypes.c_double(), ctypes.c_double(), ctypes.c_float()
+    st = load().bvml_probe_hw_error(OPS[op], lo, hi, int(negative), ctypes.byref(a),
+                                    ctypes.byref(r), ctypes.byref(g))
+    if st != 0:
+        raise RuntimeError(f"bvml_probe_hw_error failed: {st}")
+    return a.value, r.value, g.value
+
+
+def stream_read(ptr: int, n: int, out_ptr: int, stream: int = 0) -> None:
+    st = load().bvml_probe_stream_read(ptr, n, out_ptr, stream)
+    if st != 0:
+        raise RuntimeError(f"bvml_probe_stream_read failed: {st}")
+
+
+def read_blocks() -> int:
+    return load().bvml_probe_read_blocks()

@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
 
 
 def test_version():
-    assert _lib.load().bvml_dsine_version().decode() == "0.1.0"
+    assert _lib.load().bvml_dsine_version().decode() == "0.2.0"
 
 
 FAKE = 0x10000  # never dereferenced: validation fails or the call is a no-op first
@@ -137,3 +137,14 @@ def test_cpp_dropin_error_paths():
     proc = subprocess.run([CPP_TEST, "cpu"], stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
                           text=True, timeout=120)
     assert proc.returncode == 0, proc.stdout
+
+
+def test_recompute_ratio_query():
+    """The cancellation threshold the fast path recomputes below: positive for
+    the fp32 path (a larger one with the activations formed in the kernel),
+    0 for the double-precision kernel."""
+    t = _lib.angmf_recompute_ratio(_lib.DEFAULT)
+    tl = _lib.angmf_recompute_ratio(_lib.LOGITS)
+    assert 0.0 < t < 1e-2 and 0.0 < tl < 1e-2
+    assert _lib.angmf_recompute_ratio(_lib.FP64) == 0.0
+    assert _lib.angmf_recompute_ratio(_lib.FP64 | _lib.LOGITS) == 0.0

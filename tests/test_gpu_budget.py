@@ -1,0 +1,54 @@
+"""The fast kernel against the error budget of its recompute threshold, on
+the GPU: every input family of tests/budget_families.py (two 128 x 128
+draws each), through the C ABI.  For the pixels the kernel keeps (cancellation
+ratio |acc|^2 / sum (prob/|p|)^2 at or above its threshold, from the oracle's
+double sums) the error stays within 75% of the 1e-5 bar and, in the
+cancellation band, err * sqrt(ratio) within DELTA_KERNEL, the delta the
+threshold is derived from (tests/test_tier1_budget.py); every pixel,
+recomputed ones included, is within the bar."""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from brovisionml_amd import _lib
+from tests import budget_families as fam
+from tests._util import TOL_ABS
+from tests.test_tier1_budget import BAR, DELTA_KERNEL, HEADROOM
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", fam.FAMILIES)
+def test_kernel_budget(cuda, name):
+    import torch
+    worst_kept, worst_delta = 0.0, 0.0
+    for seed in (11, 12):
+        rng = np.random.default_rng(seed)
+        d = fam.family(name, rng, 128, 128)
+        H, W, k = d["H"], d["W"], d["k"]
+        want, ratio = fam.exact_terms(oracle, d)
+        flags = _lib.LOGITS if d["logits"] else _lib.DEFAULT
+        t = {key: torch.from_numpy(np.ascontiguousarray(d[key])).to(cuda)
+             for key in ("pred_norm", "prob", "xy", "angle", "ray")}
+        out = torch.full_like(t["pred_norm"], float("nan"))
+        fu, cu, fv, cv = d["intr"]
+        st = _lib.angmf_propagate_f32(t["pred_norm"].data_ptr(), t["prob"].data_ptr(),
+                                      t["xy"].data_ptr(), t["angle"].data_ptr(),
+                                      t["ray"].data_ptr(), fu, cu, fv, cv, 1, H, W, k, 0,
+                                      out.data_ptr(), flags)
+        assert st == 0, _lib.last_error()
+        torch.cuda.synchronize()
+        got = out.cpu().numpy().reshape(3, -1).astype(np.float64)
+        err = np.abs(got - want).max(axis=0)
+        assert np.isfinite(err).all()
+        assert err.max() <= TOL_ABS
+        keep = ratio >= _lib.angmf_recompute_ratio(flags)
+        band = keep & (ratio < 0.05)
+        worst_kept = max(worst_kept, float(err[keep].max()))
+        if band.any():
+            worst_delta = max(worst_delta, float((err[band] * np.sqrt(ratio[band])).max()))
+    print(f"{name}: worst kept error {worst_kept:.3e}, worst band delta {worst_delta:.3e}",
+          flush=True)
+    assert worst_kept <= HEADROOM * BAR
+    assert worst_delta <= DELTA_KERNEL

@@ -1,72 +1,88 @@
-"""The error budget behind the fast kernel's recompute threshold.
+"""The error budget behind the fast kernel's recompute threshold (CPU).
 
-tier1_model.py rounds every fp32 operation of the kernel's tier 1 as the
-kernel does; this compares its pixels with the oracle and checks that
-err * |acc| / sqrt(sum wi^2) stays within the delta the kernel's threshold
-kAccRatio2 is derived from (3.65e-7, from 1.2M emulated pixels), and that
-delta / sqrt(kAccRatio2) is inside the 1e-5 parity bar.  CPU only."""
+The fast kernel's tier 1 evaluates every neighbour in fp32; its summed error
+behaves like delta * sqrt(sum_i (prob_i/|p_i|)^2) (p_i a neighbour's RayReLU'd
+vector before its normalise), and the final normalise divides it by |acc|.
+A pixel with |acc|^2 < t * sum (prob/|p|)^2 is recomputed in double, so a
+kept pixel's error is at most about delta / sqrt(t).
+
+Two sources fix delta:
+  * the kernel itself, measured on the GPU over the input families of
+    tests/budget_families.py (tests/test_gpu_budget.py re-checks it on every
+    GPU run): DELTA_KERNEL;
+  * tests/tier1_model.py, which rounds every fp32 operation as the kernel does
+    and puts every hardware rsq, sin and cos at its measured error bound
+    (tests/test_gpu_hw_bounds.py pins the bounds): a pessimistic delta.
+The kernel's thresholds keep DELTA_KERNEL / sqrt(t) at least 25% inside the
+1e-5 bar; the pessimistic model keeps every kept pixel inside the bar itself.
+"""
 from __future__ import annotations
-
-import os
-import re
 
 import numpy as np
 import pytest
 
 import oracle
-from brovisionml_amd import workloads as wl
+from brovisionml_amd import _lib
+from tests import budget_families as fam
 from tests import tier1_model as model
 
-ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-DELTA = 3.65e-7
-DELTA_LOGITS = 4.7e-7    # with the activations formed in fp32 (BVML_DSINE_LOGITS)
+# Largest delta the kernel showed over the families' cancellation band
+# (|acc|^2 < 0.05 sum (prob/|p|)^2): 3.17e-7 (antipode) and 3.10e-7 (logits)
+# on 2.6M pixels per family, a 256x256 image per draw; rounded up.
+DELTA_KERNEL = 3.2e-7
+# The pessimistic model's delta over the same band (every hardware function
+# at its bound with a random sign; its largest value over the families here).
+DELTA_MODEL = 6.0e-7
+BAR = 1e-5
+HEADROOM = 0.75
 
 
-def kernel_constant(name: str) -> float:
-    with open(os.path.join(ROOT, "brovisionml_amd", "csrc", "dsine_ops.hip")) as f:
-        src = f.read()
-    m = re.search(r"constexpr double %s = ([0-9.eE+-]+);" % name, src)
-    assert m, name
-    return float(m.group(1))
-
-
-def test_threshold_inside_the_bar():
-    t1 = kernel_constant("kAccRatio2")
-    assert DELTA / np.sqrt(t1) <= 0.92e-5
-    t1l = kernel_constant("kAccRatio2Logits")
-    assert DELTA_LOGITS / np.sqrt(t1l) <= 0.92e-5
-
-
-@pytest.mark.parametrize("H,W,fov,angle,normals,seed", [
-    (48, 64, 60.0, "quarter", "sphere", 1),
-    (40, 40, 140.0, "wide", "sphere", 2),
-    (64, 48, 60.0, "wide", "zbias", 3),
-])
-def test_tier1_model_within_delta(H, W, fov, angle, normals, seed):
+def run_model(name: str, seed: int, H: int = 48, W: int = 48, **kw):
     rng = np.random.default_rng(seed)
-    k, HW, K2 = 5, H * W, 25
-    if normals == "sphere":
-        n = rng.standard_normal((3, HW))
-    else:
-        n = np.vstack([rng.standard_normal((2, HW)), rng.uniform(0.5, 1.0, (1, HW))])
-    n = (n / np.linalg.norm(n, axis=0)).astype(np.float32)
-    th = (rng.uniform(0, np.pi / 4, (K2, HW)) if angle == "quarter"
-          else rng.uniform(-3.2, 3.2, (K2, HW))).astype(np.float32)
-    xy = rng.standard_normal((2 * K2, HW)).astype(np.float32)
-    prob = (1 / (1 + np.exp(-rng.standard_normal((K2, HW))))).astype(np.float32)
-    intr = wl.intrins_from_fov(8 * H, 8 * W, fov)
-    fuv = wl.scaled_intrinsics(intr, H, W, 8 * H, 8 * W)
-    ray = wl.build_ray8(intr, H, W, 8 * H, 8 * W).reshape(3, HW)
-    out, a2, qs = model.tier1(n, prob, xy, th, ray, fuv, H, W, k, rng)
-    want = oracle.angmf_propagate(n[None], prob[None], xy[None], th[None], ray, fuv, H, W, k)
-    want = np.asarray(want, np.float64).reshape(3, HW)
+    d = fam.family(name, rng, H, W)
+    out, _, _ = model.tier1(d["pred_norm"], d["prob"], d["xy"], d["angle"], d["ray"], d["intr"],
+                            d["H"], d["W"], d["k"], rng, logits=d["logits"], **kw)
+    want, ratio = fam.exact_terms(oracle, d)
     err = np.abs(out.astype(np.float32).astype(np.float64) - want).max(axis=0)
-    dpix = err * np.sqrt(a2 / qs)
-    assert np.isfinite(dpix).all()
-    assert dpix.max() <= DELTA
-    # the pixels the kernel keeps are within the bar
-    keep = a2 >= kernel_constant("kAccRatio2") * qs
-    assert err[keep].max() <= 1e-5
+    return err, ratio, d["logits"]
+
+
+def test_thresholds_keep_the_kernel_inside_the_bar():
+    """DELTA_KERNEL / sqrt(t) within 75% of the bar, with and without the
+    activations formed in the kernel."""
+    for flags in (_lib.DEFAULT, _lib.LOGITS):
+        t = _lib.angmf_recompute_ratio(flags)
+        assert DELTA_KERNEL / np.sqrt(t) <= HEADROOM * BAR, (flags, t)
+
+
+@pytest.mark.parametrize("name", fam.FAMILIES)
+def test_model_budget(name):
+    """The pessimistic model over each family: its cancellation-band delta
+    stays within DELTA_MODEL, and every pixel the kernel would keep is inside
+    the bar."""
+    err, ratio, logits = [], [], False
+    for seed in (1, 2):
+        e, r, logits = run_model(name, seed)
+        err.append(e)
+        ratio.append(r)
+    err, ratio = np.concatenate(err), np.concatenate(ratio)
+    assert np.isfinite(err).all()
+    band = ratio < 0.05
+    if band.any():
+        assert (err[band] * np.sqrt(ratio[band])).max() <= DELTA_MODEL
+    t = _lib.angmf_recompute_ratio(_lib.LOGITS if logits else _lib.DEFAULT)
+    keep = ratio >= t
+    assert err[keep].max() <= BAR
+
+
+def test_budget_detects_a_weaker_formulation():
+    """Forming q in fp32 breaks the budget where q and g = P0.m both cancel
+    (normals perpendicular to the viewing ray, xy pairs perpendicular to m):
+    the axis's direction then rests on q's relative accuracy, and the check
+    can fail."""
+    err, ratio, _ = run_model("grazing_qcancel", 3, 64, 64, q_double=False)
+    band = ratio < 0.05
+    assert (err[band] * np.sqrt(ratio[band])).max() > DELTA_MODEL or err.max() > BAR
 
 
 def test_sigmoid_model_error():
@@ -82,26 +98,19 @@ def test_sigmoid_model_error():
     assert np.all(model.sigmoid(np.array([-np.inf, -1e30, -88.0], np.float32), rng) == 0)
 
 
-@pytest.mark.parametrize("H,W,fov,scale,seed", [(64, 64, 60.0, 1.0, 1), (48, 48, 140.0, 3.0, 2)])
-def test_tier1_model_logits_within_delta(H, W, fov, scale, seed):
-    rng = np.random.default_rng(seed)
-    k, HW, K2 = 5, H * W, 25
-    n = rng.standard_normal((3, HW))
-    n = (n / np.linalg.norm(n, axis=0)).astype(np.float32)
-    lp = (rng.standard_normal((K2, HW)) * scale).astype(np.float32)
-    la = (rng.standard_normal((K2, HW)) * scale).astype(np.float32)
-    xy = rng.standard_normal((2 * K2, HW)).astype(np.float32)
-    intr = wl.intrins_from_fov(8 * H, 8 * W, fov)
-    fuv = wl.scaled_intrinsics(intr, H, W, 8 * H, 8 * W)
-    ray = wl.build_ray8(intr, H, W, 8 * H, 8 * W).reshape(3, HW)
-    out, a2, qs = model.tier1(n, lp, xy, la, ray, fuv, H, W, k, rng, logits=True)
-    sp = (1.0 / (1.0 + np.exp(-lp.astype(np.float64)))).astype(np.float32)
-    sa = (1.0 / (1.0 + np.exp(-la.astype(np.float64)))).astype(np.float32)
-    ang = (sa.astype(np.float64) * np.float64(model.K_PI)).astype(np.float32)
-    want = oracle.angmf_propagate(n[None], sp[None], xy[None], ang[None], ray, fuv, H, W, k)
-    want = np.asarray(want, np.float64).reshape(3, HW)
-    err = np.abs(out.astype(np.float32).astype(np.float64) - want).max(axis=0)
-    dpix = err * np.sqrt(a2 / qs)
-    assert dpix.max() <= DELTA_LOGITS
-    keep = a2 >= kernel_constant("kAccRatio2Logits") * qs
-    assert err[keep].max() <= 1e-5
+def test_sincos_model_matches_the_kernel_form():
+    """sincos_hw's correction: with exact hardware sine and cosine the
+    corrected pair is within 1.5e-7 of sin t, cos t over |t| <= 3.2, and the
+    uncorrected argument alone would be off by up to 1.9e-7 at |t| = 3.2."""
+    t = np.linspace(-3.2, 3.2, 100001).astype(np.float32)
+    saved = model.SIN_ABS
+    try:
+        model.SIN_ABS = 0.0
+        s, c = model.sincos(t, np.random.default_rng(0))
+    finally:
+        model.SIN_ABS = saved
+    td = t.astype(np.float64)
+    assert np.abs(s - np.sin(td)).max() < 1.5e-7
+    assert np.abs(c - np.cos(td)).max() < 1.5e-7
+    a = (t * model.INV_2PI).astype(np.float32).astype(np.float64)
+    assert np.abs(np.sin(2 * np.pi * a) - np.sin(td)).max() > 1.5e-7
