@@ -33,6 +33,8 @@ EXPORTS = (
     "bvml_dsine_build_ray8_f32",
     "bvml_dsine_convex_upsample_f32",
     "bvml_dsine_angmf_recompute_ratio",
+    "bvml_dsine_ray_relu_cpu_f32",
+    "bvml_dsine_angmf_propagate_cpu_f32",
     "bvml_dsine_last_error",
     "bvml_dsine_version",
 )
@@ -63,6 +65,11 @@ def load(path: str = LIB) -> ctypes.CDLL:
     lib.bvml_dsine_convex_upsample_f32.restype = i
     lib.bvml_dsine_angmf_recompute_ratio.argtypes = [u]
     lib.bvml_dsine_angmf_recompute_ratio.restype = d
+    lib.bvml_dsine_ray_relu_cpu_f32.argtypes = [vp, vp, i, i, i, ll, i]
+    lib.bvml_dsine_ray_relu_cpu_f32.restype = i
+    lib.bvml_dsine_angmf_propagate_cpu_f32.argtypes = [
+        vp, vp, vp, vp, vp, d, d, d, d, i, i, i, i, ll, vp, u, i]
+    lib.bvml_dsine_angmf_propagate_cpu_f32.restype = i
     lib.bvml_dsine_last_error.argtypes = []
     lib.bvml_dsine_last_error.restype = ctypes.c_char_p
     lib.bvml_dsine_version.argtypes = []
@@ -109,3 +116,19 @@ def angmf_recompute_ratio(flags: int = DEFAULT) -> float:
     """The fast path's cancellation threshold: pixels with |acc|^2 below
     this times sum (prob/|p|)^2 are recomputed in double."""
     return load().bvml_dsine_angmf_recompute_ratio(flags)
+
+
+def ray_relu_cpu_f32(normal: int, ray: int, B: int, H: int, W: int, ray_bstride: int,
+                     nthreads: int = 0) -> int:
+    """Raw call of the CPU branch; pointers are host addresses."""
+    return load().bvml_dsine_ray_relu_cpu_f32(normal, ray, B, H, W, ray_bstride, nthreads)
+
+
+def angmf_propagate_cpu_f32(pred_norm: int, prob: int, xy: int, angle: int, ray: int,
+                            fu: float, cu: float, fv: float, cv: float,
+                            B: int, H: int, W: int, k: int, ray_bstride: int,
+                            out: int, flags: int = DEFAULT, nthreads: int = 0) -> int:
+    """Raw call of the CPU branch; pointers are host addresses."""
+    return load().bvml_dsine_angmf_propagate_cpu_f32(
+        pred_norm, prob, xy, angle, ray, fu, cu, fv, cv, B, H, W, k, ray_bstride, out, flags,
+        nthreads)

@@ -1,9 +1,15 @@
-"""Build recipe for the native library (hipcc, gfx950 only).
+"""Build recipe for the native libraries (hipcc for gfx950, g++ for plain C++).
 
-`build()` compiles every time it is called:
-  brovisionml_amd/lib/libbvml_dsine.so  -- HIP kernels, the C ABI
-                                          (include/bvml_dsine.h) and the C++
-                                          drop-in layer (include/brovisionml/)
+`build_library()` compiles every time it is called, into brovisionml_amd/lib/:
+  libbvml_dsine.so        HIP kernels and the CPU branch behind one C ABI
+                          (include/bvml_dsine.h); extern "C" symbols only
+  libbvml_dsine_cxx.so    the C++ drop-in brovisionml::dsine::* (dsine_ops.cpp,
+                          include/brovisionml/dsine_ops.h), plain C++ over the
+                          C ABI; brotensor::Tensor left undefined, to be
+                          resolved by brotensor or by the subset below
+  libbrotensor_subset.so  the brotensor::Tensor subset of
+                          include/brotensor/tensor.h, for standalone use and
+                          the C++ tests; a brovisionml build links brotensor
 Run as `python -m brovisionml_amd.build`.
 """
 from __future__ import annotations
@@ -15,10 +21,14 @@ import sys
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 PKG = os.path.join(ROOT, "brovisionml_amd")
 CSRC = os.path.join(PKG, "csrc")
+INCLUDE = os.path.join(ROOT, "include")
 LIBDIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIBDIR, "libbvml_dsine.so")
+LIB_CXX = os.path.join(LIBDIR, "libbvml_dsine_cxx.so")
+LIB_TENSOR = os.path.join(LIBDIR, "libbrotensor_subset.so")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
+CXX = os.environ.get("CXX", "g++")
 
 # Packed fp32 instructions are disabled for all device code: only the scalar
 # fp32 forms are generated.
@@ -35,12 +45,21 @@ HIP_FLAGS = [
     "-Wall",
 ]
 
+# Host C++ (the CPU branch, the C++ layer).  Contraction off keeps the CPU
+# branch's double arithmetic in the reference's operation order.
+CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fno-fast-math", "-Wall",
+             "-Wextra", "-pthread"]
+
 SOURCES = [
-    os.path.join(CSRC, "dsine_ops.hip"),   # kernels + C ABI
-    os.path.join(CSRC, "upsample.hip"),    # convex upsample + normalise
-    os.path.join(CSRC, "dsine_ops.cpp"),   # C++ drop-in (brovisionml::dsine)
-    os.path.join(CSRC, "tensor.cpp"),      # brotensor::Tensor subset
+    os.path.join(CSRC, "dsine_ops.hip"),      # AngMF / RayReLU kernels + C ABI
+    os.path.join(CSRC, "upsample.hip"),       # convex upsample + normalise
 ]
+HOST_SOURCES = [
+    os.path.join(CSRC, "dsine_ops_cpu.cpp"),  # CPU branch (C ABI *_cpu_f32)
+    os.path.join(CSRC, "status.cpp"),         # error state, bvml_dsine_last_error
+]
+CXX_SOURCES = [os.path.join(CSRC, "dsine_ops.cpp")]
+TENSOR_SOURCES = [os.path.join(CSRC, "tensor.cpp")]
 
 
 def _run(cmd: list[str]) -> None:
@@ -50,15 +69,44 @@ def _run(cmd: list[str]) -> None:
         raise RuntimeError("build failed: " + " ".join(cmd))
 
 
+def _install(tmp: str, dst: str) -> None:
+    os.replace(tmp, dst)
+
+
 def build_library() -> str:
+    """Builds the three libraries; returns the C ABI library's path."""
     os.makedirs(LIBDIR, exist_ok=True)
-    tmp = LIB + ".tmp"
-    cmd = [HIPCC, *HIP_FLAGS, "-I", os.path.join(ROOT, "include"), "-shared",
-           "-o", tmp, *SOURCES]
-    _run(cmd)
-    os.replace(tmp, LIB)
+    objdir = os.path.join(PKG, "_build")
+    os.makedirs(objdir, exist_ok=True)
+    host_objs = []
+    for src in HOST_SOURCES:
+        obj = os.path.join(objdir, os.path.basename(src) + ".o")
+        _run([CXX, *CXX_FLAGS, "-I", INCLUDE, "-c", src, "-o", obj])
+        host_objs.append(obj)
+    # objects first: hipcc reads every file after a .hip source as HIP
+    _run([HIPCC, *HIP_FLAGS, "-I", INCLUDE, "-shared", "-o", LIB + ".tmp", *host_objs, *SOURCES,
+          "-Wl,--version-script=" + os.path.join(CSRC, "libbvml_dsine.map")])
+    _install(LIB + ".tmp", LIB)
+    _run([CXX, *CXX_FLAGS, "-I", INCLUDE, "-shared", "-o", LIB_CXX + ".tmp", *CXX_SOURCES,
+          "-L", LIBDIR, "-lbvml_dsine", "-Wl,-rpath,$ORIGIN",
+          "-Wl,--version-script=" + os.path.join(CSRC, "libbvml_dsine_cxx.map")])
+    _install(LIB_CXX + ".tmp", LIB_CXX)
+    _run([HIPCC, "-O2", "-std=c++17", "-fPIC", "-I", INCLUDE, "-shared", "-o", LIB_TENSOR + ".tmp",
+          *TENSOR_SOURCES])
+    _install(LIB_TENSOR + ".tmp", LIB_TENSOR)
     return LIB
+
+
+def check_brotensor_api() -> None:
+    """Compiles the C++ layer and the launchers header against a header that
+    declares only what brovisionml's sources use of brotensor::Tensor
+    (tests/cpp/brotensor_api/brotensor/tensor.h)."""
+    api = os.path.join(ROOT, "tests", "cpp", "brotensor_api")
+    for src in (*CXX_SOURCES, os.path.join(api, "launchers_check.cpp")):
+        _run([CXX, "-std=c++17", "-fsyntax-only", "-Wall", "-Wextra", "-I", api, "-I", INCLUDE,
+              src])
 
 
 if __name__ == "__main__":
     print(build_library())
+    check_brotensor_api()

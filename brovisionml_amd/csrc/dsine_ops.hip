@@ -51,31 +51,21 @@
 #include <string>
 #include <type_traits>
 
+#include "angmf_ref.h"
 #include "bvml_dsine.h"
 #include "status.h"
 
 
-namespace bvml {
-
-thread_local std::string g_last_error;
-
-int fail(int code, const std::string& msg) {
-    g_last_error = msg;
-    return code;
-}
-
-bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
-    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
-    return a0 < b0 + bbytes && b0 < a0 + abytes;
-}
-
-}  // namespace bvml
-
 namespace {
 
-// src/dsine_ops.cpp:27: the float 1e-2f, widened to double where the
-// reference does arithmetic in double.
-constexpr float kRayEpsF = 1e-2f;
+using bvml::angle_ref;
+using bvml::kPiF;
+using bvml::kRayEpsF;
+using bvml::nbr_ref_f64;
+using bvml::ray_relu_ref;
+using bvml::sigmoid_ref;
+using bvml::smax;
+using bvml::synth_ray;
 
 // The fast path takes source normals with | |m|^2 - 1 | <= kUnitM2 (every
 // normal this op or RayReLU writes is one) and raw xy pairs with
@@ -117,7 +107,6 @@ constexpr double kAccRatio2 = 1.85e-3;
 // rsq(|p|^2 (1 + exp(-L))^2)); the same measurement gives delta <= 3.10e-7
 // (saturated logits N(0, 30^2)), inside the same threshold's 3.2e-7.  Tiers
 // 2 and 3 use the correctly rounded floats (sigmoid_ref).
-constexpr float kPiF = 3.14159265358979323846f;
 constexpr double kAccRatio2Logits = 1.85e-3;
 
 // Tier 2 (the double-precision reduced form of flagged pixels) hands a pixel
@@ -145,118 +134,6 @@ constexpr double kDdClampRef = 1.0001e-8;
 // view up to about 150 degrees): its |V| stays within fp32 range and its
 // error bound above holds.  Wider views run the double-precision kernel.
 constexpr double kMaxP0 = 4.0;
-
-// ---------------------------------------------------------------------------
-// Double-precision reference body
-// ---------------------------------------------------------------------------
-
-// std::max(a, b) == (a < b) ? b : a -- returns a when a is NaN, as the
-// reference CPU path does (fmax would not).
-__device__ __forceinline__ double smax(double a, double b) { return (a < b) ? b : a; }
-
-// The activations the refiner applies to the prob and angle heads
-// (src/dsine_refine.cpp:262-267), as correctly rounded floats: sigmoid in
-// double, rounded once; the angle's product with the float pi in float.
-__device__ __forceinline__ float sigmoid_ref(float x) {
-    return (float)(1.0 / (1.0 + exp(-(double)x)));
-}
-__device__ __forceinline__ float angle_ref(float x) { return sigmoid_ref(x) * kPiF; }
-
-// The ray of pixel (x, y) as build_ray8 forms it from the grid-scaled
-// intrinsics (src/dsine_decoder.cpp:252-253 and :285-290): ray_x, ray_y in
-// double rounded to float, then [ray_x, ray_y, 1] normalised in double and
-// each channel rounded to float.  IEEE double division and square root, in
-// the host's operation order with contraction off, give the host's bits.
-__device__ __forceinline__ float3 synth_ray(int x, int y, double fu, double cu, double fv,
-                                            double cv) {
-#pragma clang fp contract(off)
-    const double rx = (float)(((x + 0.5) - cu) / fu);
-    const double ry = (float)(((y + 0.5) - cv) / fv);
-    const double rz = 1.0;
-    const double inv = 1.0 / smax(sqrt(rx * rx + ry * ry + rz * rz), 1e-12);
-    return make_float3((float)(rx * inv), (float)(ry * inv), (float)(rz * inv));
-}
-
-// One neighbour's RayReLU'd rotated normal, in the operation order of
-// src/dsine_ops.cpp:110-160 (axis :110-138, axis_angle_to_matrix :31-51,
-// rotate + renormalise :140-148, RayReLU :150-160).  Contraction is off so
-// the sign-deciding dd is bit-identical to the CPU's.  pinv is the last
-// normalise's 1/max(|p|, 1e-12).
-__device__ __forceinline__ void nbr_ref_f64(double nx, double ny, double nz,
-                                            double pix_x, double pix_y,
-                                            double xs, double ys, double theta,
-                                            double rx, double ry, double rz,
-                                            double fu, double cu, double fv,
-                                            double cv, double& ox, double& oy,
-                                            double& oz, double& pinv) {
-#pragma clang fp contract(off)
-    const double xyinv = 1.0 / smax(sqrt(xs * xs + ys * ys), 1e-12);
-    xs *= xyinv;
-    ys *= xyinv;
-    const double du = xs / fu;
-    const double dv = ys / fv;
-    const double tu = (pix_x + xs - cu) / fu;
-    const double tv = (pix_y + ys - cv) / fv;
-    const double num = -(du * nx + dv * ny);
-    double dd = tu * nx + tv * ny + nz;
-    if (fabs(dd) < 1e-8) {
-        const double sgn = (dd > 0.0) ? 1.0 : (dd < 0.0 ? -1.0 : 0.0);
-        dd = 1e-8 * sgn;
-    }
-    const double dz = num / dd;
-    double axx = du + dz * tu;
-    double axy = dv + dz * tv;
-    double axz = dz;
-    const double an = sqrt(axx * axx + axy * axy + axz * axz);
-    const double ainv = 1.0 / smax(an, 1e-12);
-    axx *= ainv;
-    axy *= ainv;
-    axz *= ainv;
-    if (!isfinite(axx) || !isfinite(axy) || !isfinite(axz)) axx = axy = axz = 0.0;
-
-    // axis_angle_to_matrix(axis * theta), quaternion form.
-    const double vx = axx * theta, vy = axy * theta, vz = axz * theta;
-    const double angle = sqrt(vx * vx + vy * vy + vz * vz);
-    const double half = angle * 0.5;
-    double s;
-    if (angle < 1e-6)
-        s = 0.5 - (angle * angle) / 48.0;
-    else
-        s = sin(half) / angle;
-    const double qr = cos(half);
-    const double qi = vx * s, qj = vy * s, qk = vz * s;
-    const double two_s = 2.0 / (qr * qr + qi * qi + qj * qj + qk * qk);
-    const double R0 = 1.0 - two_s * (qj * qj + qk * qk);
-    const double R1 = two_s * (qi * qj - qk * qr);
-    const double R2 = two_s * (qi * qk + qj * qr);
-    const double R3 = two_s * (qi * qj + qk * qr);
-    const double R4 = 1.0 - two_s * (qi * qi + qk * qk);
-    const double R5 = two_s * (qj * qk - qi * qr);
-    const double R6 = two_s * (qi * qk - qj * qr);
-    const double R7 = two_s * (qj * qk + qi * qr);
-    const double R8 = 1.0 - two_s * (qi * qi + qj * qj);
-
-    double rnx = R0 * nx + R1 * ny + R2 * nz;
-    double rny = R3 * nx + R4 * ny + R5 * nz;
-    double rnz = R6 * nx + R7 * ny + R8 * nz;
-    const double rinv = 1.0 / smax(sqrt(rnx * rnx + rny * rny + rnz * rnz), 1e-12);
-    rnx *= rinv;
-    rny *= rinv;
-    rnz *= rinv;
-
-    const double nn = sqrt(rnx * rnx + rny * rny + rnz * rnz);
-    const double rr = sqrt(rx * rx + ry * ry + rz * rz);
-    const double denom = smax(nn * rr, 1e-8);
-    const double cs = (rnx * rx + rny * ry + rnz * rz) / denom;
-    const double relu_cm = smax(cs - (double)kRayEpsF, 0.0) + (double)kRayEpsF;
-    const double dcoef = relu_cm - cs;
-    double mx = rnx + rx * dcoef, my = rny + ry * dcoef, mz = rnz + rz * dcoef;
-    const double minv = 1.0 / smax(sqrt(mx * mx + my * my + mz * mz), 1e-12);
-    ox = mx * minv;
-    oy = my * minv;
-    oz = mz * minv;
-    pinv = minv;
-}
 
 __device__ __forceinline__ int clampi(int v, int lo, int hi) {
     return v < lo ? lo : (v > hi ? hi : v);
@@ -316,7 +193,7 @@ __global__ __launch_bounds__(256) void angmf_f64_kernel(AngmfArgs a) {
 
     double rx, ry, rz;
     if (a.synth_ray) {
-        const float3 r = synth_ray(x, y, a.fu, a.cu, a.fv, a.cv);
+        const bvml::Ray3f r = synth_ray(x, y, a.fu, a.cu, a.fv, a.cv);
         rx = r.x;
         ry = r.y;
         rz = r.z;
@@ -787,7 +664,7 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
         if ((int)threadIdx.x < npx) {
             const int t = threadIdx.x;
             const int rty = small_div(t, rtw), rtx = t - rty * TW;
-            const float3 r3 = synth_ray(min(tx0 + rtx, W - 1), min(ty0 + rty, H - 1), a.fu, a.cu,
+            const bvml::Ray3f r3 = synth_ray(min(tx0 + rtx, W - 1), min(ty0 + rty, H - 1), a.fu, a.cu,
                                         a.fv, a.cv);
             rayl[t] = make_float4(r3.x, r3.y, r3.z, 0.0f);
         }
@@ -965,7 +842,7 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
         float frx = 0.0f, fry = 0.0f, frz = 0.0f;
         if (act) {
             if constexpr (SR) {
-                const float3 rr3 = synth_ray(fx, fy, a.fu, a.cu, a.fv, a.cv);
+                const bvml::Ray3f rr3 = synth_ray(fx, fy, a.fu, a.cu, a.fv, a.cv);
                 frx = rr3.x;
                 fry = rr3.y;
                 frz = rr3.z;
@@ -1062,19 +939,11 @@ __global__ __launch_bounds__(256) void ray_relu_kernel(float* normal, const floa
     const long long p = gid - b * HW;
     float* n = normal + b * 3 * HW;
     const float* r = ray + b * ray_bstride;
-    const double nx = n[p], ny = n[HW + p], nz = n[2 * HW + p];
-    const double rx = r[p], ry = r[HW + p], rz = r[2 * HW + p];
-    const double nn = sqrt(nx * nx + ny * ny + nz * nz);
-    const double rr = sqrt(rx * rx + ry * ry + rz * rz);
-    const double denom = smax(nn * rr, 1e-8);
-    const double cs = (nx * rx + ny * ry + nz * rz) / denom;
-    const double relu_cm = smax(cs - (double)kRayEpsF, 0.0) + (double)kRayEpsF;
-    const double dcoef = relu_cm - cs;
-    const double mx = nx + rx * dcoef, my = ny + ry * dcoef, mz = nz + rz * dcoef;
-    const double inv = 1.0 / smax(sqrt(mx * mx + my * my + mz * mz), 1e-12);
-    n[p] = (float)(mx * inv);
-    n[HW + p] = (float)(my * inv);
-    n[2 * HW + p] = (float)(mz * inv);
+    double ox, oy, oz, inv;
+    ray_relu_ref(n[p], n[HW + p], n[2 * HW + p], r[p], r[HW + p], r[2 * HW + p], ox, oy, oz, inv);
+    n[p] = (float)ox;
+    n[HW + p] = (float)oy;
+    n[2 * HW + p] = (float)oz;
 }
 
 // ---------------------------------------------------------------------------
@@ -1086,7 +955,7 @@ __global__ __launch_bounds__(256) void build_ray8_kernel(float* ray, double fu, 
     const long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x;
     if (p >= HW) return;
     const int y = (int)(p / W), x = (int)(p - (long long)y * W);
-    const float3 r = synth_ray(x, y, fu, cu, fv, cv);
+    const bvml::Ray3f r = synth_ray(x, y, fu, cu, fv, cv);
     ray[p] = r.x;
     ray[HW + p] = r.y;
     ray[2 * HW + p] = r.z;
@@ -1237,8 +1106,6 @@ void choose_tile(AngmfArgs& a, int K) {
 }  // namespace
 
 extern "C" {
-
-const char* bvml_dsine_last_error(void) { return bvml::g_last_error.c_str(); }
 
 const char* bvml_dsine_version(void) { return "0.2.0"; }
 

@@ -14,4 +14,7 @@ int fail(int code, const std::string& msg);
 // Whether [a, a + abytes) and [b, b + bbytes) overlap.
 bool overlaps(const void* a, std::size_t abytes, const void* b, std::size_t bbytes);
 
+// The calling thread's last error message ("" if none).
+const char* last_error();
+
 }  // namespace bvml

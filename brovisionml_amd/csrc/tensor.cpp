@@ -1,5 +1,6 @@
 // Minimal brotensor::Tensor storage (include/brotensor/tensor.h): host memory
-// from operator new, device memory from hipMalloc, both reference-counted.
+// from operator new, device memory (the CUDA and Metal tags alike: this build's
+// one GPU) from hipMalloc, both reference-counted.
 
 #include "brotensor/tensor.h"
 
@@ -25,6 +26,10 @@ std::shared_ptr<void> host_alloc(std::size_t bytes) {
     return std::shared_ptr<void>(p, [](void* q) { ::operator delete(q); });
 }
 
+std::size_t elements(const Tensor& t) {
+    return static_cast<std::size_t>(t.rows) * static_cast<std::size_t>(t.cols);
+}
+
 std::shared_ptr<void> device_alloc(std::size_t bytes) {
     void* p = nullptr;
     hip_check(hipMalloc(&p, bytes == 0 ? 1 : bytes), "hipMalloc");
@@ -38,26 +43,30 @@ Tensor Tensor::mat(int rows, int cols) {
     Tensor t;
     t.rows = rows;
     t.cols = cols;
-    t.storage_ = host_alloc(t.numel() * sizeof(float));
+    t.storage_ = host_alloc(elements(t) * sizeof(float));
     t.data = t.storage_.get();
     return t;
 }
 
-Tensor Tensor::zeros_on(Device dev, int rows, int cols) {
+Tensor Tensor::empty_on(Device dev, int rows, int cols) {
     if (rows < 0 || cols < 0) fail("negative shape");
     Tensor t;
     t.device = dev;
     t.rows = rows;
     t.cols = cols;
-    const std::size_t bytes = t.numel() * sizeof(float);
-    if (dev == Device::CPU) {
-        t.storage_ = host_alloc(bytes);
-        std::memset(t.storage_.get(), 0, bytes);
-    } else {
-        t.storage_ = device_alloc(bytes);
-        hip_check(hipMemset(t.storage_.get(), 0, bytes), "hipMemset");
-    }
+    const std::size_t bytes = elements(t) * sizeof(float);
+    t.storage_ = (dev == Device::CPU) ? host_alloc(bytes) : device_alloc(bytes);
     t.data = t.storage_.get();
+    return t;
+}
+
+Tensor Tensor::zeros_on(Device dev, int rows, int cols) {
+    Tensor t = empty_on(dev, rows, cols);
+    const std::size_t bytes = elements(t) * sizeof(float);
+    if (dev == Device::CPU)
+        std::memset(t.data, 0, bytes);
+    else
+        hip_check(hipMemset(t.data, 0, bytes), "hipMemset");
     return t;
 }
 
@@ -77,7 +86,7 @@ Tensor Tensor::to(Device dev) const {
     t.device = dev;
     t.rows = rows;
     t.cols = cols;
-    const std::size_t bytes = numel() * sizeof(float);
+    const std::size_t bytes = elements(*this) * sizeof(float);
     if (dev == Device::CPU) {
         t.storage_ = host_alloc(bytes);
         hip_check(hipMemcpy(t.storage_.get(), data, bytes, hipMemcpyDeviceToHost), "hipMemcpy D2H");

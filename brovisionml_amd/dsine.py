@@ -13,15 +13,21 @@ reference is brotensor's convex_upsample_forward + l2_normalize_nchw_forward:
   convex_upsample(x, mask, N, C, H, W, scale, out)
   convex_upsample_normalize(x, mask, N, C, H, W, scale, eps, out)   fused
 
-Tensors are torch tensors on a HIP device (torch is only the allocator and
-stream provider here), fp32, contiguous, in the reference's NCHW layout:
+Tensors are torch tensors (torch is only the allocator and stream provider
+here), fp32, contiguous, in the reference's NCHW layout:
 (1, C*H*W), (C, H, W), or batched (B, C, H, W) / (B, C*H*W).  A batch of B
 samples is inferred from pred_norm / normal; the window size k from prob.
 `ray` may hold one map (3*H*W, shared) or one per sample.
 
+ray_relu and angmf_propagate dispatch on the tensors' device as the
+reference's public dispatch does (src/dsine_ops.cpp:178-215): CPU tensors run
+the library's CPU branch (double precision in the reference's operation
+order, equal to the reference CPU twin bit for bit), tensors on the GPU the
+gfx950 kernels.  The convex upsample replaces brotensor's GPU kernels only:
+CPU tensors raise.
+
 Errors raise RuntimeError with the reference's "dsine ops: " prefix
-(src/dsine_ops.cpp:18-22).  CPU tensors raise: this library is the HIP
-device path only (brovisionml keeps its CPU twin).
+(src/dsine_ops.cpp:18-22).
 """
 from __future__ import annotations
 
@@ -36,16 +42,19 @@ def _fail(msg: str):
     raise RuntimeError(_WHO + msg)
 
 
-def _check_tensors(op: str, tensors) -> None:
+def _check_tensors(op: str, tensors, cpu_ok: bool = False) -> None:
     dev = tensors[0].device
     for t in tensors[1:]:
         if t.device != dev:
             if op == "ray_relu":
                 _fail("ray_relu: normal and ray must share a device")
+            if op.startswith("convex_upsample"):
+                _fail(f"{op}: x and mask must share a device")
             _fail(f"{op}: all inputs must share a device")
-    if dev.type != "cuda":
-        _fail(f"{op}: tensors are on the {dev.type.upper()}; this library "
-              "implements the HIP device path only")
+    if dev.type == "cpu" and not cpu_ok:
+        _fail(f"{op}: tensors are on the CPU; this op replaces brotensor's GPU kernels only")
+    if dev.type not in ("cpu", "cuda"):
+        _fail(f"{op}: tensors on a device this library does not run (CPU and the HIP GPU only)")
     import torch
     for t in tensors:
         if t.dtype != torch.float32:
@@ -74,7 +83,7 @@ def _raise_status(op: str, status: int) -> None:
 
 def ray_relu(normal, ray, H: int, W: int) -> None:
     """RayReLU (eps 1e-2) in place on `normal` (src/dsine_ops.cpp:55-76)."""
-    _check_tensors("ray_relu", [normal, ray])
+    _check_tensors("ray_relu", [normal, ray], cpu_ok=True)
     HW = H * W
     if HW == 0:
         return
@@ -82,6 +91,10 @@ def ray_relu(normal, ray, H: int, W: int) -> None:
         _fail("ray_relu: normal must hold B*3*H*W elements")
     B = normal.numel() // (3 * HW)
     bstride = _ray_stride("ray_relu", ray, B, HW)
+    if normal.device.type == "cpu":
+        _raise_status("ray_relu", _lib.ray_relu_cpu_f32(normal.data_ptr(), ray.data_ptr(), B, H,
+                                                        W, bstride))
+        return
     with _device(normal):
         st = _lib.ray_relu_f32(normal.data_ptr(), ray.data_ptr(), B, H, W, bstride,
                                _stream_of(normal))
@@ -97,8 +110,11 @@ def angmf_propagate(pred_norm, prob, xy, angle, ray, fu: float, cu: float,
     pixel's ray from fu, cu, fv, cv in the kernel, bit-identical to
     build_ray8 (src/dsine_decoder.cpp:242-293).  logits=True takes prob and
     angle as the heads' raw logits and applies the refiner's activations
-    (src/dsine_refine.cpp:262-267: sigmoid, and sigmoid * pi) in the kernel."""
-    _check_tensors("angmf_propagate", [pred_norm, prob, xy, angle] + ([] if ray is None else [ray]))
+    (src/dsine_refine.cpp:262-267: sigmoid, and sigmoid * pi) in the kernel.
+    CPU tensors run the CPU branch, which is double precision in the
+    reference's order whatever `precise` says."""
+    _check_tensors("angmf_propagate", [pred_norm, prob, xy, angle] + ([] if ray is None else [ray]),
+                   cpu_ok=True)
     import torch
     HW = H * W
     if out is None:
@@ -127,6 +143,13 @@ def angmf_propagate(pred_norm, prob, xy, angle, ray, fu: float, cu: float,
         flags |= _lib.RAY_FROM_INTRINSICS
     if logits:
         flags |= _lib.LOGITS
+    if pred_norm.device.type == "cpu":
+        st = _lib.angmf_propagate_cpu_f32(
+            pred_norm.data_ptr(), prob.data_ptr(), xy.data_ptr(), angle.data_ptr(),
+            0 if ray is None else ray.data_ptr(), float(fu), float(cu), float(fv), float(cv),
+            B, H, W, k, bstride, out.data_ptr(), flags)
+        _raise_status("angmf_propagate", st)
+        return out
     with _device(pred_norm):
         st = _lib.angmf_propagate_f32(
             pred_norm.data_ptr(), prob.data_ptr(), xy.data_ptr(), angle.data_ptr(),

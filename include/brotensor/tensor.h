@@ -1,19 +1,21 @@
 #pragma once
 
 // The subset of brotensor::Tensor that brovisionml's DSINE ops touch
-// (src/dsine_ops.cpp:57-89, src/dsine_ops.cu:178): a device tag, a raw data
-// pointer, a (rows, cols) fp32 matrix shape, mat / zeros_on constructors,
-// host accessors and to().  brotensor itself is a separate project; when this
-// library is built into brovisionml, brotensor's own header takes this one's
-// place and nothing else changes.  Storage is reference-counted: copies share
-// it, as brotensor's tensors do.
+// (src/dsine_ops.cpp:57-89, src/dsine_ops.cu:178), with brotensor's own names:
+// the device tag (brotensor's enumerators CPU, CUDA and Metal; a HIP build of
+// brotensor runs its GPU device under the CUDA tag), a raw data pointer, the
+// (rows, cols) fp32 matrix shape, the mat / zeros_on / empty_on constructors,
+// the host accessors and to().  This library's C++ layer uses nothing else, so
+// it compiles unchanged against brotensor's own header
+// (tests/cpp/brotensor_api/ checks that).  Storage is reference-counted:
+// copies share it, as brotensor's tensors do.
 
 #include <cstddef>
 #include <memory>
 
 namespace brotensor {
 
-enum class Device { CPU, HIP };
+enum class Device { CPU, CUDA, Metal };
 
 class Tensor {
 public:
@@ -28,8 +30,8 @@ public:
     static Tensor mat(int rows, int cols);
     // Zero-filled fp32 (rows x cols) matrix on `dev`.
     static Tensor zeros_on(Device dev, int rows, int cols);
-
-    std::size_t numel() const { return static_cast<std::size_t>(rows) * static_cast<std::size_t>(cols); }
+    // Uninitialised fp32 (rows x cols) matrix on `dev`.
+    static Tensor empty_on(Device dev, int rows, int cols);
 
     // Host views; throw std::runtime_error unless device == CPU.
     const float* host_f32() const;

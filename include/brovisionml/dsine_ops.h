@@ -1,17 +1,19 @@
 #pragma once
 
-// DSINE NRN device ops on MI355X (gfx950) -- drop-in for brovisionml's
-// include/brovisionml/dsine_ops.h:17-56: the same namespace, names and
-// signatures, so src/dsine_refine.cpp:242 and :271-272 compile against it
-// unchanged.  Tensors are (1, C*H*W) fp32 NCHW on the HIP device; both ops
-// are asynchronous on the null stream, like the reference's default-stream
-// launches (src/dsine_ops.cu:2-4).
+// DSINE NRN ops -- drop-in for brovisionml's include/brovisionml/dsine_ops.h
+// (:17-56): the same namespace, names and signatures, so
+// src/dsine_refine.cpp:242 and :271-272 compile against it unchanged.
+// Tensors are (1, C*H*W) fp32 NCHW.  Each op dispatches on its inputs' device,
+// as the reference's does (src/dsine_ops.cpp:178-215): CPU tensors run this
+// library's CPU branch (double precision in the reference's operation order;
+// results equal the reference CPU twin's bit for bit); tensors on the GPU
+// (brotensor's CUDA tag, which a HIP build of brotensor uses for its device)
+// run the gfx950 kernels, asynchronously on the null stream like the
+// reference's default-stream launches (src/dsine_ops.cu:2-4).
 //
 // Errors throw std::runtime_error prefixed "dsine ops: " (argument and device
 // checks, src/dsine_ops.cpp:18-22) or "dsine hip: " (a HIP runtime error at
-// launch; the reference's "dsine cuda: ", src/dsine_ops.cu:25-29).  Tensors
-// on the CPU throw: this library is the device path; brovisionml's CPU twin
-// (src/dsine_ops.cpp:55-172) stays where it is.
+// launch; the reference's "dsine cuda: ", src/dsine_ops.cu:25-29).
 
 #include "brotensor/tensor.h"
 
@@ -26,9 +28,9 @@ void ray_relu(brotensor::Tensor& normal, const brotensor::Tensor& ray,
 //   pred_norm (1, 3HW), prob (1, 25HW) sigmoid(prob_head), xy (1, 50HW) raw
 //   [xs(25), ys(25)], angle (1, 25HW) sigmoid(angle_head)*pi, ray (1, 3HW);
 //   fu, cu, fv, cv the grid-scaled intrinsics (src/dsine_refine.cpp:232-237).
-// `out` becomes (1, 3HW) on the device: its buffer is reused when it already
-// has that shape on the device and does not alias an input, else (re)allocated
-// (the reference allocates a zeroed one per call, src/dsine_ops.cu:178).
+// `out` becomes a new (1, 3HW) tensor on the inputs' device, as the
+// reference allocates it (src/dsine_ops.cpp:83, src/dsine_ops.cu:178): a
+// tensor the caller held in `out` before keeps its contents.
 void angmf_propagate(const brotensor::Tensor& pred_norm,
                      const brotensor::Tensor& prob,
                      const brotensor::Tensor& xy,
@@ -38,12 +40,12 @@ void angmf_propagate(const brotensor::Tensor& pred_norm,
                      int H, int W,
                      brotensor::Tensor& out);
 
-// angmf_propagate on the prob and angle heads' raw logits: the kernel applies
+// angmf_propagate on the prob and angle heads' raw logits: the op applies
 // the activations the refiner applies before each propagate
 // (src/dsine_refine.cpp:262-267: sigmoid, and sigmoid * kPi), so the two
 // elementwise passes over them disappear.  No counterpart in the reference;
 // the result matches angmf_propagate given the correctly rounded float
-// activations, to the same tolerance.
+// activations, to the same tolerance (bit for bit on the CPU branch).
 void angmf_propagate_logits(const brotensor::Tensor& pred_norm,
                             const brotensor::Tensor& prob_logits,
                             const brotensor::Tensor& xy,
@@ -60,31 +62,13 @@ void angmf_propagate_logits(const brotensor::Tensor& pred_norm,
 // convex_upsample_normalize runs both in one pass; convex_upsample is the first
 // alone.  x (N, C*H*W) with C <= 4, mask (N, 9*scale^2*H*W) with scale <= 16
 // (channel n*scale^2 + ky*scale + kx, tap n = 3*(dy+1) + (dx+1), replicate
-// padding), both fp32 on the HIP device; `out` becomes (N, C*scale^2*H*W)
-// fp32 on the device, reused under the same rule as angmf_propagate's.
+// padding), both fp32 on the GPU; `out` becomes a new (N, C*scale^2*H*W) fp32
+// tensor on their device.  These replace brotensor's GPU kernels only: CPU
+// tensors throw (brotensor's CPU versions stay brotensor's).
 void convex_upsample_normalize(const brotensor::Tensor& x, const brotensor::Tensor& mask,
                                int N, int C, int H, int W, int scale, float eps,
                                brotensor::Tensor& out);
 void convex_upsample(const brotensor::Tensor& x, const brotensor::Tensor& mask, int N, int C,
                      int H, int W, int scale, brotensor::Tensor& out);
-
-namespace detail {
-
-// The launchers the dispatch above calls; they replace
-// detail::ray_relu_cuda / detail::angmf_propagate_cuda (src/dsine_ops_cuda.h:13-23)
-// with the same parameter lists and forward to the C ABI (include/bvml_dsine.h).
-void ray_relu_gpu(brotensor::Tensor& normal, const brotensor::Tensor& ray,
-                  int H, int W);
-
-void angmf_propagate_gpu(const brotensor::Tensor& pred_norm,
-                         const brotensor::Tensor& prob,
-                         const brotensor::Tensor& xy,
-                         const brotensor::Tensor& angle,
-                         const brotensor::Tensor& ray,
-                         double fu, double cu, double fv, double cv,
-                         int H, int W,
-                         brotensor::Tensor& out);
-
-}  // namespace detail
 
 }  // namespace brovisionml::dsine

@@ -12,6 +12,9 @@
  * stream, as the reference launches on the default stream), and nothing
  * throws.
  *
+ * The *_cpu_f32 entry points are the CPU branch of the same ops and take host
+ * pointers instead.
+ *
  * Layout (H, W: the /8 grid; HW = H*W; K2 = k*k; sample b of B):
  *   pred_norm  b*3*HW      + c*HW      + y*W + x     c in [0,3)
  *   prob       b*K2*HW     + n*HW      + ...         n = ky*k + kx
@@ -131,6 +134,24 @@ int bvml_dsine_build_ray8_f32(float* ray, double fu, double cu, double fv,
 int bvml_dsine_convex_upsample_f32(const float* x, const float* mask, int B, int C, int H,
                                    int W, int scale, int normalize, float eps, float* out,
                                    unsigned flags, void* stream);
+
+/*
+ * The CPU branch of the same two ops, for host pointers: brovisionml's public
+ * dispatch sends CPU tensors to its CPU twin (src/dsine_ops.cpp:178-215 ->
+ * ray_relu_cpu :55-76, angmf_propagate_cpu :78-172); these are this
+ * library's, in double precision in the reference's operation order (the
+ * results equal the reference CPU path's bit for bit), with the device entry
+ * points' arguments, flags (BVML_DSINE_FP64 changes nothing here) and
+ * checks.  nthreads: host threads over the rows (0 = the hardware's; the
+ * result does not depend on it).  They make no HIP call.
+ */
+int bvml_dsine_ray_relu_cpu_f32(float* normal, const float* ray, int B, int H, int W,
+                                long long ray_bstride, int nthreads);
+int bvml_dsine_angmf_propagate_cpu_f32(const float* pred_norm, const float* prob,
+                                       const float* xy, const float* angle, const float* ray,
+                                       double fu, double cu, double fv, double cv, int B, int H,
+                                       int W, int k, long long ray_bstride, float* out,
+                                       unsigned flags, int nthreads);
 
 /*
  * The fast path's cancellation threshold for a propagate call with `flags`:

@@ -1,0 +1,36 @@
+// Stand-ins for the C ABI's device entry points (include/bvml_dsine.h), for
+// the sanitizer build of test_dsine_ops: that build compiles the host code
+// (the C++ layer, the CPU branch, the error state, the oracle) with
+// AddressSanitizer and UBSan and links no GPU code.  Its cpu mode calls none
+// of these; each fails loudly if it ever is.
+
+#include "bvml_dsine.h"
+
+#include <cstdio>
+#include <cstdlib>
+
+namespace {
+[[noreturn]] void no_device(const char* fn) {
+    std::fprintf(stderr, "%s called in a build without device code\n", fn);
+    std::abort();
+}
+}  // namespace
+
+extern "C" {
+
+int bvml_dsine_ray_relu_f32(float*, const float*, int, int, int, long long, void*) {
+    no_device("bvml_dsine_ray_relu_f32");
+}
+
+int bvml_dsine_angmf_propagate_f32(const float*, const float*, const float*, const float*,
+                                   const float*, double, double, double, double, int, int, int,
+                                   int, long long, float*, unsigned, void*) {
+    no_device("bvml_dsine_angmf_propagate_f32");
+}
+
+int bvml_dsine_convex_upsample_f32(const float*, const float*, int, int, int, int, int, int,
+                                   float, float*, unsigned, void*) {
+    no_device("bvml_dsine_convex_upsample_f32");
+}
+
+}  // extern "C"

@@ -3,17 +3,19 @@
 // surface of include/brovisionml/dsine_ops.h), in the style of the
 // reference's tests (tests/test_dsine_refine.cpp:48-53: CHECK + failure count).
 //
-//   test_dsine_ops cpu   error behaviour; makes no GPU call
+//   test_dsine_ops cpu   error behaviour and the CPU branch of the dispatch
+//                        (bit for bit against the oracle); makes no GPU call
 //   test_dsine_ops gpu   the refiner's call pattern (src/dsine_refine.cpp:241-282:
 //                        ray_relu once, then chained angmf_propagate calls, then
 //                        the convex upsample + normalise)
-//                        on a 60x80 grid against the CPU oracle (links
-//                        oracle/_build/liboracle_dsine.so; test-only)
+//                        on a 60x80 grid against the CPU oracle
+// The oracle (oracle/_build/liboracle_dsine.so) is linked as the checker only.
 
 #include "brovisionml/dsine_ops.h"
 
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdio>
 #include <cstring>
@@ -59,11 +61,11 @@ static bool throws_with(F f, const char* prefix, const char* needle) {
     return false;
 }
 
-// A tensor that claims to live on the device without touching the GPU: only
+// A tensor that claims to live on a device without touching the GPU: only
 // the device tag matters for the dispatch checks exercised in cpu mode.
-static Tensor fake_device(int rows, int cols) {
+static Tensor fake_device(int rows, int cols, Device dev = Device::CUDA) {
     Tensor t = Tensor::mat(rows, cols);
-    t.device = Device::HIP;
+    t.device = dev;
     return t;
 }
 
@@ -73,10 +75,6 @@ static void test_errors() {
     Tensor n = Tensor::mat(1, 3 * HW), r = Tensor::mat(1, 3 * HW);
     Tensor pr = Tensor::mat(1, 25 * HW), xy = Tensor::mat(1, 50 * HW), an = Tensor::mat(1, 25 * HW);
     Tensor out;
-    // CPU tensors: this library is the device path.
-    CHECK(throws_with([&] { ops::ray_relu(n, r, H, W); }, "dsine ops: ", "CPU"));
-    CHECK(throws_with([&] { ops::angmf_propagate(n, pr, xy, an, r, 1, 1, 1, 1, H, W, out); },
-                      "dsine ops: ", "CPU"));
     // Device mismatch (src/dsine_ops.cpp:180-181, 200-202).
     Tensor dn = fake_device(1, 3 * HW);
     CHECK(throws_with([&] { ops::ray_relu(dn, r, H, W); }, "dsine ops: ",
@@ -90,6 +88,14 @@ static void test_errors() {
                       "dsine ops: ", "xy holds"));
     CHECK(throws_with([&] { ops::ray_relu(dn, dr, H + 1, W); }, "dsine ops: ", "normal holds"));
     CHECK(throws_with([&] { ops::ray_relu(dn, dr, -1, W); }, "dsine ops: ", "H and W"));
+    // ... and on the CPU as well
+    CHECK(throws_with([&] { ops::ray_relu(n, r, H, W + 1); }, "dsine ops: ", "normal holds"));
+    CHECK(throws_with([&] { ops::angmf_propagate(n, pr, Tensor::mat(1, 49 * HW), an, r, 1, 1, 1, 1,
+                                                 H, W, out); },
+                      "dsine ops: ", "xy holds"));
+    // Metal tensors have no path here
+    Tensor mn = fake_device(1, 3 * HW, Device::Metal), mr = fake_device(1, 3 * HW, Device::Metal);
+    CHECK(throws_with([&] { ops::ray_relu(mn, mr, H, W); }, "dsine ops: ", "does not run"));
     // convex upsample (+ normalise): the same checks
     Tensor mk = Tensor::mat(1, 576 * HW), dmk = fake_device(1, 576 * HW);
     CHECK(throws_with([&] { ops::convex_upsample_normalize(n, mk, 1, 3, H, W, 8, 1e-12f, out); },
@@ -103,6 +109,11 @@ static void test_errors() {
     CHECK(throws_with([&] { ops::convex_upsample(dn, dmk, 1, 3, H, W, 0, out); }, "dsine ops: ",
                       "scale >= 1"));
 }
+
+static Tensor from_vec(const std::vector<float>& v);
+struct Inputs;
+static Inputs make_inputs(int H, int W, unsigned seed);
+static void test_cpu_branch();
 
 // Unit normals, sigmoid probs, raw xy, angles, ray_8 of a 480x640 image
 // (intrins_from_fov + build_ray8, src/dsine_preprocess.cpp:35-46,
@@ -156,10 +167,102 @@ static Inputs make_inputs(int H, int W, unsigned seed) {
     return in;
 }
 
-static Tensor upload(const std::vector<float>& v) {
+static Tensor from_vec(const std::vector<float>& v) {
     Tensor t = Tensor::mat(1, static_cast<int>(v.size()));
     std::memcpy(t.host_f32_mut(), v.data(), v.size() * sizeof(float));
-    return t.to(Device::HIP);
+    return t;
+}
+
+static Tensor upload(const std::vector<float>& v) { return from_vec(v).to(Device::CUDA); }
+
+static bool same_bits(const Tensor& t, const std::vector<float>& want) {
+    if (t.device != Device::CPU || static_cast<std::size_t>(t.rows) * t.cols != want.size())
+        return false;
+    return std::memcmp(t.host_f32(), want.data(), want.size() * sizeof(float)) == 0;
+}
+
+// The CPU branch of the dispatch (src/dsine_ops.cpp:183-185, :203-206):
+// ray_relu in place, then chained angmf_propagate calls and the logits
+// variant, each bit for bit against the oracle, which restates the
+// reference CPU twin in its operation order.
+static void test_cpu_branch() {
+    std::printf("  CPU branch of the dispatch (37x53, bit for bit)\n");
+    const int H = 37, W = 53;
+    Inputs in = make_inputs(H, W, 3);
+    Tensor ray = from_vec(in.ray), prob = from_vec(in.prob), xy = from_vec(in.xy),
+           angle = from_vec(in.angle), pred_norm = from_vec(in.n);
+    ops::ray_relu(pred_norm, ray, H, W);
+    std::vector<float> want_n = in.n;
+    oracle_ray_relu_f32(want_n.data(), in.ray.data(), 1, H, W, 0);
+    CHECK(same_bits(pred_norm, want_n));
+    std::vector<float> want_out(3 * H * W);
+    for (int it = 0; it < 2; ++it) {
+        Tensor held = Tensor::mat(1, 3 * H * W), out = held;
+        ops::angmf_propagate(pred_norm, prob, xy, angle, ray, in.fu, in.cu, in.fv, in.cv, H, W,
+                             out);
+        CHECK(out.device == Device::CPU && out.rows == 1 && out.cols == 3 * H * W);
+        CHECK(out.data != held.data);  // a new tensor, as src/dsine_ops.cpp:83 makes
+        oracle_angmf_propagate_f32(want_n.data(), in.prob.data(), in.xy.data(), in.angle.data(),
+                                   in.ray.data(), in.fu, in.cu, in.fv, in.cv, 1, H, W, 5, 0,
+                                   want_out.data());
+        CHECK(same_bits(out, want_out));
+        pred_norm = out;
+        want_n = want_out;
+    }
+    // `out` the same object as pred_norm: the result is still the propagate
+    // of the caller's pred_norm
+    Tensor self = pred_norm;
+    ops::angmf_propagate(self, prob, xy, angle, ray, in.fu, in.cu, in.fv, in.cv, H, W, self);
+    oracle_angmf_propagate_f32(want_n.data(), in.prob.data(), in.xy.data(), in.angle.data(),
+                               in.ray.data(), in.fu, in.cu, in.fv, in.cv, 1, H, W, 5, 0,
+                               want_out.data());
+    CHECK(same_bits(self, want_out));
+    // logits: the CPU branch applies the correctly rounded float activations
+    std::mt19937 rng(5);
+    std::normal_distribution<double> nd;
+    const float kPi = 3.14159265358979323846f;
+    std::vector<float> lp(in.prob.size()), la(in.angle.size()), sp(lp.size()), ang(la.size());
+    for (std::size_t i = 0; i < lp.size(); ++i) {
+        lp[i] = static_cast<float>(3.0 * nd(rng));
+        la[i] = static_cast<float>(3.0 * nd(rng));
+        sp[i] = static_cast<float>(1.0 / (1.0 + std::exp(-static_cast<double>(lp[i]))));
+        ang[i] = static_cast<float>(1.0 / (1.0 + std::exp(-static_cast<double>(la[i])))) * kPi;
+    }
+    Tensor lout;
+    ops::angmf_propagate_logits(pred_norm, from_vec(lp), xy, from_vec(la), ray, in.fu, in.cu,
+                                in.fv, in.cv, H, W, lout);
+    oracle_angmf_propagate_f32(want_n.data(), sp.data(), in.xy.data(), ang.data(), in.ray.data(),
+                               in.fu, in.cu, in.fv, in.cv, 1, H, W, 5, 0, want_out.data());
+    CHECK(same_bits(lout, want_out));
+    // the oracle's convex upsample on a closed form: equal mask logits give
+    // each tap weight 1/9, so a constant map upsamples to itself and
+    // normalises to its direction
+    {
+        const int uh = 3, uw = 4, us = 2, uhw = uh * uw;
+        std::vector<float> x(3 * uhw), m(9 * us * us * uhw, 0.25f), up(3 * us * us * uhw);
+        for (int p = 0; p < uhw; ++p) {
+            x[p] = 3.0f;
+            x[uhw + p] = 0.0f;
+            x[2 * uhw + p] = 4.0f;
+        }
+        oracle_convex_upsample_f32(x.data(), m.data(), 1, 3, uh, uw, us, 0, 0.0, up.data(), 1);
+        double e = 0.0;
+        const int n = us * us * uhw;
+        for (int p = 0; p < n; ++p)
+            e = std::max({e, std::fabs(up[p] - 3.0), std::fabs(static_cast<double>(up[n + p])),
+                          std::fabs(up[2 * n + p] - 4.0)});
+        CHECK(e <= 1e-6);
+        oracle_convex_upsample_f32(x.data(), m.data(), 1, 3, uh, uw, us, 1, 1e-12, up.data(), 1);
+        e = 0.0;
+        for (int p = 0; p < n; ++p)
+            e = std::max({e, std::fabs(up[p] - 0.6), std::fabs(static_cast<double>(up[n + p])),
+                          std::fabs(up[2 * n + p] - 0.8)});
+        CHECK(e <= 1e-6);
+    }
+    // empty maps: out is an empty CPU tensor
+    Tensor e = Tensor::mat(1, 0), eout;
+    ops::angmf_propagate(e, e, e, e, e, 1, 1, 1, 1, 0, W, eout);
+    CHECK(eout.device == Device::CPU && eout.rows == 1 && eout.cols == 0);
 }
 
 static double max_abs(const Tensor& dev, const std::vector<float>& want) {
@@ -189,7 +292,8 @@ static void test_refiner_call_pattern() {
         Tensor new_pred;
         ops::angmf_propagate(pred_norm, prob, xy, angle, ray, in.fu, in.cu, in.fv, in.cv, H, W,
                              new_pred);
-        CHECK(new_pred.device == Device::HIP && new_pred.rows == 1 && new_pred.cols == 3 * H * W);
+        CHECK(new_pred.device == Device::CUDA && new_pred.rows == 1 &&
+              new_pred.cols == 3 * H * W);
         oracle_angmf_propagate_f32(want_n.data(), in.prob.data(), in.xy.data(), in.angle.data(),
                                    in.ray.data(), in.fu, in.cu, in.fv, in.cv, 1, H, W, 5, 0,
                                    want_out.data());
@@ -200,15 +304,22 @@ static void test_refiner_call_pattern() {
         pred_norm = std::move(new_pred);
         want_n = want_out;
     }
-    // An `out` of the right shape on the device is reused, not reallocated.
-    Tensor out = Tensor::zeros_on(Device::HIP, 1, 3 * H * W);
-    void* before = out.data;
+    // `out` becomes a new tensor on the inputs' device (src/dsine_ops.cu:178):
+    // a tensor the caller held in it keeps its contents.
+    std::vector<float> want_next(3 * H * W);
+    oracle_angmf_propagate_f32(want_n.data(), in.prob.data(), in.xy.data(), in.angle.data(),
+                               in.ray.data(), in.fu, in.cu, in.fv, in.cv, 1, H, W, 5, 0,
+                               want_next.data());
+    Tensor held = Tensor::zeros_on(Device::CUDA, 1, 3 * H * W), out = held;
     ops::angmf_propagate(pred_norm, prob, xy, angle, ray, in.fu, in.cu, in.fv, in.cv, H, W, out);
-    CHECK(out.data == before);
-    // ... but never when it aliases pred_norm (the reference reallocates).
-    Tensor alias = pred_norm;
-    ops::angmf_propagate(pred_norm, prob, xy, angle, ray, in.fu, in.cu, in.fv, in.cv, H, W, alias);
-    CHECK(alias.data != pred_norm.data);
+    CHECK(out.data != held.data && out.device == Device::CUDA);
+    CHECK(max_abs(held, std::vector<float>(3 * H * W, 0.0f)) == 0.0);
+    CHECK(max_abs(out, want_next) <= 1e-5);
+    // `out` the same object as pred_norm still propagates the caller's data.
+    Tensor self = pred_norm;
+    ops::angmf_propagate(self, prob, xy, angle, ray, in.fu, in.cu, in.fv, in.cv, H, W, self);
+    CHECK(self.data != pred_norm.data);
+    CHECK(max_abs(self, want_next) <= 1e-5);
     // the same step on the heads' raw logits: the kernel applies sigmoid and
     // sigmoid * pi (src/dsine_refine.cpp:262-267); the oracle takes the
     // correctly rounded float activations
@@ -227,7 +338,7 @@ static void test_refiner_call_pattern() {
         Tensor dlp = upload(lp), dla = upload(la), lout;
         ops::angmf_propagate_logits(pred_norm, dlp, xy, dla, ray, in.fu, in.cu, in.fv, in.cv, H,
                                     W, lout);
-        CHECK(lout.device == Device::HIP && lout.rows == 1 && lout.cols == 3 * H * W);
+        CHECK(lout.device == Device::CUDA && lout.rows == 1 && lout.cols == 3 * H * W);
         oracle_angmf_propagate_f32(want_n.data(), sp.data(), in.xy.data(), ang.data(),
                                    in.ray.data(), in.fu, in.cu, in.fv, in.cv, 1, H, W, 5, 0,
                                    want_out.data());
@@ -246,7 +357,7 @@ static void test_refiner_call_pattern() {
     }
     Tensor up_mask = upload(mask), up;
     ops::convex_upsample_normalize(pred_norm, up_mask, 1, 3, H, W, 8, 1e-12f, up);
-    CHECK(up.device == Device::HIP && up.rows == 1 && up.cols == 3 * 64 * H * W);
+    CHECK(up.device == Device::CUDA && up.rows == 1 && up.cols == 3 * 64 * H * W);
     oracle_convex_upsample_f32(pn_host.data(), mask.data(), 1, 3, H, W, 8, 1, (double)1e-12f,
                                want_up.data(), 1);
     const double eu = max_abs(up, want_up);
@@ -267,6 +378,7 @@ int main(int argc, char** argv) {
     try {
         if (mode == "cpu") {
             test_errors();
+            test_cpu_branch();
         } else if (mode == "gpu") {
             int n = 0;
             if (hipGetDeviceCount(&n) != hipSuccess || n == 0) {

@@ -148,3 +148,39 @@ def test_recompute_ratio_query():
     assert 0.0 < t < 1e-2 and 0.0 < tl < 1e-2
     assert _lib.angmf_recompute_ratio(_lib.FP64) == 0.0
     assert _lib.angmf_recompute_ratio(_lib.FP64 | _lib.LOGITS) == 0.0
+
+
+def _dynsyms(path, *flags):
+    return subprocess.run(["nm", "-D", "-C", *flags, path], stdout=subprocess.PIPE, text=True,
+                          check=True).stdout.splitlines()
+
+
+def test_c_abi_library_exports_only_the_c_abi():
+    """libbvml_dsine.so adds nothing but bvml_dsine_* to a process: no
+    brovisionml::dsine symbol that could collide with brovisionml's own
+    src/dsine_ops.cpp, no brotensor symbol."""
+    names = [ln.split()[-1] for ln in _dynsyms(LIB, "--defined-only")
+             if ln.split()[1] in "TDBRVWiu"]
+    extra = [n for n in names if not n.startswith("bvml_dsine_")]
+    assert extra == []
+    assert sorted(n for n in names) == sorted(declared_functions())
+
+
+def test_cxx_layer_exports_only_the_dropin():
+    from brovisionml_amd.build import LIB_CXX
+    defined = [ln.split(None, 2)[2] for ln in _dynsyms(LIB_CXX, "--defined-only")
+               if " T " in ln or " W " in ln]
+    assert defined and all(n.startswith("brovisionml::dsine::") for n in defined)
+    for fn in ("ray_relu(", "angmf_propagate(", "angmf_propagate_logits(",
+               "convex_upsample(", "convex_upsample_normalize("):
+        assert any(n.startswith(f"brovisionml::dsine::{fn}") for n in defined), fn
+    # brotensor::Tensor comes from outside: brotensor in a brovisionml build
+    undefined = [ln for ln in _dynsyms(LIB_CXX, "--undefined-only") if "brotensor::" in ln]
+    assert undefined
+
+
+def test_cxx_layer_compiles_against_brotensors_api():
+    """dsine_ops.cpp and the launchers header use only the brotensor::Tensor
+    members and Device enumerators brovisionml's own sources use."""
+    from brovisionml_amd import build
+    build.check_brotensor_api()
