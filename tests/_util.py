@@ -44,3 +44,28 @@ def compare(got: np.ndarray, want: np.ndarray, mask=None):
 def to_dev(a, device):
     import torch
     return torch.from_numpy(np.ascontiguousarray(a)).to(device)
+
+
+# Out-of-bounds guards: outputs live inside a larger buffer whose head and
+# tail hold a canary bit pattern (a NaN no kernel produces); a write past
+# either end of the output changes it.
+GUARD = 4096                    # floats on each side (16 KiB)
+CANARY = 0x7FBADBAD
+
+
+class Guarded:
+    """A contiguous float32 view of n elements inside a canary-filled buffer,
+    `shift` floats past a 16 KiB boundary (shift=1 misaligns it by 4 bytes)."""
+
+    def __init__(self, n: int, device, shift: int = 0, fill=None):
+        import torch
+        self.n, self.lo = n, GUARD + shift
+        self.buf = torch.full((n + 2 * GUARD + shift,), CANARY, dtype=torch.int32, device=device)
+        if fill is not None:
+            self.buf[self.lo:self.lo + n] = torch.as_tensor(
+                np.ascontiguousarray(fill, dtype=np.float32).reshape(-1)).view(torch.int32).to(device)
+        self.out = self.buf.view(torch.float32)[self.lo:self.lo + n]
+
+    def intact(self) -> bool:
+        b = self.buf.cpu().numpy()
+        return bool((b[:self.lo] == CANARY).all() and (b[self.lo + self.n:] == CANARY).all())

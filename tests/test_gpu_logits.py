@@ -13,7 +13,7 @@ import pytest
 
 import oracle
 from brovisionml_amd import dsine, workloads as wl
-from tests._util import TOL_ABS, TOL_DEG, compare, to_dev
+from tests._util import TOL_ABS, TOL_DEG, Guarded, compare, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -42,10 +42,13 @@ def run(inp, lp, la, H, W, k, device, precise=False):
     import torch
     t = {key: to_dev(inp[key], device) for key in ("pred_norm", "xy", "ray")}
     fu, cu, fv, cv = inp["intrinsics"]
+    g = Guarded(t["pred_norm"].numel(), device)
     out = dsine.angmf_propagate(t["pred_norm"], to_dev(lp, device), t["xy"], to_dev(la, device),
-                                t["ray"], fu, cu, fv, cv, H, W, precise=precise, logits=True)
+                                t["ray"], fu, cu, fv, cv, H, W, g.out, precise=precise,
+                                logits=True)
     torch.cuda.synchronize()
-    got = out.cpu().numpy()
+    assert g.intact(), "angmf_propagate (logits) wrote outside its output"
+    got = out.cpu().numpy().reshape(t["pred_norm"].shape)
     sp, ang = activate(lp, la)
     want = oracle.angmf_propagate(inp["pred_norm"], sp, inp["xy"], ang, inp["ray"],
                                   inp["intrinsics"], H, W, k, nthreads=16)

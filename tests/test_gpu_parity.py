@@ -16,7 +16,7 @@ import pytest
 
 import oracle
 from brovisionml_amd import dsine, workloads as wl
-from tests._util import TOL_ABS, TOL_DEG, compare, to_dev
+from tests._util import TOL_ABS, TOL_DEG, Guarded, compare, to_dev
 
 pytestmark = pytest.mark.gpu
 
@@ -33,10 +33,13 @@ def run_gpu(inp, H, W, device, precise=False, ray=None):
     t = {k: to_dev(inp[k], device) for k in ("pred_norm", "prob", "xy", "angle")}
     r = to_dev(inp["ray"] if ray is None else ray, device)
     fu, cu, fv, cv = inp["intrinsics"]
+    g = Guarded(t["pred_norm"].numel(), device)
     out = dsine.angmf_propagate(t["pred_norm"], t["prob"], t["xy"], t["angle"], r,
-                                fu, cu, fv, cv, H, W, precise=precise)
+                                fu, cu, fv, cv, H, W, g.out, precise=precise)
     torch.cuda.synchronize()
-    return out.cpu().numpy()
+    assert out.data_ptr() == g.out.data_ptr()
+    assert g.intact(), "angmf_propagate wrote outside its output"
+    return out.cpu().numpy().reshape(t["pred_norm"].shape)
 
 
 def run_oracle(inp, H, W, k, ray=None):
@@ -328,10 +331,11 @@ def test_ray_relu(cuda, B, H, W):
     # nearly antiparallel to the ray, the ill-conditioned end of the clamp
     m = min(HW, 50)
     n[0, :, :m] = -ray[:, :m] + 1e-4 * rng.standard_normal((3, m)).astype(np.float32)
-    t = to_dev(n, cuda)
-    dsine.ray_relu(t, to_dev(ray, cuda), H, W)
+    g = Guarded(n.size, cuda, fill=n)
+    dsine.ray_relu(g.out, to_dev(ray, cuda), H, W)
     torch.cuda.synchronize()
-    got = t.cpu().numpy()
+    assert g.intact(), "ray_relu wrote outside its tensor"
+    got = g.out.cpu().numpy().reshape(n.shape)
     want = oracle.ray_relu(n, ray, H, W)
     max_abs, max_deg, nan_mm = compare(got, want)
     say(f"    max-abs {max_abs:.3e}")

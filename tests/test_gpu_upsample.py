@@ -17,7 +17,7 @@ import pytest
 
 import oracle
 from brovisionml_amd import dsine
-from tests._util import TOL_ABS, TOL_DEG, compare, to_dev
+from tests._util import Guarded, TOL_ABS, TOL_DEG, compare, to_dev
 from tests.test_gpu_parity import NTHREADS, say
 
 pytestmark = pytest.mark.gpu
@@ -39,17 +39,14 @@ def run_gpu(x, mask, s, device, normalize=True, precise=False, eps=EPS, misalign
     B, C, H, W = x.shape
     xt, mt = to_dev(x, device), to_dev(mask, device)
     n = B * C * s * s * H * W
-    if misalign:
-        # a contiguous out whose address is 4 bytes past 16-byte alignment
-        buf = torch.full((n + 1,), float("nan"), dtype=torch.float32, device=device)
-        out = buf[1:]
-    else:
-        out = None
+    # guarded out; misalign: its address 4 bytes past 16-byte alignment
+    g = Guarded(n, device, shift=1 if misalign else 0)
     if normalize:
-        r = dsine.convex_upsample_normalize(xt, mt, B, C, H, W, s, eps, out, precise=precise)
+        r = dsine.convex_upsample_normalize(xt, mt, B, C, H, W, s, eps, g.out, precise=precise)
     else:
-        r = dsine.convex_upsample(xt, mt, B, C, H, W, s, out, precise=precise)
+        r = dsine.convex_upsample(xt, mt, B, C, H, W, s, g.out, precise=precise)
     torch.cuda.synchronize()
+    assert g.intact(), "convex upsample wrote outside its output"
     return r.cpu().numpy().reshape(B, C, s * H, s * W)
 
 
