@@ -33,6 +33,7 @@ EXPORTS = (
     "bvml_dsine_build_ray8_f32",
     "bvml_dsine_convex_upsample_f32",
     "bvml_dsine_angmf_recompute_ratio",
+    "bvml_dsine_angmf_plan",
     "bvml_dsine_ray_relu_cpu_f32",
     "bvml_dsine_angmf_propagate_cpu_f32",
     "bvml_dsine_last_error",
@@ -63,6 +64,9 @@ def load(path: str = LIB) -> ctypes.CDLL:
     lib.bvml_dsine_convex_upsample_f32.argtypes = [vp, vp, i, i, i, i, i, i, ctypes.c_float, vp,
                                                    u, vp]
     lib.bvml_dsine_convex_upsample_f32.restype = i
+    ip = ctypes.POINTER(ctypes.c_int)
+    lib.bvml_dsine_angmf_plan.argtypes = [i, i, i, i, d, d, d, d, u, ip, ip, ip]
+    lib.bvml_dsine_angmf_plan.restype = i
     lib.bvml_dsine_angmf_recompute_ratio.argtypes = [u]
     lib.bvml_dsine_angmf_recompute_ratio.restype = d
     lib.bvml_dsine_ray_relu_cpu_f32.argtypes = [vp, vp, i, i, i, ll, i]
@@ -132,3 +136,16 @@ def angmf_propagate_cpu_f32(pred_norm: int, prob: int, xy: int, angle: int, ray:
     return load().bvml_dsine_angmf_propagate_cpu_f32(
         pred_norm, prob, xy, angle, ray, fu, cu, fv, cv, B, H, W, k, ray_bstride, out, flags,
         nthreads)
+
+
+def angmf_plan(B: int, H: int, W: int, k: int, fu: float, cu: float, fv: float, cv: float,
+               flags: int = DEFAULT):
+    """(fp32 kernel?, waves per 64-pixel group, tile width, tile height) of the
+    launch bvml_dsine_angmf_propagate_f32 makes for these arguments; raises
+    on a rejected argument."""
+    g, tw, th = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    st = load().bvml_dsine_angmf_plan(B, H, W, k, fu, cu, fv, cv, flags, ctypes.byref(g),
+                                      ctypes.byref(tw), ctypes.byref(th))
+    if st < 0:
+        raise RuntimeError(f"angmf_plan: {last_error()} (status {st})")
+    return bool(st), g.value, tw.value, th.value

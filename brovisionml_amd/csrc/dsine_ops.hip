@@ -280,8 +280,12 @@ __device__ __forceinline__ int magic_div(int n, unsigned mag, int L) {
     return (int)((__umulhi((unsigned)n, mag) + (unsigned)n) >> L);
 }
 
+// Store of one output float, non-temporal: the stores of a large launch then
+// take less of the HBM bandwidth the input stream is using (measured: 3 us of
+// 155 on 4 x 512 x 512 at k = 7, 0.2 us of 8.8 at 256 x 256, k = 5).
 __device__ __forceinline__ void stf(float* base, uint32_t byte_off, float v) {
-    *reinterpret_cast<float*>(reinterpret_cast<char*>(base) + byte_off) = v;
+    __builtin_nontemporal_store(v, reinterpret_cast<float*>(reinterpret_cast<char*>(base) +
+                                                            byte_off));
 }
 
 __device__ __forceinline__ unsigned long long uniform64(unsigned long long v) {
@@ -452,19 +456,25 @@ __device__ __forceinline__ void stage_halo(float mx, float my, float mz, int sx,
 // (row-major over the window), one run per wave.  Workgroups hold kWgWaves = 8
 // waves (8/G groups): the SPI places a workgroup of n waves only where every
 // SIMD has ceil(n/4) free slots and spreads 8 waves exactly 2 per SIMD, so
-// every SIMD carries the same work.  A wave keeps at most kLookahead
+// every SIMD carries the same work.  A wave keeps at most lookahead(K, G)
 // neighbours' planes in flight, issuing the next neighbour's loads as it
 // finishes one.
 constexpr int kWgWaves = 8;
 // Measured best: 3 at k <= 5 (a 256 x 256 call in one round of waves wants
-// each wave's first neighbours' data first), 7 at k >= 7 (many rounds).
-__host__ __device__ constexpr int lookahead(int K) { return K <= 5 ? 3 : 7; }
+// each wave's first neighbours' data first), 7 at k >= 7 (many rounds); 5
+// with G = 1 (large launches, every wave runs the whole window; 2 to 6
+// measured on 4 x 512 x 512 at k = 7).
+__host__ __device__ constexpr int lookahead(int K, int G) {
+    return G == 1 ? 5 : (K <= 5 ? 3 : 7);
+}
 
 // Neighbours whose planes a wave loads before the halo staging and its
 // barrier; the rest are loaded after it.
 // Measured best: 1 at k <= 5; at k >= 7 all of the lookahead (7), which
-// overlaps the halo's staging with the first neighbours' loads.
-__host__ __device__ constexpr int preloads(int K) { return K <= 5 ? 1 : 7; }
+// overlaps the halo's staging with the first neighbours' loads; 3 with G = 1.
+__host__ __device__ constexpr int preloads(int K, int G) {
+    return G == 1 ? 3 : (K <= 5 ? 1 : 7);
+}
 
 // Source-normal halo records of a TW x TH tile.
 __host__ __device__ inline int halo_count(int K, int TW, int TH) {
@@ -475,11 +485,12 @@ __host__ __device__ inline int halo_count(int K, int TW, int TH) {
 __host__ __device__ inline int halo_slots(int K, int TW, int TH) { return halo_count(K, TW, TH) + 1; }
 
 // LDS of the fp32 kernel, in 16-byte units:
-//   part[G][64*M]      per-wave fp32 partial (acc.xyz, sum wi^2 or NaN)
+//   part[G][64*M]      per-wave fp32 partial (acc.xyz, sum wi^2 or NaN); none
+//                      when G = 1
 //   halo[nhalo + 1]    source-pixel records (HaloRec, 5 units) + a spare
 //   rayl[64*M]         each tile pixel's ray, when formed from the intrinsics
 __host__ __device__ inline int lds_units(int K, int G, int M, int TW, int TH, bool synth_ray) {
-    return G * 64 * M + 5 * halo_slots(K, TW, TH) + (synth_ray ? 64 * M : 0);
+    return (G > 1 ? G * 64 * M : 0) + 5 * halo_slots(K, TW, TH) + (synth_ray ? 64 * M : 0);
 }
 
 // TW (< 2^11), TH (< 2^11) and M (< 2^5) of the fp32 kernel's tile and the
@@ -545,7 +556,10 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     constexpr int P = K / 2, K2 = K * K;
     constexpr int RUN = K2 / G, REM = K2 % G;  // run lengths RUN + 1 (REM runs) and RUN
     constexpr int NR = RUN + (REM ? 1 : 0);    // longest run
-    constexpr int LA = lookahead(K) < NR ? lookahead(K) : NR;  // neighbours in flight
+    constexpr int LA = lookahead(K, G) < NR ? lookahead(K, G) : NR;  // neighbours in flight
+    // planes held in registers: one slot per neighbour of the run (G > 1,
+    // loop fully unrolled), or a ring of LA slots (G = 1, rolled loop)
+    constexpr int SL = (G == 1) ? LA : NR;
     extern __shared__ float4 smem[];
     const int TW = (int)(tile & 0x7ffu), TH = (int)((tile >> 11) & 0x7ffu);
     const int M = (int)((tile >> 22) & 0x1fu), LX = (int)(tile >> 27);
@@ -554,7 +568,7 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     float4* part = smem;
     const int hw = TW + 2 * P, nhalo = hw * nrow;
     const int nslot = nhalo + 1;
-    HaloRec* hl = reinterpret_cast<HaloRec*>(part + G * npx);
+    HaloRec* hl = reinterpret_cast<HaloRec*>(part + (G > 1 ? G * npx : 0));
     // (SR) the tile pixels' rays, after the halo
     float4* rayl = reinterpret_cast<float4*>(hl + nslot);
 
@@ -620,10 +634,11 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
         ryf = ldbs(rry, pb, HW4);
         rzf = ldbs(rry, pb, 2u * HW4);
     }
-    float xs[NR], ys[NR], th[NR], wt[NR];
+    float xs[SL], ys[SL], th[SL], wt[SL];
     // planes (sample b, neighbour n0 + i) of each input: one descriptor per
-    // tensor at i = 0, plane i at scalar offset i * HW4.  A run one shorter
-    // than NR re-reads its first planes in the last slot, unused.
+    // tensor at i = 0, plane i at scalar offset i * HW4, into register slot s.
+    // A run one shorter than NR re-reads its first planes in the last slot,
+    // unused.
     const uint32_t pxy = (uint32_t)b * (2u * K2) + (uint32_t)n0;
     const uint32_t pk = (uint32_t)b * K2 + (uint32_t)n0;
     const uint32_t span = (uint32_t)nrun * HW4;
@@ -631,17 +646,17 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     const __amdgpu_buffer_rsrc_t rys = plane_rsrc(at_plane(xy, pxy + K2, HW4), span);
     const __amdgpu_buffer_rsrc_t rth = plane_rsrc(at_plane(angle, pk, HW4), span);
     const __amdgpu_buffer_rsrc_t rwt = plane_rsrc(at_plane(prob, pk, HW4), span);
-    auto load_planes = [&](int i) {
+    auto load_planes = [&](int i, int sl) {
         const uint32_t so = (i < NR - 1 || nrun == NR) ? (uint32_t)i * HW4 : 0u;
-        xs[i] = ldbs(rxs, pb, so);
-        ys[i] = ldbs(rys, pb, so);
-        th[i] = ldbs(rth, pb, so);
-        wt[i] = ldbs(rwt, pb, so);
+        xs[sl] = ldbs(rxs, pb, so);
+        ys[sl] = ldbs(rys, pb, so);
+        th[sl] = ldbs(rth, pb, so);
+        wt[sl] = ldbs(rwt, pb, so);
     };
-    constexpr int PRE = preloads(K) < LA ? preloads(K) : LA;
+    constexpr int PRE = preloads(K, G) < LA ? preloads(K, G) : LA;
 #pragma unroll
     for (int i = 0; i < PRE; ++i) {
-        load_planes(i);
+        load_planes(i, i);
         __builtin_amdgcn_sched_barrier(0);
     }
     // Threads past the halo write a spare record: an unconditional use keeps
@@ -678,9 +693,10 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     }
 #pragma unroll
     for (int i = PRE; i < LA; ++i) {
-        load_planes(i);
+        load_planes(i, i);
         __builtin_amdgcn_sched_barrier(0);
     }
+    float4 mine;  // this wave's partial of its pixel
     {
         // cos(v', r) = v'.r / max(|v'||r|, 1e-8) with |v'| = 1.  1/|r| from the
         // hardware rsq and one Newton step: r-hat is shared by all the
@@ -708,17 +724,12 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
         // flags.
         uint32_t smx = 0u;
         float tmax = 0.0f, ddmin = __builtin_inff(), n2min = __builtin_inff();
-#pragma unroll
-        for (int i = 0; i < NR; ++i) {
-            // this neighbour's planes: the fence makes the wait for them the
-            // first use (and keeps the last slot's loads out of its branch)
-            asm volatile("" : "+v"(xs[i]), "+v"(ys[i]), "+v"(th[i]), "+v"(wt[i]));
-            if (i == NR - 1 && nrun != NR) break;
-            const int n = n0 + i;
+        // one neighbour n of the window, its planes' values given: the
+        // record offsets come from n in scalar registers, added once each
+        // (the compiler would otherwise fold them into a 64-bit
+        // multiply-add per neighbour)
+        auto eval = [&](int n, float xv, float yv, float thv, float wtv) {
             const int ky = n / K, kx = n - ky * K;
-            // the record offsets in scalar registers, added once each (the
-            // compiler would otherwise fold them into a 64-bit multiply-add
-            // per neighbour)
             int roff = (ky * hw + kx) * (int)sizeof(HaloRec);
             asm("" : "+s"(roff));
             const lds_byte* rb = hbase + roff;
@@ -726,8 +737,7 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
             const lds_d2 ab2 = *(const __attribute__((address_space(3))) lds_d2*)(rb + 16);
             const lds_f4 e4 = *(const __attribute__((address_space(3))) lds_f4*)(rb + 32);
             const lds_f4 f4 = *(const __attribute__((address_space(3))) lds_f4*)(rb + 48);
-            const float xv = xs[i], yv = ys[i];
-            const float t = LG ? sigmoid_f32(th[i]) * kPiF : th[i];
+            const float t = LG ? sigmoid_f32(thv) * kPiF : thv;
             // q in double (exact products, one rounding), the rest fp32;
             // dd = g + q/|xy| is formed from the raw normal as the reference
             // forms it, with 1/|xy| from the fp32 |xy|^2 and rsq (dd_min
@@ -760,10 +770,10 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
             const float p2 = fmaf(px, px, fmaf(py, py, pz * pz));
             float wi;
             if constexpr (LG) {
-                const float d = one_plus_exp_neg(wt[i]);
+                const float d = one_plus_exp_neg(wtv);
                 wi = __builtin_amdgcn_rsqf(p2 * d * d);
             } else {
-                wi = wt[i] * __builtin_amdgcn_rsqf(p2);
+                wi = wtv * __builtin_amdgcn_rsqf(p2);
             }
             acc0 = fmaf(px, wi, acc0);
             acc1 = fmaf(py, wi, acc1);
@@ -771,16 +781,46 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
             qs = fmaf(wi, wi, qs);
             // this neighbour done before the next one's data are waited for
             asm volatile("" : "+v"(acc0), "+v"(acc1), "+v"(acc2), "+v"(qs));
-            if (i + LA < NR) {
-                load_planes(i + LA);
-                __builtin_amdgcn_sched_barrier(0);
+        };
+        if constexpr (G > 1) {
+            // this wave's run, fully unrolled: slot i holds neighbour n0 + i
+#pragma unroll
+            for (int i = 0; i < NR; ++i) {
+                // this neighbour's planes: the fence makes the wait for them
+                // the first use (and keeps the last slot's loads out of its
+                // branch)
+                asm volatile("" : "+v"(xs[i]), "+v"(ys[i]), "+v"(th[i]), "+v"(wt[i]));
+                if (i == NR - 1 && nrun != NR) break;
+                eval(n0 + i, xs[i], ys[i], th[i], wt[i]);
+                if (i + LA < NR) {
+                    load_planes(i + LA, i + LA);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+            }
+        } else {
+            // the whole window, LA neighbours at a time: neighbour n lives in
+            // slot n % LA, and its slot is refilled with neighbour n + LA
+            // once it has been evaluated
+            for (int nb = 0; nb < K2; nb += LA) {
+#pragma unroll
+                for (int sl = 0; sl < LA; ++sl) {
+                    const int n = nb + sl;
+                    if (n >= K2) break;
+                    asm volatile("" : "+v"(xs[sl]), "+v"(ys[sl]), "+v"(th[sl]), "+v"(wt[sl]));
+                    eval(n, xs[sl], ys[sl], th[sl], wt[sl]);
+                    if (n + LA < K2) {
+                        load_planes(n + LA, sl);
+                        __builtin_amdgcn_sched_barrier(0);
+                    }
+                }
             }
         }
         const bool bad = (smx > kXY2Span) | !(tmax <= 3.2f) | !(ddmin >= dd_min) |
                          !(n2min >= kMinV2);
-        part[r * npx + j] = make_float4(acc0, acc1, acc2, bad ? __builtin_nanf("") : qs);
+        mine = make_float4(acc0, acc1, acc2, bad ? __builtin_nanf("") : qs);
+        if constexpr (G > 1) part[r * npx + j] = mine;
     }
-    __syncthreads();
+    if constexpr (G > 1) __syncthreads();
 
     // ---- phase B: wave r = 0 of each group reduces the G runs, writes the
     // unflagged pixels and recomputes the flagged ones by itself; the other
@@ -791,7 +831,7 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
         double s0 = 0.0, s1 = 0.0, s2 = 0.0, sw = 0.0;
 #pragma unroll
         for (int rr = 0; rr < G; ++rr) {
-            const float4 t = part[rr * npx + j];
+            const float4 t = (G > 1) ? part[rr * npx + j] : mine;
             s0 += t.x;
             s1 += t.y;
             s2 += t.z;
@@ -999,6 +1039,17 @@ auto angmf_f32_for(bool synth_ray, bool logits) {
 constexpr int kGChoices[10][2] = {{0, 0}, {1, 1}, {0, 0}, {2, 2}, {0, 0},
                                   {4, 2}, {0, 0}, {4, 8}, {0, 0}, {4, 8}};
 
+// Window sizes with a whole-window variant (G = 1: each wave evaluates all
+// k*k neighbours of its 64 pixels in a rolled loop, LA at a time, and writes
+// them itself; 64 x 8 tiles, no cross-wave reduction).  A launch of at least
+// kLargeGrid such workgroups takes it: on large images its HBM stream runs
+// faster (fewer halo records per pixel, one barrier per workgroup, fewer
+// loads in flight per lane).  k = 9's 64 x 8 halo exceeds two records per
+// thread.
+constexpr bool kWholeWindowOk[10] = {false, false, false, false, false,
+                                     true,  false, true,  false, false};
+constexpr long long kLargeGrid = 1024;
+
 template <int K>
 hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
     if (fp64) {
@@ -1013,8 +1064,18 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
     div_magic(a.tiles_x, mag, L);
     const unsigned tile = pack_tile(a.TW, a.TH, a.M, L);
     constexpr int G0 = kGChoices[K][0], G1 = kGChoices[K][1];
-    const auto kern = (a.G == G0) ? angmf_f32_for<K, G0>(a.synth_ray != 0, a.logits != 0)
-                                  : angmf_f32_for<K, G1>(a.synth_ray != 0, a.logits != 0);
+    auto kern = (a.G == G0) ? angmf_f32_for<K, G0>(a.synth_ray != 0, a.logits != 0)
+                            : angmf_f32_for<K, G1>(a.synth_ray != 0, a.logits != 0);
+    if constexpr (kWholeWindowOk[K]) {
+        if (a.G == 1) kern = angmf_f32_for<K, 1>(a.synth_ray != 0, a.logits != 0);
+    }
+    // workgroups past 64 KB of LDS (the whole-window tiles) ask for it
+    if (lds > 65536) {
+        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
+                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                 (int)lds);
+        if (e != hipSuccess) return e;
+    }
     // one launch per kMaxGridY samples (grid y = sample)
     for (int b0 = 0; b0 < a.B; b0 += kMaxGridY) {
         const int nb = (a.B - b0 < kMaxGridY) ? a.B - b0 : kMaxGridY;
@@ -1035,13 +1096,17 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
     return hipSuccess;
 }
 
-// LDS one workgroup may use.
+// LDS one workgroup may use: 64 KB for the run-split kernels (G > 1), so
+// that two to three of them share a CU; the whole-window kernel's 64 x 8
+// tiles take up to 80 KB, two per CU (gfx950 has 160 KB per CU and allows it
+// all to one workgroup).
 constexpr int kMaxLdsBytes = 65536;
+constexpr int kMaxLdsBytesG1 = 81920;
 
 // Whether a TW x TH tile of M groups of G waves fits the kernel: its LDS, and
 // at most two halo records per thread.
 bool tile_fits(int K, int G, int M, int TW, int TH, bool synth_ray) {
-    return lds_units(K, G, M, TW, TH, synth_ray) * 16 <= kMaxLdsBytes &&
+    return lds_units(K, G, M, TW, TH, synth_ray) * 16 <= (G == 1 ? kMaxLdsBytesG1 : kMaxLdsBytes) &&
            halo_count(K, TW, TH) <= 2 * 64 * M * G;
 }
 
@@ -1078,11 +1143,23 @@ double tile_for(AngmfArgs& a, int K, int G) {
 // Workgroups below which a launch is latency-bound: two per CU.
 constexpr long long kSmallGrid = 512;
 
-// G and the tile.  A launch of fewer than kSmallGrid workgroups takes the
-// candidate with more of them (its runs are shorter, so its waves finish
-// sooner); a larger one the candidate with the most lanes holding a pixel,
-// the preferred G on ties.
+// G and the tile.  A launch that fills at least kLargeGrid whole-window
+// workgroups, with at least 90% of their lanes holding a pixel, takes G = 1.
+// Otherwise, of the two run-split candidates, a launch of fewer than
+// kSmallGrid workgroups takes the one with more of them (its runs are
+// shorter, so its waves finish sooner); a larger one the one with the most
+// lanes holding a pixel, the preferred G on ties.
 void choose_tile(AngmfArgs& a, int K) {
+    auto wgs = [](const AngmfArgs& c) {
+        return (long long)((c.W + c.TW - 1) / c.TW) * ((c.H + c.TH - 1) / c.TH) * c.B;
+    };
+    if (kWholeWindowOk[K] && (long long)K * K * a.HW * 4 < (1LL << 32)) {
+        AngmfArgs one = a;
+        if (tile_for(one, K, 1) >= 0.9 && wgs(one) >= kLargeGrid) {
+            a = one;
+            return;
+        }
+    }
     AngmfArgs alt = a;
     const double u0 = tile_for(a, K, kGChoices[K][0]);
     if (kGChoices[K][1] == kGChoices[K][0]) return;
@@ -1092,15 +1169,65 @@ void choose_tile(AngmfArgs& a, int K) {
         a = alt;
         return;
     }
-    auto wgs = [](const AngmfArgs& c) {
-        return (long long)((c.W + c.TW - 1) / c.TW) * ((c.H + c.TH - 1) / c.TH) * c.B;
-    };
     const long long w0 = wgs(a), w1 = wgs(alt);
     if (w0 < kSmallGrid || w1 < kSmallGrid) {
         if (w1 > w0) a = alt;
         return;
     }
     if (u1 > u0 + 1e-9) a = alt;
+}
+
+// The launch plan of one call: the kernel arguments that depend on the
+// shapes, intrinsics and flags (a.G, the tile, dd_min, ...), and whether it
+// runs the double-precision kernel (fp64).
+int plan_angmf(AngmfArgs& a, int B, int H, int W, int k, double fu, double cu, double fv,
+               double cv, unsigned flags, bool& fp64) {
+    const long long HW = (long long)H * W;
+    const bool synth = (flags & BVML_DSINE_RAY_FROM_INTRINSICS) != 0;
+    a.fu = fu; a.cu = cu; a.fv = fv; a.cv = cv;
+    a.HW = HW; a.B = B; a.H = H; a.W = W;
+    a.ifu64 = 1.0 / fu;
+    a.ifv64 = 1.0 / fv;
+    a.tu_c = (0.5 - cu) / fu;
+    a.tv_c = (0.5 - cv) / fv;
+    // gmax: the largest |P0| over the image's pixel centres (at a corner),
+    // times the largest |m| the fast path accepts
+    double gmax = 0.0;
+    for (const int cy : {0, H - 1})
+        for (const int cx : {0, W - 1}) {
+            const double tu = (cx + 0.5 - cu) / fu, tv = (cy + 0.5 - cv) / fv;
+            gmax = std::fmax(gmax, std::sqrt(1.0 + tu * tu + tv * tv));
+        }
+    gmax *= std::sqrt(1.0 + (double)kUnitM2);
+    a.dd_min = kDdClamp + 1e-7 * gmax + 3e-7 / std::fmin(std::fabs(fu), std::fabs(fv));
+    a.synth_ray = synth ? 1 : 0;
+    a.logits = (flags & BVML_DSINE_LOGITS) ? 1 : 0;
+    a.acc_ratio2 = a.logits ? kAccRatio2Logits : kAccRatio2;
+    choose_tile(a, k);
+    if (!tile_fits(k, a.G, a.M, a.TW, a.TH, synth))
+        return fail(BVML_DSINE_ESIZE, "angmf_propagate: no tile fits the kernel's LDS");
+    a.tiles_x = (W + a.TW - 1) / a.TW;
+    const long long tiles_y = (H + a.TH - 1) / a.TH;
+    const long long tpi = (long long)a.tiles_x * tiles_y;
+    a.tiles_per_img = (int)(tpi < INT_MAX ? tpi : INT_MAX);
+
+    // The fp32 path assumes intrinsics in the range real cameras produce;
+    // anything else runs the double-precision kernel (same results as the
+    // reference, which accepts any value).
+    const bool sane = std::isfinite(fu) && std::isfinite(fv) && std::isfinite(cu) &&
+                      std::isfinite(cv) && std::fabs(fu) >= 1e-3 && std::fabs(fu) <= 1e7 &&
+                      std::fabs(fv) >= 1e-3 && std::fabs(fv) <= 1e7 &&
+                      std::fabs(cu) <= 1e7 && std::fabs(cv) <= 1e7 && gmax <= kMaxP0;
+    // The fp32 kernel addresses a wave's run of neighbour planes (and the 3
+    // planes of pred_norm and ray) from one 32-bit buffer offset, and its grid
+    // holds one image's tiles in x; larger images also run the
+    // double-precision kernel.
+    const long long gw = a.G, nrun = (k * k + gw - 1) / gw;
+    const long long nplanes = nrun > 3 ? nrun : 3;
+    const bool fits32 = nplanes * HW * 4 < (1LL << 32) && tpi < (1LL << 31) &&
+                        tpi * 64 * a.M * gw < (1LL << 32);
+    fp64 = (flags & BVML_DSINE_FP64) || !sane || !fits32;
+    return BVML_DSINE_OK;
 }
 
 }  // namespace
@@ -1156,6 +1283,27 @@ int bvml_dsine_ray_relu_f32(float* normal, const float* ray, int B, int H, int W
     return BVML_DSINE_OK;
 }
 
+int bvml_dsine_angmf_plan(int B, int H, int W, int k, double fu, double cu, double fv, double cv,
+                          unsigned flags, int* waves_per_group, int* tile_w, int* tile_h) {
+    if (flags & ~(BVML_DSINE_FP64 | BVML_DSINE_RAY_FROM_INTRINSICS | BVML_DSINE_LOGITS))
+        return fail(BVML_DSINE_EFLAGS, "angmf_plan: unknown flag bits");
+    if (B < 1 || H < 1 || W < 1)
+        return fail(BVML_DSINE_ESHAPE, "angmf_plan: B, H and W must be >= 1");
+    if (!(k == 1 || k == 3 || k == 5 || k == 7 || k == 9))
+        return fail(BVML_DSINE_EK, "angmf_plan: k must be one of 1, 3, 5, 7, 9");
+    const long long HW = (long long)H * W;
+    if ((long long)B * HW > (long long)INT_MAX * 64 || HW >= (1LL << 30))
+        return fail(BVML_DSINE_ESIZE, "angmf_plan: B*H*W too large for one launch");
+    AngmfArgs a{};
+    bool fp64 = false;
+    const int st = plan_angmf(a, B, H, W, k, fu, cu, fv, cv, flags, fp64);
+    if (st != BVML_DSINE_OK) return st;
+    if (waves_per_group) *waves_per_group = a.G;
+    if (tile_w) *tile_w = a.TW;
+    if (tile_h) *tile_h = a.TH;
+    return fp64 ? 0 : 1;
+}
+
 int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
                                    const float* xy, const float* angle,
                                    const float* ray, double fu, double cu,
@@ -1197,50 +1345,10 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
 
     AngmfArgs a{};
     a.pn = pred_norm; a.pr = prob; a.xy = xy; a.ang = angle; a.ray = ray; a.out = out;
-    a.fu = fu; a.cu = cu; a.fv = fv; a.cv = cv;
     a.ray_bstride = ray_bstride;
-    a.HW = HW; a.B = B; a.H = H; a.W = W;
-    a.ifu64 = 1.0 / fu;
-    a.ifv64 = 1.0 / fv;
-    a.tu_c = (0.5 - cu) / fu;
-    a.tv_c = (0.5 - cv) / fv;
-    // gmax: the largest |P0| over the image's pixel centres (at a corner),
-    // times the largest |m| the fast path accepts
-    double gmax = 0.0;
-    for (const int cy : {0, H - 1})
-        for (const int cx : {0, W - 1}) {
-            const double tu = (cx + 0.5 - cu) / fu, tv = (cy + 0.5 - cv) / fv;
-            gmax = std::fmax(gmax, std::sqrt(1.0 + tu * tu + tv * tv));
-        }
-    gmax *= std::sqrt(1.0 + (double)kUnitM2);
-    a.dd_min = kDdClamp + 1e-7 * gmax + 3e-7 / std::fmin(std::fabs(fu), std::fabs(fv));
-    a.synth_ray = synth ? 1 : 0;
-    a.logits = (flags & BVML_DSINE_LOGITS) ? 1 : 0;
-    a.acc_ratio2 = a.logits ? kAccRatio2Logits : kAccRatio2;
-    choose_tile(a, k);
-    if (!tile_fits(k, a.G, a.M, a.TW, a.TH, synth))
-        return fail(BVML_DSINE_ESIZE, "angmf_propagate: no tile fits the kernel's LDS");
-    a.tiles_x = (W + a.TW - 1) / a.TW;
-    const long long tiles_y = (H + a.TH - 1) / a.TH;
-    const long long tpi = (long long)a.tiles_x * tiles_y;
-    a.tiles_per_img = (int)(tpi < INT_MAX ? tpi : INT_MAX);
-
-    // The fp32 path assumes intrinsics in the range real cameras produce;
-    // anything else runs the double-precision kernel (same results as the
-    // reference, which accepts any value).
-    const bool sane = std::isfinite(fu) && std::isfinite(fv) && std::isfinite(cu) &&
-                      std::isfinite(cv) && std::fabs(fu) >= 1e-3 && std::fabs(fu) <= 1e7 &&
-                      std::fabs(fv) >= 1e-3 && std::fabs(fv) <= 1e7 &&
-                      std::fabs(cu) <= 1e7 && std::fabs(cv) <= 1e7 && gmax <= kMaxP0;
-    // The fp32 kernel addresses a wave's run of neighbour planes (and the 3
-    // planes of pred_norm and ray) from one 32-bit buffer offset, and its grid
-    // holds one image's tiles in x; larger images also run the
-    // double-precision kernel.
-    const long long gw = a.G, nrun = (k * k + gw - 1) / gw;
-    const long long nplanes = nrun > 3 ? nrun : 3;
-    const bool fits32 = nplanes * HW * 4 < (1LL << 32) && tpi < (1LL << 31) &&
-                        tpi * 64 * a.M * gw < (1LL << 32);
-    const bool fp64 = (flags & BVML_DSINE_FP64) || !sane || !fits32;
+    bool fp64 = false;
+    const int st = plan_angmf(a, B, H, W, k, fu, cu, fv, cv, flags, fp64);
+    if (st != BVML_DSINE_OK) return st;
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e;
     switch (k) {

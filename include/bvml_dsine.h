@@ -98,6 +98,19 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
                                    unsigned flags, void* stream);
 
 /*
+ * The launch plan bvml_dsine_angmf_propagate_f32 takes for these arguments,
+ * without launching anything: 1 if the call runs the fp32 kernel, 0 if it
+ * runs the double-precision kernel, or a negative BVML_DSINE_E* status.
+ * *waves_per_group receives the waves that share one 64-pixel group (1: each
+ * wave evaluates the whole window; 2, 4, 8: the window's neighbours split
+ * into runs), *tile_w and *tile_h the workgroup's tile; any of the three may
+ * be NULL.  No counterpart in the reference: for tests and tuning.
+ */
+int bvml_dsine_angmf_plan(int B, int H, int W, int k, double fu, double cu, double fv,
+                          double cv, unsigned flags, int* waves_per_group, int* tile_w,
+                          int* tile_h);
+
+/*
  * The /8-grid ray map, 3 x H x W fp32 planes, as the reference's build_ray8
  * (src/dsine_decoder.cpp:276-293, through get_ray_core :242-259) forms it on
  * the host: ray_x = float(((x + 0.5) - cu) / fu), ray_y likewise with cv, fv,

@@ -6,8 +6,8 @@
 //     (tests/test_gpu_hw_bounds.py);
 //   * a streaming read of a buffer, the same-box read ceiling bench.py
 //     reports beside the kernels' bandwidth.
-// Every kernel writes one result per workgroup, into arrays the host sizes
-// to the grid, with vector stores.
+// Every kernel writes one result per workgroup (the read: per wave), into
+// arrays the host sizes to the grid, with vector stores.
 
 #include <hip/hip_runtime.h>
 
@@ -76,29 +76,32 @@ __global__ __launch_bounds__(kBlock) void sweep(int op, uint32_t lo, uint32_t hi
     }
 }
 
-constexpr int kReadBlocks = 8192;
-
 typedef float f4v __attribute__((ext_vector_type(4)));
 
-// Sum of n floats (n4 float4s, then the tail), one partial per workgroup.
+// Sum of n floats (n4 float4s, then the tail): each lane issues U
+// independent non-temporal float4 loads (coalesced, kBlock float4s apart)
+// before using any, each wave reduces across its lanes and writes one
+// partial; one launch covers the buffer once.  Reads 16 B per lane per load,
+// writes 4 B per 64 * 16 * U bytes read.
+template <int U>
 __global__ __launch_bounds__(kBlock) void stream_read(const f4v* p, size_t n4, const float* tail,
                                                       int ntail, float* out) {
-    __shared__ float s[kBlock];
+    const size_t base = (size_t)blockIdx.x * kBlock * U + threadIdx.x;
+    f4v v[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const size_t i = base + (size_t)u * kBlock;
+        v[u] = (i < n4) ? __builtin_nontemporal_load(p + i) : f4v{0.0f, 0.0f, 0.0f, 0.0f};
+    }
     float acc = 0.0f;
-    for (size_t i = (size_t)blockIdx.x * kBlock + threadIdx.x; i < n4;
-         i += (size_t)gridDim.x * kBlock) {
-        const f4v v = __builtin_nontemporal_load(p + i);
-        acc += (v.x + v.y) + (v.z + v.w);
-    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc += (v[u].x + v[u].y) + (v[u].z + v[u].w);
     if (blockIdx.x == 0 && (int)threadIdx.x < ntail) acc += tail[threadIdx.x];
-    s[threadIdx.x] = acc;
-    __syncthreads();
-    for (int k = kBlock / 2; k > 0; k >>= 1) {
-        if ((int)threadIdx.x < k) s[threadIdx.x] += s[threadIdx.x + k];
-        __syncthreads();
-    }
-    if (threadIdx.x == 0) out[blockIdx.x] = s[0];
+    for (int o = 32; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+    if ((threadIdx.x & 63) == 0) out[(size_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6)] = acc;
 }
+
+size_t read_grid(size_t n4, int u) { return (n4 + (size_t)kBlock * u - 1) / ((size_t)kBlock * u); }
 
 uint32_t bits_of(float f) {
     uint32_t u;
@@ -155,16 +158,31 @@ int bvml_probe_hw_error(int op, float lo, float hi, int negative, double* max_ab
     return (int)e;
 }
 
-// Partial sums of n floats at p into out (kReadBlocks floats), on `stream`.
-int bvml_probe_stream_read(const float* p, size_t n, float* out, void* stream) {
+// Partials of a streaming read of n floats at p into out (out_len floats,
+// at least bvml_probe_read_partials(n, u)), U = u float4 loads per lane
+// (1, 2, 4 or 8), on `stream`.
+int bvml_probe_stream_read(const float* p, size_t n, int u, float* out, size_t out_len,
+                           void* stream) {
     const size_t n4 = n / 4;
     const int ntail = (int)(n - 4 * n4);
-    hipLaunchKernelGGL(stream_read, dim3(kReadBlocks), dim3(kBlock), 0,
-                       static_cast<hipStream_t>(stream), reinterpret_cast<const f4v*>(p), n4,
-                       p + 4 * n4, ntail, out);
+    const size_t grid = read_grid(n4, u);
+    if (grid == 0 || grid > 0x7fffffffu || out_len < grid * (kBlock / 64)) return -1;
+    const dim3 g((unsigned)grid), b(kBlock);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    const f4v* p4 = reinterpret_cast<const f4v*>(p);
+    switch (u) {
+        case 1: hipLaunchKernelGGL(stream_read<1>, g, b, 0, st, p4, n4, p + 4 * n4, ntail, out); break;
+        case 2: hipLaunchKernelGGL(stream_read<2>, g, b, 0, st, p4, n4, p + 4 * n4, ntail, out); break;
+        case 4: hipLaunchKernelGGL(stream_read<4>, g, b, 0, st, p4, n4, p + 4 * n4, ntail, out); break;
+        case 8: hipLaunchKernelGGL(stream_read<8>, g, b, 0, st, p4, n4, p + 4 * n4, ntail, out); break;
+        default: return -1;
+    }
     return (int)hipGetLastError();
 }
 
-int bvml_probe_read_blocks(void) { return kReadBlocks; }
+// The number of partials bvml_probe_stream_read writes for n floats.
+size_t bvml_probe_read_partials(size_t n, int u) {
+    return u > 0 ? (read_grid(n / 4, u) == 0 ? 1 : read_grid(n / 4, u)) * (kBlock / 64) : 0;
+}
 
 }  // extern "C"

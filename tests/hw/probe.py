@@ -23,10 +23,10 @@ def load() -> ctypes.CDLL:
         lib.bvml_probe_hw_error.argtypes = [i, f, f, i, ctypes.POINTER(d), ctypes.POINTER(d),
                                             ctypes.POINTER(f)]
         lib.bvml_probe_hw_error.restype = i
-        lib.bvml_probe_stream_read.argtypes = [vp, sz, vp, vp]
+        lib.bvml_probe_stream_read.argtypes = [vp, sz, i, vp, sz, vp]
         lib.bvml_probe_stream_read.restype = i
-        lib.bvml_probe_read_blocks.argtypes = []
-        lib.bvml_probe_read_blocks.restype = i
+        lib.bvml_probe_read_partials.argtypes = [sz, i]
+        lib.bvml_probe_read_partials.restype = sz
         _lib = lib
     return _lib
 
@@ -42,11 +42,14 @@ def hw_error(op: str, lo: float, hi: float, negative: bool = False):
     return a.value, r.value, g.value
 
 
-def stream_read(ptr: int, n: int, out_ptr: int, stream: int = 0) -> None:
-    st = load().bvml_probe_stream_read(ptr, n, out_ptr, stream)
+def stream_read(ptr: int, n: int, unroll: int, out_ptr: int, out_len: int,
+                stream: int = 0) -> None:
+    """One streaming read of n floats at ptr (unroll float4 loads per lane);
+    per-wave partial sums into out (out_len floats)."""
+    st = load().bvml_probe_stream_read(ptr, n, unroll, out_ptr, out_len, stream)
     if st != 0:
         raise RuntimeError(f"bvml_probe_stream_read failed: {st}")
 
 
-def read_blocks() -> int:
-    return load().bvml_probe_read_blocks()
+def read_partials(n: int, unroll: int) -> int:
+    return load().bvml_probe_read_partials(n, unroll)

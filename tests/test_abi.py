@@ -184,3 +184,37 @@ def test_cxx_layer_compiles_against_brotensors_api():
     members and Device enumerators brovisionml's own sources use."""
     from brovisionml_amd import build
     build.check_brotensor_api()
+
+
+def _intr(H, W):
+    from brovisionml_amd import workloads as wl
+    return wl.scaled_intrinsics(wl.intrins_from_fov(8 * H, 8 * W, 60.0), H, W, 8 * H, 8 * W)
+
+
+def test_plan_of_the_workloads():
+    """The launch plan per workload (host logic only): run-split kernels on
+    the small images, the whole-window kernel on 4 x 512 x 512 at k = 7."""
+    from brovisionml_amd import workloads as wl
+    want = {0: (True, 4, 80, 1), 1: (True, 4, 128, 1), 2: (True, 4, 64, 2), 3: (True, 2, 80, 3),
+            4: (True, 1, 64, 8)}
+    for w in wl.WORKLOADS:
+        _, intr = w.intrinsics()
+        assert _lib.angmf_plan(w.B, w.H, w.W, w.k, *intr) == want[w.index], w.name
+    # FP64 flag, and intrinsics outside the fast path's range: the fp64 kernel
+    assert _lib.angmf_plan(1, 64, 64, 5, *_intr(64, 64), flags=_lib.FP64)[0] is False
+    assert _lib.angmf_plan(1, 64, 64, 5, 1e-4, 32.0, 1e-4, 32.0)[0] is False
+    with pytest.raises(RuntimeError, match="k must be"):
+        _lib.angmf_plan(1, 4, 4, 4, 1.0, 2.0, 1.0, 2.0)
+    with pytest.raises(RuntimeError, match="flag"):
+        _lib.angmf_plan(1, 4, 4, 5, 1.0, 2.0, 1.0, 2.0, flags=64)
+
+
+def test_gpu_parity_shapes_cover_every_kernel_layout():
+    """The GPU parity shapes reach every waves-per-group layout of the fp32
+    kernel (1: whole window; 2, 4, 8: runs) and its whole-window variant
+    with logits and rays from the intrinsics."""
+    from tests.test_gpu_parity import SHAPES
+    gs = {_lib.angmf_plan(B, H, W, k, *_intr(H, W))[1] for B, H, W, k in SHAPES}
+    assert {1, 2, 4, 8} <= gs
+    flags = _lib.LOGITS | _lib.RAY_FROM_INTRINSICS
+    assert _lib.angmf_plan(2, 512, 512, 5, *_intr(512, 512), flags=flags)[1] == 1

@@ -8,6 +8,7 @@ from __future__ import annotations
 import os
 import re
 
+import numpy as np
 import pytest
 
 from tests import tier1_model as model
@@ -59,3 +60,23 @@ def test_upsample_exp_constant(cuda):
     """The upsample's kExpRel covers v_exp_f32 on its [-126, 0] weights."""
     _, r, _ = probe.hw_error("exp2", 0.0, 126.0, True)
     assert r <= upsample_exp_rel()
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("unroll", [1, 2, 4, 8])
+def test_stream_read_reads_every_element(cuda, unroll):
+    """The read ceiling's probe touches each float of the buffer once: its
+    partials add up to the buffer's sum (odd length: a float tail)."""
+    import torch
+    from tests.hw import probe
+    n = 1_000_003
+    rng = np.random.default_rng(unroll)
+    x = rng.integers(-8, 8, n).astype(np.float32)   # small integers: exact float sums
+    buf = torch.from_numpy(x).to(cuda)
+    n_part = probe.read_partials(n, unroll)
+    part = torch.full((n_part + 64,), 12345.0, dtype=torch.float32, device=cuda)
+    probe.stream_read(buf.data_ptr(), n, unroll, part.data_ptr(), n_part)
+    torch.cuda.synchronize()
+    p = part.cpu().numpy()
+    assert (p[n_part:] == 12345.0).all()
+    assert float(p[:n_part].astype(np.float64).sum()) == float(x.astype(np.float64).sum())

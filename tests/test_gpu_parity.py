@@ -15,7 +15,7 @@ import numpy as np
 import pytest
 
 import oracle
-from brovisionml_amd import dsine, workloads as wl
+from brovisionml_amd import _lib, dsine, workloads as wl
 from tests._util import TOL_ABS, TOL_DEG, Guarded, compare, to_dev
 
 pytestmark = pytest.mark.gpu
@@ -114,18 +114,22 @@ def _random_inputs(rng, B, H, W, k, theta_scale=1.0, per_sample_ray=False):
 # Tiles: wide (64 x M) above 128 columns or 64 * M pixels; narrow full-width
 # otherwise.  (1, 10, 64, 9) and (1, 5, 128, 7) stage two halo records per
 # thread; (1, 6, 100, 9) is a row longer than one k = 9 workgroup.
+# (2, 512, 512, 5) and (3, 500, 333, 7) are large enough for the whole-window
+# kernel (one wave per 64 pixels runs every neighbour; 64 x 8 tiles), the
+# second with ragged tiles on both edges.
 SHAPES = [
     (1, 1, 1, 5), (1, 1, 9, 5), (1, 9, 1, 5), (1, 3, 4, 5), (1, 7, 130, 5),
     (1, 33, 65, 3), (2, 17, 200, 7), (1, 12, 20, 9), (3, 5, 6, 1), (1, 64, 64, 5),
-    (1, 10, 64, 9), (1, 5, 128, 7), (1, 6, 100, 9),
+    (1, 10, 64, 9), (1, 5, 128, 7), (1, 6, 100, 9), (2, 512, 512, 5), (3, 500, 333, 7),
 ]
 
 
 @pytest.mark.parametrize("B,H,W,k", SHAPES)
 def test_angmf_shapes(cuda, B, H, W, k):
-    say(f"[gpu] angmf shape B={B} H={H} W={W} k={k}")
     rng = np.random.default_rng(100 + B * 1000 + H * 10 + W + k)
     inp = _random_inputs(rng, B, H, W, k)
+    fp32, g, tw, th = _lib.angmf_plan(B, H, W, k, *inp["intrinsics"])
+    say(f"[gpu] angmf shape B={B} H={H} W={W} k={k}: G={g} tile {tw}x{th} fp32={fp32}")
     got = run_gpu(inp, H, W, cuda)
     want = run_oracle(inp, H, W, k)
     max_abs, max_deg, nan_mm = compare(got.reshape(B, 3, -1), want.reshape(B, 3, -1))
