@@ -72,24 +72,38 @@ def host_share() -> int:
         return os.cpu_count() or 1
 
 
-PROFILES = {
-    "angmf": os.path.join(ROOT, "profiles", "angmf_f32_k5_256x256_traffic.json"),
-    "upsample": os.path.join(ROOT, "profiles", "upsample8_c3_256x256_traffic.json"),
-}
+PROFILES = os.path.join(ROOT, "profiles")
 
 
 def traffic_from_profile(op: str, name: str):
     """HBM bytes per launch from the committed rocprofv3 --pmc summary
-    (FETCH_SIZE + WRITE_SIZE per dispatch, scaled by the same counters on a
-    plain copy of known size), if it covers this workload."""
-    try:
-        with open(PROFILES[op]) as f:
-            p = json.load(f)
-    except (OSError, ValueError):
-        return None
-    if p.get("workload") != name:
-        return None
-    return p.get("traffic_bytes_per_launch")
+    (profiles/<op>_*_traffic.json: FETCH_SIZE + WRITE_SIZE per dispatch,
+    scaled by the same counters on a plain copy of known size) that covers
+    this workload, if any."""
+    import glob
+    for path in sorted(glob.glob(os.path.join(PROFILES, f"{op}*_traffic.json"))):
+        try:
+            with open(path) as f:
+                p = json.load(f)
+        except (OSError, ValueError):
+            continue
+        if p.get("workload") == name:
+            return p.get("traffic_bytes_per_launch")
+    return None
+
+
+def angmf_kernel_name(w, flags) -> str:
+    """The fp32 kernel instantiation a launch of workload w runs, spelled as
+    rocprofv3 prints it: angmf_f32_kernel<k, waves per group, rays from the
+    intrinsics, logits>."""
+    from brovisionml_amd import _lib
+    _, intr = w.intrinsics()
+    fp32, g, _, _ = _lib.angmf_plan(w.B, w.H, w.W, w.k, *intr, flags=flags)
+    if not fp32:
+        return f"angmf_f64_kernel<{w.k}>"
+    sr = "true" if flags & _lib.RAY_FROM_INTRINSICS else "false"
+    lg = "true" if flags & _lib.LOGITS else "false"
+    return f"angmf_f32_kernel<{w.k}, {g}, {sr}, {lg}>"
 
 
 def timed_cpu(fn, seconds: float):
@@ -461,7 +475,7 @@ def bench_angmf(args, dev) -> dict:
     line["roofline"] = roofline(
         bytes_per_call, m["launch_s"],
         None if (args.ray_from_intrinsics or args.logits) else traffic_from_profile("angmf", w.name),
-        f"angmf_f32_kernel<{k}>", m["copy_gbps"], m["read_gbps"])
+        angmf_kernel_name(w, flags), m["copy_gbps"], m["read_gbps"])
     line["per_launch"] = {
         "us_median": round(float(np.median(per)), 3),
         "us_max": round(float(per.max()), 3),
@@ -578,12 +592,14 @@ def bench_configs(args, dev, indices) -> dict:
         px_call = w.B * w.HW
         entry = {
             "B": w.B, "H": w.H, "W": w.W, "k": w.k, "calls_per_step": w.calls,
+            "kernel": angmf_kernel_name(w, 0),
             "cold_us_per_call": round(m["launch_s"] * 1e6, 3),
             "warm_us_per_call": round(m["t_warm"] / (steps * w.calls) * 1e6, 3),
             "mpixel_s": round(px_call / m["launch_s"] / 1e6, 1),
             "achieved_gbps": round(bpc / m["launch_s"] / 1e9, 1),
             "frac": round(bpc / m["launch_s"] / 1e9 / HBM_PEAK_GBPS, 4),
             "bytes_per_call": bpc,
+            "traffic": traffic_from_profile("angmf", w.name),
             "inputs": f"{nsets} independent draws ({nsets * bpc * w.calls / 1e6:.0f} MB), "
                       "timed after a 512 MB flush",
         }
