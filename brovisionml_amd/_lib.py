@@ -36,6 +36,9 @@ EXPORTS = (
     "bvml_dsine_angmf_plan",
     "bvml_dsine_ray_relu_cpu_f32",
     "bvml_dsine_angmf_propagate_cpu_f32",
+    "bvml_dsine_gru_gates_f32",
+    "bvml_dsine_gru_update_f32",
+    "bvml_dsine_bias_act_f32",
     "bvml_dsine_last_error",
     "bvml_dsine_version",
 )
@@ -74,6 +77,12 @@ def load(path: str = LIB) -> ctypes.CDLL:
     lib.bvml_dsine_angmf_propagate_cpu_f32.argtypes = [
         vp, vp, vp, vp, vp, d, d, d, d, i, i, i, i, ll, vp, u, i]
     lib.bvml_dsine_angmf_propagate_cpu_f32.restype = i
+    lib.bvml_dsine_gru_gates_f32.argtypes = [vp, vp, vp, vp, i, ll, vp, vp, vp]
+    lib.bvml_dsine_gru_gates_f32.restype = i
+    lib.bvml_dsine_gru_update_f32.argtypes = [vp, vp, vp, vp, i, ll, vp, vp, vp]
+    lib.bvml_dsine_gru_update_f32.restype = i
+    lib.bvml_dsine_bias_act_f32.argtypes = [vp, vp, i, ll, i, vp]
+    lib.bvml_dsine_bias_act_f32.restype = i
     lib.bvml_dsine_last_error.argtypes = []
     lib.bvml_dsine_last_error.restype = ctypes.c_char_p
     lib.bvml_dsine_version.argtypes = []
@@ -149,3 +158,20 @@ def angmf_plan(B: int, H: int, W: int, k: int, fu: float, cu: float, fv: float, 
     if st < 0:
         raise RuntimeError(f"angmf_plan: {last_error()} (status {st})")
     return bool(st), g.value, tw.value, th.value
+
+
+def gru_gates_f32(zr: int, bias_z: int, bias_r: int, h: int, C: int, HW: int, z: int, rh: int,
+                  stream: int = 0) -> int:
+    """Raw call; pointers are integer device addresses. Returns the status."""
+    return load().bvml_dsine_gru_gates_f32(zr, bias_z, bias_r, h, C, HW, z, rh, stream)
+
+
+def gru_update_f32(q_pre: int, bias_q: int, z: int, h: int, C: int, HW: int, h_new: int,
+                   h_copy: int = 0, stream: int = 0) -> int:
+    """Raw call; pointers are integer device addresses. Returns the status."""
+    return load().bvml_dsine_gru_update_f32(q_pre, bias_q, z, h, C, HW, h_new, h_copy, stream)
+
+
+def bias_act_f32(x: int, bias: int, C: int, HW: int, relu: bool, stream: int = 0) -> int:
+    """Raw call; pointers are integer device addresses. Returns the status."""
+    return load().bvml_dsine_bias_act_f32(x, bias, C, HW, int(bool(relu)), stream)

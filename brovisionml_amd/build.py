@@ -53,6 +53,7 @@ CXX_FLAGS = ["-O2", "-std=c++17", "-fPIC", "-ffp-contract=off", "-fno-fast-math"
 SOURCES = [
     os.path.join(CSRC, "dsine_ops.hip"),      # AngMF / RayReLU kernels + C ABI
     os.path.join(CSRC, "upsample.hip"),       # convex upsample + normalise
+    os.path.join(CSRC, "gru.hip"),            # the refiner's fused elementwise steps
 ]
 HOST_SOURCES = [
     os.path.join(CSRC, "dsine_ops_cpu.cpp"),  # CPU branch (C ABI *_cpu_f32)

@@ -220,6 +220,60 @@ def build_ray8(fu: float, cu: float, fv: float, cv: float, H: int, W: int, devic
     return ray
 
 
+def _maps(op: str, C: int, HW: int, **tensors) -> None:
+    """Every tensor a contiguous float32 map of C*HW floats (or C for a
+    bias) on one HIP device."""
+    import torch
+    dev = None
+    for name, t in tensors.items():
+        want = C if name.startswith("bias") else C * HW
+        if t.device.type != "cuda":
+            _fail(f"{op}: {name} is not on a HIP device")
+        if dev is not None and t.device != dev:
+            _fail(f"{op}: all tensors must share a device")
+        dev = t.device
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            _fail(f"{op}: {name} must be a contiguous float32 tensor")
+        if t.numel() != want:
+            _fail(f"{op}: {name} holds {t.numel()} elements, expected {want}")
+
+
+def gru_gates(zr, bias_z, bias_r, h, C: int, HW: int, z, rh) -> None:
+    """The ConvGRU's gates (src/dsine_refine.cpp:149-151) after one
+    convolution of convz and convr stacked, without bias: zr holds 2*C planes
+    (convz's, then convr's); writes z = sigmoid(zr[:C] + bias_z) and
+    rh = sigmoid(zr[C:] + bias_r) * h.  Tensors may be channel slices of
+    larger maps as long as each is contiguous."""
+    _maps("gru_gates", C, HW, h=h, z=z, rh=rh, bias_z=bias_z, bias_r=bias_r)
+    _maps("gru_gates", 2 * C, HW, zr=zr)
+    with _device(zr):
+        st = _lib.gru_gates_f32(zr.data_ptr(), bias_z.data_ptr(), bias_r.data_ptr(), h.data_ptr(),
+                                C, HW, z.data_ptr(), rh.data_ptr(), _stream_of(zr))
+    _raise_status("gru_gates", st)
+
+
+def gru_update(q_pre, bias_q, z, h, C: int, HW: int, h_new, h_copy=None) -> None:
+    """h_new = (1 - z) h + z tanh(q_pre + bias_q) (src/dsine_refine.cpp:
+    152-157), also into h_copy when given; h_new may be h."""
+    extra = {} if h_copy is None else {"h_copy": h_copy}
+    _maps("gru_update", C, HW, q_pre=q_pre, z=z, h=h, h_new=h_new, bias_q=bias_q, **extra)
+    with _device(q_pre):
+        st = _lib.gru_update_f32(q_pre.data_ptr(), bias_q.data_ptr(), z.data_ptr(), h.data_ptr(),
+                                 C, HW, h_new.data_ptr(),
+                                 0 if h_copy is None else h_copy.data_ptr(), _stream_of(q_pre))
+    _raise_status("gru_update", st)
+
+
+def bias_act(x, bias, C: int, HW: int, relu: bool) -> None:
+    """x = x + bias (per channel), then ReLU if relu, in place: a
+    convolution's bias and the head's relu_forward (src/dsine_refine.cpp:
+    119-127) in one pass."""
+    _maps("bias_act", C, HW, x=x, bias=bias)
+    with _device(x):
+        st = _lib.bias_act_f32(x.data_ptr(), bias.data_ptr(), C, HW, relu, _stream_of(x))
+    _raise_status("bias_act", st)
+
+
 class _device:
     """Make the tensor's device current for the launch."""
 

@@ -20,9 +20,12 @@ What runs where:
     (BVML_DSINE_LOGITS), so the two activation passes of :262-267 are gone;
     the upsample fuses convex_upsample_forward and l2_normalize_nchw_forward
     (:278-282); the ray map comes from bvml_dsine_build_ray8_f32 on the device.
-  * The ConvGRU and the heads are plain convolutions (the reference's
-    brotensor conv2d_forward, :94-101): torch's F.conv2d, i.e. MIOpen on ROCm,
-    in fp32 with their elementwise gates; they are not this package's hot path.
+  * The ConvGRU and the heads' convolutions (the reference's brotensor
+    conv2d_forward, :94-101) are torch's F.conv2d, i.e. MIOpen / hipBLASLt on
+    ROCm, in fp32 and without bias; their biases, activations and the GRU's
+    gate arithmetic run in the package's fused elementwise kernels
+    (bvml_dsine_gru_gates_f32, bvml_dsine_gru_update_f32,
+    bvml_dsine_bias_act_f32).
 
 Weights are the checkpoint's top-level tensors gru.conv{z,r,q}.{weight,bias}
 and {prob,xy,angle,up_prob}_head.{0,2,4}.{weight,bias} (:161-180), loaded
@@ -122,7 +125,16 @@ def uv_map(intr: workloads.Intrinsics, H: int, W: int, orig_h: int, orig_w: int)
 
 class Refiner:
     """Refiner::forward on the device.  `weights` as weight_shapes() names
-    them (numpy or torch); hidden / feature are the checkpoint's widths."""
+    them (numpy or torch); hidden / feature are the checkpoint's widths.
+
+    The convolutions run without their bias on MIOpen / hipBLASLt (torch's
+    F.conv2d): convz and convr as one 2*hidden-channel convolution, the four
+    heads' first 3x3 convolutions as one, their 1x1 middle convolutions as one
+    grouped convolution.  Biases, activations and the gate arithmetic run in
+    this package's fused kernels (bvml_dsine_gru_gates_f32,
+    bvml_dsine_gru_update_f32, bvml_dsine_bias_act_f32), which write into the
+    channel slices of persistent [h | feature | uv], [r*h | feature | uv] and
+    [h_new | uv] maps, so no concatenation is materialised per iteration."""
 
     def __init__(self, weights: dict, device, hidden: int = 64, feature: int = 64):
         import torch
@@ -133,26 +145,16 @@ class Refiner:
         for name, shape in shapes.items():
             t = torch.as_tensor(np.asarray(weights[name], np.float32)).reshape(shape)
             self.w[name] = t.to(self.device).contiguous()
-
-    def _conv(self, x, name: str, pad: int):
-        import torch.nn.functional as F
-        return F.conv2d(x, self.w[name + ".weight"], self.w[name + ".bias"], padding=pad)
-
-    def _gru(self, h, x):
-        """submodules.ConvGRU (src/dsine_refine.cpp:138-159)."""
-        import torch
-        hx = torch.cat([h, x], dim=1)
-        z = torch.sigmoid(self._conv(hx, "gru.convz", 2))
-        r = torch.sigmoid(self._conv(hx, "gru.convr", 2))
-        q = torch.tanh(self._conv(torch.cat([r * h, x], dim=1), "gru.convq", 2))
-        return (1 - z) * h + z * q
-
-    def _head(self, name: str, x):
-        """get_prediction_head (src/dsine_refine.cpp:119-127)."""
-        import torch
-        h = torch.relu(self._conv(x, name + ".0", 1))
-        h = torch.relu(self._conv(h, name + ".2", 0))
-        return self._conv(h, name + ".4", 0)
+        w = self.w
+        heads = list(HEAD_OUT)
+        self.w_zr = torch.cat([w["gru.convz.weight"], w["gru.convr.weight"]]).contiguous()
+        self.b_z, self.b_r = w["gru.convz.bias"], w["gru.convr.bias"]
+        self.w_q, self.b_q = w["gru.convq.weight"], w["gru.convq.bias"]
+        self.w_h0 = torch.cat([w[f"{h}.0.weight"] for h in heads]).contiguous()
+        self.b_h0 = torch.cat([w[f"{h}.0.bias"] for h in heads]).contiguous()
+        self.w_h2 = torch.cat([w[f"{h}.2.weight"] for h in heads]).contiguous()
+        self.b_h2 = torch.cat([w[f"{h}.2.bias"] for h in heads]).contiguous()
+        self.heads = heads
 
     def conditioning(self, intr: workloads.Intrinsics, H: int, W: int, orig_h: int, orig_w: int):
         """(ray_8, uv_8, (fu, cu, fv, cv)) on the device for an (H, W) grid: the
@@ -163,36 +165,65 @@ class Refiner:
         uv8 = torch.from_numpy(np.ascontiguousarray(uv_map(intr, H, W, orig_h, orig_w)))
         return ray8, uv8.to(self.device)[None], fuv
 
+    def _heads(self, hin, H: int, W: int):
+        """The four get_prediction_head stacks (src/dsine_refine.cpp:119-127)
+        on hin: (prob, xy, angle, up_mask) logits."""
+        import torch.nn.functional as F
+        nh = len(self.heads)
+        t = F.conv2d(hin, self.w_h0, None, padding=1)
+        dsine.bias_act(t, self.b_h0, nh * 64, H * W, relu=True)
+        t = F.conv2d(t, self.w_h2, None, groups=nh)
+        dsine.bias_act(t, self.b_h2, nh * 64, H * W, relu=True)
+        return [F.conv2d(t[:, 64 * i:64 * (i + 1)], self.w[f"{h}.4.weight"],
+                         self.w[f"{h}.4.bias"]).contiguous() for i, h in enumerate(self.heads)]
+
     def forward(self, dec: DecoderOutput, intr: workloads.Intrinsics, orig_h: int, orig_w: int,
-                crop: Crop | None = None, trace: list | None = None, cond=None):
+                crop: Crop | None = None, trace: list | None = None, cond=None,
+                hidden_trace: list | None = None):
         """The refined normals (1, 3, h, w) at the unpadded resolution
         (crop.orig_h x crop.orig_w; the whole 8*h8 x 8*w8 map without crop).
-        trace, when given, receives each iteration's (pred_norm, up) pair;
+        trace, when given, receives each iteration's (pred_norm, up) pair,
+        hidden_trace a copy of each iteration's h_new (1, C, h8, w8);
         cond, when given, is conditioning()'s result for these intrinsics (so
         the call does no host-to-device copy and can be captured in a graph)."""
         import torch
+        import torch.nn.functional as F
         _, _, H, W = dec.normal.shape
+        C, HW = self.hidden, H * W
         ray8, uv8, (fu, cu, fv, cv) = (cond if cond is not None
                                        else self.conditioning(intr, H, W, orig_h, orig_w))
         pred_norm = dec.normal.contiguous().clone()
         dsine.ray_relu(pred_norm, ray8, H, W)
-        feat_map = torch.cat([dec.feature, uv8], dim=1)
-        h = dec.hidden
+        # hx = [h | feature | uv], rhx = [r*h | feature | uv], hin = [h_new | uv]
+        # (submodules.ConvGRU's cat([h, x]) and cat([r*h, x]) with
+        # x = feat_map = cat(feature, uv_8), and the heads' cat(h_new, uv_8))
+        cx = self.feature + 2
+        hx = torch.empty((1, C + cx, H, W), dtype=torch.float32, device=self.device)
+        hx[:, :C] = dec.hidden
+        hx[:, C:C + self.feature] = dec.feature
+        hx[:, C + self.feature:] = uv8
+        rhx = torch.empty_like(hx)
+        rhx[:, C:] = hx[:, C:]
+        hin = torch.empty((1, C + 2, H, W), dtype=torch.float32, device=self.device)
+        hin[:, C:] = uv8
+        z = torch.empty((1, C, H, W), dtype=torch.float32, device=self.device)
+        h = hx[:, :C]
         up = None
         for _ in range(N_ITER):
-            h_new = self._gru(h, feat_map)
-            hin = torch.cat([h_new, uv8], dim=1)
-            prob = self._head("prob_head", hin).contiguous()
-            xy = self._head("xy_head", hin).contiguous()
-            angle = self._head("angle_head", hin).contiguous()
+            # ConvGRU (src/dsine_refine.cpp:138-159): h_new overwrites h in hx
+            zr = F.conv2d(hx, self.w_zr, None, padding=2)
+            dsine.gru_gates(zr, self.b_z, self.b_r, h, C, HW, z, rhx[:, :C])
+            qp = F.conv2d(rhx, self.w_q, None, padding=2)
+            dsine.gru_update(qp, self.b_q, z, h, C, HW, h, hin[:, :C])
+            prob, xy, angle, up_mask = self._heads(hin, H, W)
             pred_norm = dsine.angmf_propagate(pred_norm, prob, xy, angle, ray8, fu, cu, fv, cv,
                                               H, W, logits=True)
-            up_mask = self._head("up_prob_head", hin).contiguous()
             up = dsine.convex_upsample_normalize(pred_norm, up_mask, 1, 3, H, W, K_UP,
                                                  float(np.float32(1e-12)))
             if trace is not None:
                 trace.append((pred_norm, up))
-            h = h_new
+            if hidden_trace is not None:
+                hidden_trace.append(h.clone())
         if crop is None:
             return up
         return up[:, :, crop.pad_t:crop.pad_t + crop.orig_h,

@@ -177,6 +177,32 @@ int bvml_dsine_angmf_propagate_cpu_f32(const float* pred_norm, const float* prob
  */
 double bvml_dsine_angmf_recompute_ratio(unsigned flags);
 
+/*
+ * The refiner's elementwise steps around its convolutions, fused (no
+ * counterpart in the reference, whose ConvGRU and heads run each step as its
+ * own brotensor op, src/dsine_refine.cpp:104-159).  Maps are fp32 NCHW, C
+ * planes of HW floats on the device; biases hold C floats.  The convolutions
+ * run without their bias; these apply it.
+ *
+ * bvml_dsine_gru_gates_f32: zr holds 2C planes, convz's then convr's
+ *   pre-activations; z = sigmoid(zr[c] + bias_z[c]) and
+ *   rh = sigmoid(zr[C + c] + bias_r[c]) * h.  z and rh must not overlap zr,
+ *   h or each other.
+ * bvml_dsine_gru_update_f32: h_new = (1 - z) h + z tanh(q_pre + bias_q), in
+ *   the reference's rounding order (src/dsine_refine.cpp:152-157), written to
+ *   h_new and, when h_copy is non-NULL, to h_copy too.  h_new may be h.
+ * bvml_dsine_bias_act_f32: x = x + bias[c] in place, then ReLU if relu is 1
+ *   (v < 0 ? 0 : v).
+ */
+int bvml_dsine_gru_gates_f32(const float* zr, const float* bias_z, const float* bias_r,
+                             const float* h, int C, long long HW, float* z, float* rh,
+                             void* stream);
+int bvml_dsine_gru_update_f32(const float* q_pre, const float* bias_q, const float* z,
+                              const float* h, int C, long long HW, float* h_new, float* h_copy,
+                              void* stream);
+int bvml_dsine_bias_act_f32(float* x, const float* bias, int C, long long HW, int relu,
+                            void* stream);
+
 /* Message for the calling thread's last non-zero status ("" if none). */
 const char* bvml_dsine_last_error(void);
 

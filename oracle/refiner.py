@@ -22,13 +22,20 @@ def _sigmoid_f32(x):
     return (1.0 / (1.0 + np.exp(-np.asarray(x, np.float64)))).astype(np.float32)
 
 
+MUTATIONS = (None, "swap_zr", "swap_xy")
+
+
 def refine_forward(weights, normal, feature, hidden, intr, fuv, ray8, uv8, trace=None,
-                   nthreads: int = 1):
+                   nthreads: int = 1, hidden_trace=None, mutation=None):
     """weights: name -> OIHW / (C,) float32 arrays; normal (3, H, W), feature
     and hidden (C, H, W) float32; intr unused beyond fuv = (fu, cu, fv, cv);
     ray8 (3, H, W) and uv8 (2, H, W) float32 as build_ray8 / build_uv give
     them.  Returns the last up-sampled map (3, 8H, 8W) float32; trace, when
-    given, receives each iteration's (pred_norm, up)."""
+    given, receives each iteration's (pred_norm, up), hidden_trace each
+    iteration's h_new (C, H, W) float64.  mutation plants a mistake, for the
+    tests that show the checks catch one: "swap_zr" exchanges the GRU's z and
+    r gates, "swap_xy" the propagate's xs and ys planes."""
+    assert mutation in MUTATIONS
     import torch
     import torch.nn.functional as F
 
@@ -54,11 +61,15 @@ def refine_forward(weights, normal, feature, hidden, intr, fuv, ray8, uv8, trace
         hx = torch.cat([h, feat_map], dim=1)
         z = torch.sigmoid(conv(hx, "gru.convz", 2))
         r = torch.sigmoid(conv(hx, "gru.convr", 2))
+        if mutation == "swap_zr":
+            z, r = r, z
         q = torch.tanh(conv(torch.cat([r * h, feat_map], dim=1), "gru.convq", 2))
         h_new = (1 - z) * h + z * q
         hin = torch.cat([h_new, uv], dim=1)
         prob = _sigmoid_f32(head("prob_head", hin))
         xy = head("xy_head", hin)
+        if mutation == "swap_xy":
+            xy = np.concatenate([xy[PS * PS:], xy[:PS * PS]])
         angle = (_sigmoid_f32(head("angle_head", hin)).astype(np.float64)
                  * np.float64(K_PI32)).astype(np.float32)
         pred = angmf_propagate(pred.reshape(1, 3, -1), prob.reshape(1, PS * PS, -1),
@@ -70,5 +81,7 @@ def refine_forward(weights, normal, feature, hidden, intr, fuv, ray8, uv8, trace
                              eps=float(np.float32(1e-12)), nthreads=nthreads)[0]
         if trace is not None:
             trace.append((pred.reshape(3, H, W).copy(), up))
+        if hidden_trace is not None:
+            hidden_trace.append(h_new[0].numpy().copy())
         h = h_new
     return up

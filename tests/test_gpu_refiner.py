@@ -81,3 +81,65 @@ def test_refiner_crop(cuda):
     assert part.shape == (1, 3, crop.orig_h, crop.orig_w)
     assert np.array_equal(part.cpu().numpy(),
                           full.cpu().numpy()[:, :, 5:5 + crop.orig_h, 3:3 + crop.orig_w])
+
+
+# ---- closed-form pins (tests/refiner_pins.py), independent of the restatement
+def _gpu_run(pin, n0=0, H=24, W=32, fov=60.0, seed=7):
+    import torch
+    from tests import refiner_pins as pins
+    n, feature, hidden, intr, fuv, ray8, uv8 = pins.setup(H, W, fov, seed)
+    w, data = pins.pinned_weights(pin, seed, n0=n0)
+    dev = torch.device("cuda:0")
+    model = rf.Refiner(w, dev)
+    dec = rf.DecoderOutput(*(torch.from_numpy(a)[None].to(dev) for a in (n, feature, hidden)))
+    trace, htrace = [], []
+    model.forward(dec, intr, 8 * H, 8 * W, trace=trace, hidden_trace=htrace)
+    torch.cuda.synchronize()
+    trace = [(p.cpu().numpy().reshape(3, H, W), u.cpu().numpy()[0]) for p, u in trace]
+    htrace = [h.cpu().numpy()[0] for h in htrace]
+    return trace, htrace, data, (n, hidden, fuv, ray8)
+
+
+def test_pin_gate_closed(cuda):
+    """convz saturated shut: every iteration's h_new is the decoder's hidden."""
+    say("[gpu] refiner pin: gate closed")
+    _, htrace, _, (_, hidden, _, _) = _gpu_run("gate_closed")
+    err = max(float(np.abs(h - hidden).max()) for h in htrace)
+    say(f"    max-abs {err:.3e}")
+    assert err <= 1e-5
+
+
+def test_pin_gate_open(cuda):
+    """convz saturated open and convq weight 0: h_new = tanh(convq's bias)."""
+    say("[gpu] refiner pin: gate open")
+    _, htrace, data, _ = _gpu_run("gate_open")
+    want = np.tanh(data["bq"].astype(np.float64))[:, None, None]
+    err = max(float(np.abs(h - want).max()) for h in htrace)
+    say(f"    max-abs {err:.3e}")
+    assert err <= 1e-5
+
+
+def test_pin_constant_heads(cuda):
+    """Heads reduced to their biases: each iteration is one direct propagate
+    of constant planes, as the C oracle computes it."""
+    from tests import refiner_pins as pins
+    say("[gpu] refiner pin: constant heads")
+    trace, _, data, (n, _, fuv, ray8) = _gpu_run("const_heads")
+    H, W = n.shape[1:]
+    want = pins.const_heads_expected(data, n, ray8, fuv, H, W, chain=[p for p, _ in trace])
+    for it, ((p, _), w) in enumerate(zip(trace, want)):
+        err = float(np.abs(p.astype(np.float64) - w).max())
+        say(f"    iteration {it}: max-abs {err:.3e}")
+        assert err <= 1e-5
+
+
+@pytest.mark.parametrize("n0", [0, 5, 7])
+def test_pin_onehot_upsample(cuda, n0):
+    """A one-hot up_prob_head bias: the up-sampled map is the normalised
+    propagate output at each pixel's clamped tap."""
+    from tests import refiner_pins as pins
+    say(f"[gpu] refiner pin: one-hot up mask, tap {n0}")
+    trace, _, _, _ = _gpu_run("onehot_up", n0=n0)
+    err = max(float(np.abs(u - pins.onehot_up_expected(p, n0)).max()) for p, u in trace)
+    say(f"    max-abs {err:.3e}")
+    assert err <= 1e-5
