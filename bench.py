@@ -617,6 +617,60 @@ def bench_configs(args, dev, indices) -> dict:
 
 
 # ---------------------------------------------------------------------------
+# RayReLU
+# ---------------------------------------------------------------------------
+
+def bench_ray_relu(args, dev) -> dict:
+    """RayReLU in place on the normal map of a propagate workload's shape
+    (src/dsine_ops.cu:58-74; the refiner runs it once per forward on the
+    decoder's normals, src/dsine_refine.cpp:241-243): cold graph replays
+    over independent draws, like the propagate's."""
+    import torch
+    from brovisionml_amd import _lib
+    W_ = wl_mod()
+    w = W_.WORKLOADS[args.workload]
+    B, H, W, HW = w.B, w.H, w.W, w.HW
+    # normal read + written per sample, the shared ray read once
+    bytes_per_call = (B * 6 + 3) * HW * 4
+    nsets = args.sets or nsets_for(bytes_per_call)
+    bufs, normals, rays = [], [], []
+    for d in range(nsets + 1):
+        inp = W_.make_inputs(w, d if d < nsets else 0)
+        flat = torch.from_numpy(np.concatenate([inp["pred_norm"].ravel(),
+                                                inp["ray"].ravel()])).to(dev)
+        normals.append(flat[:B * 3 * HW])
+        rays.append(flat[B * 3 * HW:])
+        bufs.append(flat)
+
+    def launch(i: int) -> None:
+        sptr = torch.cuda.current_stream(dev).cuda_stream
+        st = _lib.ray_relu_f32(normals[i].data_ptr(), rays[i].data_ptr(), B, H, W, 0, sptr)
+        if st != 0:
+            raise RuntimeError(f"ray_relu_f32 failed: {st} {_lib.last_error()}")
+
+    tm = Timer(dev, launch, nsets, args.steps, args.warmup, bytes_per_call, warm_index=nsets)
+    t_cold = tm.cold()
+    t_warm = tm.warm()
+    copy_gbps = tm.copy_ceiling_gbps()
+    read_gbps = tm.read_ceiling_gbps(bufs[:nsets])
+    launch_s = t_cold / args.steps
+    vec4 = HW % 4 == 0
+    line = base_line(
+        args, f"Mpixel/s (+ achieved HBM GB/s, % of peak), DSINE RayReLU {w.name}",
+        B * HW * args.steps / t_cold / 1e6, "Mpixel/s", t_cold * 1e3 / args.steps,
+        {"workload": w.name, "B": B, "H": H, "W": W,
+         "kernel_mode": "4 pixels per lane" if vec4 else "1 pixel per lane",
+         "inputs": f"{nsets} independent seeded draws, rotating; timed replay after a 512 MB "
+                   "flush"})
+    line["roofline"] = roofline(bytes_per_call, launch_s, None,
+                                "ray_relu4_kernel" if vec4 else "ray_relu_kernel", copy_gbps,
+                                read_gbps)
+    line["warm"] = {"launch_us_mean": round(t_warm / args.steps * 1e6, 3)}
+    line["gpu"] = torch.cuda.get_device_name(dev)
+    return line
+
+
+# ---------------------------------------------------------------------------
 # convex upsample
 # ---------------------------------------------------------------------------
 
@@ -800,9 +854,10 @@ def main() -> int:
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
-    ap.add_argument("--op", choices=("angmf", "upsample", "refiner"), default="angmf")
+    ap.add_argument("--op", choices=("angmf", "upsample", "refiner", "ray_relu"), default="angmf")
     ap.add_argument("--workload", type=int, default=None,
-                    help="index into the op's workloads (default: angmf 2, upsample 0)")
+                    help="index into the op's workloads (default: angmf and ray_relu 2, "
+                         "upsample 0)")
     ap.add_argument("--sets", type=int, default=0,
                     help="rotating input sets (0 = auto: > 512 MB, at most 256)")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
@@ -822,7 +877,7 @@ def main() -> int:
                          "(the reference kernel for the FETCH_SIZE / WRITE_SIZE scale)")
     args = ap.parse_args()
     if args.workload is None and args.op != "refiner":
-        args.workload = 2 if args.op == "angmf" else 0
+        args.workload = 2 if args.op in ("angmf", "ray_relu") else 0
 
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
@@ -838,8 +893,8 @@ def main() -> int:
         return 1
     dev = torch.device("cuda:0")
     _lib.load()
-    line = {"angmf": bench_angmf, "upsample": bench_upsample,
-            "refiner": bench_refiner}[args.op](args, dev)
+    line = {"angmf": bench_angmf, "upsample": bench_upsample, "refiner": bench_refiner,
+            "ray_relu": bench_ray_relu}[args.op](args, dev)
     print(json.dumps(line), flush=True)
     return 0
 

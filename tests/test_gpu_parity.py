@@ -323,10 +323,13 @@ def test_angmf_odd_intrinsics_use_fp64(cuda):
     assert max_abs <= 2.5e-7
 
 
-@pytest.mark.parametrize("B,H,W", [(1, 60, 80), (1, 256, 256), (4, 33, 17), (1, 1, 1)])
-def test_ray_relu(cuda, B, H, W):
+# (4 pixels per lane where H*W is a multiple of 4 and the planes are 16-byte
+# aligned; one otherwise: 33 x 17, and the shifted normal)
+@pytest.mark.parametrize("B,H,W,shift", [(1, 60, 80, 0), (1, 256, 256, 0), (4, 33, 17, 0),
+                                         (1, 1, 1, 0), (2, 64, 64, 1), (3, 16, 20, 0)])
+def test_ray_relu(cuda, B, H, W, shift):
     import torch
-    say(f"[gpu] ray_relu B={B} {H}x{W}")
+    say(f"[gpu] ray_relu B={B} {H}x{W} shift={shift}")
     rng = np.random.default_rng(21 + H)
     HW = H * W
     intr = wl.intrins_from_fov(8 * H, 8 * W, 60.0)
@@ -335,7 +338,10 @@ def test_ray_relu(cuda, B, H, W):
     # nearly antiparallel to the ray, the ill-conditioned end of the clamp
     m = min(HW, 50)
     n[0, :, :m] = -ray[:, :m] + 1e-4 * rng.standard_normal((3, m)).astype(np.float32)
-    g = Guarded(n.size, cuda, fill=n)
+    if B == 3:
+        # one ray map per sample (ray_bstride 3*H*W)
+        ray = np.stack([ray, ray[[1, 0, 2]], ray[[0, 2, 1]]]).astype(np.float32)
+    g = Guarded(n.size, cuda, shift=shift, fill=n)
     dsine.ray_relu(g.out, to_dev(ray, cuda), H, W)
     torch.cuda.synchronize()
     assert g.intact(), "ray_relu wrote outside its tensor"
