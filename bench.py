@@ -47,6 +47,8 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBPS = 8000.0
 FLUSH_BYTES = 512 << 20
+# Back-to-back work before each timed region, to bring the clocks up (Timer.ramp).
+RAMP_SECONDS = 0.3
 
 
 def cpu_model() -> str:
@@ -149,11 +151,27 @@ class Timer:
                 self.launch(i)
         return g
 
+    def ramp(self, work) -> None:
+        """Run `work` back to back for RAMP_SECONDS: the GPU lowers its clocks
+        when idle (input generation on the host leaves it idle for seconds)
+        and takes tens of milliseconds of load to raise them again, so a
+        timed replay straight after idle time measures the clock ramp, not
+        the kernel (4 x 512 x 512, k = 7: 184 us per launch right after 5 s of
+        idle, 152 us at steady clocks)."""
+        torch = self.torch
+        t0 = time.perf_counter()
+        while True:
+            work()
+            torch.cuda.synchronize()
+            if time.perf_counter() - t0 >= RAMP_SECONDS:
+                return
+
     def timed_graph(self, g, flush: bool):
         torch = self.torch
         stream = torch.cuda.current_stream(self.dev)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
+        self.ramp(g.replay)
         if flush:
             self.flush()
         torch.cuda.synchronize()
@@ -184,6 +202,11 @@ class Timer:
         stream = torch.cuda.current_stream(self.dev)
         ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
               for _ in range(self.steps)]
+
+        def rotation():
+            for i in range(self.steps):
+                self.launch(i % self.nsets)
+        self.ramp(rotation)
         self.flush()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
