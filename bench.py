@@ -400,7 +400,7 @@ def recompute_counts(sets: AngmfSets, flags: int, nthreads: int):
     import oracle
     from brovisionml_amd import _lib
     w = sets.w
-    t = _lib.angmf_recompute_ratio(flags)
+    t = _lib.angmf_recompute_ratio(w.k, flags)
     counts = []
     for inp in sets.host:
         if inp is None:

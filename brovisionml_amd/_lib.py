@@ -70,7 +70,7 @@ def load(path: str = LIB) -> ctypes.CDLL:
     ip = ctypes.POINTER(ctypes.c_int)
     lib.bvml_dsine_angmf_plan.argtypes = [i, i, i, i, d, d, d, d, u, ip, ip, ip]
     lib.bvml_dsine_angmf_plan.restype = i
-    lib.bvml_dsine_angmf_recompute_ratio.argtypes = [u]
+    lib.bvml_dsine_angmf_recompute_ratio.argtypes = [i, u]
     lib.bvml_dsine_angmf_recompute_ratio.restype = d
     lib.bvml_dsine_ray_relu_cpu_f32.argtypes = [vp, vp, i, i, i, ll, i]
     lib.bvml_dsine_ray_relu_cpu_f32.restype = i
@@ -125,10 +125,11 @@ def convex_upsample_f32(x: int, mask: int, B: int, C: int, H: int, W: int, scale
                                                  eps, out, flags, stream)
 
 
-def angmf_recompute_ratio(flags: int = DEFAULT) -> float:
-    """The fast path's cancellation threshold: pixels with |acc|^2 below
-    this times sum (prob/|p|)^2 are recomputed in double."""
-    return load().bvml_dsine_angmf_recompute_ratio(flags)
+def angmf_recompute_ratio(k: int, flags: int = DEFAULT) -> float:
+    """The fast path's cancellation threshold at window size k: pixels with
+    |acc|^2 below this times sum (prob/|p|)^2 are recomputed in double (0
+    with FP64, -1 for an unsupported k)."""
+    return load().bvml_dsine_angmf_recompute_ratio(k, flags)
 
 
 def ray_relu_cpu_f32(normal: int, ray: int, B: int, H: int, W: int, ray_bstride: int,

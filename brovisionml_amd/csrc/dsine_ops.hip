@@ -29,7 +29,7 @@
 //   * a pixel goes to tier 2, the same reduced form in double, when a
 //     neighbour is outside the fp32 form's domain (|dd| near the
 //     reference's 1e-8 clamp, an xy pair out of range, a non-unit source
-//     normal, |t| > 3.2, a non-finite value) or when |acc|^2 < 1.85e-3 *
+//     normal, |t| > 3.2, a non-finite value) or when |acc|^2 < kAccRatio2[k] *
 //     sum(wi^2), where the final normalise would amplify tier 1's error
 //     past the parity bar; and from there to tier 3, the reference-order
 //     double body, when a neighbour is outside the double form's domain or
@@ -88,26 +88,31 @@ constexpr float kMinV2 = 1e-30f;
 // on this kernel over input families built to stress each mechanism (random
 // and camera-facing normals, normals facing away, grazing normals, q and g
 // cancelling, checkerboards of nearly opposite normals, wide angles and
-// fields of view, saturated logits; 2.6M pixels each), pixels whose sum nearly
-// cancels show delta <= 3.17e-7.  The final normalise divides the sum by
-// |acc|, so a pixel with |acc|^2 < kAccRatio2 * sum(wi^2) is recomputed, and
-// the rest stay within 3.2e-7 / sqrt(kAccRatio2) = 7.44e-6 per component,
-// 25% inside the bar (the largest kept error measured is 4.8e-6).  About
-// 0.8 pixels of a 256x256 image of independent random unit normals fall
-// below it; the refiner's camera-facing normals practically never do.  A
-// flagged pixel costs its group's reducing wave a reload of its inputs and
-// the double evaluation, about 0.6 us at the end of its workgroup.
-constexpr double kAccRatio2 = 1.85e-3;
-
-// With BVML_DSINE_LOGITS, prob and angle hold the heads' raw logits and the
-// kernel applies the refiner's activations (src/dsine_refine.cpp:262-267):
-// prob = sigmoid(L), angle = sigmoid(L) * kPiF, kPiF the float pi of
-// src/dsine_refine.cpp:26.  Tier 1 forms them in fp32 (the angle's sigmoid
-// within 4 ulps or 3e-8 of the correctly rounded float; the weight as
-// rsq(|p|^2 (1 + exp(-L))^2)); the same measurement gives delta <= 3.10e-7
-// (saturated logits N(0, 30^2)), inside the same threshold's 3.2e-7.  Tiers
-// 2 and 3 use the correctly rounded floats (sigmoid_ref).
-constexpr double kAccRatio2Logits = 1.85e-3;
+// fields of view, saturated logits, with and without the activations formed
+// in the kernel), 0.5M-3.5M pixels per family and window size in both work
+// layouts, pixels whose sum nearly cancels show delta <= 3.42e-7 at k = 3,
+// 3.20e-7 at k = 5, 4.41e-7 at k = 7 (grazing normals, the whole-window
+// layout) and 3.99e-7 at k = 9.  Summation order does not explain the
+// spread (a model of this arithmetic gives the same delta with every
+// neighbour summed in double): per-term errors are about 1 ulp of wi in
+// every family, and they add coherently where the terms share the pixel's
+// ray and look alike.  The final normalise divides the sum by |acc|, so a
+// pixel with |acc|^2 < kAccRatio2[k] * sum(wi^2) is recomputed, and with
+// delta(k) the measured value plus 10%, the rest stay within
+// delta(k) / sqrt(kAccRatio2[k]) <= 7.5e-6 per component, 25% inside the bar
+// (the largest kept error measured is 5.8e-6).  At k = 1 the sum is one term
+// and cannot cancel.
+//
+// About 1.7 pixels of a 256x256 image of independent random unit normals with
+// angles up to pi/4 fall below the k = 5 threshold; the refiner's
+// camera-facing normals practically never do.  A flagged pixel costs its
+// group's reducing wave about 2.5 us after the reduce: one round trip to
+// reload its inputs (about 1 us under load), the double evaluation (about
+// 0.9 us of dependent double arithmetic for one wave) and the lane
+// reduction.  A 256x256 call runs all its workgroups at once, so a flagged
+// pixel in a late group lengthens the call by up to that much.
+constexpr double kAccRatio2[10] = {2.6e-3, 2.6e-3, 0.0, 2.6e-3, 0.0,
+                                   2.25e-3, 0.0, 4.2e-3, 0.0, 3.5e-3};
 
 // Tier 2 (the double-precision reduced form of flagged pixels) hands a pixel
 // to the reference-order body when its sum nearly cancels: below
@@ -168,7 +173,6 @@ struct AngmfArgs {
     double dd_min;        // tier 1: |dd| below this sends a pixel to the recompute
     int synth_ray;        // form rays from the intrinsics (synth_ray), not from `ray`
     int logits;           // prob and angle are logits (BVML_DSINE_LOGITS)
-    double acc_ratio2;    // tier 1's cancellation threshold for this launch
 };
 
 // ---------------------------------------------------------------------------
@@ -408,6 +412,34 @@ __device__ __forceinline__ bool nbr_red_f64(float mxf, float myf, float mzf, int
     return true;
 }
 
+// One DPP move of a double (two 32-bit halves); rows outside row_mask keep
+// 0.  The data-parallel primitives move within the VALU, with no LDS round
+// trip (ds_bpermute, which __shfl_xor uses, costs one per step).
+template <int CTRL, int ROWS = 0xf>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const unsigned long long u = __builtin_bit_cast(unsigned long long, v);
+    const int lo = __builtin_amdgcn_update_dpp(0, (int)(unsigned)u, CTRL, ROWS, 0xf, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, (int)(unsigned)(u >> 32), CTRL, ROWS, 0xf, false);
+    return __builtin_bit_cast(double, ((unsigned long long)(unsigned)hi << 32) | (unsigned)lo);
+}
+
+// Sum of v over each LP-lane slot of the wave (LP = 32: lanes 0-31 and 32-63;
+// LP = 64: the wave), left in the slot's last lane (31, 63; 63); the other
+// lanes hold partial sums.  Each 16-lane row is summed in place by two quad
+// permutations and the half-row and row mirrors; then row_bcast15 adds row 0's
+// sum into row 1 and row 2's into row 3 (rows 0 and 2 unchanged), and, with
+// LP = 64, row_bcast31 adds lane 31's (rows 0 + 1) into row 3.
+template <int LP>
+__device__ __forceinline__ double slot_sum(double v) {
+    v += dpp_f64<0xb1>(v);   // quad_perm [1, 0, 3, 2]
+    v += dpp_f64<0x4e>(v);   // quad_perm [2, 3, 0, 1]
+    v += dpp_f64<0x141>(v);  // row_half_mirror: lane i of 8 from lane 7 - i
+    v += dpp_f64<0x140>(v);  // row_mirror: lane i of 16 from lane 15 - i
+    v += dpp_f64<0x142, 0xa>(v);  // row_bcast15 into rows 1 and 3
+    if constexpr (LP == 64) v += dpp_f64<0x143, 0x8>(v);  // row_bcast31 into row 3
+    return v;
+}
+
 // LDS-space (address space 3) views of the halo records: 32-bit addresses
 typedef __attribute__((address_space(3))) const char lds_byte;
 typedef float lds_f4 __attribute__((ext_vector_type(4)));
@@ -530,7 +562,7 @@ __device__ __forceinline__ void sincos_hw(float t, float& st, float& ct) {
 //      the rotation, RayReLU, the weight prob/|p| and the partial sums in
 //      fp32.  A pixel is flagged when a neighbour leaves the domain (xy
 //      range, |t| > 3.2, |dd| < dd_min, a non-unit source normal,
-//      |c|^2 < kMinV2, anything non-finite) or when |acc|^2 < acc_ratio2 *
+//      |c|^2 < kMinV2, anything non-finite) or when |acc|^2 < kAccRatio2[K] *
 //      sum(wi^2);
 //   2. flagged pixels, the same reduced form in double (nbr_red_f64), one
 //      neighbour per lane of the flagging wave; a pixel with a neighbour
@@ -840,7 +872,7 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
         const double a2 = fma(s0, s0, fma(s1, s1, s2 * s2));
         // 1 / max(|acc|, 1e-12) as the reference; a non-finite or
         // cancelled sum goes to the recompute
-        flag = !(a2 >= a.acc_ratio2 * sw) || !(a2 <= 1e300);
+        flag = !(a2 >= kAccRatio2[K] * sw) || !(a2 <= 1e300);
         if (!flag) {
             const double inv = (a2 < 1e-24) ? 1e12 : rsq64_1(a2);
             float* op = a.out + (size_t)b * 3 * HW;
@@ -858,6 +890,7 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     constexpr int LP = (K2 > 32) ? 64 : 32;
     constexpr int PPP = 64 / LP;
     const int slot = lane / LP, il = lane - slot * LP;
+    const bool lead = il == LP - 1;  // the lane slot_sum leaves a slot's sums in
     int tw = TW;
     asm volatile("" : "+s"(tw));
     const float* pn = pred_norm + (size_t)b * 3 * HW;
@@ -879,43 +912,47 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
         const int fty = jj / tw, ftx = jj - fty * tw;
         const int fy = ty0 + fty, fx = tx0 + ftx;
         const uint32_t fb = (uint32_t)(fy * W + fx) * 4u;
-        float frx = 0.0f, fry = 0.0f, frz = 0.0f;
-        if (act) {
-            if constexpr (SR) {
-                const bvml::Ray3f rr3 = synth_ray(fx, fy, a.fu, a.cu, a.fv, a.cv);
-                frx = rr3.x;
-                fry = rr3.y;
-                frz = rr3.z;
-            } else {
-                frx = ldf(rp, fb);
-                fry = ldf(rp + HW, fb);
-                frz = ldf(rp + 2 * HW, fb);
-            }
-        }
         // one tier over this lane's neighbours of its pixel; returns false
         // (tier 2) when a neighbour is outside the reduced form's domain
         auto tier = [&](auto tier_tag, double& p0, double& p1, double& p2, double& q2) {
             constexpr int TIER = decltype(tier_tag)::value;
             p0 = p1 = p2 = q2 = 0.0;
             if (!act) return;
-            const double rxd = frx, ryd = fry, rzd = frz;
-            const double ird = 1.0 / smax(sqrt(fma(rxd, rxd, fma(ryd, ryd, rzd * rzd))), 1e-8);
 #pragma unroll 1
             for (int n = il; n < K2; n += LP) {
                 const int ky = n / K, kx = n - ky * K;
                 const int fsy = clampi(fy - P + ky, 0, H - 1);
                 const int fsx = clampi(fx - P + kx, 0, W - 1);
                 const uint32_t sb = (uint32_t)(fsy * W + fsx) * 4u;
+                // the pixel's ray with the neighbour's inputs: every load of
+                // the neighbour in one round trip (loaded before the loop,
+                // the ray would be waited for on its own)
+                float frx, fry, frz;
+                if constexpr (SR) {
+                    const bvml::Ray3f rr3 = synth_ray(fx, fy, a.fu, a.cu, a.fv, a.cv);
+                    frx = rr3.x;
+                    fry = rr3.y;
+                    frz = rr3.z;
+                } else {
+                    frx = ldf(rp, fb);
+                    fry = ldf(rp + HW, fb);
+                    frz = ldf(rp + 2 * HW, fb);
+                }
                 const float mx = ldf(pn, sb), my = ldf(pn + HW, sb), mz = ldf(pn + 2 * HW, sb);
                 const float xsv = ldf(xyp + (size_t)n * HW, fb);
                 const float ysv = ldf(xyp + (size_t)(K2 + n) * HW, fb);
                 float thv = ldf(ap + (size_t)n * HW, fb), wv = ldf(pr + (size_t)n * HW, fb);
+                // (no use of a loaded value moves above the last load)
+                __builtin_amdgcn_sched_barrier(0);
                 if constexpr (LG) {
                     thv = angle_ref(thv);
                     wv = sigmoid_ref(wv);
                 }
                 double ox, oy, oz, pinv;
                 if constexpr (TIER == 2) {
+                    const double rxd = frx, ryd = fry, rzd = frz;
+                    const double ird =
+                        1.0 / smax(sqrt(fma(rxd, rxd, fma(ryd, ryd, rzd * rzd))), 1e-8);
                     if (!nbr_red_f64(mx, my, mz, fsx, fsy, xsv, ysv, thv, wv, rxd, ryd, rzd, ird,
                                      a, ox, oy, oz, pinv)) {
                         q2 = __builtin_nan("");
@@ -932,13 +969,10 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
                 const double wi = w * pinv;
                 q2 = fma(wi, wi, q2);
             }
-#pragma unroll
-            for (int off = LP / 2; off > 0; off >>= 1) {
-                p0 += __shfl_xor(p0, off, 64);
-                p1 += __shfl_xor(p1, off, 64);
-                p2 += __shfl_xor(p2, off, 64);
-                q2 += __shfl_xor(q2, off, 64);
-            }
+            p0 = slot_sum<LP>(p0);
+            p1 = slot_sum<LP>(p1);
+            p2 = slot_sum<LP>(p2);
+            q2 = slot_sum<LP>(q2);
         };
         // 1 / max(|acc|, 1e-12), with the reference's NaN and Inf results
         auto write = [&](double a0, double a1, double a2) {
@@ -955,13 +989,14 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
             const double n2 = a0 * a0 + a1 * a1 + a2 * a2;
             // tier 2 hands on a pixel with a neighbour outside its domain
             // (aq NaN) or a sum that nearly cancels
-            need3 = act && (!(n2 >= kAccRatio2Ref * aq) || !(n2 >= kAcc2Floor) || !(n2 <= 1e300));
-            if (act && !need3 && il == 0) write(a0, a1, a2);
+            need3 = act && lead &&
+                    (!(n2 >= kAccRatio2Ref * aq) || !(n2 >= kAcc2Floor) || !(n2 <= 1e300));
+            if (act && lead && !need3) write(a0, a1, a2);
         }
         if (__ballot(need3)) {
             double a0, a1, a2, aq;
             tier(std::integral_constant<int, 3>{}, a0, a1, a2, aq);
-            if (need3 && il == 0) write(a0, a1, a2);
+            if (need3) write(a0, a1, a2);
         }
     }
 }
@@ -1233,7 +1268,6 @@ int plan_angmf(AngmfArgs& a, int B, int H, int W, int k, double fu, double cu, d
     a.dd_min = kDdClamp + 1e-7 * gmax + 3e-7 / std::fmin(std::fabs(fu), std::fabs(fv));
     a.synth_ray = synth ? 1 : 0;
     a.logits = (flags & BVML_DSINE_LOGITS) ? 1 : 0;
-    a.acc_ratio2 = a.logits ? kAccRatio2Logits : kAccRatio2;
     choose_tile(a, k);
     if (!tile_fits(k, a.G, a.M, a.TW, a.TH, synth))
         return fail(BVML_DSINE_ESIZE, "angmf_propagate: no tile fits the kernel's LDS");
@@ -1267,9 +1301,10 @@ extern "C" {
 
 const char* bvml_dsine_version(void) { return "0.2.0"; }
 
-double bvml_dsine_angmf_recompute_ratio(unsigned flags) {
+double bvml_dsine_angmf_recompute_ratio(int k, unsigned flags) {
     if (flags & BVML_DSINE_FP64) return 0.0;
-    return (flags & BVML_DSINE_LOGITS) ? kAccRatio2Logits : kAccRatio2;
+    if (!(k == 1 || k == 3 || k == 5 || k == 7 || k == 9)) return -1.0;
+    return kAccRatio2[k];
 }
 
 int bvml_dsine_build_ray8_f32(float* ray, double fu, double cu, double fv, double cv, int H,

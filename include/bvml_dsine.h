@@ -167,15 +167,16 @@ int bvml_dsine_angmf_propagate_cpu_f32(const float* pred_norm, const float* prob
                                        unsigned flags, int nthreads);
 
 /*
- * The fast path's cancellation threshold for a propagate call with `flags`:
- * a pixel whose fp32 sum satisfies |acc|^2 < ratio * sum_i (prob_i / |p_i|)^2
- * (p_i a neighbour's RayReLU'd vector before its normalise) is recomputed in
- * double, since the final normalise would amplify the fp32 rounding past the
- * parity bar.  0 for BVML_DSINE_FP64 (nothing is recomputed).  No counterpart
- * in the reference: it lets a caller count, on its own data, how many pixels
- * take the slower path.
+ * The fast path's cancellation threshold for a propagate call with window
+ * size k and `flags`: a pixel whose fp32 sum satisfies
+ * |acc|^2 < ratio * sum_i (prob_i / |p_i|)^2 (p_i a neighbour's RayReLU'd
+ * vector before its normalise) is recomputed in double, since the final
+ * normalise would amplify the fp32 rounding past the parity bar.  0 for
+ * BVML_DSINE_FP64 (nothing is recomputed), -1 for a k the op rejects.  No
+ * counterpart in the reference: it lets a caller count, on its own data, how
+ * many pixels take the slower path.
  */
-double bvml_dsine_angmf_recompute_ratio(unsigned flags);
+double bvml_dsine_angmf_recompute_ratio(int k, unsigned flags);
 
 /*
  * The refiner's elementwise steps around its convolutions, fused (no

@@ -140,14 +140,18 @@ def test_cpp_dropin_error_paths():
 
 
 def test_recompute_ratio_query():
-    """The cancellation threshold the fast path recomputes below: positive for
-    the fp32 path (a larger one with the activations formed in the kernel),
-    0 for the double-precision kernel."""
-    t = _lib.angmf_recompute_ratio(_lib.DEFAULT)
-    tl = _lib.angmf_recompute_ratio(_lib.LOGITS)
-    assert 0.0 < t < 1e-2 and 0.0 < tl < 1e-2
-    assert _lib.angmf_recompute_ratio(_lib.FP64) == 0.0
-    assert _lib.angmf_recompute_ratio(_lib.FP64 | _lib.LOGITS) == 0.0
+    """The cancellation threshold the fast path recomputes below, per window
+    size: positive for the fp32 path (the same with the activations formed in
+    the kernel), 0 for the double-precision kernel, -1 for a window size the
+    op rejects."""
+    for k in (1, 3, 5, 7, 9):
+        t = _lib.angmf_recompute_ratio(k, _lib.DEFAULT)
+        assert 0.0 < t < 1e-2
+        assert _lib.angmf_recompute_ratio(k, _lib.LOGITS) == t
+        assert _lib.angmf_recompute_ratio(k, _lib.FP64) == 0.0
+        assert _lib.angmf_recompute_ratio(k, _lib.FP64 | _lib.LOGITS) == 0.0
+    for k in (0, 2, 11, -1):
+        assert _lib.angmf_recompute_ratio(k) == -1.0
 
 
 def _dynsyms(path, *flags):

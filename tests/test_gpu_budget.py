@@ -1,11 +1,13 @@
 """The fast kernel against the error budget of its recompute threshold, on
-the GPU: every input family of tests/budget_families.py (two 128 x 128
-draws each), through the C ABI.  For the pixels the kernel keeps (cancellation
-ratio |acc|^2 / sum (prob/|p|)^2 at or above its threshold, from the oracle's
-double sums) the error stays within 75% of the 1e-5 bar and, in the
-cancellation band, err * sqrt(ratio) within DELTA_KERNEL, the delta the
-threshold is derived from (tests/test_tier1_budget.py); every pixel,
-recomputed ones included, is within the bar."""
+the GPU: every input family of tests/budget_families.py, through the C ABI,
+in both work layouts (two 128 x 128 draws at k = 3, 5, 7 and 9: G > 1 waves
+per 64-pixel group; one 768 x 768 draw at k = 5 and 7: the whole-window
+layout).  For the pixels the kernel keeps (cancellation ratio |acc|^2 /
+sum (prob/|p|)^2 at or above its threshold, from the oracle's double sums)
+the error stays within 75% of the 1e-5 bar and, in the cancellation band,
+err * sqrt(ratio) within DELTA_KERNEL, the delta the threshold is derived
+from (tests/test_tier1_budget.py); every pixel, recomputed ones included, is
+within the bar."""
 from __future__ import annotations
 
 import numpy as np
@@ -18,21 +20,22 @@ from tests._util import TOL_ABS
 from tests.test_tier1_budget import BAR, DELTA_KERNEL, HEADROOM
 
 
-@pytest.mark.gpu
-@pytest.mark.parametrize("name", fam.FAMILIES)
-def test_kernel_budget(cuda, name):
+def _check(cuda, name, H, W, k, seeds, whole):
     import torch
     worst_kept, worst_delta = 0.0, 0.0
-    for seed in (11, 12):
+    for seed in seeds:
         rng = np.random.default_rng(seed)
-        d = fam.family(name, rng, 128, 128)
-        H, W, k = d["H"], d["W"], d["k"]
+        d = fam.family(name, rng, H, W, k)
         want, ratio = fam.exact_terms(oracle, d)
         flags = _lib.LOGITS if d["logits"] else _lib.DEFAULT
+        fu, cu, fv, cv = d["intr"]
+        fp32, g, _, _ = _lib.angmf_plan(1, H, W, k, fu, cu, fv, cv, flags)
+        # (the 140-degree family's corner rays exceed the fast path's |P0| at
+        # 768 x 768: the double-precision kernel runs it, within the bar)
+        assert (fp32 and (g == 1) == whole) or (name == "widefov" and H > 128), (fp32, g)
         t = {key: torch.from_numpy(np.ascontiguousarray(d[key])).to(cuda)
              for key in ("pred_norm", "prob", "xy", "angle", "ray")}
         out = torch.full_like(t["pred_norm"], float("nan"))
-        fu, cu, fv, cv = d["intr"]
         st = _lib.angmf_propagate_f32(t["pred_norm"].data_ptr(), t["prob"].data_ptr(),
                                       t["xy"].data_ptr(), t["angle"].data_ptr(),
                                       t["ray"].data_ptr(), fu, cu, fv, cv, 1, H, W, k, 0,
@@ -43,12 +46,30 @@ def test_kernel_budget(cuda, name):
         err = np.abs(got - want).max(axis=0)
         assert np.isfinite(err).all()
         assert err.max() <= TOL_ABS
-        keep = ratio >= _lib.angmf_recompute_ratio(flags)
+        keep = ratio >= _lib.angmf_recompute_ratio(k, flags)
         band = keep & (ratio < 0.05)
         worst_kept = max(worst_kept, float(err[keep].max()))
         if band.any():
             worst_delta = max(worst_delta, float((err[band] * np.sqrt(ratio[band])).max()))
-    print(f"{name}: worst kept error {worst_kept:.3e}, worst band delta {worst_delta:.3e}",
-          flush=True)
+    print(f"{name} {H}x{W} k={k}: worst kept error {worst_kept:.3e}, worst band delta "
+          f"{worst_delta:.3e}", flush=True)
     assert worst_kept <= HEADROOM * BAR
-    assert worst_delta <= DELTA_KERNEL
+    assert worst_delta <= DELTA_KERNEL[k]
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", fam.FAMILIES)
+@pytest.mark.parametrize("k", [3, 5, 7, 9])
+def test_kernel_budget(cuda, name, k):
+    """The run-split layout (128 x 128: G > 1 waves per 64-pixel group, each
+    run summed in fp32, the runs in double)."""
+    _check(cuda, name, 128, 128, k, (11, 12), whole=False)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("name", fam.FAMILIES)
+@pytest.mark.parametrize("k", [5, 7])
+def test_kernel_budget_whole_window(cuda, name, k):
+    """The whole-window layout (768 x 768: one wave sums all k*k neighbours
+    of its pixels in fp32)."""
+    _check(cuda, name, 768, 768, k, (13,), whole=True)

@@ -6,9 +6,14 @@ weights and decoder outputs (no checkpoint ships here).
 
 The device convolutions run in fp32, the restatement's in float64, so the
 heads' outputs differ by float rounding and the differences pass through five
-recurrent iterations: the bar here is 2e-5 per component on every
-iteration's propagated and up-sampled normals (the ops alone hold 1e-5 on
-identical inputs, tests/test_gpu_parity.py)."""
+recurrent iterations.  How much they differ depends on the convolution
+algorithm MIOpen picks, which can change with the process's history (the
+same forward measured 6.8e-6 on its own and 2.7e-5 after the rest of the GPU
+suite, at a pixel with no cancellation, while the propagate kernel alone is
+within 2.6e-7 of the oracle on those heads' outputs): the bar here is 1e-4
+per component on every iteration's propagated and up-sampled normals.  The
+ops alone hold 1e-5 on identical inputs (tests/test_gpu_parity.py), and the
+closed-form pins below, whose heads are exact, hold 1e-5 through the loop."""
 from __future__ import annotations
 
 import numpy as np
@@ -18,7 +23,7 @@ from brovisionml_amd import refiner as rf, workloads as wl
 from oracle import refiner as oref
 
 pytestmark = pytest.mark.gpu
-TOL = 2e-5
+TOL = 1e-4
 
 
 def say(msg: str) -> None:
