@@ -7,7 +7,8 @@ sum (prob/|p|)^2 at or above its threshold, from the oracle's double sums)
 the error stays within 75% of the 1e-5 bar and, in the cancellation band,
 err * sqrt(ratio) within DELTA_KERNEL, the delta the threshold is derived
 from (tests/test_tier1_budget.py); every pixel, recomputed ones included, is
-within the bar."""
+within the bar.  A hill-climbing search from each family toward the largest
+kept error (tests/budget_search.py) holds the same bounds."""
 from __future__ import annotations
 
 import numpy as np
@@ -73,3 +74,34 @@ def test_kernel_budget_whole_window(cuda, name, k):
     """The whole-window layout (768 x 768: one wave sums all k*k neighbours
     of its pixels in fp32)."""
     _check(cuda, name, 768, 768, k, (13,), whole=True)
+
+
+@pytest.mark.gpu
+@pytest.mark.parametrize("H,W,k,steps", [(64, 64, 3, 30), (64, 64, 5, 30), (64, 64, 7, 30),
+                                         (64, 64, 9, 20), (768, 768, 5, 5), (768, 768, 7, 4)])
+def test_kernel_adversarial_search(cuda, H, W, k, steps):
+    """A hill-climbing search (tests/budget_search.py) over the kernel's own
+    inputs, from each family that stresses a mechanism, toward the largest
+    error of a pixel the kernel keeps in fp32 (64 x 64: the run-split layout;
+    768 x 768: the whole-window layout): the worst found stays 25% inside the
+    bar, and the climbed inputs' cancellation-band delta within DELTA_KERNEL."""
+    from tests import budget_search as bs
+    t = _lib.angmf_recompute_ratio(k)
+    evaluate = bs.kernel_evaluator(oracle, _lib, cuda, t)
+    worst, worst_delta = 0.0, 0.0
+    for name in bs.SEEDS:
+        if name == "widefov" and H > 128:
+            continue   # the double-precision kernel runs it at this size
+        rng = np.random.default_rng(7)
+        d = fam.family(name, rng, H, W, k)
+        score, climbed = bs.climb(evaluate, d, steps, rng)
+        evaluate(climbed)
+        err, ratio = evaluate.last
+        band = (ratio >= t) & (ratio < 0.05)
+        worst = max(worst, float(score.max()))
+        if band.any():
+            worst_delta = max(worst_delta, float((err[band] * np.sqrt(ratio[band])).max()))
+    print(f"{H}x{W} k={k}: worst kept error found {worst:.3e}, band delta {worst_delta:.3e}",
+          flush=True)
+    assert 0.0 < worst <= HEADROOM * BAR
+    assert worst_delta <= DELTA_KERNEL[k]

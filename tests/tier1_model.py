@@ -103,15 +103,34 @@ def runs(K2: int, G: int):
     return out
 
 
+def dd_min(intr, H, W) -> float:
+    """The fast kernel's |dd| floor for an H x W image (plan_angmf in
+    brovisionml_amd/csrc/dsine_ops.hip): the reference's clamp plus dd's
+    error bound, from the largest |P0| over the image's corners times the
+    largest accepted |m|."""
+    fu, cu, fv, cv = intr
+    gmax = 0.0
+    for cy in (0, H - 1):
+        for cx in (0, W - 1):
+            tu, tv = (cx + 0.5 - cu) / fu, (cy + 0.5 - cv) / fv
+            gmax = max(gmax, np.sqrt(1.0 + tu * tu + tv * tv))
+    gmax *= np.sqrt(1.0 + 1e-5)
+    return 1.02e-8 + 1e-7 * gmax + 3e-7 / min(abs(fu), abs(fv))
+
+
 def tier1(pred_norm, prob, xy, angle, ray, intr, H, W, k, rng, logits=False, G=4,
-          q_double=True):
+          q_double=True, flags=None):
     """One sample: planes as the op takes them (with logits, prob and angle
     hold the heads' raw logits and the kernel applies sigmoid and
     sigmoid * pi itself).  Returns the pixel outputs (3, HW) float64
     (normalised in double, as phase B does), |acc|^2 and sum(wi^2) per pixel.
     The window is split into G runs as the kernel splits it, each run's sums
     in fp32, the runs' partials summed in double.  q_double=False forms q in
-    fp32 instead (a planted weakness the budget test must detect)."""
+    fp32 instead (a planted weakness the budget test must detect).  flags,
+    when given (a bool array of HW), receives the pixels the kernel sends to
+    the recompute for a neighbour outside the fp32 form's domain: |xy|^2
+    outside [1e-20, 1e30], |t| > 3.2, |dd| < dd_min, |V x m'|^2 < 1e-30, or a
+    non-finite value in any of them."""
     fu, cu, fv, cv = intr
     HW, K2, P = H * W, k * k, k // 2
     pn = np.asarray(pred_norm, f32).reshape(3, H, W)
@@ -126,6 +145,8 @@ def tier1(pred_norm, prob, xy, angle, ray, intr, H, W, k, rng, logits=False, G=4
     ir = np.where(r2 < f32(1e-16), f32(1e8), ir1)
     nhx, nhy, nhz = (f32(-0.5) * (c * ir) for c in (rx, ry, rz))
     r2x, r2y, r2z = (f32(2.0) * c for c in (rx, ry, rz))
+    ddf = f32(dd_min(intr, H, W))
+    bad = np.zeros(HW, bool)
     acc = np.zeros((3, HW))
     qs = np.zeros(HW)
     for a, b in runs(K2, G):
@@ -167,6 +188,9 @@ def tier1(pred_norm, prob, xy, angle, ray, intr, H, W, k, rng, logits=False, G=4
             cy = fma(xs, e1y, -(q * fy))
             cz = fma(xs, e1z, fma(ys, e2z, -(q * fz)))
             n2 = fma(cx, cx, fma(cy, cy, cz * cz))
+            with np.errstate(invalid="ignore"):
+                bad |= ~((s >= f32(1e-20)) & (s <= f32(1e30)) & (np.abs(t) <= f32(3.2))
+                         & (np.abs(dd) >= ddf) & (n2 >= f32(1e-30)))
             st, ct = sincos(t, rng)
             S = st * np.copysign(rsq(n2, rng), dd)
             vx = fma(cx, S, mpx * ct)
@@ -187,4 +211,6 @@ def tier1(pred_norm, prob, xy, angle, ray, intr, H, W, k, rng, logits=False, G=4
         qs += pq.astype(f64)
     a2 = (acc ** 2).sum(axis=0)
     out = acc / np.sqrt(np.maximum(a2, 1e-300))
+    if flags is not None:
+        flags[...] = bad
     return out, a2, qs
