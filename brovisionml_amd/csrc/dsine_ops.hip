@@ -862,10 +862,11 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     if (r != 0) return;
     bool flag = false;
     if (valid) {
-        double s0 = 0.0, s1 = 0.0, s2 = 0.0, sw = 0.0;
+        const float4 t0 = (G > 1) ? part[j] : mine;
+        double s0 = t0.x, s1 = t0.y, s2 = t0.z, sw = t0.w;
 #pragma unroll
-        for (int rr = 0; rr < G; ++rr) {
-            const float4 t = (G > 1) ? part[rr * npx + j] : mine;
+        for (int rr = 1; rr < G; ++rr) {
+            const float4 t = part[rr * npx + j];
             s0 += t.x;
             s1 += t.y;
             s2 += t.z;
