@@ -74,10 +74,11 @@ def climb(evaluate, d: dict, steps: int, rng: np.random.Generator, step: float =
     return score, d
 
 
-def model_evaluator(oracle, model, threshold: float, rng_seed: int = 0):
-    """The CPU model's error per pixel, on the pixels the kernel would keep
-    in fp32 (not flagged by domain, ratio at or above `threshold`), 0
-    elsewhere.  Every hardware function sits at its error bound with a fixed
+def model_evaluator(oracle, model, lib, threshold: float, rng_seed: int = 0):
+    """The CPU model's error per pixel (the runs summed as the kernel's
+    launch plan splits them; lib is brovisionml_amd._lib), on the pixels the
+    kernel would keep in fp32 (not flagged by domain, ratio at or above
+    `threshold`), 0 elsewhere.  Every hardware function sits at its error bound with a fixed
     random sign pattern, so the score is a deterministic function of the
     inputs.  Also returns, through .last, the last call's (err, ratio,
     flags)."""
@@ -86,7 +87,7 @@ def model_evaluator(oracle, model, threshold: float, rng_seed: int = 0):
         flags = np.zeros(H * W, bool)
         out, _, _ = model.tier1(d["pred_norm"], d["prob"], d["xy"], d["angle"], d["ray"],
                                 d["intr"], H, W, k, np.random.default_rng(rng_seed),
-                                logits=d["logits"], flags=flags)
+                                logits=d["logits"], flags=flags, G=model.kernel_waves(lib, d))
         want, ratio = fam.exact_terms(oracle, d)
         err = np.abs(out.astype(np.float32).astype(np.float64) - want).max(axis=0)
         evaluate.last = (err, ratio, flags)

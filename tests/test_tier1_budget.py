@@ -44,6 +44,7 @@ HEADROOM = 0.75
 def run_model(name: str, seed: int, H: int = 48, W: int = 48, **kw):
     rng = np.random.default_rng(seed)
     d = fam.family(name, rng, H, W)
+    kw.setdefault("G", model.kernel_waves(_lib, d))
     out, _, _ = model.tier1(d["pred_norm"], d["prob"], d["xy"], d["angle"], d["ray"], d["intr"],
                             d["H"], d["W"], d["k"], rng, logits=d["logits"], **kw)
     want, ratio = fam.exact_terms(oracle, d)
@@ -131,7 +132,7 @@ def test_model_adversarial_search(k):
     import oracle
     from tests import budget_search as bs
     t = _lib.angmf_recompute_ratio(k)
-    evaluate = bs.model_evaluator(oracle, model, t)
+    evaluate = bs.model_evaluator(oracle, model, _lib, t)
     worst = 0.0
     for name in bs.SEEDS:
         rng = np.random.default_rng(7)

@@ -103,6 +103,15 @@ def runs(K2: int, G: int):
     return out
 
 
+def kernel_waves(lib, d: dict) -> int:
+    """The waves per 64-pixel group the kernel's launch plan takes for draw d
+    (lib is brovisionml_amd._lib): the G of its run split, so the model sums
+    the runs as that launch does."""
+    fu, cu, fv, cv = d["intr"]
+    flags = lib.LOGITS if d["logits"] else lib.DEFAULT
+    return lib.angmf_plan(1, d["H"], d["W"], d["k"], fu, cu, fv, cv, flags)[1]
+
+
 def dd_min(intr, H, W) -> float:
     """The fast kernel's |dd| floor for an H x W image (plan_angmf in
     brovisionml_amd/csrc/dsine_ops.hip): the reference's clamp plus dd's
