@@ -1108,6 +1108,15 @@ auto angmf_f32_for(bool synth_ray, bool logits) {
 constexpr int kGChoices[10][2] = {{0, 0}, {1, 1}, {0, 0}, {2, 2}, {0, 0},
                                   {4, 2}, {0, 0}, {4, 8}, {0, 0}, {4, 8}};
 
+// A G with more waves per group for launches that leave CUs idle (fewer
+// workgroups than CUs with the first choice): the shorter runs shorten each
+// wave's dependent chain, which is what such a launch waits on.  k = 5 at
+// 60 x 80: 4.47 against 5.19 us; 96 x 96: 4.53 against 5.30; 128 x 128: 4.06
+// against 4.96; k = 3 at 60 x 80: 5.11 against 5.72; 128 x 128: 5.44 against
+// 6.37 (at 256 x 256, 256 workgroups with G = 2, G = 4 is slower).
+constexpr int kGSmall[10] = {0, 0, 0, 4, 0, 8, 0, 0, 0, 0};
+constexpr long long kIdleGrid = 256;
+
 // Window sizes with a whole-window variant (G = 1: each wave evaluates all
 // k*k neighbours of its 64 pixels in a rolled loop, LA at a time, and writes
 // them itself; 64 x 8 tiles, no cross-wave reduction).  A launch of at least
@@ -1135,6 +1144,9 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
     constexpr int G0 = kGChoices[K][0], G1 = kGChoices[K][1];
     auto kern = (a.G == G0) ? angmf_f32_for<K, G0>(a.synth_ray != 0, a.logits != 0)
                             : angmf_f32_for<K, G1>(a.synth_ray != 0, a.logits != 0);
+    if constexpr (kGSmall[K] != 0) {
+        if (a.G == kGSmall[K]) kern = angmf_f32_for<K, kGSmall[K]>(a.synth_ray != 0, a.logits != 0);
+    }
     if constexpr (kWholeWindowOk[K]) {
         if (a.G == 1) kern = angmf_f32_for<K, 1>(a.synth_ray != 0, a.logits != 0);
     }
@@ -1231,19 +1243,25 @@ void choose_tile(AngmfArgs& a, int K) {
     }
     AngmfArgs alt = a;
     const double u0 = tile_for(a, K, kGChoices[K][0]);
-    if (kGChoices[K][1] == kGChoices[K][0]) return;
-    const double u1 = tile_for(alt, K, kGChoices[K][1]);
-    if (u1 <= 0.0) return;
-    if (u0 <= 0.0) {
-        a = alt;
-        return;
+    const long long w0 = wgs(a);
+    if (kGChoices[K][1] != kGChoices[K][0]) {
+        const double u1 = tile_for(alt, K, kGChoices[K][1]);
+        if (u1 > 0.0) {
+            const long long w1 = wgs(alt);
+            if (u0 <= 0.0)
+                a = alt;
+            else if (w0 < kSmallGrid || w1 < kSmallGrid)
+                a = (w1 > w0) ? alt : a;
+            else if (u1 > u0 + 1e-9)
+                a = alt;
+        }
     }
-    const long long w0 = wgs(a), w1 = wgs(alt);
-    if (w0 < kSmallGrid || w1 < kSmallGrid) {
-        if (w1 > w0) a = alt;
-        return;
+    // a launch the first choice leaves with idle CUs takes kGSmall's G when
+    // that gives it more workgroups
+    if (kGSmall[K] != 0 && u0 > 0.0 && w0 < kIdleGrid) {
+        AngmfArgs sm = a;
+        if (tile_for(sm, K, kGSmall[K]) > 0.0 && wgs(sm) > wgs(a)) a = sm;
     }
-    if (u1 > u0 + 1e-9) a = alt;
 }
 
 // The launch plan of one call: the kernel arguments that depend on the

@@ -197,9 +197,10 @@ def _intr(H, W):
 
 def test_plan_of_the_workloads():
     """The launch plan per workload (host logic only): run-split kernels on
-    the small images, the whole-window kernel on 4 x 512 x 512 at k = 7."""
+    the small images (8 waves per group where 4 would leave CUs idle), the
+    whole-window kernel on 4 x 512 x 512 at k = 7."""
     from brovisionml_amd import workloads as wl
-    want = {0: (True, 4, 80, 1), 1: (True, 4, 128, 1), 2: (True, 4, 64, 2), 3: (True, 2, 80, 3),
+    want = {0: (True, 8, 64, 1), 1: (True, 8, 64, 1), 2: (True, 4, 64, 2), 3: (True, 2, 80, 3),
             4: (True, 1, 64, 8)}
     for w in wl.WORKLOADS:
         _, intr = w.intrinsics()
@@ -213,12 +214,18 @@ def test_plan_of_the_workloads():
         _lib.angmf_plan(1, 4, 4, 5, 1.0, 2.0, 1.0, 2.0, flags=64)
 
 
+# Every (k, waves per group) the fp32 kernel is instantiated for
+# (kGChoices, kGSmall and kWholeWindowOk in brovisionml_amd/csrc/dsine_ops.hip).
+KERNEL_LAYOUTS = {(1, 1), (3, 2), (3, 4), (5, 1), (5, 2), (5, 4), (5, 8), (7, 1), (7, 4), (7, 8),
+                  (9, 4), (9, 8)}
+
+
 def test_gpu_parity_shapes_cover_every_kernel_layout():
-    """The GPU parity shapes reach every waves-per-group layout of the fp32
-    kernel (1: whole window; 2, 4, 8: runs) and its whole-window variant
-    with logits and rays from the intrinsics."""
+    """The GPU parity shapes reach every instantiated (k, waves per group)
+    layout of the fp32 kernel (1: whole window; 2, 4, 8: runs) and its
+    whole-window variant with logits and rays from the intrinsics."""
     from tests.test_gpu_parity import SHAPES
-    gs = {_lib.angmf_plan(B, H, W, k, *_intr(H, W))[1] for B, H, W, k in SHAPES}
-    assert {1, 2, 4, 8} <= gs
+    got = {(k, _lib.angmf_plan(B, H, W, k, *_intr(H, W))[1]) for B, H, W, k in SHAPES}
+    assert got == KERNEL_LAYOUTS, (KERNEL_LAYOUTS - got, got - KERNEL_LAYOUTS)
     flags = _lib.LOGITS | _lib.RAY_FROM_INTRINSICS
     assert _lib.angmf_plan(2, 512, 512, 5, *_intr(512, 512), flags=flags)[1] == 1
