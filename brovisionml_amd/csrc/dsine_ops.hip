@@ -1119,14 +1119,20 @@ constexpr long long kIdleGrid = 256;
 
 // Window sizes with a whole-window variant (G = 1: each wave evaluates all
 // k*k neighbours of its 64 pixels in a rolled loop, LA at a time, and writes
-// them itself; 64 x 8 tiles, no cross-wave reduction).  A launch of at least
-// kLargeGrid such workgroups takes it: on large images its HBM stream runs
-// faster (fewer halo records per pixel, one barrier per workgroup, fewer
-// loads in flight per lane).  k = 9's 64 x 8 halo exceeds two records per
-// thread.
+// them itself; 64 x 8 tiles, no cross-wave reduction).  A launch that fills
+// the chip's kWholeWindowSlots resident workgroups (two per CU) at least
+// once, and its last round at least kRoundFill of the way, takes it: its HBM
+// stream runs faster (fewer halo records per pixel, one barrier per
+// workgroup, fewer loads in flight per lane).  Measured against the
+// run-split kernel: 512 x 512 at k = 5, 23.4 against 27.7 us; at k = 7, 39.3
+// against 46.4; 4 x 256 x 256, 23.7 against 26.8; 600 x 800 (1.46 rounds),
+// 42.8 against 48.9; 1030 x 512 (2.02 rounds), 51.9 against 52.9; but
+// 2 x 384 x 384 (1.13 rounds), 31.5 against 30.1.  k = 9's 64 x 8 halo
+// exceeds two records per thread.
 constexpr bool kWholeWindowOk[10] = {false, false, false, false, false,
                                      true,  false, true,  false, false};
-constexpr long long kLargeGrid = 1024;
+constexpr long long kWholeWindowSlots = 512;
+constexpr double kRoundFill = 0.6;
 
 template <int K>
 hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
@@ -1224,10 +1230,10 @@ double tile_for(AngmfArgs& a, int K, int G) {
 // Workgroups below which a launch is latency-bound: two per CU.
 constexpr long long kSmallGrid = 512;
 
-// G and the tile.  A launch that fills at least kLargeGrid whole-window
-// workgroups, with at least 90% of their lanes holding a pixel, takes G = 1.
-// Otherwise, of the two run-split candidates, a launch of fewer than
-// kSmallGrid workgroups takes the one with more of them (its runs are
+// G and the tile.  A launch that fills the resident whole-window workgroups
+// as kWholeWindowOk's note says, with at least 90% of their lanes holding a
+// pixel, takes G = 1.  Otherwise, of the two run-split candidates, a launch of
+// fewer than kSmallGrid workgroups takes the one with more of them (its runs are
 // shorter, so its waves finish sooner); a larger one the one with the most
 // lanes holding a pixel, the preferred G on ties.
 void choose_tile(AngmfArgs& a, int K) {
@@ -1236,7 +1242,11 @@ void choose_tile(AngmfArgs& a, int K) {
     };
     if (kWholeWindowOk[K] && (long long)K * K * a.HW * 4 < (1LL << 32)) {
         AngmfArgs one = a;
-        if (tile_for(one, K, 1) >= 0.9 && wgs(one) >= kLargeGrid) {
+        const double util = tile_for(one, K, 1);
+        const long long n = util > 0.0 ? wgs(one) : 0;
+        const long long rounds = (n + kWholeWindowSlots - 1) / kWholeWindowSlots;
+        if (util >= 0.9 && n >= kWholeWindowSlots &&
+            (double)n >= kRoundFill * (double)(rounds * kWholeWindowSlots)) {
             a = one;
             return;
         }

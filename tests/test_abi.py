@@ -214,6 +214,20 @@ def test_plan_of_the_workloads():
         _lib.angmf_plan(1, 4, 4, 5, 1.0, 2.0, 1.0, 2.0, flags=64)
 
 
+def test_plan_layout_rules():
+    """The layout choice (host logic only): the whole-window kernel once a
+    launch fills the resident whole-window workgroups (512: two per CU) and
+    its last round at least 60% of the way; more waves per group when the
+    first choice leaves CUs idle (fewer than 256 workgroups); at k = 9 a
+    64-wide tile's halo needs the 8 waves' threads to stage it."""
+    cases = {(1, 512, 512, 5): 1, (4, 256, 256, 5): 1, (1, 1030, 512, 5): 1,
+             (1, 512, 512, 7): 1, (2, 384, 384, 5): 4, (3, 256, 256, 5): 4,
+             (1, 256, 256, 5): 4, (1, 96, 96, 5): 8, (1, 200, 200, 5): 4,
+             (1, 128, 128, 3): 4, (1, 256, 256, 3): 2, (1, 512, 512, 9): 8}
+    for (B, H, W, k), g in cases.items():
+        assert _lib.angmf_plan(B, H, W, k, *_intr(H, W))[1] == g, (B, H, W, k)
+
+
 # Every (k, waves per group) the fp32 kernel is instantiated for
 # (kGChoices, kGSmall and kWholeWindowOk in brovisionml_amd/csrc/dsine_ops.hip).
 KERNEL_LAYOUTS = {(1, 1), (3, 2), (3, 4), (5, 1), (5, 2), (5, 4), (5, 8), (7, 1), (7, 4), (7, 8),
