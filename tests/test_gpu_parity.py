@@ -280,7 +280,7 @@ def test_angmf_recompute_tiers(cuda, far_angles):
     inp["angle"] = rng.normal(0.0, 1e-3, inp["angle"].shape).astype(np.float32)
     if far_angles:
         inp["angle"][0, 0] = 5.0  # slot 0 has prob 0
-    n_cancel = _cancel_count(inp, H, W, k, 1.6e-3)
+    n_cancel = _cancel_count(inp, H, W, k, _lib.angmf_recompute_ratio(k))
     say(f"    pixels below the fast path's cancellation threshold: >= {n_cancel}")
     assert n_cancel >= 2 * H
     got = run_gpu(inp, H, W, cuda)
