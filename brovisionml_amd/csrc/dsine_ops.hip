@@ -44,6 +44,7 @@
 
 #include <hip/hip_runtime.h>
 
+#include <atomic>
 #include <climits>
 #include <cmath>
 #include <cstdint>
@@ -1134,6 +1135,45 @@ constexpr bool kWholeWindowOk[10] = {false, false, false, false, false,
 constexpr long long kWholeWindowSlots = 512;
 constexpr double kRoundFill = 0.6;
 
+// LDS one workgroup may use: 64 KB for the run-split kernels (G > 1), so
+// that two to three of them share a CU; the whole-window kernel's 64 x 8
+// tiles take up to 80 KB, two per CU (gfx950 has 160 KB per CU and allows it
+// all to one workgroup).
+constexpr int kMaxLdsBytes = 65536;
+constexpr int kMaxLdsBytesG1 = 81920;
+
+// A kernel whose workgroups take more than 64 KB of LDS must be granted it
+// (hipFuncSetAttribute) on each device before its launch.  The grant is made
+// once per kernel and device (kMaxLdsBytesG1, every whole-window tile's
+// ceiling) and remembered here, so that launches after the first make no
+// runtime call for it.
+struct LdsGrant {
+    std::atomic<const void*> fn{nullptr};
+    std::atomic<unsigned long long> devices{0};  // bit d: granted on device d (< 64)
+};
+LdsGrant g_lds_grants[32];
+
+hipError_t grant_lds(const void* fn) {
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return e;
+    const unsigned long long bit = (dev >= 0 && dev < 64) ? (1ull << dev) : 0ull;
+    for (LdsGrant& g : g_lds_grants) {
+        const void* cur = g.fn.load(std::memory_order_acquire);
+        if (cur == nullptr) {
+            const void* none = nullptr;
+            cur = g.fn.compare_exchange_strong(none, fn, std::memory_order_acq_rel) ? fn : none;
+        }
+        if (cur != fn) continue;
+        if (bit != 0 && (g.devices.load(std::memory_order_acquire) & bit) != 0) return hipSuccess;
+        e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLdsBytesG1);
+        if (e == hipSuccess) g.devices.fetch_or(bit, std::memory_order_acq_rel);
+        return e;
+    }
+    // (more kernels than slots: grant on every launch)
+    return hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, kMaxLdsBytesG1);
+}
+
 template <int K>
 hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
     if (fp64) {
@@ -1158,9 +1198,7 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
     }
     // workgroups past 64 KB of LDS (the whole-window tiles) ask for it
     if (lds > 65536) {
-        const hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(kern),
-                                                 hipFuncAttributeMaxDynamicSharedMemorySize,
-                                                 (int)lds);
+        const hipError_t e = grant_lds(reinterpret_cast<const void*>(kern));
         if (e != hipSuccess) return e;
     }
     // one launch per kMaxGridY samples (grid y = sample)
@@ -1182,13 +1220,6 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
     }
     return hipSuccess;
 }
-
-// LDS one workgroup may use: 64 KB for the run-split kernels (G > 1), so
-// that two to three of them share a CU; the whole-window kernel's 64 x 8
-// tiles take up to 80 KB, two per CU (gfx950 has 160 KB per CU and allows it
-// all to one workgroup).
-constexpr int kMaxLdsBytes = 65536;
-constexpr int kMaxLdsBytesG1 = 81920;
 
 // Whether a TW x TH tile of M groups of G waves fits the kernel: its LDS, and
 // at most two halo records per thread.
