@@ -36,9 +36,11 @@
 //     the sum still nearly cancels.  The wave that reduces a pixel group
 //     recomputes its flagged pixels by itself, one neighbour per lane.
 // Workgroups are 8 waves: G waves per 64-pixel group, each evaluating one run
-// of the window's neighbours (G = 4 or 2 at k=5, 4 at k = 7, 9), so the SPI
+// of the window's neighbours (G = 2, 4 or 8, chosen per launch), so the SPI
 // places 2 waves per SIMD and every SIMD carries the same work; two
-// workgroups per CU run a 256x256 image in one round.
+// workgroups per CU run a 256x256 image in one round.  Launches that fill the
+// chip take G = 1 at k = 5 and 7: each wave evaluates the whole window for its
+// pixels, with no cross-wave reduction.
 // The double-precision body is also available as its own kernel
 // (BVML_DSINE_FP64), which reproduces the CPU reference to a few ulps.
 
@@ -1100,8 +1102,8 @@ auto angmf_f32_for(bool synth_ray, bool logits) {
 }
 
 // Candidate G values per window size, in order of preference (the first
-// wins ties in lane utilisation).  Runs longer than kLookahead neighbours
-// keep only kLookahead of them in flight.
+// wins ties in lane utilisation).  Runs longer than lookahead(K, G)
+// neighbours keep only that many of them in flight.
 //   K = 5: 4 (runs of 6-7) on wide images; 2 (runs of 12-13) gives narrow
 //          images (W = 60, 80) full-width tiles of 3-4 rows with few idle lanes
 //   K = 7, 9: 4 (runs of 12-13 / 20-21; 64 x 2 tiles halve the halo per pixel
