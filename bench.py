@@ -97,15 +97,15 @@ def traffic_from_profile(op: str, name: str):
 def angmf_kernel_name(w, flags) -> str:
     """The fp32 kernel instantiation a launch of workload w runs, spelled as
     rocprofv3 prints it: angmf_f32_kernel<k, waves per group, rays from the
-    intrinsics, logits>."""
+    intrinsics, logits, non-temporal plane loads>."""
     from brovisionml_amd import _lib
     _, intr = w.intrinsics()
-    fp32, g, _, _ = _lib.angmf_plan(w.B, w.H, w.W, w.k, *intr, flags=flags)
+    fp32, g, _, _, nt = _lib.angmf_plan_full(w.B, w.H, w.W, w.k, *intr, flags=flags)
     if not fp32:
         return f"angmf_f64_kernel<{w.k}>"
-    sr = "true" if flags & _lib.RAY_FROM_INTRINSICS else "false"
-    lg = "true" if flags & _lib.LOGITS else "false"
-    return f"angmf_f32_kernel<{w.k}, {g}, {sr}, {lg}>"
+    tf = lambda b: "true" if b else "false"
+    return (f"angmf_f32_kernel<{w.k}, {g}, {tf(flags & _lib.RAY_FROM_INTRINSICS)}, "
+            f"{tf(flags & _lib.LOGITS)}, {tf(nt)}>")
 
 
 def timed_cpu(fn, seconds: float):

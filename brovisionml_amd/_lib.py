@@ -68,7 +68,7 @@ def load(path: str = LIB) -> ctypes.CDLL:
                                                    u, vp]
     lib.bvml_dsine_convex_upsample_f32.restype = i
     ip = ctypes.POINTER(ctypes.c_int)
-    lib.bvml_dsine_angmf_plan.argtypes = [i, i, i, i, d, d, d, d, u, ip, ip, ip]
+    lib.bvml_dsine_angmf_plan.argtypes = [i, i, i, i, d, d, d, d, u, ip, ip, ip, ip]
     lib.bvml_dsine_angmf_plan.restype = i
     lib.bvml_dsine_angmf_recompute_ratio.argtypes = [i, u]
     lib.bvml_dsine_angmf_recompute_ratio.restype = d
@@ -148,17 +148,25 @@ def angmf_propagate_cpu_f32(pred_norm: int, prob: int, xy: int, angle: int, ray:
         nthreads)
 
 
+def angmf_plan_full(B: int, H: int, W: int, k: int, fu: float, cu: float, fv: float,
+                    cv: float, flags: int = DEFAULT):
+    """(fp32 kernel?, waves per 64-pixel group, tile width, tile height,
+    non-temporal plane loads?) of the launch bvml_dsine_angmf_propagate_f32
+    makes for these arguments; raises on a rejected argument."""
+    g, tw, th, nt = ctypes.c_int(), ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
+    st = load().bvml_dsine_angmf_plan(B, H, W, k, fu, cu, fv, cv, flags, ctypes.byref(g),
+                                      ctypes.byref(tw), ctypes.byref(th), ctypes.byref(nt))
+    if st < 0:
+        raise RuntimeError(f"angmf_plan: {last_error()} (status {st})")
+    return bool(st), g.value, tw.value, th.value, bool(nt.value)
+
+
 def angmf_plan(B: int, H: int, W: int, k: int, fu: float, cu: float, fv: float, cv: float,
                flags: int = DEFAULT):
     """(fp32 kernel?, waves per 64-pixel group, tile width, tile height) of the
     launch bvml_dsine_angmf_propagate_f32 makes for these arguments; raises
     on a rejected argument."""
-    g, tw, th = ctypes.c_int(), ctypes.c_int(), ctypes.c_int()
-    st = load().bvml_dsine_angmf_plan(B, H, W, k, fu, cu, fv, cv, flags, ctypes.byref(g),
-                                      ctypes.byref(tw), ctypes.byref(th))
-    if st < 0:
-        raise RuntimeError(f"angmf_plan: {last_error()} (status {st})")
-    return bool(st), g.value, tw.value, th.value
+    return angmf_plan_full(B, H, W, k, fu, cu, fv, cv, flags)[:4]
 
 
 def gru_gates_f32(zr: int, bias_z: int, bias_r: int, h: int, C: int, HW: int, z: int, rh: int,

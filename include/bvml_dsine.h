@@ -103,12 +103,14 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
  * runs the double-precision kernel, or a negative BVML_DSINE_E* status.
  * *waves_per_group receives the waves that share one 64-pixel group (1: each
  * wave evaluates the whole window; 2, 4, 8: the window's neighbours split
- * into runs), *tile_w and *tile_h the workgroup's tile; any of the three may
- * be NULL.  No counterpart in the reference: for tests and tuning.
+ * into runs), *tile_w and *tile_h the workgroup's tile, *stream_planes 1
+ * when the launch reads its neighbour planes with the non-temporal cache
+ * policy (a whole-window launch larger than the Infinity Cache); any of the
+ * four may be NULL.  No counterpart in the reference: for tests and tuning.
  */
 int bvml_dsine_angmf_plan(int B, int H, int W, int k, double fu, double cu, double fv,
                           double cv, unsigned flags, int* waves_per_group, int* tile_w,
-                          int* tile_h);
+                          int* tile_h, int* stream_planes);
 
 /*
  * The /8-grid ray map, 3 x H x W fp32 planes, as the reference's build_ray8

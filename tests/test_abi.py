@@ -226,6 +226,11 @@ def test_plan_layout_rules():
              (1, 128, 128, 3): 4, (1, 256, 256, 3): 2, (1, 512, 512, 9): 8}
     for (B, H, W, k), g in cases.items():
         assert _lib.angmf_plan(B, H, W, k, *_intr(H, W))[1] == g, (B, H, W, k)
+    # non-temporal plane loads: whole-window launches past the 256 MB cache
+    assert _lib.angmf_plan_full(4, 512, 512, 7, *_intr(512, 512))[4] is True
+    assert _lib.angmf_plan_full(1, 800, 800, 5, *_intr(800, 800))[4] is True
+    assert _lib.angmf_plan_full(2, 512, 512, 5, *_intr(512, 512))[4] is False
+    assert _lib.angmf_plan_full(1, 256, 256, 5, *_intr(256, 256))[4] is False
 
 
 # Every (k, waves per group) the fp32 kernel is instantiated for
@@ -241,5 +246,9 @@ def test_gpu_parity_shapes_cover_every_kernel_layout():
     from tests.test_gpu_parity import SHAPES
     got = {(k, _lib.angmf_plan(B, H, W, k, *_intr(H, W))[1]) for B, H, W, k in SHAPES}
     assert got == KERNEL_LAYOUTS, (KERNEL_LAYOUTS - got, got - KERNEL_LAYOUTS)
+    # the whole-window kernels with and without non-temporal plane loads
+    whole = {(k, _lib.angmf_plan_full(B, H, W, k, *_intr(H, W))[4]) for B, H, W, k in SHAPES
+             if k in (5, 7) and _lib.angmf_plan(B, H, W, k, *_intr(H, W))[1] == 1}
+    assert whole == {(5, False), (5, True), (7, True)}, whole
     flags = _lib.LOGITS | _lib.RAY_FROM_INTRINSICS
     assert _lib.angmf_plan(2, 512, 512, 5, *_intr(512, 512), flags=flags)[1] == 1
