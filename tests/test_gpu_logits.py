@@ -137,12 +137,13 @@ def _random_logit_inputs(seed, B, H, W, k):
 
 @pytest.mark.parametrize("B,H,W,k", [(2, 9, 13, 1), (1, 33, 65, 3), (1, 20, 140, 5),
                                      (2, 17, 70, 7), (1, 12, 20, 9), (1, 6, 100, 9),
-                                     (2, 512, 512, 5), (3, 500, 333, 7)])
+                                     (2, 512, 512, 5), (3, 500, 333, 7), (1, 800, 800, 5)])
 def test_logits_window_sizes(cuda, B, H, W, k):
     """Every window size's logits kernel (the workloads above are all k = 5):
     random logits N(0, 2^2) for prob and angle, so the activated angles
-    span (0, pi), on narrow and wide tiles and (the last two) the
-    whole-window kernel."""
+    span (0, pi), on narrow and wide tiles and (the last three) the
+    whole-window kernel, with non-temporal plane loads at 3 x 500 x 333 and
+    800 x 800."""
     say(f"[gpu] angmf logits shape B={B} H={H} W={W} k={k}")
     inp, lp, la = _random_logit_inputs(700, B, H, W, k)
     got, want = run(inp, lp, la, H, W, k, cuda)
@@ -152,7 +153,8 @@ def test_logits_window_sizes(cuda, B, H, W, k):
     assert max_abs <= TOL_ABS and max_deg <= TOL_DEG
 
 
-@pytest.mark.parametrize("B,H,W,k", [(1, 20, 200, 5), (2, 9, 13, 7), (2, 512, 512, 5)])
+@pytest.mark.parametrize("B,H,W,k", [(1, 20, 200, 5), (2, 9, 13, 7), (2, 512, 512, 5),
+                                     (1, 800, 800, 5)])
 @pytest.mark.parametrize("precise", [False, True])
 def test_logits_ray_from_intrinsics(cuda, B, H, W, k, precise):
     """Logits with the ray formed in the kernel (BVML_DSINE_LOGITS |

@@ -53,10 +53,10 @@ def _run(inp, H, W, device, ray, precise):
 
 
 # wide and narrow tiles, k = 3, 5, 7, a batch, the whole-window kernel
-# (2 x 512 x 512, k = 5); flagged pixels (zero xy pairs, large angles) take
-# the reference-order recompute
+# (2 x 512 x 512, k = 5; 800 x 800 with non-temporal plane loads); flagged
+# pixels (zero xy pairs, large angles) take the reference-order recompute
 @pytest.mark.parametrize("B,H,W,k", [(1, 20, 200, 5), (2, 9, 13, 7), (1, 33, 65, 3), (1, 64, 64, 5),
-                                     (2, 512, 512, 5)])
+                                     (2, 512, 512, 5), (1, 800, 800, 5)])
 @pytest.mark.parametrize("precise", [False, True])
 def test_angmf_ray_from_intrinsics(cuda, B, H, W, k, precise):
     say(f"[gpu] angmf ray from intrinsics B={B} {H}x{W} k={k} precise={precise}")
