@@ -918,7 +918,7 @@ def main() -> int:
         args.workload = 2 if args.op in ("angmf", "ray_relu") else 0
 
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (--gpus {args.gpus} requested); "
+        print(f"bench.py: measures one GPU only (--gpus {args.gpus} requested); "
               "the op shards by frames or row bands with no collective on the path, "
               "so run --gpus 1", file=sys.stderr)
         return 2

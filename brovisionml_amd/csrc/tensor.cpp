@@ -1,6 +1,6 @@
 // Minimal brotensor::Tensor storage (include/brotensor/tensor.h): host memory
-// from operator new, device memory (the CUDA and Metal tags alike: this build's
-// one GPU) from hipMalloc, both reference-counted.
+// from operator new, device memory (the CUDA and Metal tags alike: the one
+// HIP device) from hipMalloc, both reference-counted.
 
 #include "brotensor/tensor.h"
 

@@ -5,7 +5,7 @@ restatement of brovisionml's CPU twin (src/dsine_ops.cpp:24-172) and of the
 refiner's convex upsample + L2 normalise (src/dsine_refine.cpp:276-282,
 spec include/brovisionml/dsine_refine.h:91-97).  Only the
 tests, the smoke check and the CPU-baseline leg of the benchmark may use it,
-as the checker or the timed CPU reference; the product never does.
+to check results or as the timed CPU reference; the product never does.
 
 `Oracle(path)` binds any build of oracle/dsine_ops_oracle.c (the mutation
 test loads deliberately broken ones); the module-level functions use the

@@ -5,7 +5,8 @@
  *
  * TEST INFRASTRUCTURE ONLY.  Nothing in the product library links, loads or
  * calls this file; only the tests, the smoke check and the CPU-baseline leg of
- * the benchmark use it, and only as the checker / the timed CPU reference.
+ * the benchmark use it, and only to check results or as the timed CPU
+ * reference.
  *
  * It restates brovisionml's CPU twin (src/dsine_ops.cpp, the reference CPU
  * path) operation for operation in double precision:

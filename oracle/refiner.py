@@ -5,8 +5,8 @@ the four heads as float64 torch convolutions (the reference's brotensor
 conv2d_forward, :94-101, in higher precision), each head's output rounded to
 float as the reference's fp32 tensors are; the activations of :262-267 as
 correctly rounded floats; RayReLU, angmf_propagate and the convex upsample +
-normalise from this directory's C oracle.  The checker for
-brovisionml_amd/refiner.py; the product never imports it.
+normalise from this directory's C oracle.  The tests check
+brovisionml_amd/refiner.py against it; the product never imports it.
 """
 from __future__ import annotations
 

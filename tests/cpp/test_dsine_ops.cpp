@@ -9,7 +9,7 @@
 //                        ray_relu once, then chained angmf_propagate calls, then
 //                        the convex upsample + normalise)
 //                        on a 60x80 grid against the CPU oracle
-// The oracle (oracle/_build/liboracle_dsine.so) is linked as the checker only.
+// The oracle (oracle/_build/liboracle_dsine.so) is linked to check results only.
 
 #include "brovisionml/dsine_ops.h"
 
