@@ -32,6 +32,7 @@ EXPORTS = (
     "bvml_dsine_angmf_propagate_f32",
     "bvml_dsine_build_ray8_f32",
     "bvml_dsine_convex_upsample_f32",
+    "bvml_dsine_convex_upsample_bias_f32",
     "bvml_dsine_angmf_recompute_ratio",
     "bvml_dsine_angmf_plan",
     "bvml_dsine_ray_relu_cpu_f32",
@@ -67,6 +68,9 @@ def load(path: str = LIB) -> ctypes.CDLL:
     lib.bvml_dsine_convex_upsample_f32.argtypes = [vp, vp, i, i, i, i, i, i, ctypes.c_float, vp,
                                                    u, vp]
     lib.bvml_dsine_convex_upsample_f32.restype = i
+    lib.bvml_dsine_convex_upsample_bias_f32.argtypes = [vp, vp, vp, i, i, i, i, i, i,
+                                                        ctypes.c_float, vp, u, vp]
+    lib.bvml_dsine_convex_upsample_bias_f32.restype = i
     ip = ctypes.POINTER(ctypes.c_int)
     lib.bvml_dsine_angmf_plan.argtypes = [i, i, i, i, d, d, d, d, u, ip, ip, ip, ip]
     lib.bvml_dsine_angmf_plan.restype = i
@@ -123,6 +127,16 @@ def convex_upsample_f32(x: int, mask: int, B: int, C: int, H: int, W: int, scale
     """Raw call; pointers are integer device addresses. Returns the status."""
     return load().bvml_dsine_convex_upsample_f32(x, mask, B, C, H, W, scale, int(bool(normalize)),
                                                  eps, out, flags, stream)
+
+
+def convex_upsample_bias_f32(x: int, mask: int, mask_bias: int, B: int, C: int, H: int, W: int,
+                             scale: int, normalize: bool, eps: float, out: int,
+                             flags: int = DEFAULT, stream: int = 0) -> int:
+    """Raw call with a per-channel mask bias (0 for none); pointers are
+    integer device addresses. Returns the status."""
+    return load().bvml_dsine_convex_upsample_bias_f32(x, mask, mask_bias, B, C, H, W, scale,
+                                                      int(bool(normalize)), eps, out, flags,
+                                                      stream)
 
 
 def angmf_recompute_ratio(k: int, flags: int = DEFAULT) -> float:

@@ -222,6 +222,7 @@ constexpr int kPxPerWave = 64 / kLanesPerPx;
 template <int C>
 __global__ __launch_bounds__(256) void upsample8_kernel(const float* __restrict__ x,
                                                         const float* __restrict__ mask,
+                                                        const float* __restrict__ mbias,
                                                         float* __restrict__ out, int H, int W,
                                                         int groups, int mode, float eps_s,
                                                         double eps) {
@@ -247,6 +248,15 @@ __global__ __launch_bounds__(256) void upsample8_kernel(const float* __restrict_
         for (int n = 0; n < 9; ++n) m[j][n] = mb[(long long)(n * 64 + j) * HW];
     Taps<C> t;
     load_taps<C>(xb, HW, H, W, y, xx, t);
+    // the mask's per-channel bias (the up-mask head's last convolution run
+    // without it): one fp32 add per value, as a separate bias pass would do
+    if (mbias) {
+        const float* bb = mbias + ky * 8 + h * kSubPerLane;
+#pragma unroll
+        for (int j = 0; j < kSubPerLane; ++j)
+#pragma unroll
+            for (int n = 0; n < 9; ++n) m[j][n] += bb[n * 64 + j];
+    }
 
     // a flagged sub-pixel's 9 mask values wait in LDS for its recompute
     // (36 KB per workgroup: the 3 workgroups per CU the registers allow use
@@ -297,6 +307,7 @@ __global__ __launch_bounds__(256) void upsample8_kernel(const float* __restrict_
 template <int C>
 __global__ __launch_bounds__(256) void upsample_kernel(const float* __restrict__ x,
                                                        const float* __restrict__ mask,
+                                                       const float* __restrict__ mbias,
                                                        float* __restrict__ out, int H, int W,
                                                        int s, int groups, int mode,
                                                        float eps_s, double eps) {
@@ -320,6 +331,10 @@ __global__ __launch_bounds__(256) void upsample_kernel(const float* __restrict__
         float m[9];
 #pragma unroll
         for (int n = 0; n < 9; ++n) m[n] = mb[(n * s2 + kx) * HW];
+        if (mbias) {
+#pragma unroll
+            for (int n = 0; n < 9; ++n) m[n] += mbias[n * s2 + (long long)ky * s + kx];
+        }
         float r[C];
         if (!fast_subpixel<C>(m, t, mode, eps_s, r))
             exact_subpixel<C>(m, t, (mode & kNormalize) != 0, eps, r);
@@ -332,9 +347,9 @@ __global__ __launch_bounds__(256) void upsample_kernel(const float* __restrict__
 constexpr int kMaxGridY = 65535;
 
 template <int C>
-hipError_t launch_upsample(const float* x, const float* mask, float* out, int B, int H, int W,
-                           int s, int mode, float eps_s, double eps, bool fast8,
-                           hipStream_t stream) {
+hipError_t launch_upsample(const float* x, const float* mask, const float* mbias, float* out,
+                           int B, int H, int W, int s, int mode, float eps_s, double eps,
+                           bool fast8, hipStream_t stream) {
     const long long HW = (long long)H * W;
     const long long s2 = (long long)s * s;
     for (int b0 = 0; b0 < B; b0 += kMaxGridY) {
@@ -346,14 +361,14 @@ hipError_t launch_upsample(const float* x, const float* mask, float* out, int B,
             const int groups = (int)((HW + kPxPerWave - 1) / kPxPerWave);
             const long long waves = (long long)groups * 8;
             const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)nb);
-            hipLaunchKernelGGL(upsample8_kernel<C>, grid, dim3(256), 0, stream, xc, mc, oc, H, W,
-                               groups, mode, eps_s, eps);
+            hipLaunchKernelGGL(upsample8_kernel<C>, grid, dim3(256), 0, stream, xc, mc, mbias, oc,
+                               H, W, groups, mode, eps_s, eps);
         } else {
             const int groups = (int)((HW + 63) / 64);
             const long long waves = (long long)groups * s;
             const dim3 grid((unsigned)((waves + 3) / 4), (unsigned)nb);
-            hipLaunchKernelGGL(upsample_kernel<C>, grid, dim3(256), 0, stream, xc, mc, oc, H, W,
-                               s, groups, mode, eps_s, eps);
+            hipLaunchKernelGGL(upsample_kernel<C>, grid, dim3(256), 0, stream, xc, mc, mbias, oc,
+                               H, W, s, groups, mode, eps_s, eps);
         }
         const hipError_t e = hipGetLastError();
         if (e != hipSuccess) return e;
@@ -365,9 +380,10 @@ hipError_t launch_upsample(const float* x, const float* mask, float* out, int B,
 
 extern "C" {
 
-int bvml_dsine_convex_upsample_f32(const float* x, const float* mask, int B, int C, int H,
-                                   int W, int scale, int normalize, float eps, float* out,
-                                   unsigned flags, void* stream) {
+int bvml_dsine_convex_upsample_bias_f32(const float* x, const float* mask,
+                                        const float* mask_bias, int B, int C, int H, int W,
+                                        int scale, int normalize, float eps, float* out,
+                                        unsigned flags, void* stream) {
     if (flags & ~BVML_DSINE_FP64)
         return fail(BVML_DSINE_EFLAGS, "convex_upsample: unknown flag bits");
     if (B < 0 || H < 0 || W < 0 || C < 1 || scale < 1)
@@ -388,7 +404,8 @@ int bvml_dsine_convex_upsample_f32(const float* x, const float* mask, int B, int
     const size_t x_b = (size_t)B * C * HW * f;
     const size_t m_b = (size_t)B * 9 * s2 * HW * f;
     const size_t o_b = (size_t)B * C * s2 * HW * f;
-    if (overlaps(out, o_b, x, x_b) || overlaps(out, o_b, mask, m_b))
+    if (overlaps(out, o_b, x, x_b) || overlaps(out, o_b, mask, m_b) ||
+        (mask_bias && overlaps(out, o_b, mask_bias, (size_t)9 * s2 * f)))
         return fail(BVML_DSINE_EALIAS, "convex_upsample: out overlaps an input");
 
     const int mode = (normalize ? kNormalize : 0) | ((flags & BVML_DSINE_FP64) ? kExact : 0);
@@ -399,14 +416,25 @@ int bvml_dsine_convex_upsample_f32(const float* x, const float* mask, int B, int
     hipStream_t s = static_cast<hipStream_t>(stream);
     hipError_t e;
     switch (C) {
-        case 1: e = launch_upsample<1>(x, mask, out, B, H, W, scale, mode, eps_s, epsd, fast8, s); break;
-        case 2: e = launch_upsample<2>(x, mask, out, B, H, W, scale, mode, eps_s, epsd, fast8, s); break;
-        case 3: e = launch_upsample<3>(x, mask, out, B, H, W, scale, mode, eps_s, epsd, fast8, s); break;
-        default: e = launch_upsample<4>(x, mask, out, B, H, W, scale, mode, eps_s, epsd, fast8, s); break;
+        case 1: e = launch_upsample<1>(x, mask, mask_bias, out, B, H, W, scale, mode, eps_s, epsd,
+                                       fast8, s); break;
+        case 2: e = launch_upsample<2>(x, mask, mask_bias, out, B, H, W, scale, mode, eps_s, epsd,
+                                       fast8, s); break;
+        case 3: e = launch_upsample<3>(x, mask, mask_bias, out, B, H, W, scale, mode, eps_s, epsd,
+                                       fast8, s); break;
+        default: e = launch_upsample<4>(x, mask, mask_bias, out, B, H, W, scale, mode, eps_s, epsd,
+                                       fast8, s); break;
     }
     if (e != hipSuccess)
         return fail((int)e, std::string("convex_upsample launch: ") + hipGetErrorString(e));
     return BVML_DSINE_OK;
+}
+
+int bvml_dsine_convex_upsample_f32(const float* x, const float* mask, int B, int C, int H,
+                                   int W, int scale, int normalize, float eps, float* out,
+                                   unsigned flags, void* stream) {
+    return bvml_dsine_convex_upsample_bias_f32(x, mask, nullptr, B, C, H, W, scale, normalize,
+                                               eps, out, flags, stream);
 }
 
 }  // extern "C"

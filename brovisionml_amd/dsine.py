@@ -160,8 +160,8 @@ def angmf_propagate(pred_norm, prob, xy, angle, ray, fu: float, cu: float,
 
 
 def _upsample(op: str, x, mask, N: int, C: int, H: int, W: int, scale: int, out,
-              normalize: bool, eps: float, precise: bool):
-    _check_tensors(op, [x, mask])
+              normalize: bool, eps: float, precise: bool, mask_bias=None):
+    _check_tensors(op, [x, mask] + ([] if mask_bias is None else [mask_bias]))
     import torch
     if min(N, C, H, W) < 0 or scale < 1:
         _fail(f"{op}: N, C, H and W must be >= 0 and scale >= 1")
@@ -170,6 +170,8 @@ def _upsample(op: str, x, mask, N: int, C: int, H: int, W: int, scale: int, out,
         _fail(f"{op}: x holds {x.numel()} elements, expected N*C*H*W = {N * C * HW}")
     if mask.numel() != N * 9 * scale * scale * HW:
         _fail(f"{op}: mask holds {mask.numel()} elements, expected N*9*scale^2*H*W")
+    if mask_bias is not None and mask_bias.numel() != 9 * scale * scale:
+        _fail(f"{op}: mask_bias holds {mask_bias.numel()} elements, expected 9*scale^2")
     n_out = N * C * scale * scale * HW
     if out is None:
         out = torch.empty((N, C, scale * H, scale * W), dtype=torch.float32, device=x.device)
@@ -181,28 +183,33 @@ def _upsample(op: str, x, mask, N: int, C: int, H: int, W: int, scale: int, out,
         return out
     flags = _lib.FP64 if precise else _lib.DEFAULT
     with _device(x):
-        st = _lib.convex_upsample_f32(x.data_ptr(), mask.data_ptr(), N, C, H, W, scale,
-                                      normalize, float(eps), out.data_ptr(), flags, _stream_of(x))
+        st = _lib.convex_upsample_bias_f32(x.data_ptr(), mask.data_ptr(),
+                                           0 if mask_bias is None else mask_bias.data_ptr(),
+                                           N, C, H, W, scale, normalize, float(eps),
+                                           out.data_ptr(), flags, _stream_of(x))
     _raise_status(op, st)
     return out
 
 
 def convex_upsample(x, mask, N: int, C: int, H: int, W: int, scale: int = 8, out=None, *,
-                    precise: bool = False):
+                    precise: bool = False, mask_bias=None):
     """Convex upsample by `scale` with a 9-tap softmax mask: brotensor's
     convex_upsample_forward as the refiner calls it (src/dsine_refine.cpp:278,
     arithmetic of include/brovisionml/dsine_refine.h:91-97).  x (N, C, H, W),
-    mask (N, 9*scale^2, H, W); returns out (N, C, scale*H, scale*W)."""
-    return _upsample("convex_upsample", x, mask, N, C, H, W, scale, out, False, 0.0, precise)
+    mask (N, 9*scale^2, H, W), mask_bias an optional (9*scale^2,) per-channel
+    bias added to the mask; returns out (N, C, scale*H, scale*W)."""
+    return _upsample("convex_upsample", x, mask, N, C, H, W, scale, out, False, 0.0, precise,
+                     mask_bias)
 
 
 def convex_upsample_normalize(x, mask, N: int, C: int, H: int, W: int, scale: int = 8,
-                              eps: float = 1e-12, out=None, *, precise: bool = False):
+                              eps: float = 1e-12, out=None, *, precise: bool = False,
+                              mask_bias=None):
     """convex_upsample followed by the channel L2-normalise with eps, fused:
     the pair the refiner runs after each propagate (src/dsine_refine.cpp:276-282,
     l2_normalize_nchw_forward with eps 1e-12f)."""
     return _upsample("convex_upsample_normalize", x, mask, N, C, H, W, scale, out, True, eps,
-                     precise)
+                     precise, mask_bias)
 
 
 def build_ray8(fu: float, cu: float, fv: float, cv: float, H: int, W: int, device=None):

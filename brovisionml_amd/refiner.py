@@ -25,7 +25,8 @@ What runs where:
     ROCm, in fp32 and without bias; their biases, activations and the GRU's
     gate arithmetic run in the package's fused elementwise kernels
     (bvml_dsine_gru_gates_f32, bvml_dsine_gru_update_f32,
-    bvml_dsine_bias_act_f32).
+    bvml_dsine_bias_act_f32), the up-mask head's last bias in the upsample
+    (bvml_dsine_convex_upsample_bias_f32).
 
 Weights are the checkpoint's top-level tensors gru.conv{z,r,q}.{weight,bias}
 and {prob,xy,angle,up_prob}_head.{0,2,4}.{weight,bias} (:161-180), loaded
@@ -167,15 +168,21 @@ class Refiner:
 
     def _heads(self, hin, H: int, W: int):
         """The four get_prediction_head stacks (src/dsine_refine.cpp:119-127)
-        on hin: (prob, xy, angle, up_mask) logits."""
+        on hin: (prob, xy, angle, up_mask) logits, up_mask without its last
+        layer's bias (the upsample adds it)."""
         import torch.nn.functional as F
         nh = len(self.heads)
         t = F.conv2d(hin, self.w_h0, None, padding=1)
         dsine.bias_act(t, self.b_h0, nh * 64, H * W, relu=True)
         t = F.conv2d(t, self.w_h2, None, groups=nh)
         dsine.bias_act(t, self.b_h2, nh * 64, H * W, relu=True)
+        # the up-mask head's last layer runs without its bias: the upsample
+        # adds it to the mask as it loads it (one fp32 add per value, as the
+        # bias pass would round it), so the 576 planes are not read and
+        # written once more
         return [F.conv2d(t[:, 64 * i:64 * (i + 1)], self.w[f"{h}.4.weight"],
-                         self.w[f"{h}.4.bias"]).contiguous() for i, h in enumerate(self.heads)]
+                         None if h == "up_prob_head" else self.w[f"{h}.4.bias"]).contiguous()
+                for i, h in enumerate(self.heads)]
 
     def forward(self, dec: DecoderOutput, intr: workloads.Intrinsics, orig_h: int, orig_w: int,
                 crop: Crop | None = None, trace: list | None = None, cond=None,
@@ -219,7 +226,8 @@ class Refiner:
             pred_norm = dsine.angmf_propagate(pred_norm, prob, xy, angle, ray8, fu, cu, fv, cv,
                                               H, W, logits=True)
             up = dsine.convex_upsample_normalize(pred_norm, up_mask, 1, 3, H, W, K_UP,
-                                                 float(np.float32(1e-12)))
+                                                 float(np.float32(1e-12)),
+                                                 mask_bias=self.w["up_prob_head.4.bias"])
             if trace is not None:
                 trace.append((pred_norm, up))
             if hidden_trace is not None:

@@ -151,6 +151,19 @@ int bvml_dsine_convex_upsample_f32(const float* x, const float* mask, int B, int
                                    unsigned flags, void* stream);
 
 /*
+ * The same with a per-channel bias on the mask (mask_bias: 9*scale^2 floats,
+ * or NULL for none): each mask value is mask + mask_bias[channel], one fp32
+ * add, as the bias add after the refiner's up-mask head (its last 1x1
+ * convolution, src/dsine_refine.cpp:119-127) would round it, so that
+ * convolution can run without its bias and the separate pass over the
+ * 9*scale^2 planes goes.  No counterpart in the reference.
+ */
+int bvml_dsine_convex_upsample_bias_f32(const float* x, const float* mask,
+                                        const float* mask_bias, int B, int C, int H, int W,
+                                        int scale, int normalize, float eps, float* out,
+                                        unsigned flags, void* stream);
+
+/*
  * The CPU branch of the same two ops, for host pointers: brovisionml's public
  * dispatch sends CPU tensors to its CPU twin (src/dsine_ops.cpp:178-215 ->
  * ray_relu_cpu :55-76, angmf_propagate_cpu :78-172); these are this

@@ -219,3 +219,34 @@ def test_upsample_golden(cuda, path):
     s, normalize = int(d["s"]), bool(int(d["normalize"]))
     got = run_gpu(d["x"], d["mask"], s, cuda, normalize)
     check(got, d["expect"], normalize, scale=float(np.abs(d["x"]).max()))
+
+
+@pytest.mark.parametrize("s,misalign", [(8, False), (8, True), (4, False)])
+@pytest.mark.parametrize("normalize,precise", [(True, False), (False, False), (True, True)])
+def test_upsample_mask_bias(cuda, s, misalign, normalize, precise):
+    """A per-channel mask bias added in the kernel (the up-mask head's last
+    bias, bvml_dsine_convex_upsample_bias_f32) equals the call on the mask
+    with the bias added beforehand in fp32, bit for bit: the s = 8 kernel, its
+    unaligned-out fallback and another scale, fast and double paths; the
+    result is also within the bar of the oracle on the biased mask."""
+    import torch
+    say(f"[gpu] upsample mask bias s={s} misalign={misalign} normalize={normalize} "
+        f"precise={precise}")
+    rng = np.random.default_rng(300 + s + 2 * misalign + 4 * normalize + 8 * precise)
+    B, C, H, W = 2, 3, 7, 13
+    x, mask = _inputs(rng, B, C, H, W, s)
+    bias = (3.0 * rng.standard_normal(9 * s * s)).astype(np.float32)
+    biased = (mask + bias[None, :, None, None]).astype(np.float32)
+    want = run_gpu(x, biased, s, cuda, normalize, precise, misalign=misalign)
+    xt, mt, bt = to_dev(x, cuda), to_dev(mask, cuda), to_dev(bias, cuda)
+    g = Guarded(B * C * s * s * H * W, cuda, shift=1 if misalign else 0)
+    if normalize:
+        r = dsine.convex_upsample_normalize(xt, mt, B, C, H, W, s, EPS, g.out, precise=precise,
+                                            mask_bias=bt)
+    else:
+        r = dsine.convex_upsample(xt, mt, B, C, H, W, s, g.out, precise=precise, mask_bias=bt)
+    torch.cuda.synchronize()
+    assert g.intact(), "convex upsample wrote outside its output"
+    got = r.cpu().numpy().reshape(B, C, s * H, s * W)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+    check(got, run_oracle(x, biased, s, normalize), normalize, exact=precise)
