@@ -105,8 +105,8 @@ constexpr float kMinV2 = 1e-30f;
 // pixel with |acc|^2 < kAccRatio2[k] * sum(wi^2) is recomputed, and with
 // delta(k) the measured value plus 10%, the rest stay within
 // delta(k) / sqrt(kAccRatio2[k]) <= 7.5e-6 per component, 25% inside the bar
-// (the largest kept error measured is 5.8e-6, and the search's 5.2e-6).  At k = 1 the sum is one term
-// and cannot cancel.
+// (the largest kept error measured is 5.8e-6, and the search's 5.2e-6).  At
+// k = 1 the sum is one term and cannot cancel.
 //
 // About 2.3 pixels of a 256x256 image of independent random unit normals with
 // angles up to pi/4 fall below the k = 5 threshold; the refiner's
@@ -463,8 +463,9 @@ typedef double lds_d2 __attribute__((ext_vector_type(2)));
 // The source-normal halo of a tile in LDS: one 80-byte record per source
 // pixel of the tile's replicate-padded window, read with one address per
 // neighbour and immediate offsets (the 80-byte stride leaves consecutive
-// lanes' ds_read_b128 free of bank conflicts, where 64 bytes would not).  With m the raw normal, m' = m/|m|, P0 = (tu0, tv0, 1)
-// the source pixel's ray at depth 1 and g = P0.m, the rotation's cross product
+// lanes' ds_read_b128 free of bank conflicts, where 64 bytes would not).
+// With m the raw normal, m' = m/|m|, P0 = (tu0, tv0, 1) the source pixel's
+// ray at depth 1 and g = P0.m, the rotation's cross product
 // for a neighbour with raw xy pair (xs, ys) and q = xs mx/fu + ys my/fv is
 //   c = V x m' = g (D x m') - q (P0 x m'),   D = (xs/fu, ys/fv, 0),
 // i.e. c = xs e1 + ys e2 - q f with the per-source vectors
