@@ -8,7 +8,7 @@ from __future__ import annotations
 import ctypes
 import os
 
-from .build import LIB
+from .build import LIB, LIB_REFINE
 
 # Status codes (include/bvml_dsine.h)
 OK = 0
@@ -31,6 +31,7 @@ EXPORTS = (
     "bvml_dsine_ray_relu_f32",
     "bvml_dsine_angmf_propagate_f32",
     "bvml_dsine_build_ray8_f32",
+    "bvml_dsine_build_uv8_f32",
     "bvml_dsine_convex_upsample_f32",
     "bvml_dsine_convex_upsample_bias_f32",
     "bvml_dsine_angmf_recompute_ratio",
@@ -44,7 +45,23 @@ EXPORTS = (
     "bvml_dsine_version",
 )
 
+# Every symbol include/bvml_dsine_refine.h declares.
+REFINE_EXPORTS = (
+    "bvml_dsine_refiner_create",
+    "bvml_dsine_refiner_destroy",
+    "bvml_dsine_refiner_load_file",
+    "bvml_dsine_refiner_set_tensor",
+    "bvml_dsine_refiner_tensor_numel",
+    "bvml_dsine_refiner_get_tensor",
+    "bvml_dsine_refiner_forward",
+    "bvml_dsine_refiner_last_error",
+)
+EWEIGHTS = -9
+EFILE = -10
+ELIB = -11
+
 _lib = None
+_refine = None
 
 
 def load(path: str = LIB) -> ctypes.CDLL:
@@ -65,6 +82,8 @@ def load(path: str = LIB) -> ctypes.CDLL:
     lib.bvml_dsine_angmf_propagate_f32.restype = i
     lib.bvml_dsine_build_ray8_f32.argtypes = [vp, d, d, d, d, i, i, vp]
     lib.bvml_dsine_build_ray8_f32.restype = i
+    lib.bvml_dsine_build_uv8_f32.argtypes = [vp, d, d, d, d, i, i, vp]
+    lib.bvml_dsine_build_uv8_f32.restype = i
     lib.bvml_dsine_convex_upsample_f32.argtypes = [vp, vp, i, i, i, i, i, i, ctypes.c_float, vp,
                                                    u, vp]
     lib.bvml_dsine_convex_upsample_f32.restype = i
@@ -95,6 +114,44 @@ def load(path: str = LIB) -> ctypes.CDLL:
     return lib
 
 
+def load_refine(path: str = LIB_REFINE) -> ctypes.CDLL:
+    """Load (once) and type the native refiner library (include/bvml_dsine_refine.h);
+    raises if it was not built."""
+    global _refine
+    if _refine is not None:
+        return _refine
+    load()
+    if not os.path.exists(path):
+        raise RuntimeError(
+            f"brovisionml_amd: native library {path} is missing; run "
+            "`python -m brovisionml_amd.build` first")
+    lib = ctypes.CDLL(path)
+    vp, i, ll, f = ctypes.c_void_p, ctypes.c_int, ctypes.c_longlong, ctypes.c_float
+    lib.bvml_dsine_refiner_create.argtypes = [ctypes.POINTER(vp)]
+    lib.bvml_dsine_refiner_create.restype = i
+    lib.bvml_dsine_refiner_destroy.argtypes = [vp]
+    lib.bvml_dsine_refiner_destroy.restype = None
+    lib.bvml_dsine_refiner_load_file.argtypes = [vp, ctypes.c_char_p]
+    lib.bvml_dsine_refiner_load_file.restype = i
+    lib.bvml_dsine_refiner_set_tensor.argtypes = [vp, ctypes.c_char_p, vp, ll]
+    lib.bvml_dsine_refiner_set_tensor.restype = i
+    lib.bvml_dsine_refiner_tensor_numel.argtypes = [ctypes.c_char_p]
+    lib.bvml_dsine_refiner_tensor_numel.restype = ll
+    lib.bvml_dsine_refiner_get_tensor.argtypes = [vp, ctypes.c_char_p, vp, ll]
+    lib.bvml_dsine_refiner_get_tensor.restype = i
+    lib.bvml_dsine_refiner_forward.argtypes = [vp, vp, vp, vp, i, i, f, f, f, f, i, i, i, i, i, i,
+                                               vp, vp, vp]
+    lib.bvml_dsine_refiner_forward.restype = i
+    lib.bvml_dsine_refiner_last_error.argtypes = []
+    lib.bvml_dsine_refiner_last_error.restype = ctypes.c_char_p
+    _refine = lib
+    return lib
+
+
+def refine_last_error() -> str:
+    return load_refine().bvml_dsine_refiner_last_error().decode()
+
+
 def last_error() -> str:
     return load().bvml_dsine_last_error().decode()
 
@@ -119,6 +176,12 @@ def build_ray8_f32(ray: int, fu: float, cu: float, fv: float, cv: float, H: int,
                    stream: int = 0) -> int:
     """Raw call; `ray` is an integer device address of 3*H*W floats."""
     return load().bvml_dsine_build_ray8_f32(ray, fu, cu, fv, cv, H, W, stream)
+
+
+def build_uv8_f32(uv: int, fu: float, cu: float, fv: float, cv: float, H: int, W: int,
+                  stream: int = 0) -> int:
+    """Raw call; `uv` is an integer device address of 2*H*W floats."""
+    return load().bvml_dsine_build_uv8_f32(uv, fu, cu, fv, cv, H, W, stream)
 
 
 def convex_upsample_f32(x: int, mask: int, B: int, C: int, H: int, W: int, scale: int,

@@ -7,6 +7,9 @@
                           include/brovisionml/dsine_ops.h), plain C++ over the
                           C ABI; brotensor::Tensor left undefined, to be
                           resolved by brotensor or by the subset below
+  libbvml_dsine_refine.so the native NRN refiner (refiner.cpp,
+                          include/bvml_dsine_refine.h): C++ over the C ABI
+                          and MIOpen; extern "C" symbols only
   libbrotensor_subset.so  the brotensor::Tensor subset of
                           include/brotensor/tensor.h, for standalone use and
                           the C++ tests; a brovisionml build links brotensor
@@ -26,6 +29,8 @@ LIBDIR = os.path.join(PKG, "lib")
 LIB = os.path.join(LIBDIR, "libbvml_dsine.so")
 LIB_CXX = os.path.join(LIBDIR, "libbvml_dsine_cxx.so")
 LIB_TENSOR = os.path.join(LIBDIR, "libbrotensor_subset.so")
+LIB_REFINE = os.path.join(LIBDIR, "libbvml_dsine_refine.so")
+ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
 CXX = os.environ.get("CXX", "g++")
@@ -61,6 +66,9 @@ HOST_SOURCES = [
 ]
 CXX_SOURCES = [os.path.join(CSRC, "dsine_ops.cpp")]
 TENSOR_SOURCES = [os.path.join(CSRC, "tensor.cpp")]
+REFINE_SOURCES = [os.path.join(CSRC, "refiner.cpp")]
+# host C++ against the HIP runtime and MIOpen headers
+HIP_HOST_FLAGS = ["-D__HIP_PLATFORM_AMD__", "-isystem", os.path.join(ROCM, "include")]
 
 
 def _run(cmd: list[str]) -> None:
@@ -75,7 +83,7 @@ def _install(tmp: str, dst: str) -> None:
 
 
 def build_library() -> str:
-    """Builds the three libraries; returns the C ABI library's path."""
+    """Builds the four libraries; returns the C ABI library's path."""
     os.makedirs(LIBDIR, exist_ok=True)
     objdir = os.path.join(PKG, "_build")
     os.makedirs(objdir, exist_ok=True)
@@ -88,6 +96,11 @@ def build_library() -> str:
     _run([HIPCC, *HIP_FLAGS, "-I", INCLUDE, "-shared", "-o", LIB + ".tmp", *host_objs, *SOURCES,
           "-Wl,--version-script=" + os.path.join(CSRC, "libbvml_dsine.map")])
     _install(LIB + ".tmp", LIB)
+    _run([CXX, *CXX_FLAGS, *HIP_HOST_FLAGS, "-I", INCLUDE, "-shared", "-o", LIB_REFINE + ".tmp",
+          *REFINE_SOURCES, "-L", LIBDIR, "-lbvml_dsine", "-L", os.path.join(ROCM, "lib"),
+          "-lMIOpen", "-lamdhip64", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath," + os.path.join(ROCM, "lib"),
+          "-Wl,--version-script=" + os.path.join(CSRC, "libbvml_dsine_refine.map")])
+    _install(LIB_REFINE + ".tmp", LIB_REFINE)
     _run([CXX, *CXX_FLAGS, "-I", INCLUDE, "-shared", "-o", LIB_CXX + ".tmp", *CXX_SOURCES,
           "-L", LIBDIR, "-lbvml_dsine", "-Wl,-rpath,$ORIGIN",
           "-Wl,--version-script=" + os.path.join(CSRC, "libbvml_dsine_cxx.map")])

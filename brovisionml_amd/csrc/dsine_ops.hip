@@ -1091,6 +1091,18 @@ __global__ __launch_bounds__(256) void build_ray8_kernel(float* ray, double fu, 
     ray[2 * HW + p] = r.z;
 }
 
+// build_uv: the ray map's first two channels before the normalise
+// (src/dsine_decoder.cpp:253-256), one pixel per thread.
+__global__ __launch_bounds__(256) void build_uv8_kernel(float* uv, double fu, double cu,
+                                                        double fv, double cv, int H, int W) {
+    const long long HW = (long long)H * W;
+    const long long p = (long long)blockIdx.x * blockDim.x + threadIdx.x;
+    if (p >= HW) return;
+    const int y = (int)(p / W), x = (int)(p - (long long)y * W);
+    uv[p] = (float)(((x + 0.5) - cu) / fu);
+    uv[HW + p] = (float)(((y + 0.5) - cv) / fv);
+}
+
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
@@ -1419,6 +1431,23 @@ int bvml_dsine_build_ray8_f32(float* ray, double fu, double cu, double fv, doubl
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return fail((int)e, std::string("build_ray8 launch: ") + hipGetErrorString(e));
+    return BVML_DSINE_OK;
+}
+
+int bvml_dsine_build_uv8_f32(float* uv, double fu, double cu, double fv, double cv, int H,
+                             int W, void* stream) {
+    if (H < 0 || W < 0) return fail(BVML_DSINE_ESHAPE, "build_uv8: H and W must be >= 0");
+    const long long HW = (long long)H * W;
+    if (HW == 0) return BVML_DSINE_OK;
+    if (!uv) return fail(BVML_DSINE_ENULL, "build_uv8: uv must be non-NULL");
+    if (HW > (long long)INT_MAX * 64)
+        return fail(BVML_DSINE_ESIZE, "build_uv8: H*W too large for one launch");
+    const long long grid = (HW + 255) / 256;
+    hipLaunchKernelGGL(build_uv8_kernel, dim3((unsigned)grid), dim3(256), 0,
+                       static_cast<hipStream_t>(stream), uv, fu, cu, fv, cv, H, W);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return fail((int)e, std::string("build_uv8 launch: ") + hipGetErrorString(e));
     return BVML_DSINE_OK;
 }
 

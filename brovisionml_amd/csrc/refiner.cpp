@@ -1,0 +1,918 @@
+// The native NRN refiner (include/bvml_dsine_refine.h): brovisionml's Refiner
+// (src/dsine_refine.cpp:161-294) on one HIP device, over this library's C ABI
+// (include/bvml_dsine.h) and MIOpen.
+//
+// Per iteration (src/dsine_refine.cpp:255-287), on persistent per-grid maps:
+//   zr   = conv5x5([h | feature | uv], [W_z; W_r])           MIOpen, 130 -> 128
+//   z, r*h                                                   bvml_dsine_gru_gates_f32
+//   qp   = conv5x5([r*h | feature | uv], W_q)                MIOpen, 130 -> 64
+//   h    = (1 - z) h + z tanh(qp + b_q), also into [h | uv]  bvml_dsine_gru_update_f32
+//   t0   = relu(conv3x3([h | uv], the heads' first layers))  MIOpen + bias_act
+//   t1   = relu(grouped 1x1 conv(t0))                        MIOpen + bias_act
+//   prob, xy, angle = 1x1 convs of t1's slices + bias        MIOpen + bias_act
+//   pred = angmf_propagate(pred, prob, xy, angle) on logits  bvml_dsine_angmf_propagate_f32
+// and, in the last iteration only, the up-mask head's last 1x1 convolution
+// and the convex upsample + normalise with its bias (the reference computes
+// an up-sampled map every iteration but returns the last one only,
+// src/dsine_refine.cpp:276-283, :289-293, so the others are dead work).  In
+// the first four iterations the heads' first two layers run for the three
+// heads the propagate reads (192 channels); the last iteration runs all four
+// (256).  The convolutions run without their bias; the fused kernels add it
+// in the reference's rounding (a bias add after the convolution's sum).
+//
+// The convolutions are MIOpen's immediate mode, the solution with the lowest
+// time estimate for each shape, as PyTorch picks them on ROCm without
+// benchmarking; the plans are made once per grid size.
+
+#include "bvml_dsine_refine.h"
+
+#include <hip/hip_runtime.h>
+#include <miopen/miopen.h>
+
+#include <cmath>
+#include <cstdint>
+#include <cstdio>
+#include <cstring>
+#include <memory>
+#include <string>
+#include <utility>
+#include <vector>
+
+namespace {
+
+// The calling thread's last error message (bvml_dsine_refiner_last_error);
+// this library's own, apart from the kernel library's.
+thread_local std::string g_last_error;
+
+int fail(int code, const std::string& msg) {
+    g_last_error = msg;
+    return code;
+}
+
+bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
+    const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
+    return a0 < b0 + bbytes && b0 < a0 + abytes;
+}
+
+constexpr int kHidden = 64;           // hidden_dim (src/dsine_refine.cpp:172)
+constexpr int kFeature = 64;          // the decoder's feature channels
+constexpr int kX = kFeature + 2;      // feat_map = cat(feature, uv_8)
+constexpr int kHx = kHidden + kX;     // cat(h, feat_map): 130
+constexpr int kHin = kHidden + 2;     // cat(h_new, uv_8): 66
+constexpr int kUp = 8;                // downsample_ratio (:24)
+constexpr int kIter = 5;              // num_iter_test (:25)
+constexpr int kPs = 5;                // the propagate's window
+constexpr int kHeads = 4;
+constexpr int kMid = 64;              // the heads' hidden width (:119-127)
+constexpr float kUpEps = 1e-12f;      // l2_normalize_nchw_forward's eps (:281)
+const char* const kHeadName[kHeads] = {"prob_head", "xy_head", "angle_head", "up_prob_head"};
+constexpr int kHeadOut[kHeads] = {kPs * kPs, 2 * kPs * kPs, kPs * kPs, 9 * kUp * kUp};
+
+// ---------------------------------------------------------------------------
+// The checkpoint tensors the refiner reads
+// ---------------------------------------------------------------------------
+struct TensorSpec {
+    std::string name;
+    int c_out;
+    long long numel;
+};
+
+// Index order: gru.convz, convr, convq (weight, bias), then per head
+// .0, .2, .4 (weight, bias).
+const std::vector<TensorSpec>& specs() {
+    static const std::vector<TensorSpec> v = [] {
+        std::vector<TensorSpec> s;
+        auto conv = [&s](const std::string& p, int co, int ci, int k) {
+            s.push_back({p + ".weight", co, (long long)co * ci * k * k});
+            s.push_back({p + ".bias", co, co});
+        };
+        for (const char* g : {"convz", "convr", "convq"})
+            conv(std::string("gru.") + g, kHidden, kHx, 5);
+        for (int h = 0; h < kHeads; ++h) {
+            const std::string p = kHeadName[h];
+            conv(p + ".0", kMid, kHin, 3);
+            conv(p + ".2", kMid, kMid, 1);
+            conv(p + ".4", kHeadOut[h], kMid, 1);
+        }
+        return s;
+    }();
+    return v;
+}
+
+enum : int { kZw = 0, kZb, kRw, kRb, kQw, kQb, kHead0 };
+int head_w(int h, int layer) { return kHead0 + 6 * h + 2 * layer; }  // layer 0, 1, 2 = .0 .2 .4
+int head_b(int h, int layer) { return head_w(h, layer) + 1; }
+
+int spec_index(const char* name) {
+    const auto& s = specs();
+    for (size_t i = 0; i < s.size(); ++i)
+        if (s[i].name == name) return (int)i;
+    return -1;
+}
+
+// ---------------------------------------------------------------------------
+// safetensors: an 8-byte little-endian header length, a JSON header mapping
+// each tensor name to {"dtype", "shape", "data_offsets": [begin, end]} (byte
+// offsets into the data that follows the header), optional "__metadata__".
+// ---------------------------------------------------------------------------
+struct Json {
+    enum Kind { Null, Bool, Num, Str, Arr, Obj } kind = Null;
+    double num = 0.0;
+    bool integral = false;        // a literal with no fraction or exponent
+    unsigned long long uint = 0;  // its value when integral and non-negative
+    std::string str;
+    std::vector<Json> arr;
+    std::vector<std::pair<std::string, Json>> obj;
+
+    const Json* get(const std::string& key) const {
+        for (const auto& kv : obj)
+            if (kv.first == key) return &kv.second;
+        return nullptr;
+    }
+};
+
+class JsonParser {
+public:
+    JsonParser(const char* p, const char* end) : p_(p), end_(end) {}
+
+    bool document(Json& out) {
+        if (!value(out, 0)) return false;
+        ws();
+        return p_ == end_;
+    }
+
+private:
+    const char* p_;
+    const char* end_;
+
+    void ws() {
+        while (p_ < end_ && (*p_ == ' ' || *p_ == '\t' || *p_ == '\n' || *p_ == '\r')) ++p_;
+    }
+    bool lit(const char* s) {
+        const size_t n = std::strlen(s);
+        if ((size_t)(end_ - p_) < n || std::memcmp(p_, s, n) != 0) return false;
+        p_ += n;
+        return true;
+    }
+    static void put_utf8(std::string& s, unsigned cp) {
+        if (cp < 0x80) {
+            s += (char)cp;
+        } else if (cp < 0x800) {
+            s += (char)(0xC0 | (cp >> 6));
+            s += (char)(0x80 | (cp & 0x3F));
+        } else if (cp < 0x10000) {
+            s += (char)(0xE0 | (cp >> 12));
+            s += (char)(0x80 | ((cp >> 6) & 0x3F));
+            s += (char)(0x80 | (cp & 0x3F));
+        } else {
+            s += (char)(0xF0 | (cp >> 18));
+            s += (char)(0x80 | ((cp >> 12) & 0x3F));
+            s += (char)(0x80 | ((cp >> 6) & 0x3F));
+            s += (char)(0x80 | (cp & 0x3F));
+        }
+    }
+    bool hex4(unsigned& v) {
+        if (end_ - p_ < 4) return false;
+        v = 0;
+        for (int i = 0; i < 4; ++i) {
+            const char c = *p_++;
+            v <<= 4;
+            if (c >= '0' && c <= '9') v |= (unsigned)(c - '0');
+            else if (c >= 'a' && c <= 'f') v |= (unsigned)(c - 'a' + 10);
+            else if (c >= 'A' && c <= 'F') v |= (unsigned)(c - 'A' + 10);
+            else return false;
+        }
+        return true;
+    }
+    bool string(std::string& s) {
+        if (p_ >= end_ || *p_ != '"') return false;
+        ++p_;
+        while (p_ < end_) {
+            const char c = *p_++;
+            if (c == '"') return true;
+            if ((unsigned char)c < 0x20) return false;
+            if (c != '\\') {
+                s += c;
+                continue;
+            }
+            if (p_ >= end_) return false;
+            const char e = *p_++;
+            switch (e) {
+                case '"': s += '"'; break;
+                case '\\': s += '\\'; break;
+                case '/': s += '/'; break;
+                case 'b': s += '\b'; break;
+                case 'f': s += '\f'; break;
+                case 'n': s += '\n'; break;
+                case 'r': s += '\r'; break;
+                case 't': s += '\t'; break;
+                case 'u': {
+                    unsigned cp;
+                    if (!hex4(cp)) return false;
+                    if (cp >= 0xD800 && cp < 0xDC00) {  // a surrogate pair
+                        unsigned lo;
+                        if (!lit("\\u") || !hex4(lo) || lo < 0xDC00 || lo >= 0xE000) return false;
+                        cp = 0x10000 + ((cp - 0xD800) << 10) + (lo - 0xDC00);
+                    } else if (cp >= 0xDC00 && cp < 0xE000) {
+                        return false;
+                    }
+                    put_utf8(s, cp);
+                    break;
+                }
+                default: return false;
+            }
+        }
+        return false;
+    }
+    bool number(Json& v) {
+        const char* s = p_;
+        if (p_ < end_ && *p_ == '-') ++p_;
+        const char* digits = p_;
+        while (p_ < end_ && *p_ >= '0' && *p_ <= '9') ++p_;
+        if (p_ == digits) return false;
+        bool integral = true;
+        if (p_ < end_ && *p_ == '.') {
+            integral = false;
+            ++p_;
+            const char* f = p_;
+            while (p_ < end_ && *p_ >= '0' && *p_ <= '9') ++p_;
+            if (p_ == f) return false;
+        }
+        if (p_ < end_ && (*p_ == 'e' || *p_ == 'E')) {
+            integral = false;
+            ++p_;
+            if (p_ < end_ && (*p_ == '+' || *p_ == '-')) ++p_;
+            const char* f = p_;
+            while (p_ < end_ && *p_ >= '0' && *p_ <= '9') ++p_;
+            if (p_ == f) return false;
+        }
+        const std::string text(s, p_);
+        v.kind = Json::Num;
+        v.num = std::strtod(text.c_str(), nullptr);
+        v.integral = integral && *s != '-' && (p_ - digits) <= 19;
+        if (v.integral) v.uint = std::strtoull(text.c_str(), nullptr, 10);
+        return true;
+    }
+    bool value(Json& v, int depth) {
+        if (depth > 16) return false;
+        ws();
+        if (p_ >= end_) return false;
+        const char c = *p_;
+        if (c == '{') {
+            ++p_;
+            v.kind = Json::Obj;
+            ws();
+            if (p_ < end_ && *p_ == '}') {
+                ++p_;
+                return true;
+            }
+            for (;;) {
+                ws();
+                std::string key;
+                if (!string(key)) return false;
+                ws();
+                if (p_ >= end_ || *p_ != ':') return false;
+                ++p_;
+                Json child;
+                if (!value(child, depth + 1)) return false;
+                v.obj.emplace_back(std::move(key), std::move(child));
+                ws();
+                if (p_ < end_ && *p_ == ',') {
+                    ++p_;
+                    continue;
+                }
+                if (p_ < end_ && *p_ == '}') {
+                    ++p_;
+                    return true;
+                }
+                return false;
+            }
+        }
+        if (c == '[') {
+            ++p_;
+            v.kind = Json::Arr;
+            ws();
+            if (p_ < end_ && *p_ == ']') {
+                ++p_;
+                return true;
+            }
+            for (;;) {
+                Json child;
+                if (!value(child, depth + 1)) return false;
+                v.arr.push_back(std::move(child));
+                ws();
+                if (p_ < end_ && *p_ == ',') {
+                    ++p_;
+                    continue;
+                }
+                if (p_ < end_ && *p_ == ']') {
+                    ++p_;
+                    return true;
+                }
+                return false;
+            }
+        }
+        if (c == '"') {
+            v.kind = Json::Str;
+            return string(v.str);
+        }
+        if (lit("true") || lit("false")) {
+            v.kind = Json::Bool;
+            return true;
+        }
+        if (lit("null")) {
+            v.kind = Json::Null;
+            return true;
+        }
+        return number(v);
+    }
+};
+
+// IEEE binary16 bits to float (exact: every half is a float).
+float half_to_float(uint16_t h) {
+    const uint32_t sign = (uint32_t)(h & 0x8000u) << 16;
+    const uint32_t e = (h >> 10) & 0x1Fu, m = h & 0x3FFu;
+    uint32_t bits;
+    if (e == 0) {
+        const float mag = std::ldexp((float)m, -24);  // zero or a subnormal
+        std::memcpy(&bits, &mag, 4);
+        bits |= sign;
+    } else if (e == 31) {
+        bits = sign | 0x7F800000u | (m << 13);
+    } else {
+        bits = sign | ((e + 112u) << 23) | (m << 13);
+    }
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+float bf16_to_float(uint16_t b) {
+    const uint32_t bits = (uint32_t)b << 16;
+    float f;
+    std::memcpy(&f, &bits, 4);
+    return f;
+}
+
+struct FileCloser {
+    void operator()(std::FILE* f) const { std::fclose(f); }
+};
+
+// Reads the refiner's tensors of a safetensors file into `out` (one vector
+// per spec); returns a status and sets the error message.
+int read_checkpoint(const char* path, std::vector<std::vector<float>>& out) {
+    const std::string who = "load_file: ";
+    std::unique_ptr<std::FILE, FileCloser> f(std::fopen(path, "rb"));
+    if (!f) return fail(BVML_DSINE_EFILE, who + "cannot open '" + path + "'");
+    if (std::fseek(f.get(), 0, SEEK_END) != 0)
+        return fail(BVML_DSINE_EFILE, who + "cannot seek '" + path + "'");
+    const long long size = std::ftell(f.get());
+    std::rewind(f.get());
+    unsigned char len8[8];
+    if (size < 8 || std::fread(len8, 1, 8, f.get()) != 8)
+        return fail(BVML_DSINE_EFILE, who + "'" + path + "' is too short for a safetensors file");
+    unsigned long long hlen = 0;
+    for (int i = 7; i >= 0; --i) hlen = (hlen << 8) | len8[i];
+    if (hlen == 0 || hlen > 100000000ull || (long long)hlen > size - 8)
+        return fail(BVML_DSINE_EFILE, who + "'" + path + "' has a bad header length");
+    std::string header(hlen, '\0');
+    if (std::fread(&header[0], 1, hlen, f.get()) != hlen)
+        return fail(BVML_DSINE_EFILE, who + "cannot read the header of '" + path + "'");
+    Json root;
+    if (!JsonParser(header.data(), header.data() + header.size()).document(root) ||
+        root.kind != Json::Obj)
+        return fail(BVML_DSINE_EFILE, who + "'" + path + "' has a malformed JSON header");
+    const long long data0 = 8 + (long long)hlen, data_bytes = size - data0;
+
+    const auto& s = specs();
+    std::vector<std::vector<float>> got(s.size());
+    for (size_t i = 0; i < s.size(); ++i) {
+        const std::string& name = s[i].name;
+        const Json* t = root.get(name);
+        if (!t) return fail(BVML_DSINE_EWEIGHTS, who + "missing tensor '" + name + "'");
+        const Json* dt = t->get("dtype");
+        const Json* shape = t->get("shape");
+        const Json* offs = t->get("data_offsets");
+        if (t->kind != Json::Obj || !dt || dt->kind != Json::Str || !shape ||
+            shape->kind != Json::Arr || !offs || offs->kind != Json::Arr || offs->arr.size() != 2 ||
+            !offs->arr[0].integral || !offs->arr[1].integral)
+            return fail(BVML_DSINE_EFILE, who + "tensor '" + name + "' has a malformed entry");
+        int item;
+        if (dt->str == "F32") item = 4;
+        else if (dt->str == "F16" || dt->str == "BF16") item = 2;
+        else
+            return fail(BVML_DSINE_EWEIGHTS,
+                        who + "unsupported dtype " + dt->str + " (key '" + name + "')");
+        long long numel = 1;
+        for (const Json& d : shape->arr) {
+            if (!d.integral || d.uint > (1ull << 40))
+                return fail(BVML_DSINE_EFILE, who + "tensor '" + name + "' has a bad shape");
+            numel *= (long long)d.uint;
+            if (numel > (1ll << 40))
+                return fail(BVML_DSINE_EFILE, who + "tensor '" + name + "' has a bad shape");
+        }
+        if (numel != s[i].numel)
+            return fail(BVML_DSINE_EWEIGHTS, who + "tensor '" + name + "' has " +
+                                                 std::to_string(numel) + " elements, expected " +
+                                                 std::to_string(s[i].numel));
+        if (shape->arr.empty() || (long long)shape->arr[0].uint != s[i].c_out)
+            return fail(BVML_DSINE_EWEIGHTS, who + "tensor '" + name + "' has " +
+                                                 std::to_string(shape->arr.empty()
+                                                                    ? 0ull
+                                                                    : shape->arr[0].uint) +
+                                                 " output channels, expected " +
+                                                 std::to_string(s[i].c_out));
+        const unsigned long long b = offs->arr[0].uint, e = offs->arr[1].uint;
+        if (e < b || e > (unsigned long long)data_bytes ||
+            e - b != (unsigned long long)numel * item)
+            return fail(BVML_DSINE_EFILE, who + "tensor '" + name + "' has bad data offsets");
+        std::vector<unsigned char> raw(e - b);
+        if (std::fseek(f.get(), (long)(data0 + (long long)b), SEEK_SET) != 0 ||
+            std::fread(raw.data(), 1, raw.size(), f.get()) != raw.size())
+            return fail(BVML_DSINE_EFILE, who + "cannot read tensor '" + name + "'");
+        std::vector<float>& dst = got[i];
+        dst.resize((size_t)numel);
+        for (long long j = 0; j < numel; ++j) {
+            const unsigned char* q = raw.data() + j * item;
+            if (item == 4) {
+                uint32_t bits = (uint32_t)q[0] | ((uint32_t)q[1] << 8) | ((uint32_t)q[2] << 16) |
+                                ((uint32_t)q[3] << 24);
+                std::memcpy(&dst[j], &bits, 4);
+            } else {
+                const uint16_t h = (uint16_t)(q[0] | (q[1] << 8));
+                dst[j] = dt->str == "F16" ? half_to_float(h) : bf16_to_float(h);
+            }
+        }
+    }
+    out = std::move(got);
+    return BVML_DSINE_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Device side
+// ---------------------------------------------------------------------------
+int hip_fail(hipError_t e, const std::string& what) {
+    return fail((int)e, "forward: " + what + ": " + hipGetErrorString(e));
+}
+
+int mio_fail(miopenStatus_t s, const std::string& what) {
+    return fail(BVML_DSINE_ELIB,
+                "forward: MIOpen " + what + ": " + miopenGetErrorString(s));
+}
+
+struct ConvPlan {
+    miopenTensorDescriptor_t x = nullptr, w = nullptr, y = nullptr;
+    miopenConvolutionDescriptor_t conv = nullptr;
+    uint64_t solution = 0;
+    size_t ws = 0;
+
+    void reset() {
+        if (x) miopenDestroyTensorDescriptor(x);
+        if (w) miopenDestroyTensorDescriptor(w);
+        if (y) miopenDestroyTensorDescriptor(y);
+        if (conv) miopenDestroyConvolutionDescriptor(conv);
+        *this = ConvPlan{};
+    }
+};
+
+// Restores the caller's current device on scope exit.
+class DeviceScope {
+public:
+    explicit DeviceScope(int dev) {
+        if (hipGetDevice(&prev_) != hipSuccess) prev_ = -1;
+        if (prev_ != dev) status_ = hipSetDevice(dev);
+    }
+    ~DeviceScope() {
+        int cur = -1;
+        if (prev_ >= 0 && hipGetDevice(&cur) == hipSuccess && cur != prev_)
+            (void)hipSetDevice(prev_);
+    }
+    hipError_t status() const { return status_; }
+
+private:
+    int prev_ = -1;
+    hipError_t status_ = hipSuccess;
+};
+
+size_t round64(size_t n) { return (n + 63) & ~(size_t)63; }
+
+}  // namespace
+
+struct bvml_dsine_refiner {
+    std::vector<std::vector<float>> host = std::vector<std::vector<float>>(specs().size());
+    bool dirty = true;  // host weights newer than the device copy
+
+    int device = -1;  // bound at the first forward
+    miopenHandle_t mio = nullptr;
+
+    // weights on the device, one allocation
+    float* warena = nullptr;
+    const float *w_zr = nullptr, *b_z = nullptr, *b_r = nullptr, *w_q = nullptr, *b_q = nullptr;
+    const float *w_h0 = nullptr, *b_h0 = nullptr, *w_h2 = nullptr, *b_h2 = nullptr;
+    const float* w4[kHeads] = {};
+    const float* b4[kHeads] = {};
+
+    // the maps of one grid size, one allocation
+    int H = 0, W = 0;
+    float* arena = nullptr;
+    float *hx = nullptr, *rhx = nullptr, *hin = nullptr, *zr = nullptr, *z = nullptr;
+    float *qp = nullptr, *t0 = nullptr, *t1 = nullptr, *head[kHeads] = {}, *ray = nullptr;
+    float *pred[2] = {}, *up = nullptr;
+    void* ws = nullptr;
+    size_t ws_bytes = 0;
+    // [0]: the three heads the propagate reads, [1]: all four
+    ConvPlan zr_p, q_p, h0_p[2], h2_p[2], c4_p[kHeads];
+
+    void drop_grid() {
+        zr_p.reset();
+        q_p.reset();
+        for (auto& p : h0_p) p.reset();
+        for (auto& p : h2_p) p.reset();
+        for (auto& p : c4_p) p.reset();
+        if (arena) (void)hipFree(arena);
+        if (ws) (void)hipFree(ws);
+        arena = nullptr;
+        ws = nullptr;
+        ws_bytes = 0;
+        H = W = 0;
+    }
+
+    ~bvml_dsine_refiner() {
+        if (device < 0) return;
+        DeviceScope scope(device);
+        drop_grid();
+        if (warena) (void)hipFree(warena);
+        if (mio) miopenDestroy(mio);
+    }
+
+    int upload();
+    int plan(int H, int W);
+    int make_plan(ConvPlan& p, int cin, int cout, int k, int groups, int H, int W);
+    int conv(const ConvPlan& p, const float* w, const float* x, float* y);
+};
+
+// Copies the host weights into the device arena, in the layout the
+// convolutions read: [W_z; W_r] as one 128-filter weight, the four heads'
+// first layers as one 256-filter weight and their middle layers as one
+// 4-group weight (each head's filters contiguous, prob, xy, angle, up_mask:
+// the first three heads are a prefix).
+int bvml_dsine_refiner::upload() {
+    const auto& s = specs();
+    std::vector<std::pair<const float**, std::vector<int>>> parts;
+    parts.push_back({&w_zr, {kZw, kRw}});
+    parts.push_back({&b_z, {kZb}});
+    parts.push_back({&b_r, {kRb}});
+    parts.push_back({&w_q, {kQw}});
+    parts.push_back({&b_q, {kQb}});
+    std::vector<int> h0w, h0b, h2w, h2b;
+    for (int h = 0; h < kHeads; ++h) {
+        h0w.push_back(head_w(h, 0));
+        h0b.push_back(head_b(h, 0));
+        h2w.push_back(head_w(h, 1));
+        h2b.push_back(head_b(h, 1));
+    }
+    parts.push_back({&w_h0, h0w});
+    parts.push_back({&b_h0, h0b});
+    parts.push_back({&w_h2, h2w});
+    parts.push_back({&b_h2, h2b});
+    for (int h = 0; h < kHeads; ++h) {
+        parts.push_back({&w4[h], {head_w(h, 2)}});
+        parts.push_back({&b4[h], {head_b(h, 2)}});
+    }
+    std::vector<size_t> offset;
+    size_t total = 0;
+    for (const auto& p : parts) {
+        offset.push_back(total);
+        size_t n = 0;
+        for (int i : p.second) n += (size_t)s[i].numel;
+        total += round64(n);
+    }
+    std::vector<float> staging(total, 0.0f);
+    for (size_t k = 0; k < parts.size(); ++k) {
+        size_t at = offset[k];
+        for (int i : parts[k].second) {
+            std::memcpy(&staging[at], host[i].data(), host[i].size() * sizeof(float));
+            at += host[i].size();
+        }
+    }
+    if (!warena) {
+        const hipError_t e = hipMalloc(&warena, total * sizeof(float));
+        if (e != hipSuccess) {
+            warena = nullptr;
+            return hip_fail(e, "hipMalloc of the weights");
+        }
+    }
+    const hipError_t e = hipMemcpy(warena, staging.data(), total * sizeof(float),
+                                   hipMemcpyHostToDevice);
+    if (e != hipSuccess) return hip_fail(e, "weight upload");
+    for (size_t k = 0; k < parts.size(); ++k) *parts[k].first = warena + offset[k];
+    dirty = false;
+    return BVML_DSINE_OK;
+}
+
+int bvml_dsine_refiner::make_plan(ConvPlan& p, int cin, int cout, int k, int groups, int H,
+                                  int W) {
+    miopenStatus_t st;
+    if ((st = miopenCreateTensorDescriptor(&p.x)) != miopenStatusSuccess ||
+        (st = miopenSet4dTensorDescriptor(p.x, miopenFloat, 1, cin, H, W)) != miopenStatusSuccess ||
+        (st = miopenCreateTensorDescriptor(&p.w)) != miopenStatusSuccess ||
+        (st = miopenSet4dTensorDescriptor(p.w, miopenFloat, cout, cin / groups, k, k)) !=
+            miopenStatusSuccess ||
+        (st = miopenCreateTensorDescriptor(&p.y)) != miopenStatusSuccess ||
+        (st = miopenSet4dTensorDescriptor(p.y, miopenFloat, 1, cout, H, W)) != miopenStatusSuccess ||
+        (st = miopenCreateConvolutionDescriptor(&p.conv)) != miopenStatusSuccess ||
+        (st = miopenInitConvolutionDescriptor(p.conv, miopenConvolution, k / 2, k / 2, 1, 1, 1,
+                                              1)) != miopenStatusSuccess ||
+        (groups > 1 &&
+         (st = miopenSetConvolutionGroupCount(p.conv, groups)) != miopenStatusSuccess))
+        return mio_fail(st, "descriptors");
+    size_t count = 0;
+    if ((st = miopenConvolutionForwardGetSolutionCount(mio, p.w, p.x, p.conv, p.y, &count)) !=
+        miopenStatusSuccess)
+        return mio_fail(st, "solution count");
+    if (count == 0) return fail(BVML_DSINE_ELIB, "forward: MIOpen has no solution for a convolution");
+    std::vector<miopenConvSolution_t> sols(count);
+    size_t got = 0;
+    if ((st = miopenConvolutionForwardGetSolution(mio, p.w, p.x, p.conv, p.y, count, &got,
+                                                  sols.data())) != miopenStatusSuccess)
+        return mio_fail(st, "solutions");
+    if (got == 0) return fail(BVML_DSINE_ELIB, "forward: MIOpen has no solution for a convolution");
+    size_t best = 0;
+    for (size_t i = 1; i < got; ++i)
+        if (sols[i].time < sols[best].time) best = i;
+    p.solution = sols[best].solution_id;
+    p.ws = sols[best].workspace_size;
+    if ((st = miopenConvolutionForwardCompileSolution(mio, p.w, p.x, p.conv, p.y, p.solution)) !=
+        miopenStatusSuccess)
+        return mio_fail(st, "compile");
+    return BVML_DSINE_OK;
+}
+
+// Allocates the maps of an H x W grid and plans its convolutions.
+int bvml_dsine_refiner::plan(int h, int w) {
+    if (arena && H == h && W == w) return BVML_DSINE_OK;
+    drop_grid();
+    const size_t hw = (size_t)h * w;
+    const int planes[] = {kHx, kHx, kHin, 2 * kHidden, kHidden, kHidden, kHeads * kMid,
+                          kHeads * kMid, kHeadOut[0], kHeadOut[1], kHeadOut[2], kHeadOut[3],
+                          3, 3, 3, 3 * kUp * kUp};
+    float** dst[] = {&hx, &rhx, &hin, &zr, &z, &qp, &t0, &t1, &head[0], &head[1], &head[2],
+                     &head[3], &pred[0], &pred[1], &ray, &up};
+    size_t total = 0;
+    std::vector<size_t> offset;
+    for (int c : planes) {
+        offset.push_back(total);
+        total += round64((size_t)c * hw);
+    }
+    hipError_t e = hipMalloc(&arena, total * sizeof(float));
+    if (e != hipSuccess) {
+        arena = nullptr;
+        return hip_fail(e, "hipMalloc of the maps");
+    }
+    for (size_t i = 0; i < offset.size(); ++i) *dst[i] = arena + offset[i];
+    int st;
+    if ((st = make_plan(zr_p, kHx, 2 * kHidden, 5, 1, h, w)) ||
+        (st = make_plan(q_p, kHx, kHidden, 5, 1, h, w)))
+        return drop_grid(), st;
+    for (int i = 0; i < 2; ++i) {
+        const int nh = 3 + i;
+        if ((st = make_plan(h0_p[i], kHin, nh * kMid, 3, 1, h, w)) ||
+            (st = make_plan(h2_p[i], nh * kMid, nh * kMid, 1, nh, h, w)))
+            return drop_grid(), st;
+    }
+    for (int i = 0; i < kHeads; ++i)
+        if ((st = make_plan(c4_p[i], kMid, kHeadOut[i], 1, 1, h, w))) return drop_grid(), st;
+    size_t need = 0;
+    for (const ConvPlan* p : {&zr_p, &q_p, &h0_p[0], &h0_p[1], &h2_p[0], &h2_p[1], &c4_p[0],
+                              &c4_p[1], &c4_p[2], &c4_p[3]})
+        need = p->ws > need ? p->ws : need;
+    if (need) {
+        e = hipMalloc(&ws, need);
+        if (e != hipSuccess) {
+            ws = nullptr;
+            drop_grid();
+            return hip_fail(e, "hipMalloc of the MIOpen workspace");
+        }
+        ws_bytes = need;
+    }
+    H = h;
+    W = w;
+    return BVML_DSINE_OK;
+}
+
+int bvml_dsine_refiner::conv(const ConvPlan& p, const float* w, const float* x, float* y) {
+    const miopenStatus_t st = miopenConvolutionForwardImmediate(mio, p.w, w, p.x, x, p.conv, p.y, y,
+                                                                ws, ws_bytes, p.solution);
+    return st == miopenStatusSuccess ? BVML_DSINE_OK : mio_fail(st, "convolution");
+}
+
+// ---------------------------------------------------------------------------
+// C ABI
+// ---------------------------------------------------------------------------
+extern "C" {
+
+int bvml_dsine_refiner_create(bvml_dsine_refiner** out) {
+    if (!out) return fail(BVML_DSINE_ENULL, "create: out must be non-NULL");
+    *out = new (std::nothrow) bvml_dsine_refiner();
+    if (!*out) return fail(BVML_DSINE_ESIZE, "create: out of host memory");
+    return BVML_DSINE_OK;
+}
+
+void bvml_dsine_refiner_destroy(bvml_dsine_refiner* r) { delete r; }
+
+long long bvml_dsine_refiner_tensor_numel(const char* name) {
+    if (!name) return -1;
+    const int i = spec_index(name);
+    return i < 0 ? -1 : specs()[i].numel;
+}
+
+int bvml_dsine_refiner_load_file(bvml_dsine_refiner* r, const char* path) {
+    if (!r || !path) return fail(BVML_DSINE_ENULL, "load_file: refiner and path must be non-NULL");
+    std::vector<std::vector<float>> got;
+    const int st = read_checkpoint(path, got);
+    if (st != BVML_DSINE_OK) return st;
+    r->host = std::move(got);
+    r->dirty = true;
+    return BVML_DSINE_OK;
+}
+
+int bvml_dsine_refiner_set_tensor(bvml_dsine_refiner* r, const char* name, const float* data,
+                                  long long numel) {
+    if (!r || !name || !data)
+        return fail(BVML_DSINE_ENULL, "set_tensor: refiner, name and data must be non-NULL");
+    const int i = spec_index(name);
+    if (i < 0) return fail(BVML_DSINE_EWEIGHTS, std::string("set_tensor: unknown tensor '") + name +
+                                                    "'");
+    if (numel != specs()[i].numel)
+        return fail(BVML_DSINE_EWEIGHTS, std::string("set_tensor: tensor '") + name + "' has " +
+                                             std::to_string(numel) + " elements, expected " +
+                                             std::to_string(specs()[i].numel));
+    r->host[i].assign(data, data + numel);
+    r->dirty = true;
+    return BVML_DSINE_OK;
+}
+
+int bvml_dsine_refiner_get_tensor(const bvml_dsine_refiner* r, const char* name, float* data,
+                                  long long numel) {
+    if (!r || !name || !data)
+        return fail(BVML_DSINE_ENULL, "get_tensor: refiner, name and data must be non-NULL");
+    const int i = spec_index(name);
+    if (i < 0) return fail(BVML_DSINE_EWEIGHTS, std::string("get_tensor: unknown tensor '") + name +
+                                                    "'");
+    if (r->host[i].empty())
+        return fail(BVML_DSINE_EWEIGHTS, std::string("get_tensor: tensor '") + name + "' not set");
+    if (numel != specs()[i].numel)
+        return fail(BVML_DSINE_EWEIGHTS, std::string("get_tensor: tensor '") + name + "' has " +
+                                             std::to_string(specs()[i].numel) + " elements, not " +
+                                             std::to_string(numel));
+    std::memcpy(data, r->host[i].data(), (size_t)numel * sizeof(float));
+    return BVML_DSINE_OK;
+}
+
+const char* bvml_dsine_refiner_last_error(void) { return g_last_error.c_str(); }
+
+int bvml_dsine_refiner_forward(bvml_dsine_refiner* r, const float* normal, const float* feature,
+                               const float* hidden, int h8, int w8, float fx, float fy,
+                               float cx, float cy, int orig_h, int orig_w, int pad_t, int pad_l,
+                               int out_h, int out_w, float* out, float* coarse, void* stream) {
+    if (!r || !normal || !feature || !hidden || !out)
+        return fail(BVML_DSINE_ENULL,
+                    "forward: refiner, normal, feature, hidden and out must be non-NULL");
+    if (h8 < 1 || w8 < 1 || orig_h < 1 || orig_w < 1)
+        return fail(BVML_DSINE_ESHAPE, "forward: h8, w8, orig_h and orig_w must be >= 1");
+    const long long fh = (long long)kUp * h8, fw = (long long)kUp * w8;
+    if (pad_t < 0 || pad_l < 0 || out_h < 1 || out_w < 1 || pad_t + (long long)out_h > fh ||
+        pad_l + (long long)out_w > fw)
+        return fail(BVML_DSINE_ESHAPE, "forward: the crop (pad_t " + std::to_string(pad_t) +
+                                           ", pad_l " + std::to_string(pad_l) + ", " +
+                                           std::to_string(out_h) + " x " + std::to_string(out_w) +
+                                           ") must lie inside the " + std::to_string(fh) + " x " +
+                                           std::to_string(fw) + " result");
+    if (3 * fh * fw > 0x7FFFFFFFll)
+        return fail(BVML_DSINE_ESIZE, "forward: 3 x 8h8 x 8w8 exceeds a tensor row");
+    if (!std::isfinite(fx) || !std::isfinite(fy) || fx == 0.0f || fy == 0.0f ||
+        !std::isfinite(cx) || !std::isfinite(cy))
+        return fail(BVML_DSINE_EPARAM, "forward: fx, fy must be finite and non-zero, cx, cy finite");
+    const auto& s = specs();
+    for (size_t i = 0; i < s.size(); ++i)
+        if (r->host[i].empty())
+            return fail(BVML_DSINE_EWEIGHTS, "forward: tensor '" + s[i].name + "' not set");
+    const size_t hw = (size_t)h8 * w8, b = sizeof(float);
+    const size_t outb = (size_t)3 * out_h * out_w * b;
+    for (const auto& in : {std::make_pair((const void*)normal, 3 * hw * b),
+                           std::make_pair((const void*)feature, kFeature * hw * b),
+                           std::make_pair((const void*)hidden, kHidden * hw * b)}) {
+        if (overlaps(out, outb, in.first, in.second) ||
+            (coarse && overlaps(coarse, kIter * 3 * hw * b, in.first, in.second)))
+            return fail(BVML_DSINE_EALIAS, "forward: out and coarse must not overlap the inputs");
+    }
+    if (coarse && overlaps(coarse, kIter * 3 * hw * b, out, outb))
+        return fail(BVML_DSINE_EALIAS, "forward: out and coarse must not overlap");
+
+    if (r->device < 0) {
+        int d = 0;
+        const hipError_t e = hipGetDevice(&d);
+        if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+        r->device = d;
+    }
+    DeviceScope scope(r->device);
+    if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
+    miopenStatus_t ms;
+    if (!r->mio && (ms = miopenCreate(&r->mio)) != miopenStatusSuccess) {
+        r->mio = nullptr;
+        return mio_fail(ms, "handle");
+    }
+    int st;
+    if (r->dirty && (st = r->upload()) != BVML_DSINE_OK) return st;
+    if ((st = r->plan(h8, w8)) != BVML_DSINE_OK) return st;
+    const hipStream_t strm = static_cast<hipStream_t>(stream);
+    if ((ms = miopenSetStream(r->mio, strm)) != miopenStatusSuccess) return mio_fail(ms, "stream");
+
+    // the grid-scaled intrinsics (src/dsine_refine.cpp:232-237)
+    const double sw = (double)w8 / orig_w, sh = (double)h8 / orig_h;
+    const double fu = fx * sw, cu = (cx + 0.5) * sw, fv = fy * sh, cv = (cy + 0.5) * sh;
+    const int C = kHidden;
+    const long long HW = (long long)hw;
+    auto copy = [&](float* dst, const float* src, size_t planes) {
+        return hipMemcpyAsync(dst, src, planes * hw * b, hipMemcpyDeviceToDevice, strm);
+    };
+    // a kernel library status, with its message
+    auto ck = [](int status, const char* what) {
+        return status == BVML_DSINE_OK
+                   ? BVML_DSINE_OK
+                   : fail(status, std::string("forward: ") + what + ": " + bvml_dsine_last_error());
+    };
+    hipError_t e;
+    // hx = [h | feature | uv], rhx = [r*h | feature | uv], hin = [h_new | uv]
+    float* uv = r->hx + (size_t)(kHidden + kFeature) * hw;
+    if ((st = ck(bvml_dsine_build_uv8_f32(uv, fu, cu, fv, cv, h8, w8, stream), "build_uv8")) ||
+        (st = ck(bvml_dsine_build_ray8_f32(r->ray, fu, cu, fv, cv, h8, w8, stream), "build_ray8")))
+        return st;
+    if ((e = copy(r->hx, hidden, kHidden)) != hipSuccess ||
+        (e = copy(r->hx + (size_t)kHidden * hw, feature, kFeature)) != hipSuccess ||
+        (e = copy(r->rhx + (size_t)kHidden * hw, r->hx + (size_t)kHidden * hw, kX)) != hipSuccess ||
+        (e = copy(r->hin + (size_t)kHidden * hw, uv, 2)) != hipSuccess ||
+        (e = copy(r->pred[0], normal, 3)) != hipSuccess)
+        return hip_fail(e, "hipMemcpyAsync");
+    // pred_norm = RayReLU(decoder.normal, ray_8)  (:240-242)
+    if ((st = ck(bvml_dsine_ray_relu_f32(r->pred[0], r->ray, 1, h8, w8, 0, stream), "ray_relu")))
+        return st;
+
+    const bool direct = pad_t == 0 && pad_l == 0 && out_h == fh && out_w == fw;
+    int cur = 0;
+    for (int it = 0; it < kIter; ++it) {
+        const bool last = it == kIter - 1;
+        const int nh = last ? kHeads : kHeads - 1;
+        // ConvGRU (:138-159); h_new overwrites h in hx and is copied into hin
+        if ((st = r->conv(r->zr_p, r->w_zr, r->hx, r->zr)) ||
+            (st = ck(bvml_dsine_gru_gates_f32(r->zr, r->b_z, r->b_r, r->hx, C, HW, r->z, r->rhx,
+                                              stream), "gru_gates")) ||
+            (st = r->conv(r->q_p, r->w_q, r->rhx, r->qp)) ||
+            (st = ck(bvml_dsine_gru_update_f32(r->qp, r->b_q, r->z, r->hx, C, HW, r->hx, r->hin,
+                                               stream), "gru_update")))
+            return st;
+        // the heads (:119-127, :257-267, :276)
+        const ConvPlan& h0 = r->h0_p[last ? 1 : 0];
+        const ConvPlan& h2 = r->h2_p[last ? 1 : 0];
+        if ((st = r->conv(h0, r->w_h0, r->hin, r->t0)) ||
+            (st = ck(bvml_dsine_bias_act_f32(r->t0, r->b_h0, nh * kMid, HW, 1, stream), "bias_act")) ||
+            (st = r->conv(h2, r->w_h2, r->t0, r->t1)) ||
+            (st = ck(bvml_dsine_bias_act_f32(r->t1, r->b_h2, nh * kMid, HW, 1, stream), "bias_act")))
+            return st;
+        for (int h = 0; h < kHeads - 1; ++h)
+            if ((st = r->conv(r->c4_p[h], r->w4[h], r->t1 + (size_t)h * kMid * hw, r->head[h])) ||
+                (st = ck(bvml_dsine_bias_act_f32(r->head[h], r->b4[h], kHeadOut[h], HW, 0, stream),
+                         "bias_act")))
+                return st;
+        // the propagate on the logits (:262-274)
+        if ((st = ck(bvml_dsine_angmf_propagate_f32(r->pred[cur], r->head[0], r->head[1],
+                                                    r->head[2], r->ray, fu, cu, fv, cv, 1, h8, w8,
+                                                    kPs, 0, r->pred[cur ^ 1], BVML_DSINE_LOGITS,
+                                                    stream), "angmf_propagate")))
+            return st;
+        cur ^= 1;
+        if (coarse && (e = copy(coarse + (size_t)it * 3 * hw, r->pred[cur], 3)) != hipSuccess)
+            return hip_fail(e, "hipMemcpyAsync");
+        if (!last) continue;
+        // up_pred_norm = normalize(convex_upsample(pred_norm, up_mask))  (:276-283)
+        float* dst = direct ? out : r->up;
+        if ((st = r->conv(r->c4_p[3], r->w4[3], r->t1 + (size_t)3 * kMid * hw, r->head[3])) ||
+            (st = ck(bvml_dsine_convex_upsample_bias_f32(r->pred[cur], r->head[3], r->b4[3], 1, 3,
+                                                         h8, w8, kUp, 1, kUpEps, dst, 0, stream),
+                     "convex_upsample")))
+            return st;
+    }
+    if (!direct) {
+        // the crop to the unpadded image (:289-293)
+        for (int c = 0; c < 3; ++c) {
+            const float* src = r->up + (size_t)c * fh * fw + (size_t)pad_t * fw + pad_l;
+            e = hipMemcpy2DAsync(out + (size_t)c * out_h * out_w, (size_t)out_w * b, src,
+                                 (size_t)fw * b, (size_t)out_w * b, (size_t)out_h,
+                                 hipMemcpyDeviceToDevice, strm);
+            if (e != hipSuccess) return hip_fail(e, "hipMemcpy2DAsync");
+        }
+    }
+    return BVML_DSINE_OK;
+}
+
+}  // extern "C"

@@ -236,3 +236,81 @@ class Refiner:
             return up
         return up[:, :, crop.pad_t:crop.pad_t + crop.orig_h,
                   crop.pad_l:crop.pad_l + crop.orig_w].contiguous()
+
+
+class NativeRefiner:
+    """Refiner::forward in C++ (libbvml_dsine_refine.so, the C ABI of
+    include/bvml_dsine_refine.h): the same loop as Refiner above, with no
+    Python or torch in it; the convolutions on MIOpen's immediate mode, the
+    rest this package's kernels, the up-mask head and the upsample in the
+    last iteration only.  Weights from a safetensors file (`path`, read by
+    the library) or a dict as weight_shapes() names them."""
+
+    def __init__(self, weights: dict | None = None, path: str | None = None):
+        import ctypes
+        from . import _lib
+        self._lib = _lib.load_refine()
+        h = ctypes.c_void_p()
+        self._check("create", self._lib.bvml_dsine_refiner_create(ctypes.byref(h)))
+        self._h = h
+        if path is not None:
+            self.load_file(path)
+        if weights is not None:
+            for name in weight_shapes():
+                self.set_tensor(name, weights[name])
+
+    def __del__(self):
+        h = getattr(self, "_h", None)
+        if h is not None and h.value:
+            self._lib.bvml_dsine_refiner_destroy(h)
+            self._h = None
+
+    def _check(self, op: str, status: int) -> None:
+        if status != 0:
+            from . import _lib
+            raise RuntimeError(f"dsine::Refiner: {_lib.refine_last_error()} (status {status})")
+
+    def load_file(self, path: str) -> None:
+        self._check("load_file", self._lib.bvml_dsine_refiner_load_file(self._h, path.encode()))
+
+    def set_tensor(self, name: str, value) -> None:
+        a = np.ascontiguousarray(np.asarray(value, np.float32)).reshape(-1)
+        self._check("set_tensor", self._lib.bvml_dsine_refiner_set_tensor(
+            self._h, name.encode(), a.ctypes.data, a.size))
+
+    def get_tensor(self, name: str) -> np.ndarray:
+        n = self._lib.bvml_dsine_refiner_tensor_numel(name.encode())
+        if n < 0:
+            raise RuntimeError(f"dsine::Refiner: unknown tensor '{name}'")
+        a = np.empty(n, np.float32)
+        self._check("get_tensor", self._lib.bvml_dsine_refiner_get_tensor(
+            self._h, name.encode(), a.ctypes.data, n))
+        return a
+
+    def forward(self, dec: DecoderOutput, intr: workloads.Intrinsics, orig_h: int, orig_w: int,
+                crop: Crop | None = None, coarse: bool = False, out=None):
+        """The refined normals (1, 3, h, w) at the unpadded resolution (the
+        whole 8*h8 x 8*w8 map without crop); with coarse=True also each
+        iteration's propagated /8-grid normal, (N_ITER, 3, h8, w8).  `out`,
+        when given, is the result tensor to fill (so the call allocates
+        nothing once the refiner has run at this grid size)."""
+        import torch
+        _, _, H, W = dec.normal.shape
+        for t in (dec.normal, dec.feature, dec.hidden):
+            if t.device.type != "cuda" or t.dtype != torch.float32 or not t.is_contiguous():
+                raise RuntimeError("dsine::Refiner: decoder maps must be contiguous fp32 on the "
+                                   "GPU")
+        c = crop if crop is not None else Crop(8 * H, 8 * W)
+        dev = dec.normal.device
+        if out is None:
+            out = torch.empty((1, 3, c.orig_h, c.orig_w), dtype=torch.float32, device=dev)
+        cz = (torch.empty((N_ITER, 3, H, W), dtype=torch.float32, device=dev) if coarse
+              else None)
+        with torch.cuda.device(dev):
+            st = self._lib.bvml_dsine_refiner_forward(
+                self._h, dec.normal.data_ptr(), dec.feature.data_ptr(), dec.hidden.data_ptr(),
+                H, W, intr.fx, intr.fy, intr.cx, intr.cy, orig_h, orig_w, c.pad_t, c.pad_l,
+                c.orig_h, c.orig_w, out.data_ptr(), cz.data_ptr() if cz is not None else None,
+                torch.cuda.current_stream(dev).cuda_stream)
+        self._check("forward", st)
+        return (out, cz) if coarse else out

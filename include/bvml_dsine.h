@@ -126,6 +126,17 @@ int bvml_dsine_build_ray8_f32(float* ray, double fu, double cu, double fv,
                               double cv, int H, int W, void* stream);
 
 /*
+ * The /8-grid uv map, 2 x H x W fp32 planes, as the reference's build_uv
+ * (src/dsine_decoder.cpp:262-274, through get_ray_core :242-259) forms it on
+ * the host: u = float(((x + 0.5) - cu) / fu), v = float(((y + 0.5) - cv) / fv),
+ * bit-identical to the host's; the same fu, cu, fv, cv as build_ray8.  No
+ * counterpart on the reference's device path (the refiner builds the map on
+ * the host and copies it over, src/dsine_refine.cpp:222-228).
+ */
+int bvml_dsine_build_uv8_f32(float* uv, double fu, double cu, double fv, double cv, int H,
+                             int W, void* stream);
+
+/*
  * Convex upsample by `scale` with a 9-tap softmax mask, fused with the channel
  * L2-normalise (normalize != 0), B samples.  Replaces the two brotensor calls
  * the refiner makes after each propagate (src/dsine_refine.cpp:276-282:

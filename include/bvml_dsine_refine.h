@@ -1,0 +1,105 @@
+/*
+ * bvml_dsine_refine.h -- C ABI of the native NRN refiner: DSINE's
+ * 5-iteration refinement loop on one HIP device (MI355X, gfx950).
+ *
+ * It replaces brovisionml's Refiner (the reference's
+ * include/brovisionml/dsine_refine.h:113-145, src/dsine_refine.cpp:161-294):
+ * the same weights, the same loop and the same result, in C++ over this
+ * library's kernels (bvml_dsine.h) -- RayReLU, the propagate on the heads'
+ * raw logits, the fused ConvGRU and head elementwise steps, the convex
+ * upsample with its mask bias -- with the ConvGRU's and heads'
+ * convolutions on MIOpen (fp32, immediate mode).  The C++ class of
+ * include/brovisionml/dsine_refine.h sits on top of it.
+ *
+ * Lifecycle: create (no HIP call) -> weights (load_file, or set_tensor per
+ * tensor) -> forward, any number of times, at any grid size -> destroy.
+ * The first forward binds the refiner to the calling thread's current HIP
+ * device; later forwards make that device current and restore the caller's.
+ * The first forward after a weight change uploads the weights (a
+ * synchronous copy), and the first forward at a grid size allocates its
+ * buffers and plans its convolutions: run one forward eagerly before
+ * capturing forwards into a HIP graph.  Calls on one refiner must not
+ * overlap; distinct refiners are independent.
+ *
+ * Return value: 0 on success, a negative BVML_DSINE_E* code for a rejected
+ * argument or missing weights (nothing is launched), a positive hipError_t
+ * value for a HIP runtime error.  bvml_dsine_refiner_last_error() returns
+ * the calling thread's message for the last non-zero status.
+ */
+#ifndef BVML_DSINE_REFINE_H
+#define BVML_DSINE_REFINE_H
+
+#include "bvml_dsine.h"
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define BVML_DSINE_EWEIGHTS (-9)  /* a checkpoint tensor missing, of the wrong size or dtype */
+#define BVML_DSINE_EFILE (-10)    /* the checkpoint cannot be read or is not safetensors */
+#define BVML_DSINE_ELIB (-11)     /* MIOpen reported an error */
+
+typedef struct bvml_dsine_refiner bvml_dsine_refiner;
+
+/* A refiner with no weights; makes no HIP call. */
+int bvml_dsine_refiner_create(bvml_dsine_refiner** out);
+
+/* Frees the refiner's device memory and MIOpen state (NULL is a no-op). */
+void bvml_dsine_refiner_destroy(bvml_dsine_refiner* r);
+
+/*
+ * Loads every refiner tensor from a safetensors checkpoint: the top-level
+ * gru.conv{z,r,q}.{weight,bias} and {prob,xy,angle,up_prob}_head.{0,2,4}.
+ * {weight,bias} (src/dsine_refine.cpp:51-91, :185-195), F32, F16 or BF16,
+ * widened to fp32 as the reference's loader widens them (src/weights_util.h:27-63).
+ * Other tensors in the file are ignored.  On error nothing changes.
+ */
+int bvml_dsine_refiner_load_file(bvml_dsine_refiner* r, const char* path);
+
+/*
+ * Sets one tensor, by its checkpoint name, from numel host fp32 values
+ * (weights in OIHW order).  numel must be what the name holds:
+ * bvml_dsine_refiner_tensor_numel(name).
+ */
+int bvml_dsine_refiner_set_tensor(bvml_dsine_refiner* r, const char* name, const float* data,
+                                  long long numel);
+
+/* The element count of the named checkpoint tensor, -1 for a name the
+ * refiner does not read. */
+long long bvml_dsine_refiner_tensor_numel(const char* name);
+
+/* Copies a tensor the refiner holds back to numel host floats (for tests).
+ * BVML_DSINE_EWEIGHTS if it has not been set. */
+int bvml_dsine_refiner_get_tensor(const bvml_dsine_refiner* r, const char* name, float* data,
+                                  long long numel);
+
+/*
+ * Runs Refiner::forward (src/dsine_refine.cpp:212-294) on device pointers:
+ *   normal, feature, hidden: the decoder's /8-grid maps, 3, 64 and 64 fp32
+ *     planes of h8 x w8 (include/brovisionml/dsine_decoder.h:96-102)
+ *   fx, fy, cx, cy: the raw preprocess intrinsics (the +0.5 on the principal
+ *     point is applied here, as build_ray8 applies it)
+ *   orig_h, orig_w: the padded image size the /8 grid came from
+ *   pad_t, pad_l, out_h, out_w: the crop of the 8*h8 x 8*w8 result
+ *     (DsineTransform's pad_t, pad_l, orig_h, orig_w, src/dsine_refine.cpp:289-293)
+ *   out: 3 x out_h x out_w fp32 planes, the refined unit normals
+ *   coarse: NULL, or 5 x 3 x h8 x w8 floats that receive each iteration's
+ *     propagated /8-grid normal (the loop's pred_norm)
+ * Asynchronous on `stream` (NULL = the null stream).  Only the last
+ * iteration's up-sampled map is the result (the reference computes and
+ * discards the others), so the up-mask head's work runs in the last
+ * iteration only.  out and coarse must not overlap the inputs.
+ */
+int bvml_dsine_refiner_forward(bvml_dsine_refiner* r, const float* normal, const float* feature,
+                               const float* hidden, int h8, int w8, float fx, float fy,
+                               float cx, float cy, int orig_h, int orig_w, int pad_t, int pad_l,
+                               int out_h, int out_w, float* out, float* coarse, void* stream);
+
+/* Message for the calling thread's last non-zero refiner status ("" if none). */
+const char* bvml_dsine_refiner_last_error(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* BVML_DSINE_REFINE_H */

@@ -41,6 +41,22 @@ def test_build_ray8_bit_exact(cuda, H, W, intr):
     assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
 
 
+@pytest.mark.parametrize("H,W,intr", RAY_CASES)
+def test_build_uv8_bit_exact(cuda, H, W, intr):
+    """bvml_dsine_build_uv8_f32 against the host restatement of build_uv
+    (src/dsine_decoder.cpp:242-274)."""
+    import torch
+    from brovisionml_amd import _lib, refiner as rf
+    intr, (fu, cu, fv, cv) = _intrinsics(H, W, intr)
+    say(f"[gpu] build_uv8 {H}x{W}")
+    uv = torch.empty((2, H, W), dtype=torch.float32, device=cuda)
+    assert _lib.build_uv8_f32(uv.data_ptr(), fu, cu, fv, cv, H, W,
+                              torch.cuda.current_stream().cuda_stream) == _lib.OK
+    torch.cuda.synchronize()
+    want = rf.uv_map(intr, H, W, 8 * H, 8 * W)
+    assert np.array_equal(uv.cpu().numpy().view(np.uint32), want.view(np.uint32))
+
+
 def _run(inp, H, W, device, ray, precise):
     import torch
     t = {k: to_dev(inp[k], device) for k in ("pred_norm", "prob", "xy", "angle")}
