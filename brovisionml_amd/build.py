@@ -66,7 +66,8 @@ HOST_SOURCES = [
 ]
 CXX_SOURCES = [os.path.join(CSRC, "dsine_ops.cpp")]
 TENSOR_SOURCES = [os.path.join(CSRC, "tensor.cpp")]
-REFINE_SOURCES = [os.path.join(CSRC, "refiner.cpp")]
+REFINE_SOURCES = [os.path.join(CSRC, "refiner.cpp"),      # device path, weights, C ABI
+                  os.path.join(CSRC, "refiner_cpu.cpp")]  # host path
 # host C++ against the HIP runtime and MIOpen headers
 HIP_HOST_FLAGS = ["-D__HIP_PLATFORM_AMD__", "-isystem", os.path.join(ROCM, "include")]
 

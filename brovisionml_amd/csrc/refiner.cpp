@@ -25,6 +25,7 @@
 // benchmarking; the plans are made once per grid size.
 
 #include "bvml_dsine_refine.h"
+#include "refiner_common.h"
 
 #include <hip/hip_runtime.h>
 #include <miopen/miopen.h>
@@ -38,47 +39,24 @@
 #include <utility>
 #include <vector>
 
-namespace {
+namespace bvml_refine {
 
-// The calling thread's last error message (bvml_dsine_refiner_last_error);
-// this library's own, apart from the kernel library's.
+namespace {
 thread_local std::string g_last_error;
+}  // namespace
 
 int fail(int code, const std::string& msg) {
     g_last_error = msg;
     return code;
 }
 
+const char* last_error() { return g_last_error.c_str(); }
+
 bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes) {
     const uintptr_t a0 = reinterpret_cast<uintptr_t>(a), b0 = reinterpret_cast<uintptr_t>(b);
     return a0 < b0 + bbytes && b0 < a0 + abytes;
 }
 
-constexpr int kHidden = 64;           // hidden_dim (src/dsine_refine.cpp:172)
-constexpr int kFeature = 64;          // the decoder's feature channels
-constexpr int kX = kFeature + 2;      // feat_map = cat(feature, uv_8)
-constexpr int kHx = kHidden + kX;     // cat(h, feat_map): 130
-constexpr int kHin = kHidden + 2;     // cat(h_new, uv_8): 66
-constexpr int kUp = 8;                // downsample_ratio (:24)
-constexpr int kIter = 5;              // num_iter_test (:25)
-constexpr int kPs = 5;                // the propagate's window
-constexpr int kHeads = 4;
-constexpr int kMid = 64;              // the heads' hidden width (:119-127)
-constexpr float kUpEps = 1e-12f;      // l2_normalize_nchw_forward's eps (:281)
-const char* const kHeadName[kHeads] = {"prob_head", "xy_head", "angle_head", "up_prob_head"};
-constexpr int kHeadOut[kHeads] = {kPs * kPs, 2 * kPs * kPs, kPs * kPs, 9 * kUp * kUp};
-
-// ---------------------------------------------------------------------------
-// The checkpoint tensors the refiner reads
-// ---------------------------------------------------------------------------
-struct TensorSpec {
-    std::string name;
-    int c_out;
-    long long numel;
-};
-
-// Index order: gru.convz, convr, convq (weight, bias), then per head
-// .0, .2, .4 (weight, bias).
 const std::vector<TensorSpec>& specs() {
     static const std::vector<TensorSpec> v = [] {
         std::vector<TensorSpec> s;
@@ -99,16 +77,57 @@ const std::vector<TensorSpec>& specs() {
     return v;
 }
 
-enum : int { kZw = 0, kZb, kRw, kRb, kQw, kQb, kHead0 };
-int head_w(int h, int layer) { return kHead0 + 6 * h + 2 * layer; }  // layer 0, 1, 2 = .0 .2 .4
-int head_b(int h, int layer) { return head_w(h, layer) + 1; }
-
 int spec_index(const char* name) {
     const auto& s = specs();
     for (size_t i = 0; i < s.size(); ++i)
         if (s[i].name == name) return (int)i;
     return -1;
 }
+
+int check_forward(const std::vector<std::vector<float>>& host, const ForwardArgs& a,
+                  const std::string& who) {
+    if (!a.normal || !a.feature || !a.hidden || !a.out)
+        return fail(BVML_DSINE_ENULL,
+                    who + "refiner, normal, feature, hidden and out must be non-NULL");
+    if (a.h8 < 1 || a.w8 < 1 || a.orig_h < 1 || a.orig_w < 1)
+        return fail(BVML_DSINE_ESHAPE, who + "h8, w8, orig_h and orig_w must be >= 1");
+    const long long fh = (long long)kUp * a.h8, fw = (long long)kUp * a.w8;
+    if (a.pad_t < 0 || a.pad_l < 0 || a.out_h < 1 || a.out_w < 1 ||
+        a.pad_t + (long long)a.out_h > fh || a.pad_l + (long long)a.out_w > fw)
+        return fail(BVML_DSINE_ESHAPE, who + "the crop (pad_t " + std::to_string(a.pad_t) +
+                                           ", pad_l " + std::to_string(a.pad_l) + ", " +
+                                           std::to_string(a.out_h) + " x " +
+                                           std::to_string(a.out_w) + ") must lie inside the " +
+                                           std::to_string(fh) + " x " + std::to_string(fw) +
+                                           " result");
+    if (3 * fh * fw > 0x7FFFFFFFll)
+        return fail(BVML_DSINE_ESIZE, who + "3 x 8h8 x 8w8 exceeds a tensor row");
+    if (!std::isfinite(a.fx) || !std::isfinite(a.fy) || a.fx == 0.0f || a.fy == 0.0f ||
+        !std::isfinite(a.cx) || !std::isfinite(a.cy))
+        return fail(BVML_DSINE_EPARAM, who + "fx, fy must be finite and non-zero, cx, cy finite");
+    const auto& s = specs();
+    for (size_t i = 0; i < s.size(); ++i)
+        if (host[i].empty())
+            return fail(BVML_DSINE_EWEIGHTS, who + "tensor '" + s[i].name + "' not set");
+    const size_t hw = (size_t)a.h8 * a.w8, b = sizeof(float);
+    const size_t outb = (size_t)3 * a.out_h * a.out_w * b, cb = (size_t)kIter * 3 * hw * b;
+    for (const auto& in : {std::make_pair((const void*)a.normal, 3 * hw * b),
+                           std::make_pair((const void*)a.feature, kFeature * hw * b),
+                           std::make_pair((const void*)a.hidden, kHidden * hw * b)}) {
+        if (overlaps(a.out, outb, in.first, in.second) ||
+            (a.coarse && overlaps(a.coarse, cb, in.first, in.second)))
+            return fail(BVML_DSINE_EALIAS, who + "out and coarse must not overlap the inputs");
+    }
+    if (a.coarse && overlaps(a.coarse, cb, a.out, outb))
+        return fail(BVML_DSINE_EALIAS, who + "out and coarse must not overlap");
+    return BVML_DSINE_OK;
+}
+
+}  // namespace bvml_refine
+
+namespace {
+
+using namespace bvml_refine;
 
 // ---------------------------------------------------------------------------
 // safetensors: an 8-byte little-endian header length, a JSON header mapping
@@ -706,6 +725,10 @@ int bvml_dsine_refiner::conv(const ConvPlan& p, const float* w, const float* x, 
     return st == miopenStatusSuccess ? BVML_DSINE_OK : mio_fail(st, "convolution");
 }
 
+const std::vector<std::vector<float>>& bvml_refine::host_weights(const bvml_dsine_refiner* r) {
+    return r->host;
+}
+
 // ---------------------------------------------------------------------------
 // C ABI
 // ---------------------------------------------------------------------------
@@ -769,45 +792,18 @@ int bvml_dsine_refiner_get_tensor(const bvml_dsine_refiner* r, const char* name,
     return BVML_DSINE_OK;
 }
 
-const char* bvml_dsine_refiner_last_error(void) { return g_last_error.c_str(); }
+const char* bvml_dsine_refiner_last_error(void) { return bvml_refine::last_error(); }
 
 int bvml_dsine_refiner_forward(bvml_dsine_refiner* r, const float* normal, const float* feature,
                                const float* hidden, int h8, int w8, float fx, float fy,
                                float cx, float cy, int orig_h, int orig_w, int pad_t, int pad_l,
                                int out_h, int out_w, float* out, float* coarse, void* stream) {
-    if (!r || !normal || !feature || !hidden || !out)
-        return fail(BVML_DSINE_ENULL,
-                    "forward: refiner, normal, feature, hidden and out must be non-NULL");
-    if (h8 < 1 || w8 < 1 || orig_h < 1 || orig_w < 1)
-        return fail(BVML_DSINE_ESHAPE, "forward: h8, w8, orig_h and orig_w must be >= 1");
-    const long long fh = (long long)kUp * h8, fw = (long long)kUp * w8;
-    if (pad_t < 0 || pad_l < 0 || out_h < 1 || out_w < 1 || pad_t + (long long)out_h > fh ||
-        pad_l + (long long)out_w > fw)
-        return fail(BVML_DSINE_ESHAPE, "forward: the crop (pad_t " + std::to_string(pad_t) +
-                                           ", pad_l " + std::to_string(pad_l) + ", " +
-                                           std::to_string(out_h) + " x " + std::to_string(out_w) +
-                                           ") must lie inside the " + std::to_string(fh) + " x " +
-                                           std::to_string(fw) + " result");
-    if (3 * fh * fw > 0x7FFFFFFFll)
-        return fail(BVML_DSINE_ESIZE, "forward: 3 x 8h8 x 8w8 exceeds a tensor row");
-    if (!std::isfinite(fx) || !std::isfinite(fy) || fx == 0.0f || fy == 0.0f ||
-        !std::isfinite(cx) || !std::isfinite(cy))
-        return fail(BVML_DSINE_EPARAM, "forward: fx, fy must be finite and non-zero, cx, cy finite");
-    const auto& s = specs();
-    for (size_t i = 0; i < s.size(); ++i)
-        if (r->host[i].empty())
-            return fail(BVML_DSINE_EWEIGHTS, "forward: tensor '" + s[i].name + "' not set");
+    if (!r) return fail(BVML_DSINE_ENULL, "forward: refiner must be non-NULL");
+    const ForwardArgs args{normal, feature, hidden, h8, w8, fx, fy, cx, cy, orig_h, orig_w,
+                           pad_t, pad_l, out_h, out_w, out, coarse};
+    if (const int st = check_forward(r->host, args, "forward: ")) return st;
     const size_t hw = (size_t)h8 * w8, b = sizeof(float);
-    const size_t outb = (size_t)3 * out_h * out_w * b;
-    for (const auto& in : {std::make_pair((const void*)normal, 3 * hw * b),
-                           std::make_pair((const void*)feature, kFeature * hw * b),
-                           std::make_pair((const void*)hidden, kHidden * hw * b)}) {
-        if (overlaps(out, outb, in.first, in.second) ||
-            (coarse && overlaps(coarse, kIter * 3 * hw * b, in.first, in.second)))
-            return fail(BVML_DSINE_EALIAS, "forward: out and coarse must not overlap the inputs");
-    }
-    if (coarse && overlaps(coarse, kIter * 3 * hw * b, out, outb))
-        return fail(BVML_DSINE_EALIAS, "forward: out and coarse must not overlap");
+    const long long fh = (long long)kUp * h8, fw = (long long)kUp * w8;
 
     if (r->device < 0) {
         int d = 0;

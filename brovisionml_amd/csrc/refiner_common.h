@@ -1,0 +1,71 @@
+// What the native refiner's device path (refiner.cpp) and host path
+// (refiner_cpu.cpp) share: the loop's sizes, the checkpoint tensors it reads,
+// the error state of bvml_dsine_refiner_last_error and forward's argument
+// checks.  Private to libbvml_dsine_refine.so.
+#pragma once
+
+#include <cstddef>
+#include <string>
+#include <vector>
+
+#include "bvml_dsine_refine.h"
+
+namespace bvml_refine {
+
+constexpr int kHidden = 64;           // hidden_dim (src/dsine_refine.cpp:172)
+constexpr int kFeature = 64;          // the decoder's feature channels
+constexpr int kX = kFeature + 2;      // feat_map = cat(feature, uv_8)
+constexpr int kHx = kHidden + kX;     // cat(h, feat_map): 130
+constexpr int kHin = kHidden + 2;     // cat(h_new, uv_8): 66
+constexpr int kUp = 8;                // downsample_ratio (:24)
+constexpr int kIter = 5;              // num_iter_test (:25)
+constexpr int kPs = 5;                // the propagate's window
+constexpr int kHeads = 4;
+constexpr int kMid = 64;              // the heads' hidden width (:119-127)
+constexpr float kUpEps = 1e-12f;      // l2_normalize_nchw_forward's eps (:281)
+constexpr const char* kHeadName[kHeads] = {"prob_head", "xy_head", "angle_head",
+                                           "up_prob_head"};
+constexpr int kHeadOut[kHeads] = {kPs * kPs, 2 * kPs * kPs, kPs * kPs, 9 * kUp * kUp};
+
+// One checkpoint tensor: its name, output channels and element count.
+struct TensorSpec {
+    std::string name;
+    int c_out;
+    long long numel;
+};
+
+// The tensors in a fixed order: gru.convz, convr, convq (weight, bias), then
+// per head .0, .2, .4 (weight, bias).
+const std::vector<TensorSpec>& specs();
+int spec_index(const char* name);  // -1 for a name not in specs()
+
+enum : int { kZw = 0, kZb, kRw, kRb, kQw, kQb, kHead0 };
+// index of head h's layer (0, 1, 2 = .0, .2, .4) weight / bias
+inline int head_w(int h, int layer) { return kHead0 + 6 * h + 2 * layer; }
+inline int head_b(int h, int layer) { return head_w(h, layer) + 1; }
+
+// Record msg as the calling thread's last error and return code.
+int fail(int code, const std::string& msg);
+const char* last_error();
+bool overlaps(const void* a, size_t abytes, const void* b, size_t bbytes);
+
+struct ForwardArgs {
+    const float* normal;
+    const float* feature;
+    const float* hidden;
+    int h8, w8;
+    float fx, fy, cx, cy;
+    int orig_h, orig_w, pad_t, pad_l, out_h, out_w;
+    float* out;
+    float* coarse;
+};
+
+// forward's argument checks (pointers, sizes, the crop, the intrinsics,
+// weights present, no overlap), messages prefixed `who`; 0 or a status.
+int check_forward(const std::vector<std::vector<float>>& host, const ForwardArgs& a,
+                  const std::string& who);
+
+// The host copy of the refiner's weights, one vector per spec.
+const std::vector<std::vector<float>>& host_weights(const bvml_dsine_refiner* r);
+
+}  // namespace bvml_refine

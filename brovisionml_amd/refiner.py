@@ -288,29 +288,34 @@ class NativeRefiner:
         return a
 
     def forward(self, dec: DecoderOutput, intr: workloads.Intrinsics, orig_h: int, orig_w: int,
-                crop: Crop | None = None, coarse: bool = False, out=None):
+                crop: Crop | None = None, coarse: bool = False, out=None, nthreads: int = 0):
         """The refined normals (1, 3, h, w) at the unpadded resolution (the
         whole 8*h8 x 8*w8 map without crop); with coarse=True also each
-        iteration's propagated /8-grid normal, (N_ITER, 3, h8, w8).  `out`,
-        when given, is the result tensor to fill (so the call allocates
-        nothing once the refiner has run at this grid size)."""
+        iteration's propagated /8-grid normal, (N_ITER, 3, h8, w8).  The
+        decoder maps are contiguous fp32 torch tensors, all on the GPU (the
+        device path, asynchronous on the current stream) or all on the CPU
+        (the host path, on nthreads threads, 0 = all); the results live
+        there too.  `out`, when given, is the result tensor to fill."""
         import torch
         _, _, H, W = dec.normal.shape
-        for t in (dec.normal, dec.feature, dec.hidden):
-            if t.device.type != "cuda" or t.dtype != torch.float32 or not t.is_contiguous():
-                raise RuntimeError("dsine::Refiner: decoder maps must be contiguous fp32 on the "
-                                   "GPU")
-        c = crop if crop is not None else Crop(8 * H, 8 * W)
         dev = dec.normal.device
+        for t in (dec.normal, dec.feature, dec.hidden):
+            if t.device != dev or t.dtype != torch.float32 or not t.is_contiguous():
+                raise RuntimeError("dsine::Refiner: decoder maps must be contiguous fp32 tensors "
+                                   "on one device")
+        c = crop if crop is not None else Crop(8 * H, 8 * W)
         if out is None:
             out = torch.empty((1, 3, c.orig_h, c.orig_w), dtype=torch.float32, device=dev)
         cz = (torch.empty((N_ITER, 3, H, W), dtype=torch.float32, device=dev) if coarse
               else None)
-        with torch.cuda.device(dev):
-            st = self._lib.bvml_dsine_refiner_forward(
-                self._h, dec.normal.data_ptr(), dec.feature.data_ptr(), dec.hidden.data_ptr(),
+        args = (self._h, dec.normal.data_ptr(), dec.feature.data_ptr(), dec.hidden.data_ptr(),
                 H, W, intr.fx, intr.fy, intr.cx, intr.cy, orig_h, orig_w, c.pad_t, c.pad_l,
-                c.orig_h, c.orig_w, out.data_ptr(), cz.data_ptr() if cz is not None else None,
-                torch.cuda.current_stream(dev).cuda_stream)
+                c.orig_h, c.orig_w, out.data_ptr(), cz.data_ptr() if cz is not None else None)
+        if dev.type == "cpu":
+            st = self._lib.bvml_dsine_refiner_forward_cpu(*args, nthreads)
+        else:
+            with torch.cuda.device(dev):
+                st = self._lib.bvml_dsine_refiner_forward(
+                    *args, torch.cuda.current_stream(dev).cuda_stream)
         self._check("forward", st)
         return (out, cz) if coarse else out

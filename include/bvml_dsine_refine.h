@@ -95,6 +95,22 @@ int bvml_dsine_refiner_forward(bvml_dsine_refiner* r, const float* normal, const
                                float cx, float cy, int orig_h, int orig_w, int pad_t, int pad_l,
                                int out_h, int out_w, float* out, float* coarse, void* stream);
 
+/*
+ * The same loop on the CPU, for host pointers (Refiner::forward on
+ * brotensor's CPU device, every step a CPU op in the reference): fp32
+ * convolutions (a float sum over each output's taps, then the bias), the
+ * ConvGRU's and heads' activations in float, RayReLU and the propagate from
+ * the CPU branch of bvml_dsine.h (double precision in the reference's
+ * operation order), the convex upsample + normalise in double rounded to
+ * float once.  nthreads: host threads (0 = the hardware's; the result does
+ * not depend on it).  Makes no HIP call.
+ */
+int bvml_dsine_refiner_forward_cpu(bvml_dsine_refiner* r, const float* normal,
+                                   const float* feature, const float* hidden, int h8, int w8,
+                                   float fx, float fy, float cx, float cy, int orig_h,
+                                   int orig_w, int pad_t, int pad_l, int out_h, int out_w,
+                                   float* out, float* coarse, int nthreads);
+
 /* Message for the calling thread's last non-zero refiner status ("" if none). */
 const char* bvml_dsine_refiner_last_error(void);
 
