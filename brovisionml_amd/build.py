@@ -4,8 +4,9 @@
   libbvml_dsine.so        HIP kernels and the CPU branch behind one C ABI
                           (include/bvml_dsine.h); extern "C" symbols only
   libbvml_dsine_cxx.so    the C++ drop-in brovisionml::dsine::* (dsine_ops.cpp,
-                          include/brovisionml/dsine_ops.h), plain C++ over the
-                          C ABI; brotensor::Tensor left undefined, to be
+                          include/brovisionml/dsine_ops.h; dsine_refine.cpp,
+                          include/brovisionml/dsine_refine.h), plain C++ over
+                          the C ABIs; brotensor::Tensor left undefined, to be
                           resolved by brotensor or by the subset below
   libbvml_dsine_refine.so the native NRN refiner (refiner.cpp,
                           include/bvml_dsine_refine.h): C++ over the C ABI
@@ -64,7 +65,8 @@ HOST_SOURCES = [
     os.path.join(CSRC, "dsine_ops_cpu.cpp"),  # CPU branch (C ABI *_cpu_f32)
     os.path.join(CSRC, "status.cpp"),         # error state, bvml_dsine_last_error
 ]
-CXX_SOURCES = [os.path.join(CSRC, "dsine_ops.cpp")]
+CXX_SOURCES = [os.path.join(CSRC, "dsine_ops.cpp"),     # the ops' public dispatch
+               os.path.join(CSRC, "dsine_refine.cpp")]  # the Refiner class
 TENSOR_SOURCES = [os.path.join(CSRC, "tensor.cpp")]
 REFINE_SOURCES = [os.path.join(CSRC, "refiner.cpp"),      # device path, weights, C ABI
                   os.path.join(CSRC, "refiner_cpu.cpp")]  # host path
@@ -103,7 +105,7 @@ def build_library() -> str:
           "-Wl,--version-script=" + os.path.join(CSRC, "libbvml_dsine_refine.map")])
     _install(LIB_REFINE + ".tmp", LIB_REFINE)
     _run([CXX, *CXX_FLAGS, "-I", INCLUDE, "-shared", "-o", LIB_CXX + ".tmp", *CXX_SOURCES,
-          "-L", LIBDIR, "-lbvml_dsine", "-Wl,-rpath,$ORIGIN",
+          "-L", LIBDIR, "-lbvml_dsine_refine", "-lbvml_dsine", "-Wl,-rpath,$ORIGIN",
           "-Wl,--version-script=" + os.path.join(CSRC, "libbvml_dsine_cxx.map")])
     _install(LIB_CXX + ".tmp", LIB_CXX)
     _run([HIPCC, "-O2", "-std=c++17", "-fPIC", "-I", INCLUDE, "-shared", "-o", LIB_TENSOR + ".tmp",

@@ -163,3 +163,27 @@ def test_native_load_file(cuda, tmp_path, dtype):
         dec, intr, 8 * H, 8 * W)
     torch.cuda.synchronize()
     assert float((a - b).abs().max()) <= 1e-5
+
+
+def test_cpp_refiner_on_device(cuda, tmp_path):
+    """brovisionml::dsine::Refiner (tests/cpp/test_dsine_refine.cpp, run on
+    brotensor's CUDA tag) against the native refiner's device forward in
+    this process, and its host path against its device path."""
+    import torch
+    from tests.test_refiner_native_host import _cpu_dec, cpp_case, run_cpp_refine
+    wpath, cpath, weights, maps, intr, crop = cpp_case(tmp_path)
+    say("[gpu] C++ Refiner class, run gpu")
+    opath = str(tmp_path / "out.bin")
+    rc, out = run_cpp_refine("run", "gpu", wpath, cpath, opath, timeout=110)
+    say(out)
+    assert rc == 0 and "OK" in out, out
+    got = np.fromfile(opath, np.float32).reshape(1, 3, crop.orig_h, crop.orig_w)
+    H, W = maps[0].shape[1:]
+    dev = rf.NativeRefiner(weights).forward(_dec(maps), intr, 8 * H, 8 * W, crop=crop)
+    host = rf.NativeRefiner(weights).forward(_cpu_dec(maps), intr, 8 * H, 8 * W, crop=crop)
+    torch.cuda.synchronize()
+    dev = dev.cpu().numpy()
+    e_cpp = float(np.abs(got - dev).max())
+    e_host = float(np.abs(host.numpy() - dev).max())
+    say(f"    C++ class vs device forward max-abs {e_cpp:.3e}; host vs device {e_host:.3e}")
+    assert e_cpp <= 1e-5 and e_host <= TOL

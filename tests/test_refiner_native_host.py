@@ -286,3 +286,61 @@ def test_cpu_forward_pins_and_crop():
     part = model.forward(dec, intr, 8 * H, 8 * W, crop=crop, nthreads=1)
     assert part.shape == (1, 3, crop.orig_h, crop.orig_w)
     assert np.array_equal(part.numpy(), out.numpy()[:, :, 5:5 + crop.orig_h, 3:3 + crop.orig_w])
+
+
+# ---- the C++ class (tests/cpp/test_dsine_refine.cpp over libbvml_dsine_cxx.so)
+CPP_REFINE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "cpp", "_build",
+                          "test_dsine_refine")
+
+
+def write_case(path, n, feature, hidden, intr, orig_h, orig_w, crop):
+    """The case file tests/cpp/test_dsine_refine.cpp reads."""
+    H, W = n.shape[1:]
+    with open(path, "wb") as f:
+        f.write(struct.pack("<8i", H, W, orig_h, orig_w, crop.pad_t, crop.pad_l, crop.orig_h,
+                            crop.orig_w))
+        f.write(struct.pack("<4f", intr.fx, intr.fy, intr.cx, intr.cy))
+        for a in (n, feature, hidden):
+            f.write(np.ascontiguousarray(a, "<f4").tobytes())
+
+
+def cpp_case(tmp_path, seed=21, H=10, W=13):
+    """(weights file, case file, weights, maps, intrinsics, crop) for a run."""
+    from safetensors.numpy import save_file
+    from brovisionml_amd import workloads as wl
+    from tests import refiner_pins as pins
+    weights = rf.random_weights(seed)
+    wpath = str(tmp_path / "model.safetensors")
+    save_file(weights, wpath)
+    maps = pins.inputs(H, W, seed)
+    intr = wl.intrins_from_fov(8 * H, 8 * W, 65.0)
+    crop = rf.Crop(orig_h=8 * H - 9, orig_w=8 * W - 4, pad_t=4, pad_l=2)
+    cpath = str(tmp_path / "case.bin")
+    write_case(cpath, *maps, intr, 8 * H, 8 * W, crop)
+    return wpath, cpath, weights, maps, intr, crop
+
+
+def run_cpp_refine(*args, timeout=300):
+    import subprocess
+    assert os.path.exists(CPP_REFINE), "build() compiles tests/cpp/test_dsine_refine"
+    proc = subprocess.run([CPP_REFINE, *args], stdout=subprocess.PIPE, stderr=subprocess.STDOUT,
+                          text=True, timeout=timeout)
+    return proc.returncode, proc.stdout
+
+
+def test_cpp_refiner_errors():
+    rc, out = run_cpp_refine("errors")
+    assert rc == 0 and "OK" in out, out
+
+
+def test_cpp_refiner_cpu(tmp_path):
+    """Refiner::load_file, to(CPU), forward with a crop: the native refiner's
+    host path, bit for bit."""
+    wpath, cpath, weights, maps, intr, crop = cpp_case(tmp_path)
+    opath = str(tmp_path / "out.bin")
+    rc, out = run_cpp_refine("run", "cpu", wpath, cpath, opath)
+    assert rc == 0 and "OK" in out, out
+    got = np.fromfile(opath, np.float32).reshape(1, 3, crop.orig_h, crop.orig_w)
+    H, W = maps[0].shape[1:]
+    want = rf.NativeRefiner(weights).forward(_cpu_dec(maps), intr, 8 * H, 8 * W, crop=crop)
+    assert np.array_equal(got.view(np.uint32), want.numpy().view(np.uint32))
