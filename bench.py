@@ -814,12 +814,16 @@ def bench_upsample(args, dev) -> dict:
 # ---------------------------------------------------------------------------
 
 def bench_refiner(args, dev) -> dict:
-    """The whole NRN refiner forward (brovisionml_amd/refiner.py: 5 iterations
-    of ConvGRU + heads on MIOpen, the package's propagate with fused
-    activations and its upsample + normalise) at a 256x256 grid (a 2048x2048
-    image), synthetic weights and decoder outputs, one forward per step,
-    captured in one graph.  The CPU leg is its restatement in oracle/refiner.py
-    (float64 convolutions, the C oracle's ops) on a 24x32 grid."""
+    """The whole NRN refiner forward at a 256x256 grid (a 2048x2048 image),
+    synthetic weights and decoder outputs, one forward per step, `steps`
+    forwards captured in one graph: the native refiner
+    (libbvml_dsine_refine.so: the loop in C++, ConvGRU + heads on MIOpen,
+    the package's propagate with fused activations and its upsample +
+    normalise; the line's value) and the Python driver
+    (brovisionml_amd/refiner.py, the same kernels and convolutions, with the
+    up-mask head and upsample in every iteration) beside it.  The CPU leg is
+    the restatement in oracle/refiner.py (float64 convolutions, the C
+    oracle's ops) on a 24x32 grid."""
     import torch
     from brovisionml_amd import refiner as rf, workloads as wl
 
@@ -830,33 +834,50 @@ def bench_refiner(args, dev) -> dict:
     normal = (normal / np.linalg.norm(normal, axis=1, keepdims=True)).astype(np.float32)
     feature = rng.standard_normal((1, 64, H, W)).astype(np.float32)
     hidden = rng.uniform(-1, 1, (1, 64, H, W)).astype(np.float32)
-    model = rf.Refiner(rf.random_weights(0), dev)
+    weights = rf.random_weights(0)
     dec = rf.DecoderOutput(*(torch.from_numpy(a).to(dev) for a in (normal, feature, hidden)))
     intr = wl.intrins_from_fov(8 * H, 8 * W, 60.0)
-    cond = model.conditioning(intr, H, W, 8 * H, 8 * W)
-    for _ in range(3):
-        model.forward(dec, intr, 8 * H, 8 * W, cond=cond)
-    torch.cuda.synchronize()
-    g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
-        for _ in range(args.steps):
-            model.forward(dec, intr, 8 * H, 8 * W, cond=cond)
-    g.replay()
-    torch.cuda.synchronize()
     stream = torch.cuda.current_stream(dev)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    g.replay()
-    e1.record(stream)
-    torch.cuda.synchronize()
-    t = e0.elapsed_time(e1) * 1e-3
+
+    def graph_time(step) -> float:
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            for _ in range(args.steps):
+                step()
+        g.replay()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        g.replay()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3
+
+    t = t_py = None
+    if args.driver in ("native", "both"):
+        native = rf.NativeRefiner(weights)
+        out = torch.empty((1, 3, 8 * H, 8 * W), dtype=torch.float32, device=dev)
+        t = graph_time(lambda: native.forward(dec, intr, 8 * H, 8 * W, out=out))
+    if args.driver in ("python", "both"):
+        model = rf.Refiner(weights, dev)
+        cond = model.conditioning(intr, H, W, 8 * H, 8 * W)
+        t_py = graph_time(lambda: model.forward(dec, intr, 8 * H, 8 * W, cond=cond))
     opx = 64 * H * W * args.steps
+    driver = "native refiner (C++, libbvml_dsine_refine.so)"
+    if t is None:
+        t, t_py, driver = t_py, None, "Python driver (brovisionml_amd/refiner.py)"
     line = base_line(args, f"output Mpixel/s, DSINE NRN refiner forward (5 iterations), {H}x{W} "
                            f"grid -> {8 * H}x{8 * W} fp32", opx / t / 1e6, "Mpixel/s",
                      t * 1e3 / args.steps,
                      {"workload": f"dsine-refiner-{H}x{W}", "H": H, "W": W, "iterations": 5,
                       "weights": "synthetic (uniform +-1/sqrt(fan_in))",
-                      "convolutions": "torch F.conv2d (MIOpen), fp32"})
+                      "driver": driver, "convolutions": "MIOpen immediate mode, fp32"})
+    if t_py is not None:
+        line["python_driver"] = {"ms_per_step": round(t_py * 1e3 / args.steps, 4),
+                                 "value": round(opx / t_py / 1e6, 2)}
     line["gpu"] = torch.cuda.get_device_name(dev)
     if not args.no_cpu:
         import oracle.refiner as oref
@@ -889,6 +910,9 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=200)
     ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--op", choices=("angmf", "upsample", "refiner", "ray_relu"), default="angmf")
+    ap.add_argument("--driver", choices=("native", "python", "both"), default="both",
+                    help="--op refiner: the native refiner, the Python driver, or both (the "
+                         "native one is the line's value)")
     ap.add_argument("--workload", type=int, default=None,
                     help="index into the op's workloads (default: angmf and ray_relu 2, "
                          "upsample 0)")

@@ -3,14 +3,18 @@
 `build_library()` compiles every time it is called, into brovisionml_amd/lib/:
   libbvml_dsine.so        HIP kernels and the CPU branch behind one C ABI
                           (include/bvml_dsine.h); extern "C" symbols only
-  libbvml_dsine_cxx.so    the C++ drop-in brovisionml::dsine::* (dsine_ops.cpp,
-                          include/brovisionml/dsine_ops.h; dsine_refine.cpp,
-                          include/brovisionml/dsine_refine.h), plain C++ over
-                          the C ABIs; brotensor::Tensor left undefined, to be
-                          resolved by brotensor or by the subset below
+  libbvml_dsine_cxx.so    the C++ drop-in of the ops, brovisionml::dsine::*
+                          (dsine_ops.cpp, include/brovisionml/dsine_ops.h),
+                          plain C++ over the C ABI; brotensor::Tensor left
+                          undefined, to be resolved by brotensor or by the
+                          subset below
   libbvml_dsine_refine.so the native NRN refiner (refiner.cpp,
-                          include/bvml_dsine_refine.h): C++ over the C ABI
-                          and MIOpen; extern "C" symbols only
+                          refiner_cpu.cpp, include/bvml_dsine_refine.h): C++
+                          over the C ABI and MIOpen; extern "C" symbols only
+  libbvml_dsine_refine_cxx.so  the C++ drop-in brovisionml::dsine::Refiner
+                          (dsine_refine.cpp, include/brovisionml/dsine_refine.h)
+                          over the refiner's C ABI; brotensor::Tensor left
+                          undefined, like libbvml_dsine_cxx.so
   libbrotensor_subset.so  the brotensor::Tensor subset of
                           include/brotensor/tensor.h, for standalone use and
                           the C++ tests; a brovisionml build links brotensor
@@ -31,6 +35,7 @@ LIB = os.path.join(LIBDIR, "libbvml_dsine.so")
 LIB_CXX = os.path.join(LIBDIR, "libbvml_dsine_cxx.so")
 LIB_TENSOR = os.path.join(LIBDIR, "libbrotensor_subset.so")
 LIB_REFINE = os.path.join(LIBDIR, "libbvml_dsine_refine.so")
+LIB_REFINE_CXX = os.path.join(LIBDIR, "libbvml_dsine_refine_cxx.so")
 ROCM = os.environ.get("ROCM_PATH", "/opt/rocm")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")
@@ -65,8 +70,8 @@ HOST_SOURCES = [
     os.path.join(CSRC, "dsine_ops_cpu.cpp"),  # CPU branch (C ABI *_cpu_f32)
     os.path.join(CSRC, "status.cpp"),         # error state, bvml_dsine_last_error
 ]
-CXX_SOURCES = [os.path.join(CSRC, "dsine_ops.cpp"),     # the ops' public dispatch
-               os.path.join(CSRC, "dsine_refine.cpp")]  # the Refiner class
+CXX_SOURCES = [os.path.join(CSRC, "dsine_ops.cpp")]     # the ops' public dispatch
+REFINE_CXX_SOURCES = [os.path.join(CSRC, "dsine_refine.cpp")]  # the Refiner class
 TENSOR_SOURCES = [os.path.join(CSRC, "tensor.cpp")]
 REFINE_SOURCES = [os.path.join(CSRC, "refiner.cpp"),      # device path, weights, C ABI
                   os.path.join(CSRC, "refiner_cpu.cpp")]  # host path
@@ -86,7 +91,7 @@ def _install(tmp: str, dst: str) -> None:
 
 
 def build_library() -> str:
-    """Builds the four libraries; returns the C ABI library's path."""
+    """Builds the five libraries; returns the C ABI library's path."""
     os.makedirs(LIBDIR, exist_ok=True)
     objdir = os.path.join(PKG, "_build")
     os.makedirs(objdir, exist_ok=True)
@@ -104,8 +109,12 @@ def build_library() -> str:
           "-lMIOpen", "-lamdhip64", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath," + os.path.join(ROCM, "lib"),
           "-Wl,--version-script=" + os.path.join(CSRC, "libbvml_dsine_refine.map")])
     _install(LIB_REFINE + ".tmp", LIB_REFINE)
+    _run([CXX, *CXX_FLAGS, "-I", INCLUDE, "-shared", "-o", LIB_REFINE_CXX + ".tmp",
+          *REFINE_CXX_SOURCES, "-L", LIBDIR, "-lbvml_dsine_refine", "-Wl,-rpath,$ORIGIN",
+          "-Wl,--version-script=" + os.path.join(CSRC, "libbvml_dsine_refine_cxx.map")])
+    _install(LIB_REFINE_CXX + ".tmp", LIB_REFINE_CXX)
     _run([CXX, *CXX_FLAGS, "-I", INCLUDE, "-shared", "-o", LIB_CXX + ".tmp", *CXX_SOURCES,
-          "-L", LIBDIR, "-lbvml_dsine_refine", "-lbvml_dsine", "-Wl,-rpath,$ORIGIN",
+          "-L", LIBDIR, "-lbvml_dsine", "-Wl,-rpath,$ORIGIN",
           "-Wl,--version-script=" + os.path.join(CSRC, "libbvml_dsine_cxx.map")])
     _install(LIB_CXX + ".tmp", LIB_CXX)
     _run([HIPCC, "-O2", "-std=c++17", "-fPIC", "-I", INCLUDE, "-shared", "-o", LIB_TENSOR + ".tmp",
@@ -119,7 +128,7 @@ def check_brotensor_api() -> None:
     declares only what brovisionml's sources use of brotensor::Tensor
     (tests/cpp/brotensor_api/brotensor/tensor.h)."""
     api = os.path.join(ROOT, "tests", "cpp", "brotensor_api")
-    for src in (*CXX_SOURCES, os.path.join(api, "launchers_check.cpp")):
+    for src in (*CXX_SOURCES, *REFINE_CXX_SOURCES, os.path.join(api, "launchers_check.cpp")):
         _run([CXX, "-std=c++17", "-fsyntax-only", "-Wall", "-Wextra", "-I", api, "-I", INCLUDE,
               src])
 

@@ -183,6 +183,29 @@ def test_cxx_layer_exports_only_the_dropin():
     assert undefined
 
 
+def test_refiner_libraries_export_only_their_interfaces():
+    """libbvml_dsine_refine.so adds bvml_dsine_refiner_* (the declarations of
+    include/bvml_dsine_refine.h) and nothing else; libbvml_dsine_refine_cxx.so
+    adds brovisionml::dsine::Refiner's members and nothing else, so a
+    brovisionml build can take the ops' C++ layer and the Refiner class
+    independently, each in place of exactly one of its own sources."""
+    import re
+    from brovisionml_amd.build import LIB_CXX, LIB_REFINE, LIB_REFINE_CXX, INCLUDE
+    names = [ln.split()[-1] for ln in _dynsyms(LIB_REFINE, "--defined-only")
+             if ln.split()[1] in "TDBRVWiu"]
+    with open(os.path.join(INCLUDE, "bvml_dsine_refine.h")) as f:
+        declared = set(re.findall(r"\b(bvml_dsine_refiner_\w+)\s*\(", f.read()))
+    assert sorted(names) == sorted(declared)
+    defined = [ln.split(None, 2)[2] for ln in _dynsyms(LIB_REFINE_CXX, "--defined-only")
+               if " T " in ln or " W " in ln]
+    assert defined and all(n.startswith("brovisionml::dsine::Refiner::") for n in defined)
+    for fn in ("load(", "load_file(", "to(", "device(", "forward(", "Refiner()"):
+        assert any(n.startswith(f"brovisionml::dsine::Refiner::{fn}") for n in defined), fn
+    ops = {ln.split(None, 2)[2] for ln in _dynsyms(LIB_CXX, "--defined-only")
+           if " T " in ln or " W " in ln}
+    assert not ops & set(defined)
+
+
 def test_cxx_layer_compiles_against_brotensors_api():
     """dsine_ops.cpp and the launchers header use only the brotensor::Tensor
     members and Device enumerators brovisionml's own sources use."""
