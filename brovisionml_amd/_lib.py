@@ -41,6 +41,14 @@ EXPORTS = (
     "bvml_dsine_gru_gates_f32",
     "bvml_dsine_gru_update_f32",
     "bvml_dsine_bias_act_f32",
+    "bvml_dsine_heads_mlp_f32",
+    "bvml_dsine_heads_pack_f32",
+    "bvml_dsine_heads_packed_size",
+    "bvml_dsine_conv_packed_size",
+    "bvml_dsine_conv_pack_f32",
+    "bvml_dsine_conv_f32",
+    "bvml_dsine_conv_gru_gates_f32",
+    "bvml_dsine_conv_gru_update_f32",
     "bvml_dsine_last_error",
     "bvml_dsine_version",
 )
@@ -107,6 +115,23 @@ def load(path: str = LIB) -> ctypes.CDLL:
     lib.bvml_dsine_gru_update_f32.restype = i
     lib.bvml_dsine_bias_act_f32.argtypes = [vp, vp, i, ll, i, vp]
     lib.bvml_dsine_bias_act_f32.restype = i
+    pp = ctypes.POINTER(vp)
+    lib.bvml_dsine_heads_mlp_f32.argtypes = [vp, vp, vp, vp, pp, pp, ip, i, i, i, pp, vp]
+    lib.bvml_dsine_heads_mlp_f32.restype = i
+    lib.bvml_dsine_heads_pack_f32.argtypes = [vp, pp, ip, i, vp, pp]
+    lib.bvml_dsine_heads_pack_f32.restype = i
+    lib.bvml_dsine_heads_packed_size.argtypes = [i]
+    lib.bvml_dsine_heads_packed_size.restype = ll
+    lib.bvml_dsine_conv_packed_size.argtypes = [i, i, i]
+    lib.bvml_dsine_conv_packed_size.restype = ll
+    lib.bvml_dsine_conv_pack_f32.argtypes = [vp, i, i, i, i, vp]
+    lib.bvml_dsine_conv_pack_f32.restype = i
+    lib.bvml_dsine_conv_f32.argtypes = [vp, i, i, i, vp, i, i, vp, vp]
+    lib.bvml_dsine_conv_f32.restype = i
+    lib.bvml_dsine_conv_gru_gates_f32.argtypes = [vp, i, i, i, vp, i, vp, vp, vp, vp, vp, vp]
+    lib.bvml_dsine_conv_gru_gates_f32.restype = i
+    lib.bvml_dsine_conv_gru_update_f32.argtypes = [vp, i, i, i, vp, i, vp, vp, vp, vp, vp, vp]
+    lib.bvml_dsine_conv_gru_update_f32.restype = i
     lib.bvml_dsine_last_error.argtypes = []
     lib.bvml_dsine_last_error.restype = ctypes.c_char_p
     lib.bvml_dsine_version.argtypes = []
@@ -260,6 +285,56 @@ def gru_update_f32(q_pre: int, bias_q: int, z: int, h: int, C: int, HW: int, h_n
                    h_copy: int = 0, stream: int = 0) -> int:
     """Raw call; pointers are integer device addresses. Returns the status."""
     return load().bvml_dsine_gru_update_f32(q_pre, bias_q, z, h, C, HW, h_new, h_copy, stream)
+
+
+def heads_pack_f32(w2, w4s):
+    """Host packing of the heads' 1x1 weights for bvml_dsine_heads_mlp_f32:
+    w2 (nheads, 64, 64[, 1, 1]) float32, w4s a list of (outs[h], 64[, 1, 1]);
+    returns (w2p, [w4p_h]) as float32 numpy arrays."""
+    import numpy as np
+    lib = load()
+    w2 = np.ascontiguousarray(np.asarray(w2, np.float32).reshape(-1, 64, 64))
+    nh = w2.shape[0]
+    w4s = [np.ascontiguousarray(np.asarray(w, np.float32).reshape(-1, 64)) for w in w4s]
+    outs = (ctypes.c_int * nh)(*[w.shape[0] for w in w4s])
+    w2p = np.empty(nh * 4096, np.float32)
+    w4p = [np.empty(lib.bvml_dsine_heads_packed_size(w.shape[0]), np.float32) for w in w4s]
+    vp = ctypes.c_void_p
+    st = lib.bvml_dsine_heads_pack_f32(w2.ctypes.data, (vp * nh)(*[w.ctypes.data for w in w4s]),
+                                       outs, nh, w2p.ctypes.data,
+                                       (vp * nh)(*[w.ctypes.data for w in w4p]))
+    if st != OK:
+        raise RuntimeError(f"heads_pack: {last_error()} (status {st})")
+    return w2p, w4p
+
+
+def heads_mlp_f32(t0: int, b0: int, w2p: int, b2: int, w4p, b4, outs, H: int, W: int, out,
+                  stream: int = 0) -> int:
+    """Raw call; pointers are integer device addresses, w4p / b4 / out lists
+    of them (0 in b4 for no bias), outs the output counts. Returns the status."""
+    vp = ctypes.c_void_p
+    nh = len(outs)
+    return load().bvml_dsine_heads_mlp_f32(
+        t0, b0, w2p, b2, (vp * nh)(*w4p), (vp * nh)(*[b or None for b in b4]),
+        (ctypes.c_int * nh)(*outs), nh, H, W, (vp * nh)(*out), stream)
+
+
+def conv_pack_f32(w, interleave: bool = False):
+    """Host packing of OIHW conv weights (cout, cin, k, k) for the
+    bvml_dsine_conv_* kernels; returns a float32 numpy array."""
+    import numpy as np
+    w = np.ascontiguousarray(np.asarray(w, np.float32))
+    cout, cin, k, _ = w.shape
+    lib = load()
+    n = lib.bvml_dsine_conv_packed_size(cout, cin, k)
+    if n < 0:
+        raise RuntimeError("conv_pack: unsupported shape")
+    wp = np.empty(n, np.float32)
+    st = lib.bvml_dsine_conv_pack_f32(w.ctypes.data, cout, cin, k, int(bool(interleave)),
+                                      wp.ctypes.data)
+    if st != OK:
+        raise RuntimeError(f"conv_pack: {last_error()} (status {st})")
+    return wp
 
 
 def bias_act_f32(x: int, bias: int, C: int, HW: int, relu: bool, stream: int = 0) -> int:

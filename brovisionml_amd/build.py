@@ -65,6 +65,8 @@ SOURCES = [
     os.path.join(CSRC, "dsine_ops.hip"),      # AngMF / RayReLU kernels + C ABI
     os.path.join(CSRC, "upsample.hip"),       # convex upsample + normalise
     os.path.join(CSRC, "gru.hip"),            # the refiner's fused elementwise steps
+    os.path.join(CSRC, "heads.hip"),          # the refiner's heads after their 3x3 layer
+    os.path.join(CSRC, "conv.hip"),           # the refiner's 3x3 / 5x5 convolutions
 ]
 HOST_SOURCES = [
     os.path.join(CSRC, "dsine_ops_cpu.cpp"),  # CPU branch (C ABI *_cpu_f32)

@@ -1,0 +1,342 @@
+// The refiner's k x k convolutions (k = 3, 5; stride 1, zero "same" padding)
+// as implicit GEMMs on the fp32 matrix cores (the C ABI's bvml_dsine_conv_*):
+// rows = output channels, columns = pixels, the reduction over (input
+// channel, tap).  No im2col buffer: a workgroup of 4 waves owns a 16 x 16
+// pixel tile and 64 or 128 output channels (each wave 64 channels x 4 or 8
+// tile rows: 16 or 32 accumulator blocks, so each weight load feeds 4 or 8
+// products); for every chunk of 4 input channels it stages the
+// tile's halo (TH + k - 1) x (16 + k - 1) in LDS (double-buffered, the next
+// chunk's loads in flight during the current chunk's products), then for each
+// tap runs v_mfma_f32_16x16x4_f32 steps with
+//   A = the packed weights of 16 output channels x the chunk's 4 channels at
+//       that tap (one coalesced 256-byte load per step, from L2; see
+//       bvml_dsine_conv_pack_f32),
+//   B = the halo at the tap's shift: 4 channels x 16 pixels of one tile row.
+// Each sum is fp32 in the matrix instruction's order.  The epilogues fuse
+// what the refiner does next (src/dsine_refine.cpp:138-159):
+//   kPlain   out = the sum (the bias is added by the consumer)
+//   kGates   convz and convr as one convolution whose 16-channel blocks
+//            alternate z, r: z = sigmoid(s_z + b_z), rh = sigmoid(s_r + b_r) h
+//   kUpdate  convq: h_new = (1 - z) h + z tanh(s + b_q), to h_new and h_copy
+// in the rounding of bvml_dsine_gru_gates_f32 / bvml_dsine_gru_update_f32.
+
+#include <hip/hip_runtime.h>
+
+#include <climits>
+#include <cstdint>
+#include <string>
+
+#include "bvml_dsine.h"
+#include "status.h"
+
+namespace {
+
+using bvml::fail;
+using bvml::overlaps;
+
+typedef float v4f __attribute__((ext_vector_type(4)));
+
+constexpr int kTW = 16;      // tile width: one MFMA column block per tile row
+constexpr int kCC = 4;       // input channels per chunk (one MFMA k-step per tap)
+constexpr int kThreads = 256;
+
+enum Epi : int { kPlain = 0, kGates = 1, kUpdate = 2 };
+
+struct ConvArgs {
+    const float* x;     // cin planes of H x W
+    const float* wp;    // packed: [chunk][tap][mblock][64]
+    float* out;         // kPlain: cout planes
+    const float* b0;    // kGates: b_z, kUpdate: b_q
+    const float* b1;    // kGates: b_r
+    const float* h;     // kGates, kUpdate: the hidden state (64 planes)
+    const float* z;     // kUpdate: the update gate
+    float* o0;          // kGates: z, kUpdate: h_new
+    float* o1;          // kGates: rh, kUpdate: h_copy (may be NULL)
+    int cin, cout, H, W, mblocks, tiles_x;
+    long long HW;
+};
+
+__device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
+
+__device__ __forceinline__ float gru_mix(float z, float h, float q) {
+#pragma clang fp contract(off)
+    const float omz = 1.0f - z;
+    return omz * h + z * q;
+}
+
+// K: kernel size; TH: tile rows; WM x WN waves (WM along the channels, WN
+// along the tile rows); each wave 4 M-blocks (64 output channels) x NB tile rows.
+template <int K, int TH, int WM, int WN, int EPI>
+__global__ __launch_bounds__(kThreads) void conv_kernel(ConvArgs a) {
+    constexpr int P = K / 2;
+    constexpr int HR = TH + K - 1, HC = kTW + K - 1, HS = HR * HC;  // halo rows, cols, size
+    constexpr int HALO = kCC * HS;                                   // floats per chunk
+    constexpr int PER_T = (HALO + kThreads - 1) / kThreads;
+    constexpr int NB = TH / WN;                                      // tile rows per wave
+    constexpr int TAPS = K * K;
+    static_assert(WM * WN == kThreads / 64, "4 waves");
+    __shared__ float halo[2][HALO];
+
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, col = lane & 15;
+    const int wm = wave % WM, wn = wave / WM;
+    const int tx0 = (blockIdx.x % a.tiles_x) * kTW, ty0 = (blockIdx.x / a.tiles_x) * TH;
+    const int mb0 = blockIdx.y * (4 * WM) + 4 * wm;  // the wave's first M-block
+    const int nchunks = (a.cin + kCC - 1) / kCC;
+
+    // halo element e of a chunk: (channel, halo row, halo col), its source
+    auto halo_load = [&](int chunk, float (&v)[PER_T]) {
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            const int e = tid + i * kThreads;
+            float val = 0.0f;
+            if (e < HALO) {
+                const int c = chunk * kCC + e / HS, rem = e % HS;
+                const int y = ty0 + rem / HC - P, x = tx0 + rem % HC - P;
+                if (c < a.cin && y >= 0 && y < a.H && x >= 0 && x < a.W)
+                    val = a.x[(size_t)c * a.HW + (size_t)y * a.W + x];
+            }
+            v[i] = val;
+        }
+    };
+    auto halo_store = [&](int buf, const float (&v)[PER_T]) {
+#pragma unroll
+        for (int i = 0; i < PER_T; ++i) {
+            const int e = tid + i * kThreads;
+            if (e < HALO) halo[buf][e] = v[i];
+        }
+    };
+
+    v4f acc[4][NB];
+#pragma unroll
+    for (int m = 0; m < 4; ++m)
+#pragma unroll
+        for (int n = 0; n < NB; ++n) acc[m][n] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+
+    float pre[PER_T];
+    halo_load(0, pre);
+    halo_store(0, pre);
+    __syncthreads();
+    const float* wbase = a.wp + (size_t)mb0 * 64 + lane;
+    const size_t tap_stride = (size_t)a.mblocks * 64;
+    for (int chunk = 0; chunk < nchunks; ++chunk) {
+        const int buf = chunk & 1;
+        const bool more = chunk + 1 < nchunks;
+        if (more) halo_load(chunk + 1, pre);
+        const float* hb = halo[buf] + g * HS + (wn * NB) * HC + col;
+        const float* wc = wbase + (size_t)chunk * TAPS * tap_stride;
+        // the A operands one tap ahead, the B operands (LDS) one tap ahead
+        float af[3][4];
+#pragma unroll
+        for (int q = 0; q < 2; ++q)
+#pragma unroll
+            for (int m = 0; m < 4; ++m) af[q][m] = wc[(size_t)q * tap_stride + m * 64];
+        float bf[2][NB];
+#pragma unroll
+        for (int n = 0; n < NB; ++n) bf[0][n] = hb[n * HC];
+#pragma unroll
+        for (int t = 0; t < TAPS; ++t) {
+            if (t + 1 < TAPS) {
+                const int ky = (t + 1) / K, kx = (t + 1) % K;
+#pragma unroll
+                for (int n = 0; n < NB; ++n) bf[(t + 1) & 1][n] = hb[(n + ky) * HC + kx];
+            }
+            if (t + 2 < TAPS) {
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+                    af[(t + 2) % 3][m] = wc[(size_t)(t + 2) * tap_stride + m * 64];
+            }
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int n = 0; n < NB; ++n)
+                    acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[t % 3][m], bf[t & 1][n],
+                                                                    acc[m][n], 0, 0, 0);
+        }
+        if (more) halo_store(buf ^ 1, pre);
+        __syncthreads();
+    }
+
+    // epilogue: lane (g, col), register r of acc[m][n] is output channel
+    // 16 (mb0 + m) + 4 g + r (in the packed order) at pixel
+    // (ty0 + wn NB + n, tx0 + col)
+    const int x = tx0 + col;
+    if (x >= a.W) return;
+#pragma unroll
+    for (int n = 0; n < NB; ++n) {
+        const int y = ty0 + wn * NB + n;
+        if (y >= a.H) continue;
+        const size_t px = (size_t)y * a.W + x;
+        if constexpr (EPI == kPlain) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int o = 16 * (mb0 + m) + 4 * g + r;
+                    if (o < a.cout) a.out[(size_t)o * a.HW + px] = acc[m][n][r];
+                }
+        } else if constexpr (EPI == kGates) {
+            // M-blocks alternate z, r: block 2i holds z channels 16i.., 2i + 1
+            // the r channels 16i.. (mb0 is a multiple of 4, so m = 0, 2 are z)
+#pragma unroll
+            for (int m = 0; m < 4; m += 2)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int c = 16 * ((mb0 + m) / 2) + 4 * g + r;
+                    if (c >= a.cout / 2) continue;
+                    const size_t i = (size_t)c * a.HW + px;
+                    const float zz = sigmoid(acc[m][n][r] + a.b0[c]);
+                    const float rr = sigmoid(acc[m + 1][n][r] + a.b1[c]);
+                    a.o0[i] = zz;
+                    a.o1[i] = rr * a.h[i];
+                }
+        } else {
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int c = 16 * (mb0 + m) + 4 * g + r;
+                    if (c >= a.cout) continue;
+                    const size_t i = (size_t)c * a.HW + px;
+                    const float v = gru_mix(a.z[i], a.h[i], tanhf(acc[m][n][r] + a.b0[c]));
+                    a.o0[i] = v;
+                    if (a.o1) a.o1[i] = v;
+                }
+        }
+    }
+}
+
+template <int K, int TH, int WM, int WN, int EPI>
+int launch(const ConvArgs& a0, hipStream_t stream, const char* op) {
+    ConvArgs a = a0;
+    a.tiles_x = (a.W + kTW - 1) / kTW;
+    const int tiles_y = (a.H + TH - 1) / TH;
+    const int mtiles = a.mblocks / (4 * WM);
+    const long long tiles = (long long)a.tiles_x * tiles_y;
+    if (tiles > INT_MAX) return fail(BVML_DSINE_ESIZE, std::string(op) + ": too many tiles");
+    hipLaunchKernelGGL((conv_kernel<K, TH, WM, WN, EPI>), dim3((unsigned)tiles, (unsigned)mtiles),
+                       dim3(kThreads), 0, stream, a);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return fail((int)e, std::string(op) + " launch: " + hipGetErrorString(e));
+    return BVML_DSINE_OK;
+}
+
+// 16-channel M-blocks of the packed weights: a multiple of 4 (each wave
+// takes 4); launches with two waves along the channels need a multiple of 8.
+int mblocks_for(int cout) { return (cout + 63) / 64 * 4; }
+
+int check_common(const char* op, const float* x, int cin, int H, int W, const float* wp, int k) {
+    if (H < 0 || W < 0 || cin < 1) return fail(BVML_DSINE_ESHAPE, std::string(op) + ": bad shape");
+    if (k != 3 && k != 5) return fail(BVML_DSINE_EK, std::string(op) + ": k must be 3 or 5");
+    if (!x || !wp) return fail(BVML_DSINE_ENULL, std::string(op) + ": x and wp must be non-NULL");
+    if ((long long)H * W * (cin > 256 ? cin : 256) > (1LL << 40))
+        return fail(BVML_DSINE_ESIZE, std::string(op) + ": map too large");
+    return BVML_DSINE_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+long long bvml_dsine_conv_packed_size(int cout, int cin, int k) {
+    if (cout < 1 || cin < 1 || (k != 3 && k != 5)) return -1;
+    const long long chunks = (cin + kCC - 1) / kCC;
+    return chunks * k * k * mblocks_for(cout) * 64LL;
+}
+
+int bvml_dsine_conv_pack_f32(const float* w, int cout, int cin, int k, int interleave,
+                             float* wp) {
+    if (!w || !wp) return fail(BVML_DSINE_ENULL, "conv_pack: w and wp must be non-NULL");
+    if (cout < 1 || cin < 1) return fail(BVML_DSINE_ESHAPE, "conv_pack: bad shape");
+    if (k != 3 && k != 5) return fail(BVML_DSINE_EK, "conv_pack: k must be 3 or 5");
+    if (interleave && cout % 32 != 0)
+        return fail(BVML_DSINE_EPARAM, "conv_pack: interleaved weights need cout % 32 == 0");
+    const int mblocks = mblocks_for(cout), taps = k * k, chunks = (cin + kCC - 1) / kCC;
+    for (int ch = 0; ch < chunks; ++ch)
+        for (int t = 0; t < taps; ++t)
+            for (int mb = 0; mb < mblocks; ++mb)
+                for (int l = 0; l < 64; ++l) {
+                    const int c = ch * kCC + (l >> 4);
+                    int o = 16 * mb + (l & 15);
+                    if (interleave) {
+                        // block 2i: channels 16i.. of the first half (z), 2i + 1:
+                        // channels 16i.. of the second half (r)
+                        const int half = cout / 2;
+                        o = (mb & 1 ? half : 0) + 16 * (mb >> 1) + (l & 15);
+                        if (16 * (mb >> 1) >= half) o = cout;  // padding block
+                    }
+                    const size_t dst = (((size_t)ch * taps + t) * mblocks + mb) * 64 + l;
+                    wp[dst] = (o < cout && c < cin) ? w[((size_t)o * cin + c) * taps + t] : 0.0f;
+                }
+    return BVML_DSINE_OK;
+}
+
+int bvml_dsine_conv_f32(const float* x, int cin, int H, int W, const float* wp, int cout, int k,
+                        float* out, void* stream) {
+    if (int st = check_common("conv", x, cin, H, W, wp, k)) return st;
+    if (cout < 1) return fail(BVML_DSINE_ESHAPE, "conv: bad shape");
+    if (!out) return fail(BVML_DSINE_ENULL, "conv: out must be non-NULL");
+    const long long HW = (long long)H * W;
+    if (HW == 0) return BVML_DSINE_OK;
+    if (overlaps(out, (size_t)cout * HW * 4, x, (size_t)cin * HW * 4))
+        return fail(BVML_DSINE_EALIAS, "conv: out overlaps x");
+    ConvArgs a{};
+    a.x = x; a.wp = wp; a.out = out; a.cin = cin; a.cout = cout; a.H = H; a.W = W; a.HW = HW;
+    a.mblocks = mblocks_for(cout);
+    const hipStream_t s = static_cast<hipStream_t>(stream);
+    if (a.mblocks % 8 == 0)
+        return k == 5 ? launch<5, 16, 2, 2, kPlain>(a, s, "conv")
+                      : launch<3, 16, 2, 2, kPlain>(a, s, "conv");
+    return k == 5 ? launch<5, 16, 1, 4, kPlain>(a, s, "conv")
+                  : launch<3, 16, 1, 4, kPlain>(a, s, "conv");
+}
+
+int bvml_dsine_conv_gru_gates_f32(const float* x, int cin, int H, int W, const float* wp,
+                                  int C, const float* bias_z, const float* bias_r,
+                                  const float* h, float* z, float* rh, void* stream) {
+    if (int st = check_common("conv_gru_gates", x, cin, H, W, wp, 5)) return st;
+    if (C < 1 || C % 32 != 0)
+        return fail(BVML_DSINE_ESHAPE, "conv_gru_gates: C must be a multiple of 32");
+    if (!bias_z || !bias_r || !h || !z || !rh)
+        return fail(BVML_DSINE_ENULL, "conv_gru_gates: pointers must be non-NULL");
+    const long long HW = (long long)H * W;
+    if (HW == 0) return BVML_DSINE_OK;
+    const size_t xb = (size_t)cin * HW * 4, cb = (size_t)C * HW * 4;
+    if (overlaps(z, cb, x, xb) || overlaps(rh, cb, x, xb) || overlaps(z, cb, rh, cb) ||
+        overlaps(z, cb, h, cb) || overlaps(rh, cb, h, cb))
+        return fail(BVML_DSINE_EALIAS, "conv_gru_gates: z and rh must not overlap x, h or each other");
+    ConvArgs a{};
+    a.x = x; a.wp = wp; a.cin = cin; a.cout = 2 * C; a.H = H; a.W = W; a.HW = HW;
+    a.b0 = bias_z; a.b1 = bias_r; a.h = h; a.o0 = z; a.o1 = rh;
+    a.mblocks = mblocks_for(2 * C);
+    if (a.mblocks % 8 == 0)
+        return launch<5, 16, 2, 2, kGates>(a, static_cast<hipStream_t>(stream), "conv_gru_gates");
+    return launch<5, 16, 1, 4, kGates>(a, static_cast<hipStream_t>(stream), "conv_gru_gates");
+}
+
+int bvml_dsine_conv_gru_update_f32(const float* x, int cin, int H, int W, const float* wp, int C,
+                                   const float* bias_q, const float* z, const float* h,
+                                   float* h_new, float* h_copy, void* stream) {
+    if (int st = check_common("conv_gru_update", x, cin, H, W, wp, 5)) return st;
+    if (C < 1 || C % 64 != 0)
+        return fail(BVML_DSINE_ESHAPE, "conv_gru_update: C must be a multiple of 64");
+    if (!bias_q || !z || !h || !h_new)
+        return fail(BVML_DSINE_ENULL, "conv_gru_update: pointers must be non-NULL");
+    const long long HW = (long long)H * W;
+    if (HW == 0) return BVML_DSINE_OK;
+    const size_t xb = (size_t)cin * HW * 4, cb = (size_t)C * HW * 4;
+    if (overlaps(h_new, cb, x, xb) || (h_copy && overlaps(h_copy, cb, x, xb)) ||
+        overlaps(h_new, cb, z, cb) || (h_copy && (overlaps(h_copy, cb, z, cb) ||
+                                                 overlaps(h_copy, cb, h, cb) ||
+                                                 overlaps(h_copy, cb, h_new, cb))))
+        return fail(BVML_DSINE_EALIAS, "conv_gru_update: outputs overlap an input");
+    ConvArgs a{};
+    a.x = x; a.wp = wp; a.cin = cin; a.cout = C; a.H = H; a.W = W; a.HW = HW;
+    a.b0 = bias_q; a.z = z; a.h = h; a.o0 = h_new; a.o1 = h_copy;
+    a.mblocks = mblocks_for(C);
+    // 64 channels: one M tile of 4 blocks per wave, all four waves along the rows
+    return launch<5, 16, 1, 4, kUpdate>(a, static_cast<hipStream_t>(stream), "conv_gru_update");
+}
+
+}  // extern "C"

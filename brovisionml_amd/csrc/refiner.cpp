@@ -3,26 +3,27 @@
 // (include/bvml_dsine.h) and MIOpen.
 //
 // Per iteration (src/dsine_refine.cpp:255-287), on persistent per-grid maps:
-//   zr   = conv5x5([h | feature | uv], [W_z; W_r])           MIOpen, 130 -> 128
-//   z, r*h                                                   bvml_dsine_gru_gates_f32
-//   qp   = conv5x5([r*h | feature | uv], W_q)                MIOpen, 130 -> 64
-//   h    = (1 - z) h + z tanh(qp + b_q), also into [h | uv]  bvml_dsine_gru_update_f32
-//   t0   = relu(conv3x3([h | uv], the heads' first layers))  MIOpen + bias_act
-//   t1   = relu(grouped 1x1 conv(t0))                        MIOpen + bias_act
-//   prob, xy, angle = 1x1 convs of t1's slices + bias        MIOpen + bias_act
+//   z, r*h = gates of conv5x5([h | feature | uv], [W_z; W_r])  bvml_dsine_conv_gru_gates_f32
+//   h    = (1 - z) h + z tanh(conv5x5([r*h | feature | uv], W_q) + b_q),
+//          also into [h | uv]                                bvml_dsine_conv_gru_update_f32
+//   t0   = conv3x3([h | uv], the heads' first layers)        MIOpen, 66 -> 192 or 256
+//   prob, xy, angle = the heads' 1x1 layers on relu(t0 + b0) bvml_dsine_heads_mlp_f32
 //   pred = angmf_propagate(pred, prob, xy, angle) on logits  bvml_dsine_angmf_propagate_f32
-// and, in the last iteration only, the up-mask head's last 1x1 convolution
-// and the convex upsample + normalise with its bias (the reference computes
+// and, in the last iteration only, the up-mask head (its 1x1 layers in the
+// same heads pass) and the convex upsample + normalise with its bias (the
+// reference computes
 // an up-sampled map every iteration but returns the last one only,
 // src/dsine_refine.cpp:276-283, :289-293, so the others are dead work).  In
-// the first four iterations the heads' first two layers run for the three
-// heads the propagate reads (192 channels); the last iteration runs all four
+// the first four iterations the heads run for the three heads the propagate
+// reads (their 3x3 layer at 192 channels); the last iteration runs all four
 // (256).  The convolutions run without their bias; the fused kernels add it
 // in the reference's rounding (a bias add after the convolution's sum).
 //
-// The convolutions are MIOpen's immediate mode, the solution with the lowest
-// time estimate for each shape, as PyTorch picks them on ROCm without
-// benchmarking; the plans are made once per grid size.
+// The 5x5 convolutions are this library's implicit GEMMs on the fp32 matrix
+// cores (conv.hip); the heads' 3x3 layer is MIOpen's immediate mode, the
+// solution with the lowest time estimate, as PyTorch picks it on ROCm without
+// benchmarking (its Winograd kernel beats the direct product there); the
+// plans are made once per grid size.
 
 #include "bvml_dsine_refine.h"
 #include "refiner_common.h"
@@ -526,28 +527,25 @@ struct bvml_dsine_refiner {
 
     // weights on the device, one allocation
     float* warena = nullptr;
+    // convz + convr and convq, packed for the implicit-GEMM kernels
     const float *w_zr = nullptr, *b_z = nullptr, *b_r = nullptr, *w_q = nullptr, *b_q = nullptr;
-    const float *w_h0 = nullptr, *b_h0 = nullptr, *w_h2 = nullptr, *b_h2 = nullptr;
-    const float* w4[kHeads] = {};
+    const float *w_h0 = nullptr, *b_h0 = nullptr, *w2p = nullptr, *b_h2 = nullptr;
+    const float* w4p[kHeads] = {};  // the 1x1 layers packed for bvml_dsine_heads_mlp_f32
     const float* b4[kHeads] = {};
 
     // the maps of one grid size, one allocation
     int H = 0, W = 0;
     float* arena = nullptr;
-    float *hx = nullptr, *rhx = nullptr, *hin = nullptr, *zr = nullptr, *z = nullptr;
-    float *qp = nullptr, *t0 = nullptr, *t1 = nullptr, *head[kHeads] = {}, *ray = nullptr;
+    float *hx = nullptr, *rhx = nullptr, *hin = nullptr, *z = nullptr;
+    float *t0 = nullptr, *head[kHeads] = {}, *ray = nullptr;
     float *pred[2] = {}, *up = nullptr;
     void* ws = nullptr;
     size_t ws_bytes = 0;
     // [0]: the three heads the propagate reads, [1]: all four
-    ConvPlan zr_p, q_p, h0_p[2], h2_p[2], c4_p[kHeads];
+    ConvPlan h0_p[2];
 
     void drop_grid() {
-        zr_p.reset();
-        q_p.reset();
         for (auto& p : h0_p) p.reset();
-        for (auto& p : h2_p) p.reset();
-        for (auto& p : c4_p) p.reset();
         if (arena) (void)hipFree(arena);
         if (ws) (void)hipFree(ws);
         arena = nullptr;
@@ -570,48 +568,70 @@ struct bvml_dsine_refiner {
     int conv(const ConvPlan& p, const float* w, const float* x, float* y);
 };
 
-// Copies the host weights into the device arena, in the layout the
-// convolutions read: [W_z; W_r] as one 128-filter weight, the four heads'
-// first layers as one 256-filter weight and their middle layers as one
-// 4-group weight (each head's filters contiguous, prob, xy, angle, up_mask:
-// the first three heads are a prefix).
+// Copies the host weights into the device arena, in the layout the kernels
+// read: [W_z; W_r] as one 128-filter weight, the four heads' first layers as
+// one 256-filter weight (each head's filters contiguous, prob, xy, angle,
+// up_mask: the first three heads are a prefix), their 1x1 layers packed for
+// bvml_dsine_heads_mlp_f32.
 int bvml_dsine_refiner::upload() {
-    const auto& s = specs();
-    std::vector<std::pair<const float**, std::vector<int>>> parts;
-    parts.push_back({&w_zr, {kZw, kRw}});
-    parts.push_back({&b_z, {kZb}});
-    parts.push_back({&b_r, {kRb}});
-    parts.push_back({&w_q, {kQw}});
-    parts.push_back({&b_q, {kQb}});
-    std::vector<int> h0w, h0b, h2w, h2b;
+    std::vector<float> w2(kHeads * kMid * kMid), w2p_h((size_t)kHeads * 4096);
+    std::vector<std::vector<float>> w4p_h(kHeads);
+    const float* w4src[kHeads];
+    float* w4dst[kHeads];
     for (int h = 0; h < kHeads; ++h) {
-        h0w.push_back(head_w(h, 0));
-        h0b.push_back(head_b(h, 0));
-        h2w.push_back(head_w(h, 1));
-        h2b.push_back(head_b(h, 1));
+        std::memcpy(&w2[(size_t)h * kMid * kMid], host[head_w(h, 1)].data(),
+                    (size_t)kMid * kMid * sizeof(float));
+        w4p_h[h].resize((size_t)bvml_dsine_heads_packed_size(kHeadOut[h]));
+        w4src[h] = host[head_w(h, 2)].data();
+        w4dst[h] = w4p_h[h].data();
+    }
+    if (const int st = bvml_dsine_heads_pack_f32(w2.data(), w4src, kHeadOut, kHeads, w2p_h.data(),
+                                                 w4dst))
+        return fail(st, std::string("forward: heads_pack: ") + bvml_dsine_last_error());
+    // [W_z; W_r] with their 16-channel blocks interleaved, W_q
+    std::vector<float> wzr(host[kZw]);
+    wzr.insert(wzr.end(), host[kRw].begin(), host[kRw].end());
+    std::vector<float> wzr_p((size_t)bvml_dsine_conv_packed_size(2 * kHidden, kHx, 5));
+    std::vector<float> wq_p((size_t)bvml_dsine_conv_packed_size(kHidden, kHx, 5));
+    if (const int st = bvml_dsine_conv_pack_f32(wzr.data(), 2 * kHidden, kHx, 5, 1, wzr_p.data()))
+        return fail(st, std::string("forward: conv_pack: ") + bvml_dsine_last_error());
+    if (const int st = bvml_dsine_conv_pack_f32(host[kQw].data(), kHidden, kHx, 5, 0, wq_p.data()))
+        return fail(st, std::string("forward: conv_pack: ") + bvml_dsine_last_error());
+    using Src = std::vector<const std::vector<float>*>;
+    std::vector<std::pair<const float**, Src>> parts;
+    parts.push_back({&w_zr, {&wzr_p}});
+    parts.push_back({&b_z, {&host[kZb]}});
+    parts.push_back({&b_r, {&host[kRb]}});
+    parts.push_back({&w_q, {&wq_p}});
+    parts.push_back({&b_q, {&host[kQb]}});
+    Src h0w, h0b, h2b;
+    for (int h = 0; h < kHeads; ++h) {
+        h0w.push_back(&host[head_w(h, 0)]);
+        h0b.push_back(&host[head_b(h, 0)]);
+        h2b.push_back(&host[head_b(h, 1)]);
     }
     parts.push_back({&w_h0, h0w});
     parts.push_back({&b_h0, h0b});
-    parts.push_back({&w_h2, h2w});
+    parts.push_back({&w2p, {&w2p_h}});
     parts.push_back({&b_h2, h2b});
     for (int h = 0; h < kHeads; ++h) {
-        parts.push_back({&w4[h], {head_w(h, 2)}});
-        parts.push_back({&b4[h], {head_b(h, 2)}});
+        parts.push_back({&w4p[h], {&w4p_h[h]}});
+        parts.push_back({&b4[h], {&host[head_b(h, 2)]}});
     }
     std::vector<size_t> offset;
     size_t total = 0;
     for (const auto& p : parts) {
         offset.push_back(total);
         size_t n = 0;
-        for (int i : p.second) n += (size_t)s[i].numel;
+        for (const std::vector<float>* v : p.second) n += v->size();
         total += round64(n);
     }
     std::vector<float> staging(total, 0.0f);
     for (size_t k = 0; k < parts.size(); ++k) {
         size_t at = offset[k];
-        for (int i : parts[k].second) {
-            std::memcpy(&staging[at], host[i].data(), host[i].size() * sizeof(float));
-            at += host[i].size();
+        for (const std::vector<float>* v : parts[k].second) {
+            std::memcpy(&staging[at], v->data(), v->size() * sizeof(float));
+            at += v->size();
         }
     }
     if (!warena) {
@@ -672,11 +692,10 @@ int bvml_dsine_refiner::plan(int h, int w) {
     if (arena && H == h && W == w) return BVML_DSINE_OK;
     drop_grid();
     const size_t hw = (size_t)h * w;
-    const int planes[] = {kHx, kHx, kHin, 2 * kHidden, kHidden, kHidden, kHeads * kMid,
-                          kHeads * kMid, kHeadOut[0], kHeadOut[1], kHeadOut[2], kHeadOut[3],
-                          3, 3, 3, 3 * kUp * kUp};
-    float** dst[] = {&hx, &rhx, &hin, &zr, &z, &qp, &t0, &t1, &head[0], &head[1], &head[2],
-                     &head[3], &pred[0], &pred[1], &ray, &up};
+    const int planes[] = {kHx, kHx, kHin, kHidden, kHeads * kMid, kHeadOut[0], kHeadOut[1],
+                          kHeadOut[2], kHeadOut[3], 3, 3, 3, 3 * kUp * kUp};
+    float** dst[] = {&hx, &rhx, &hin, &z, &t0, &head[0], &head[1], &head[2], &head[3],
+                     &pred[0], &pred[1], &ray, &up};
     size_t total = 0;
     std::vector<size_t> offset;
     for (int c : planes) {
@@ -690,20 +709,10 @@ int bvml_dsine_refiner::plan(int h, int w) {
     }
     for (size_t i = 0; i < offset.size(); ++i) *dst[i] = arena + offset[i];
     int st;
-    if ((st = make_plan(zr_p, kHx, 2 * kHidden, 5, 1, h, w)) ||
-        (st = make_plan(q_p, kHx, kHidden, 5, 1, h, w)))
-        return drop_grid(), st;
-    for (int i = 0; i < 2; ++i) {
-        const int nh = 3 + i;
-        if ((st = make_plan(h0_p[i], kHin, nh * kMid, 3, 1, h, w)) ||
-            (st = make_plan(h2_p[i], nh * kMid, nh * kMid, 1, nh, h, w)))
-            return drop_grid(), st;
-    }
-    for (int i = 0; i < kHeads; ++i)
-        if ((st = make_plan(c4_p[i], kMid, kHeadOut[i], 1, 1, h, w))) return drop_grid(), st;
+    for (int i = 0; i < 2; ++i)
+        if ((st = make_plan(h0_p[i], kHin, (3 + i) * kMid, 3, 1, h, w))) return drop_grid(), st;
     size_t need = 0;
-    for (const ConvPlan* p : {&zr_p, &q_p, &h0_p[0], &h0_p[1], &h2_p[0], &h2_p[1], &c4_p[0],
-                              &c4_p[1], &c4_p[2], &c4_p[3]})
+    for (const ConvPlan* p : {&h0_p[0], &h0_p[1]})
         need = p->ws > need ? p->ws : need;
     if (need) {
         e = hipMalloc(&ws, need);
@@ -828,7 +837,6 @@ int bvml_dsine_refiner_forward(bvml_dsine_refiner* r, const float* normal, const
     const double sw = (double)w8 / orig_w, sh = (double)h8 / orig_h;
     const double fu = fx * sw, cu = (cx + 0.5) * sw, fv = fy * sh, cv = (cy + 0.5) * sh;
     const int C = kHidden;
-    const long long HW = (long long)hw;
     auto copy = [&](float* dst, const float* src, size_t planes) {
         return hipMemcpyAsync(dst, src, planes * hw * b, hipMemcpyDeviceToDevice, strm);
     };
@@ -859,27 +867,23 @@ int bvml_dsine_refiner_forward(bvml_dsine_refiner* r, const float* normal, const
     for (int it = 0; it < kIter; ++it) {
         const bool last = it == kIter - 1;
         const int nh = last ? kHeads : kHeads - 1;
-        // ConvGRU (:138-159); h_new overwrites h in hx and is copied into hin
-        if ((st = r->conv(r->zr_p, r->w_zr, r->hx, r->zr)) ||
-            (st = ck(bvml_dsine_gru_gates_f32(r->zr, r->b_z, r->b_r, r->hx, C, HW, r->z, r->rhx,
-                                              stream), "gru_gates")) ||
-            (st = r->conv(r->q_p, r->w_q, r->rhx, r->qp)) ||
-            (st = ck(bvml_dsine_gru_update_f32(r->qp, r->b_q, r->z, r->hx, C, HW, r->hx, r->hin,
-                                               stream), "gru_update")))
+        // ConvGRU (:138-159): the two 5x5 convolutions with the gates and
+        // the update in their epilogues; h_new overwrites h in hx and is
+        // copied into hin
+        if ((st = ck(bvml_dsine_conv_gru_gates_f32(r->hx, kHx, h8, w8, r->w_zr, C, r->b_z, r->b_r,
+                                                   r->hx, r->z, r->rhx, stream),
+                     "conv_gru_gates")) ||
+            (st = ck(bvml_dsine_conv_gru_update_f32(r->rhx, kHx, h8, w8, r->w_q, C, r->b_q, r->z,
+                                                    r->hx, r->hx, r->hin, stream),
+                     "conv_gru_update")))
             return st;
-        // the heads (:119-127, :257-267, :276)
-        const ConvPlan& h0 = r->h0_p[last ? 1 : 0];
-        const ConvPlan& h2 = r->h2_p[last ? 1 : 0];
-        if ((st = r->conv(h0, r->w_h0, r->hin, r->t0)) ||
-            (st = ck(bvml_dsine_bias_act_f32(r->t0, r->b_h0, nh * kMid, HW, 1, stream), "bias_act")) ||
-            (st = r->conv(h2, r->w_h2, r->t0, r->t1)) ||
-            (st = ck(bvml_dsine_bias_act_f32(r->t1, r->b_h2, nh * kMid, HW, 1, stream), "bias_act")))
+        // the heads (:119-127, :257-267, :276): the 3x3 layers, then the rest
+        // in one pass; the up-mask head's last bias is the upsample's
+        const float* b4[kHeads] = {r->b4[0], r->b4[1], r->b4[2], nullptr};
+        if ((st = r->conv(r->h0_p[last ? 1 : 0], r->w_h0, r->hin, r->t0)) ||
+            (st = ck(bvml_dsine_heads_mlp_f32(r->t0, r->b_h0, r->w2p, r->b_h2, r->w4p, b4, kHeadOut,
+                                              nh, h8, w8, r->head, stream), "heads_mlp")))
             return st;
-        for (int h = 0; h < kHeads - 1; ++h)
-            if ((st = r->conv(r->c4_p[h], r->w4[h], r->t1 + (size_t)h * kMid * hw, r->head[h])) ||
-                (st = ck(bvml_dsine_bias_act_f32(r->head[h], r->b4[h], kHeadOut[h], HW, 0, stream),
-                         "bias_act")))
-                return st;
         // the propagate on the logits (:262-274)
         if ((st = ck(bvml_dsine_angmf_propagate_f32(r->pred[cur], r->head[0], r->head[1],
                                                     r->head[2], r->ray, fu, cu, fv, cv, 1, h8, w8,
@@ -892,8 +896,7 @@ int bvml_dsine_refiner_forward(bvml_dsine_refiner* r, const float* normal, const
         if (!last) continue;
         // up_pred_norm = normalize(convex_upsample(pred_norm, up_mask))  (:276-283)
         float* dst = direct ? out : r->up;
-        if ((st = r->conv(r->c4_p[3], r->w4[3], r->t1 + (size_t)3 * kMid * hw, r->head[3])) ||
-            (st = ck(bvml_dsine_convex_upsample_bias_f32(r->pred[cur], r->head[3], r->b4[3], 1, 3,
+        if ((st = ck(bvml_dsine_convex_upsample_bias_f32(r->pred[cur], r->head[3], r->b4[3], 1, 3,
                                                          h8, w8, kUp, 1, kUpEps, dst, 0, stream),
                      "convex_upsample")))
             return st;

@@ -230,6 +230,65 @@ int bvml_dsine_gru_update_f32(const float* q_pre, const float* bias_q, const flo
 int bvml_dsine_bias_act_f32(float* x, const float* bias, int C, long long HW, int relu,
                             void* stream);
 
+/*
+ * The refiner's four prediction heads after their first layer, fused into one
+ * per-pixel pass on the fp32 matrix cores (no counterpart in the reference,
+ * where each head is conv3x3 -> ReLU -> conv1x1 -> ReLU -> conv1x1 of
+ * brotensor ops, src/dsine_refine.cpp:119-127).  For heads h < nheads and
+ * every pixel p of the H x W map:
+ *   a = relu(t0[64h + c][p] + b0[64h + c])       c < 64: the 3x3 layer's
+ *                                                output without its bias
+ *   t = relu(W2_h a + b2_h)                      W2_h: head h's 64 x 64 1x1
+ *   out[h][o][p] = (W4_h t)[o] + b4[h][o]        o < outs[h]; b4[h] NULL: no bias
+ * Each sum in fp32, then its bias added once.  W2 and W4 in the layout
+ * bvml_dsine_heads_pack_f32 writes: w2p holds nheads * 4096 floats, w4p[h]
+ * bvml_dsine_heads_packed_size(outs[h]).  t0: 64 * nheads planes; b0, b2:
+ * 64 * nheads floats; out[h]: outs[h] planes, not overlapping t0 or each
+ * other.  nheads 1..4, outs 1..4096.  ReLU is v < 0 ? 0 : v.
+ * bvml_dsine_heads_pack_f32 runs on the host: w2 holds the nheads 64 x 64
+ * middle-layer weights (OIHW, 1x1) back to back, w4[h] head h's outs[h] x 64
+ * last-layer weights.
+ */
+int bvml_dsine_heads_mlp_f32(const float* t0, const float* b0, const float* w2p,
+                             const float* b2, const float* const* w4p, const float* const* b4,
+                             const int* outs, int nheads, int H, int W, float* const* out,
+                             void* stream);
+int bvml_dsine_heads_pack_f32(const float* w2, const float* const* w4, const int* outs,
+                              int nheads, float* w2p, float* const* w4p);
+long long bvml_dsine_heads_packed_size(int out);
+
+/*
+ * The refiner's k x k convolutions (k = 3 or 5, stride 1, zero padding k/2:
+ * the ConvGRU's 5x5 layers and the heads' 3x3 first layers,
+ * src/dsine_refine.cpp:94-101, :119-158), as implicit GEMMs on the fp32
+ * matrix cores, with no im2col buffer.  x: cin planes of H x W; the weights
+ * in the layout bvml_dsine_conv_pack_f32 writes from OIHW weights (cout, cin,
+ * k, k), bvml_dsine_conv_packed_size(cout, cin, k) floats, 16-byte aligned.
+ * Each sum in fp32; no bias (the consumer adds it, or the fused epilogue):
+ *   bvml_dsine_conv_f32            out = conv(x) (cout planes)
+ *   bvml_dsine_conv_gru_gates_f32  convz and convr as one 5x5 convolution of
+ *     2C filters (packed with interleave = 1 from [W_z; W_r]); writes
+ *     z = sigmoid(s_z + bias_z) and rh = sigmoid(s_r + bias_r) * h, as
+ *     bvml_dsine_gru_gates_f32 does from the two sums; C % 32 == 0
+ *   bvml_dsine_conv_gru_update_f32 convq (C filters, 5x5); writes
+ *     h_new = (1 - z) h + z tanh(s + bias_q) to h_new and, when non-NULL,
+ *     h_copy, as bvml_dsine_gru_update_f32 does; h_new may be h; C % 64 == 0
+ * Outputs must not overlap x (or, for the fused ones, the other inputs and
+ * each other).  No counterpart in the reference (brotensor's conv2d_forward
+ * followed by its elementwise ops).
+ */
+long long bvml_dsine_conv_packed_size(int cout, int cin, int k);
+int bvml_dsine_conv_pack_f32(const float* w, int cout, int cin, int k, int interleave,
+                             float* wp);
+int bvml_dsine_conv_f32(const float* x, int cin, int H, int W, const float* wp, int cout, int k,
+                        float* out, void* stream);
+int bvml_dsine_conv_gru_gates_f32(const float* x, int cin, int H, int W, const float* wp, int C,
+                                  const float* bias_z, const float* bias_r, const float* h,
+                                  float* z, float* rh, void* stream);
+int bvml_dsine_conv_gru_update_f32(const float* x, int cin, int H, int W, const float* wp, int C,
+                                   const float* bias_q, const float* z, const float* h,
+                                   float* h_new, float* h_copy, void* stream);
+
 /* Message for the calling thread's last non-zero status ("" if none). */
 const char* bvml_dsine_last_error(void);
 

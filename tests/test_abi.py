@@ -20,11 +20,35 @@ CPP_TEST = os.path.join(ROOT, "tests", "cpp", "_build", "test_dsine_ops")
 
 def declared_functions():
     text = open(HEADER).read()
-    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\s*\*?\s*(bvml_dsine_\w+)\s*\(", text, re.M)))
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?(?:long\s+)?\w+\s*\*?\s*(bvml_dsine_\w+)\s*\(",
+                                 text, re.M)))
 
 
 def test_header_declares_the_binding_exports():
     assert declared_functions() == sorted(_lib.EXPORTS)
+
+
+def test_heads_pack_host_checks():
+    """bvml_dsine_heads_pack_f32 and _packed_size run on the host: sizes and
+    argument checks (the packed layout itself is checked on the GPU through
+    the kernel, tests/test_gpu_heads.py)."""
+    lib = _lib.load()
+    assert lib.bvml_dsine_heads_packed_size(25) == 2 * 1024
+    assert lib.bvml_dsine_heads_packed_size(576) == 36 * 1024
+    assert lib.bvml_dsine_heads_packed_size(0) == -1
+    assert lib.bvml_dsine_heads_packed_size(4097) == -1
+    import numpy as np
+    w2p, w4p = _lib.heads_pack_f32(np.ones((2, 64, 64), np.float32),
+                                   [np.ones((17, 64), np.float32), np.ones((1, 64), np.float32)])
+    assert w2p.shape == (8192,) and (w2p == 1).all()
+    # the first output block of the 17-output head holds 16 real rows, the
+    # second 1 real row and 15 zero rows
+    assert w4p[0].shape == (2048,) and w4p[0].sum() == 17 * 64
+    assert w4p[1].sum() == 64
+    vp = ctypes.c_void_p
+    outs = (ctypes.c_int * 1)(25)
+    assert lib.bvml_dsine_heads_pack_f32(None, (vp * 1)(), outs, 1, None, (vp * 1)()) == _lib.ENULL
+    assert lib.bvml_dsine_heads_pack_f32(None, None, outs, 0, None, None) == _lib.EPARAM
 
 
 def test_library_exports_every_declared_symbol():
