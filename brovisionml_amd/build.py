@@ -71,6 +71,7 @@ SOURCES = [
 HOST_SOURCES = [
     os.path.join(CSRC, "dsine_ops_cpu.cpp"),  # CPU branch (C ABI *_cpu_f32)
     os.path.join(CSRC, "status.cpp"),         # error state, bvml_dsine_last_error
+    os.path.join(CSRC, "pack.cpp"),           # weight packing for the matrix-core kernels
 ]
 CXX_SOURCES = [os.path.join(CSRC, "dsine_ops.cpp")]     # the ops' public dispatch
 REFINE_CXX_SOURCES = [os.path.join(CSRC, "dsine_refine.cpp")]  # the Refiner class

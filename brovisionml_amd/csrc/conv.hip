@@ -27,6 +27,7 @@
 #include <string>
 
 #include "bvml_dsine.h"
+#include "pack_layout.h"
 #include "status.h"
 
 namespace {
@@ -37,7 +38,7 @@ using bvml::overlaps;
 typedef float v4f __attribute__((ext_vector_type(4)));
 
 constexpr int kTW = 16;      // tile width: one MFMA column block per tile row
-constexpr int kCC = 4;       // input channels per chunk (one MFMA k-step per tap)
+constexpr int kCC = bvml::pack::kConvChunk;  // input channels per chunk (one k-step per tap)
 constexpr int kThreads = 256;
 
 enum Epi : int { kPlain = 0, kGates = 1, kUpdate = 2 };
@@ -222,9 +223,7 @@ int launch(const ConvArgs& a0, hipStream_t stream, const char* op) {
     return BVML_DSINE_OK;
 }
 
-// 16-channel M-blocks of the packed weights: a multiple of 4 (each wave
-// takes 4); launches with two waves along the channels need a multiple of 8.
-int mblocks_for(int cout) { return (cout + 63) / 64 * 4; }
+using bvml::pack::conv_mblocks;
 
 int check_common(const char* op, const float* x, int cin, int H, int W, const float* wp, int k) {
     if (H < 0 || W < 0 || cin < 1) return fail(BVML_DSINE_ESHAPE, std::string(op) + ": bad shape");
@@ -239,39 +238,6 @@ int check_common(const char* op, const float* x, int cin, int H, int W, const fl
 
 extern "C" {
 
-long long bvml_dsine_conv_packed_size(int cout, int cin, int k) {
-    if (cout < 1 || cin < 1 || (k != 3 && k != 5)) return -1;
-    const long long chunks = (cin + kCC - 1) / kCC;
-    return chunks * k * k * mblocks_for(cout) * 64LL;
-}
-
-int bvml_dsine_conv_pack_f32(const float* w, int cout, int cin, int k, int interleave,
-                             float* wp) {
-    if (!w || !wp) return fail(BVML_DSINE_ENULL, "conv_pack: w and wp must be non-NULL");
-    if (cout < 1 || cin < 1) return fail(BVML_DSINE_ESHAPE, "conv_pack: bad shape");
-    if (k != 3 && k != 5) return fail(BVML_DSINE_EK, "conv_pack: k must be 3 or 5");
-    if (interleave && cout % 32 != 0)
-        return fail(BVML_DSINE_EPARAM, "conv_pack: interleaved weights need cout % 32 == 0");
-    const int mblocks = mblocks_for(cout), taps = k * k, chunks = (cin + kCC - 1) / kCC;
-    for (int ch = 0; ch < chunks; ++ch)
-        for (int t = 0; t < taps; ++t)
-            for (int mb = 0; mb < mblocks; ++mb)
-                for (int l = 0; l < 64; ++l) {
-                    const int c = ch * kCC + (l >> 4);
-                    int o = 16 * mb + (l & 15);
-                    if (interleave) {
-                        // block 2i: channels 16i.. of the first half (z), 2i + 1:
-                        // channels 16i.. of the second half (r)
-                        const int half = cout / 2;
-                        o = (mb & 1 ? half : 0) + 16 * (mb >> 1) + (l & 15);
-                        if (16 * (mb >> 1) >= half) o = cout;  // padding block
-                    }
-                    const size_t dst = (((size_t)ch * taps + t) * mblocks + mb) * 64 + l;
-                    wp[dst] = (o < cout && c < cin) ? w[((size_t)o * cin + c) * taps + t] : 0.0f;
-                }
-    return BVML_DSINE_OK;
-}
-
 int bvml_dsine_conv_f32(const float* x, int cin, int H, int W, const float* wp, int cout, int k,
                         float* out, void* stream) {
     if (int st = check_common("conv", x, cin, H, W, wp, k)) return st;
@@ -283,7 +249,7 @@ int bvml_dsine_conv_f32(const float* x, int cin, int H, int W, const float* wp, 
         return fail(BVML_DSINE_EALIAS, "conv: out overlaps x");
     ConvArgs a{};
     a.x = x; a.wp = wp; a.out = out; a.cin = cin; a.cout = cout; a.H = H; a.W = W; a.HW = HW;
-    a.mblocks = mblocks_for(cout);
+    a.mblocks = conv_mblocks(cout);
     const hipStream_t s = static_cast<hipStream_t>(stream);
     if (a.mblocks % 8 == 0)
         return k == 5 ? launch<5, 16, 2, 2, kPlain>(a, s, "conv")
@@ -309,7 +275,7 @@ int bvml_dsine_conv_gru_gates_f32(const float* x, int cin, int H, int W, const f
     ConvArgs a{};
     a.x = x; a.wp = wp; a.cin = cin; a.cout = 2 * C; a.H = H; a.W = W; a.HW = HW;
     a.b0 = bias_z; a.b1 = bias_r; a.h = h; a.o0 = z; a.o1 = rh;
-    a.mblocks = mblocks_for(2 * C);
+    a.mblocks = conv_mblocks(2 * C);
     if (a.mblocks % 8 == 0)
         return launch<5, 16, 2, 2, kGates>(a, static_cast<hipStream_t>(stream), "conv_gru_gates");
     return launch<5, 16, 1, 4, kGates>(a, static_cast<hipStream_t>(stream), "conv_gru_gates");
@@ -334,7 +300,7 @@ int bvml_dsine_conv_gru_update_f32(const float* x, int cin, int H, int W, const 
     ConvArgs a{};
     a.x = x; a.wp = wp; a.cin = cin; a.cout = C; a.H = H; a.W = W; a.HW = HW;
     a.b0 = bias_q; a.z = z; a.h = h; a.o0 = h_new; a.o1 = h_copy;
-    a.mblocks = mblocks_for(C);
+    a.mblocks = conv_mblocks(C);
     // 64 channels: one M tile of 4 blocks per wave, all four waves along the rows
     return launch<5, 16, 1, 4, kUpdate>(a, static_cast<hipStream_t>(stream), "conv_gru_update");
 }

@@ -32,6 +32,7 @@
 #include <string>
 
 #include "bvml_dsine.h"
+#include "pack_layout.h"
 #include "status.h"
 
 namespace {
@@ -39,12 +40,12 @@ namespace {
 using bvml::fail;
 using bvml::overlaps;
 
-constexpr int kHid = 64;       // the heads' hidden width
+constexpr int kHid = bvml::pack::kHeadsHidden;  // the heads' hidden width
 constexpr int kMaxHeads = 4;
 constexpr int kWaves = 8;      // waves per workgroup
 constexpr int kPx = 32;        // pixels per wave
 constexpr int kOb = 4;         // last-layer output blocks per pass
-constexpr int kW2Floats = 16 * 4 * 64;  // one head's packed middle layer
+constexpr int kW2Floats = bvml::pack::kHeadsW2Floats;  // one head's packed middle layer
 // Last layers of at most this many output blocks in all are staged in LDS
 // with the middle layers (the prob, xy and angle heads: 2 + 4 + 2 blocks);
 // the others (the up-mask head, 36 blocks) pass through an LDS chunk buffer.
@@ -238,41 +239,6 @@ __global__ __launch_bounds__(kWaves * 64) void heads_mlp_kernel(HeadsArgs a) {
 }  // namespace
 
 extern "C" {
-
-int bvml_dsine_heads_pack_f32(const float* w2, const float* const* w4, const int* outs,
-                              int nheads, float* w2p, float* const* w4p) {
-    if (nheads < 1 || nheads > kMaxHeads)
-        return fail(BVML_DSINE_EPARAM, "heads_pack: nheads must be 1..4");
-    if (!w2 || !w4 || !outs || !w2p || !w4p)
-        return fail(BVML_DSINE_ENULL, "heads_pack: pointers must be non-NULL");
-    for (int h = 0; h < nheads; ++h) {
-        if (outs[h] < 1 || outs[h] > 4096)
-            return fail(BVML_DSINE_EPARAM, "heads_pack: outs must be 1..4096");
-        if (!w4[h] || !w4p[h]) return fail(BVML_DSINE_ENULL, "heads_pack: pointers must be non-NULL");
-    }
-    for (int h = 0; h < nheads; ++h) {
-        for (int j = 0; j < 16; ++j)
-            for (int mb = 0; mb < 4; ++mb)
-                for (int l = 0; l < 64; ++l)
-                    w2p[(((size_t)h * 16 + j) * 4 + mb) * 64 + l] =
-                        w2[((size_t)h * kHid + 16 * mb + (l & 15)) * kHid + 4 * j + (l >> 4)];
-        const int nob = (outs[h] + 15) / 16;
-        for (int ob = 0; ob < nob; ++ob)
-            for (int mb = 0; mb < 4; ++mb)
-                for (int r = 0; r < 4; ++r)
-                    for (int l = 0; l < 64; ++l) {
-                        const int o = 16 * ob + (l & 15), k = 16 * mb + 4 * (l >> 4) + r;
-                        w4p[h][(((size_t)ob * 4 + mb) * 4 + r) * 64 + l] =
-                            o < outs[h] ? w4[h][(size_t)o * kHid + k] : 0.0f;
-                    }
-    }
-    return BVML_DSINE_OK;
-}
-
-long long bvml_dsine_heads_packed_size(int out) {
-    if (out < 1 || out > 4096) return -1;
-    return (long long)((out + 15) / 16) * 4 * 4 * 64;
-}
 
 int bvml_dsine_heads_mlp_f32(const float* t0, const float* b0, const float* w2p, const float* b2,
                              const float* const* w4p, const float* const* b4, const int* outs,

@@ -61,4 +61,24 @@ int bvml_dsine_bias_act_f32(float*, const float*, int, long long, int, void*) {
     no_device("bvml_dsine_bias_act_f32");
 }
 
+int bvml_dsine_heads_mlp_f32(const float*, const float*, const float*, const float*,
+                             const float* const*, const float* const*, const int*, int, int, int,
+                             float* const*, void*) {
+    no_device("bvml_dsine_heads_mlp_f32");
+}
+
+int bvml_dsine_conv_f32(const float*, int, int, int, const float*, int, int, float*, void*) {
+    no_device("bvml_dsine_conv_f32");
+}
+
+int bvml_dsine_conv_gru_gates_f32(const float*, int, int, int, const float*, int, const float*,
+                                  const float*, const float*, float*, float*, void*) {
+    no_device("bvml_dsine_conv_gru_gates_f32");
+}
+
+int bvml_dsine_conv_gru_update_f32(const float*, int, int, int, const float*, int, const float*,
+                                   const float*, const float*, float*, float*, void*) {
+    no_device("bvml_dsine_conv_gru_update_f32");
+}
+
 }  // extern "C"

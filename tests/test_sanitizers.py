@@ -60,7 +60,8 @@ def sanitized_refine_exe(sanitized_exe):
                 os.path.join(ROOT, "tests", "cpp", "no_device.cpp"),
                 os.path.join(CSRC, "dsine_refine.cpp"), os.path.join(CSRC, "refiner.cpp"),
                 os.path.join(CSRC, "refiner_cpu.cpp"), os.path.join(CSRC, "dsine_ops_cpu.cpp"),
-                os.path.join(CSRC, "status.cpp"), os.path.join(CSRC, "tensor.cpp")):
+                os.path.join(CSRC, "pack.cpp"), os.path.join(CSRC, "status.cpp"),
+                os.path.join(CSRC, "tensor.cpp")):
         obj = os.path.join(OUT, os.path.basename(src) + ".o")
         _run(["g++", "-std=c++17", "-ffp-contract=off", "-pthread", *SAN, *HIP_HOST,
               "-I", INCLUDE, "-c", src, "-o", obj])
