@@ -35,6 +35,7 @@ from __future__ import annotations
 
 import argparse
 import json
+import math
 import os
 import platform
 import sys
@@ -45,6 +46,7 @@ import numpy as np
 ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
+FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix peak
 HBM_PEAK_GBPS = 8000.0
 FLUSH_BYTES = 512 << 20
 # Back-to-back work before each timed region, to bring the clocks up (Timer.ramp).
@@ -813,6 +815,62 @@ def bench_upsample(args, dev) -> dict:
 # refiner forward
 # ---------------------------------------------------------------------------
 
+def refiner_kernel_rooflines(dev, H: int, W: int, reps: int):
+    """The refiner's two 5x5 ConvGRU convolutions (the implicit-GEMM kernels
+    of brovisionml_amd/csrc/conv.hip, gates and update epilogues) timed alone
+    on the refiner's map size with HIP events on their stream, against the
+    fp32 matrix peak: algorithmic flops per launch = 2 * cout * cin * 25 *
+    H * W (convz + convr: cout 128; convq: 64; cin 130).  Returns (the
+    convz + convr kernel's roofline, both kernels' figures)."""
+    import torch
+    from brovisionml_amd import _lib
+    lib = _lib.load()
+    C, cin = 64, 130
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(cin, H, W, generator=g).to(dev)
+    h = x[:C]
+    w = (torch.rand(3 * C, cin, 5, 5, generator=g) - 0.5) / math.sqrt(cin * 25)
+    wzr = torch.from_numpy(_lib.conv_pack_f32(w[:2 * C].numpy(), interleave=True)).to(dev)
+    wq = torch.from_numpy(_lib.conv_pack_f32(w[2 * C:].numpy())).to(dev)
+    b = torch.zeros(C, device=dev)
+    z, rh, hn, hc = (torch.empty(C, H, W, device=dev) for _ in range(4))
+    stream = torch.cuda.current_stream(dev)
+    sp = stream.cuda_stream
+    calls = {
+        "conv_gru_gates (convz + convr, 5x5, 130 -> 128)": (
+            2 * 2 * C * cin * 25 * H * W,
+            lambda: lib.bvml_dsine_conv_gru_gates_f32(x.data_ptr(), cin, H, W, wzr.data_ptr(), C,
+                                                       b.data_ptr(), b.data_ptr(), h.data_ptr(),
+                                                       z.data_ptr(), rh.data_ptr(), sp)),
+        "conv_gru_update (convq, 5x5, 130 -> 64)": (
+            2 * C * cin * 25 * H * W,
+            lambda: lib.bvml_dsine_conv_gru_update_f32(x.data_ptr(), cin, H, W, wq.data_ptr(), C,
+                                                        b.data_ptr(), z.data_ptr(), h.data_ptr(),
+                                                        hn.data_ptr(), hc.data_ptr(), sp)),
+    }
+    out = {}
+    for name, (flops, call) in calls.items():
+        for _ in range(3):
+            call()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            call()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        t = e0.elapsed_time(e1) * 1e-3 / reps
+        tf = flops / t / 1e12
+        out[name] = {"us": round(t * 1e6, 1), "tflops": round(tf, 1),
+                     "frac": round(tf / FP32_MFMA_PEAK_TFLOPS, 4), "flops": flops}
+    first = next(iter(out))
+    r = out[first]
+    roof = {"bound": "mfma", "achieved": r["tflops"], "peak": FP32_MFMA_PEAK_TFLOPS,
+            "unit": "TFLOP/s", "frac": r["frac"], "traffic": None, "kernel": first,
+            "flops_per_launch": r["flops"], "launch_us_mean": r["us"]}
+    return roof, out
+
+
 def bench_refiner(args, dev) -> dict:
     """The whole NRN refiner forward at a 256x256 grid (a 2048x2048 image),
     synthetic weights and decoder outputs, one forward per step, `steps`
@@ -874,10 +932,11 @@ def bench_refiner(args, dev) -> dict:
                      t * 1e3 / args.steps,
                      {"workload": f"dsine-refiner-{H}x{W}", "H": H, "W": W, "iterations": 5,
                       "weights": "synthetic (uniform +-1/sqrt(fan_in))",
-                      "driver": driver, "convolutions": "MIOpen immediate mode, fp32"})
+                      "driver": driver, "convolutions": "5x5: implicit-GEMM fp32 MFMA kernels; 3x3: MIOpen immediate mode, fp32"})
     if t_py is not None:
         line["python_driver"] = {"ms_per_step": round(t_py * 1e3 / args.steps, 4),
                                  "value": round(opx / t_py / 1e6, 2)}
+    line["roofline"], line["kernels"] = refiner_kernel_rooflines(dev, H, W, args.steps)
     line["gpu"] = torch.cuda.get_device_name(dev)
     if not args.no_cpu:
         import oracle.refiner as oref

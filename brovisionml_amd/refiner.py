@@ -241,9 +241,11 @@ class Refiner:
 class NativeRefiner:
     """Refiner::forward in C++ (libbvml_dsine_refine.so, the C ABI of
     include/bvml_dsine_refine.h): the same loop as Refiner above, with no
-    Python or torch in it; the convolutions on MIOpen's immediate mode, the
-    rest this package's kernels, the up-mask head and the upsample in the
-    last iteration only.  Weights from a safetensors file (`path`, read by
+    Python or torch in it: the 5x5 ConvGRU convolutions on this package's
+    fp32 matrix-core kernels with the gates and update fused, the heads
+    after their 3x3 layer (MIOpen) in one fused pass, the rest this
+    package's kernels, the up-mask head and the upsample in the last
+    iteration only.  Weights from a safetensors file (`path`, read by
     the library) or a dict as weight_shapes() names them."""
 
     def __init__(self, weights: dict | None = None, path: str | None = None):

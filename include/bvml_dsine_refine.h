@@ -5,11 +5,12 @@
  * It replaces brovisionml's Refiner (the reference's
  * include/brovisionml/dsine_refine.h:113-145, src/dsine_refine.cpp:161-294):
  * the same weights, the same loop and the same result, in C++ over this
- * library's kernels (bvml_dsine.h) -- RayReLU, the propagate on the heads'
- * raw logits, the fused ConvGRU and head elementwise steps, the convex
- * upsample with its mask bias -- with the ConvGRU's and heads'
- * convolutions on MIOpen (fp32, immediate mode).  The C++ class of
- * include/brovisionml/dsine_refine.h sits on top of it.
+ * library's kernels (bvml_dsine.h) -- RayReLU, the ConvGRU's 5x5
+ * convolutions as fp32 matrix-core implicit GEMMs with the gates and the
+ * update fused, the heads after their 3x3 layer in one fused pass, the
+ * propagate on the heads' raw logits, the convex upsample with its mask
+ * bias -- and the heads' 3x3 layer on MIOpen (fp32, immediate mode).  The
+ * C++ class of include/brovisionml/dsine_refine.h sits on top of it.
  *
  * Lifecycle: create (no HIP call) -> weights (load_file, or set_tensor per
  * tensor) -> forward, any number of times, at any grid size -> destroy.
