@@ -63,6 +63,7 @@ REFINE_EXPORTS = (
     "bvml_dsine_refiner_get_tensor",
     "bvml_dsine_refiner_forward",
     "bvml_dsine_refiner_forward_cpu",
+    "bvml_dsine_refiner_forward_noalloc",
     "bvml_dsine_refiner_last_error",
 )
 EWEIGHTS = -9
@@ -171,6 +172,8 @@ def load_refine(path: str = LIB_REFINE) -> ctypes.CDLL:
     lib.bvml_dsine_refiner_forward_cpu.argtypes = [vp, vp, vp, vp, i, i, f, f, f, f, i, i, i, i,
                                                    i, i, vp, vp, i]
     lib.bvml_dsine_refiner_forward_cpu.restype = i
+    lib.bvml_dsine_refiner_forward_noalloc.argtypes = lib.bvml_dsine_refiner_forward.argtypes
+    lib.bvml_dsine_refiner_forward_noalloc.restype = i
     lib.bvml_dsine_refiner_last_error.argtypes = []
     lib.bvml_dsine_refiner_last_error.restype = ctypes.c_char_p
     _refine = lib

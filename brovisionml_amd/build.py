@@ -78,6 +78,8 @@ REFINE_CXX_SOURCES = [os.path.join(CSRC, "dsine_refine.cpp")]  # the Refiner cla
 TENSOR_SOURCES = [os.path.join(CSRC, "tensor.cpp")]
 REFINE_SOURCES = [os.path.join(CSRC, "refiner.cpp"),      # device path, weights, C ABI
                   os.path.join(CSRC, "refiner_cpu.cpp")]  # host path
+# the allocation-free forward and its device scratch array (hipcc)
+REFINE_HIP_SOURCE = os.path.join(CSRC, "refiner_noalloc.hip")
 # host C++ against the HIP runtime and MIOpen headers
 HIP_HOST_FLAGS = ["-D__HIP_PLATFORM_AMD__", "-isystem", os.path.join(ROCM, "include")]
 
@@ -107,8 +109,10 @@ def build_library() -> str:
     _run([HIPCC, *HIP_FLAGS, "-I", INCLUDE, "-shared", "-o", LIB + ".tmp", *host_objs, *SOURCES,
           "-Wl,--version-script=" + os.path.join(CSRC, "libbvml_dsine.map")])
     _install(LIB + ".tmp", LIB)
+    noalloc_obj = os.path.join(objdir, "refiner_noalloc.hip.o")
+    _run([HIPCC, *HIP_FLAGS, "-I", INCLUDE, "-c", REFINE_HIP_SOURCE, "-o", noalloc_obj])
     _run([CXX, *CXX_FLAGS, *HIP_HOST_FLAGS, "-I", INCLUDE, "-shared", "-o", LIB_REFINE + ".tmp",
-          *REFINE_SOURCES, "-L", LIBDIR, "-lbvml_dsine", "-L", os.path.join(ROCM, "lib"),
+          *REFINE_SOURCES, noalloc_obj, "-L", LIBDIR, "-lbvml_dsine", "-L", os.path.join(ROCM, "lib"),
           "-lMIOpen", "-lamdhip64", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath," + os.path.join(ROCM, "lib"),
           "-Wl,--version-script=" + os.path.join(CSRC, "libbvml_dsine_refine.map")])
     _install(LIB_REFINE + ".tmp", LIB_REFINE)

@@ -530,15 +530,14 @@ struct bvml_dsine_refiner {
     // convz + convr and convq, packed for the implicit-GEMM kernels
     const float *w_zr = nullptr, *b_z = nullptr, *b_r = nullptr, *w_q = nullptr, *b_q = nullptr;
     const float *w_h0 = nullptr, *b_h0 = nullptr, *w2p = nullptr, *b_h2 = nullptr;
+    const float* w_h0p[2] = {};  // the 3x3 layer packed for bvml_dsine_conv_f32 (192, 256 filters)
     const float* w4p[kHeads] = {};  // the 1x1 layers packed for bvml_dsine_heads_mlp_f32
     const float* b4[kHeads] = {};
 
     // the maps of one grid size, one allocation
     int H = 0, W = 0;
     float* arena = nullptr;
-    float *hx = nullptr, *rhx = nullptr, *hin = nullptr, *z = nullptr;
-    float *t0 = nullptr, *head[kHeads] = {}, *ray = nullptr;
-    float *pred[2] = {}, *up = nullptr;
+    Maps maps{};  // the maps' places in `arena` (maps_at)
     void* ws = nullptr;
     size_t ws_bytes = 0;
     // [0]: the three heads the propagate reads, [1]: all four
@@ -597,6 +596,16 @@ int bvml_dsine_refiner::upload() {
         return fail(st, std::string("forward: conv_pack: ") + bvml_dsine_last_error());
     if (const int st = bvml_dsine_conv_pack_f32(host[kQw].data(), kHidden, kHx, 5, 0, wq_p.data()))
         return fail(st, std::string("forward: conv_pack: ") + bvml_dsine_last_error());
+    std::vector<float> wh0;
+    for (int h = 0; h < kHeads; ++h)
+        wh0.insert(wh0.end(), host[head_w(h, 0)].begin(), host[head_w(h, 0)].end());
+    std::vector<float> wh0_p[2];
+    for (int i = 0; i < 2; ++i) {
+        const int co = (3 + i) * kMid;
+        wh0_p[i].resize((size_t)bvml_dsine_conv_packed_size(co, kHin, 3));
+        if (const int st = bvml_dsine_conv_pack_f32(wh0.data(), co, kHin, 3, 0, wh0_p[i].data()))
+            return fail(st, std::string("forward: conv_pack: ") + bvml_dsine_last_error());
+    }
     using Src = std::vector<const std::vector<float>*>;
     std::vector<std::pair<const float**, Src>> parts;
     parts.push_back({&w_zr, {&wzr_p}});
@@ -611,6 +620,8 @@ int bvml_dsine_refiner::upload() {
         h2b.push_back(&host[head_b(h, 1)]);
     }
     parts.push_back({&w_h0, h0w});
+    parts.push_back({&w_h0p[0], {&wh0_p[0]}});
+    parts.push_back({&w_h0p[1], {&wh0_p[1]}});
     parts.push_back({&b_h0, h0b});
     parts.push_back({&w2p, {&w2p_h}});
     parts.push_back({&b_h2, h2b});
@@ -692,22 +703,12 @@ int bvml_dsine_refiner::plan(int h, int w) {
     if (arena && H == h && W == w) return BVML_DSINE_OK;
     drop_grid();
     const size_t hw = (size_t)h * w;
-    const int planes[] = {kHx, kHx, kHin, kHidden, kHeads * kMid, kHeadOut[0], kHeadOut[1],
-                          kHeadOut[2], kHeadOut[3], 3, 3, 3, 3 * kUp * kUp};
-    float** dst[] = {&hx, &rhx, &hin, &z, &t0, &head[0], &head[1], &head[2], &head[3],
-                     &pred[0], &pred[1], &ray, &up};
-    size_t total = 0;
-    std::vector<size_t> offset;
-    for (int c : planes) {
-        offset.push_back(total);
-        total += round64((size_t)c * hw);
-    }
-    hipError_t e = hipMalloc(&arena, total * sizeof(float));
+    hipError_t e = hipMalloc(&arena, maps_floats(hw) * sizeof(float));
     if (e != hipSuccess) {
         arena = nullptr;
         return hip_fail(e, "hipMalloc of the maps");
     }
-    for (size_t i = 0; i < offset.size(); ++i) *dst[i] = arena + offset[i];
+    maps = maps_at(arena, hw);
     int st;
     for (int i = 0; i < 2; ++i)
         if ((st = make_plan(h0_p[i], kHin, (3 + i) * kMid, 3, 1, h, w))) return drop_grid(), st;
@@ -736,6 +737,110 @@ int bvml_dsine_refiner::conv(const ConvPlan& p, const float* w, const float* x, 
 
 const std::vector<std::vector<float>>& bvml_refine::host_weights(const bvml_dsine_refiner* r) {
     return r->host;
+}
+
+// The loop of Refiner::forward on the maps `m`, after forward's checks, with
+// the refiner's device current and its weights on it: the 3x3 heads layer on
+// MIOpen (its plans made for this grid size) or, with own_h0, on this
+// library's convolution kernel.
+int bvml_refine::forward_maps(bvml_dsine_refiner* r, const Maps& m, const ForwardArgs& a,
+                              void* stream, bool own_h0) {
+    const int h8 = a.h8, w8 = a.w8, pad_t = a.pad_t, pad_l = a.pad_l;
+    const int out_h = a.out_h, out_w = a.out_w;
+    float* out = a.out;
+    float* coarse = a.coarse;
+    const size_t hw = (size_t)h8 * w8, b = sizeof(float);
+    const long long fh = (long long)kUp * h8, fw = (long long)kUp * w8;
+    const hipStream_t strm = static_cast<hipStream_t>(stream);
+    int st;
+    // the grid-scaled intrinsics (src/dsine_refine.cpp:232-237)
+    const double sw = (double)w8 / a.orig_w, sh = (double)h8 / a.orig_h;
+    const double fu = a.fx * sw, cu = (a.cx + 0.5) * sw, fv = a.fy * sh, cv = (a.cy + 0.5) * sh;
+    const int C = kHidden;
+    auto copy = [&](float* dst, const float* src, size_t planes) {
+        return hipMemcpyAsync(dst, src, planes * hw * b, hipMemcpyDeviceToDevice, strm);
+    };
+    // a kernel library status, with its message
+    auto ck = [](int status, const char* what) {
+        return status == BVML_DSINE_OK
+                   ? BVML_DSINE_OK
+                   : fail(status, std::string("forward: ") + what + ": " + bvml_dsine_last_error());
+    };
+    hipError_t e;
+    // hx = [h | feature | uv], rhx = [r*h | feature | uv], hin = [h_new | uv]
+    float* uv = m.hx + (size_t)(kHidden + kFeature) * hw;
+    if ((st = ck(bvml_dsine_build_uv8_f32(uv, fu, cu, fv, cv, h8, w8, stream), "build_uv8")) ||
+        (st = ck(bvml_dsine_build_ray8_f32(m.ray, fu, cu, fv, cv, h8, w8, stream), "build_ray8")))
+        return st;
+    if ((e = copy(m.hx, a.hidden, kHidden)) != hipSuccess ||
+        (e = copy(m.hx + (size_t)kHidden * hw, a.feature, kFeature)) != hipSuccess ||
+        (e = copy(m.rhx + (size_t)kHidden * hw, m.hx + (size_t)kHidden * hw, kX)) != hipSuccess ||
+        (e = copy(m.hin + (size_t)kHidden * hw, uv, 2)) != hipSuccess ||
+        (e = copy(m.pred[0], a.normal, 3)) != hipSuccess)
+        return hip_fail(e, "hipMemcpyAsync");
+    // pred_norm = RayReLU(decoder.normal, ray_8)  (:240-242)
+    if ((st = ck(bvml_dsine_ray_relu_f32(m.pred[0], m.ray, 1, h8, w8, 0, stream), "ray_relu")))
+        return st;
+
+    const bool direct = pad_t == 0 && pad_l == 0 && out_h == fh && out_w == fw;
+    int cur = 0;
+    for (int it = 0; it < kIter; ++it) {
+        const bool last = it == kIter - 1;
+        const int nh = last ? kHeads : kHeads - 1;
+        // ConvGRU (:138-159): the two 5x5 convolutions with the gates and
+        // the update in their epilogues; h_new overwrites h in hx and is
+        // copied into hin
+        if ((st = ck(bvml_dsine_conv_gru_gates_f32(m.hx, kHx, h8, w8, r->w_zr, C, r->b_z, r->b_r,
+                                                   m.hx, m.z, m.rhx, stream),
+                     "conv_gru_gates")) ||
+            (st = ck(bvml_dsine_conv_gru_update_f32(m.rhx, kHx, h8, w8, r->w_q, C, r->b_q, m.z,
+                                                    m.hx, m.hx, m.hin, stream),
+                     "conv_gru_update")))
+            return st;
+        // the heads (:119-127, :257-267, :276): the 3x3 layers, then the rest
+        // in one pass; the up-mask head's last bias is the upsample's
+        const float* b4[kHeads] = {r->b4[0], r->b4[1], r->b4[2], nullptr};
+        const int st0 = own_h0 ? ck(bvml_dsine_conv_f32(m.hin, kHin, h8, w8, r->w_h0p[last ? 1 : 0],
+                                                        nh * kMid, 3, m.t0, stream), "conv")
+                               : r->conv(r->h0_p[last ? 1 : 0], r->w_h0, m.hin, m.t0);
+        if ((st = st0) ||
+            (st = ck(bvml_dsine_heads_mlp_f32(m.t0, r->b_h0, r->w2p, r->b_h2, r->w4p, b4, kHeadOut,
+                                              nh, h8, w8, m.head, stream), "heads_mlp")))
+            return st;
+        // the propagate on the logits (:262-274)
+        if ((st = ck(bvml_dsine_angmf_propagate_f32(m.pred[cur], m.head[0], m.head[1],
+                                                    m.head[2], m.ray, fu, cu, fv, cv, 1, h8, w8,
+                                                    kPs, 0, m.pred[cur ^ 1], BVML_DSINE_LOGITS,
+                                                    stream), "angmf_propagate")))
+            return st;
+        cur ^= 1;
+        if (coarse && (e = copy(coarse + (size_t)it * 3 * hw, m.pred[cur], 3)) != hipSuccess)
+            return hip_fail(e, "hipMemcpyAsync");
+        if (!last) continue;
+        // up_pred_norm = normalize(convex_upsample(pred_norm, up_mask))  (:276-283)
+        float* dst = direct ? out : m.up;
+        if ((st = ck(bvml_dsine_convex_upsample_bias_f32(m.pred[cur], m.head[3], r->b4[3], 1, 3,
+                                                         h8, w8, kUp, 1, kUpEps, dst, 0, stream),
+                     "convex_upsample")))
+            return st;
+    }
+    if (!direct) {
+        // the crop to the unpadded image (:289-293)
+        for (int c = 0; c < 3; ++c) {
+            const float* src = m.up + (size_t)c * fh * fw + (size_t)pad_t * fw + pad_l;
+            e = hipMemcpy2DAsync(out + (size_t)c * out_h * out_w, (size_t)out_w * b, src,
+                                 (size_t)fw * b, (size_t)out_w * b, (size_t)out_h,
+                                 hipMemcpyDeviceToDevice, strm);
+            if (e != hipSuccess) return hip_fail(e, "hipMemcpy2DAsync");
+        }
+    }
+    return BVML_DSINE_OK;
+}
+
+int bvml_refine::refiner_device(const bvml_dsine_refiner* r) { return r->device; }
+
+bool bvml_refine::refiner_uploaded(const bvml_dsine_refiner* r) {
+    return r->warena != nullptr && !r->dirty;
 }
 
 // ---------------------------------------------------------------------------
@@ -811,9 +916,6 @@ int bvml_dsine_refiner_forward(bvml_dsine_refiner* r, const float* normal, const
     const ForwardArgs args{normal, feature, hidden, h8, w8, fx, fy, cx, cy, orig_h, orig_w,
                            pad_t, pad_l, out_h, out_w, out, coarse};
     if (const int st = check_forward(r->host, args, "forward: ")) return st;
-    const size_t hw = (size_t)h8 * w8, b = sizeof(float);
-    const long long fh = (long long)kUp * h8, fw = (long long)kUp * w8;
-
     if (r->device < 0) {
         int d = 0;
         const hipError_t e = hipGetDevice(&d);
@@ -830,88 +932,9 @@ int bvml_dsine_refiner_forward(bvml_dsine_refiner* r, const float* normal, const
     int st;
     if (r->dirty && (st = r->upload()) != BVML_DSINE_OK) return st;
     if ((st = r->plan(h8, w8)) != BVML_DSINE_OK) return st;
-    const hipStream_t strm = static_cast<hipStream_t>(stream);
-    if ((ms = miopenSetStream(r->mio, strm)) != miopenStatusSuccess) return mio_fail(ms, "stream");
-
-    // the grid-scaled intrinsics (src/dsine_refine.cpp:232-237)
-    const double sw = (double)w8 / orig_w, sh = (double)h8 / orig_h;
-    const double fu = fx * sw, cu = (cx + 0.5) * sw, fv = fy * sh, cv = (cy + 0.5) * sh;
-    const int C = kHidden;
-    auto copy = [&](float* dst, const float* src, size_t planes) {
-        return hipMemcpyAsync(dst, src, planes * hw * b, hipMemcpyDeviceToDevice, strm);
-    };
-    // a kernel library status, with its message
-    auto ck = [](int status, const char* what) {
-        return status == BVML_DSINE_OK
-                   ? BVML_DSINE_OK
-                   : fail(status, std::string("forward: ") + what + ": " + bvml_dsine_last_error());
-    };
-    hipError_t e;
-    // hx = [h | feature | uv], rhx = [r*h | feature | uv], hin = [h_new | uv]
-    float* uv = r->hx + (size_t)(kHidden + kFeature) * hw;
-    if ((st = ck(bvml_dsine_build_uv8_f32(uv, fu, cu, fv, cv, h8, w8, stream), "build_uv8")) ||
-        (st = ck(bvml_dsine_build_ray8_f32(r->ray, fu, cu, fv, cv, h8, w8, stream), "build_ray8")))
-        return st;
-    if ((e = copy(r->hx, hidden, kHidden)) != hipSuccess ||
-        (e = copy(r->hx + (size_t)kHidden * hw, feature, kFeature)) != hipSuccess ||
-        (e = copy(r->rhx + (size_t)kHidden * hw, r->hx + (size_t)kHidden * hw, kX)) != hipSuccess ||
-        (e = copy(r->hin + (size_t)kHidden * hw, uv, 2)) != hipSuccess ||
-        (e = copy(r->pred[0], normal, 3)) != hipSuccess)
-        return hip_fail(e, "hipMemcpyAsync");
-    // pred_norm = RayReLU(decoder.normal, ray_8)  (:240-242)
-    if ((st = ck(bvml_dsine_ray_relu_f32(r->pred[0], r->ray, 1, h8, w8, 0, stream), "ray_relu")))
-        return st;
-
-    const bool direct = pad_t == 0 && pad_l == 0 && out_h == fh && out_w == fw;
-    int cur = 0;
-    for (int it = 0; it < kIter; ++it) {
-        const bool last = it == kIter - 1;
-        const int nh = last ? kHeads : kHeads - 1;
-        // ConvGRU (:138-159): the two 5x5 convolutions with the gates and
-        // the update in their epilogues; h_new overwrites h in hx and is
-        // copied into hin
-        if ((st = ck(bvml_dsine_conv_gru_gates_f32(r->hx, kHx, h8, w8, r->w_zr, C, r->b_z, r->b_r,
-                                                   r->hx, r->z, r->rhx, stream),
-                     "conv_gru_gates")) ||
-            (st = ck(bvml_dsine_conv_gru_update_f32(r->rhx, kHx, h8, w8, r->w_q, C, r->b_q, r->z,
-                                                    r->hx, r->hx, r->hin, stream),
-                     "conv_gru_update")))
-            return st;
-        // the heads (:119-127, :257-267, :276): the 3x3 layers, then the rest
-        // in one pass; the up-mask head's last bias is the upsample's
-        const float* b4[kHeads] = {r->b4[0], r->b4[1], r->b4[2], nullptr};
-        if ((st = r->conv(r->h0_p[last ? 1 : 0], r->w_h0, r->hin, r->t0)) ||
-            (st = ck(bvml_dsine_heads_mlp_f32(r->t0, r->b_h0, r->w2p, r->b_h2, r->w4p, b4, kHeadOut,
-                                              nh, h8, w8, r->head, stream), "heads_mlp")))
-            return st;
-        // the propagate on the logits (:262-274)
-        if ((st = ck(bvml_dsine_angmf_propagate_f32(r->pred[cur], r->head[0], r->head[1],
-                                                    r->head[2], r->ray, fu, cu, fv, cv, 1, h8, w8,
-                                                    kPs, 0, r->pred[cur ^ 1], BVML_DSINE_LOGITS,
-                                                    stream), "angmf_propagate")))
-            return st;
-        cur ^= 1;
-        if (coarse && (e = copy(coarse + (size_t)it * 3 * hw, r->pred[cur], 3)) != hipSuccess)
-            return hip_fail(e, "hipMemcpyAsync");
-        if (!last) continue;
-        // up_pred_norm = normalize(convex_upsample(pred_norm, up_mask))  (:276-283)
-        float* dst = direct ? out : r->up;
-        if ((st = ck(bvml_dsine_convex_upsample_bias_f32(r->pred[cur], r->head[3], r->b4[3], 1, 3,
-                                                         h8, w8, kUp, 1, kUpEps, dst, 0, stream),
-                     "convex_upsample")))
-            return st;
-    }
-    if (!direct) {
-        // the crop to the unpadded image (:289-293)
-        for (int c = 0; c < 3; ++c) {
-            const float* src = r->up + (size_t)c * fh * fw + (size_t)pad_t * fw + pad_l;
-            e = hipMemcpy2DAsync(out + (size_t)c * out_h * out_w, (size_t)out_w * b, src,
-                                 (size_t)fw * b, (size_t)out_w * b, (size_t)out_h,
-                                 hipMemcpyDeviceToDevice, strm);
-            if (e != hipSuccess) return hip_fail(e, "hipMemcpy2DAsync");
-        }
-    }
-    return BVML_DSINE_OK;
+    if ((ms = miopenSetStream(r->mio, static_cast<hipStream_t>(stream))) != miopenStatusSuccess)
+        return mio_fail(ms, "stream");
+    return bvml_refine::forward_maps(r, r->maps, args, stream, false);
 }
 
 }  // extern "C"

@@ -68,4 +68,41 @@ int check_forward(const std::vector<std::vector<float>>& host, const ForwardArgs
 // The host copy of the refiner's weights, one vector per spec.
 const std::vector<std::vector<float>>& host_weights(const bvml_dsine_refiner* r);
 
+// The device maps of one forward: [h | feature | uv], [r*h | feature | uv],
+// [h_new | uv], the update gate, the heads' 3x3 output, the heads' outputs,
+// the two propagate buffers, the ray map, the full-resolution result before
+// the crop.
+struct Maps {
+    float *hx, *rhx, *hin, *z, *t0, *head[kHeads], *pred[2], *ray, *up;
+};
+
+// The planes of each map in Maps order (up: 3 * kUp^2 planes); each map
+// starts on a 64-float boundary.
+constexpr int kMapPlanes[] = {kHx, kHx, kHin, kHidden, kHeads * kMid, kHeadOut[0], kHeadOut[1],
+                              kHeadOut[2], kHeadOut[3], 3, 3, 3, 3 * kUp * kUp};
+inline size_t maps_floats(size_t hw) {
+    size_t total = 0;
+    for (int c : kMapPlanes) total += ((size_t)c * hw + 63) & ~(size_t)63;
+    return total;
+}
+inline Maps maps_at(float* base, size_t hw) {
+    Maps m{};
+    float** order[] = {&m.hx, &m.rhx, &m.hin, &m.z, &m.t0, &m.head[0], &m.head[1], &m.head[2],
+                       &m.head[3], &m.pred[0], &m.pred[1], &m.ray, &m.up};
+    size_t at = 0;
+    for (int i = 0; i < 13; ++i) {
+        *order[i] = base + at;
+        at += ((size_t)kMapPlanes[i] * hw + 63) & ~(size_t)63;
+    }
+    return m;
+}
+
+// The loop of the device forward on the maps m (refiner.cpp), after the
+// checks, with the refiner's device current and its weights uploaded;
+// own_h0: the heads' 3x3 layer on bvml_dsine_conv_f32 instead of MIOpen.
+int forward_maps(bvml_dsine_refiner* r, const Maps& m, const ForwardArgs& a, void* stream,
+                 bool own_h0);
+int refiner_device(const bvml_dsine_refiner* r);    // -1 before the first forward
+bool refiner_uploaded(const bvml_dsine_refiner* r);  // weights on the device and current
+
 }  // namespace bvml_refine

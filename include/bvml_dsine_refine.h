@@ -112,6 +112,28 @@ int bvml_dsine_refiner_forward_cpu(bvml_dsine_refiner* r, const float* normal,
                                    int orig_w, int pad_t, int pad_l, int out_h, int out_w,
                                    float* out, float* coarse, int nthreads);
 
+/*
+ * bvml_dsine_refiner_forward on maps in a fixed device array of this library
+ * instead of allocated ones: the variant for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.  It
+ * calls no hipMalloc, hipFree or MIOpen routine: the heads' 3x3 layer runs
+ * on bvml_dsine_conv_f32 (the same fp32 convolution within rounding), and
+ * the weights must already be on the device: a bvml_dsine_refiner_forward
+ * after the last load_file / set_tensor uploads them (else
+ * BVML_DSINE_EWEIGHTS).  The array holds 8,388,608 floats (32 MiB) per GPU,
+ * the maps of a grid of up to about 5,500 pixels (1,523 planes; a 60 x 80
+ * grid needs 7,310,400 floats); a larger grid returns BVML_DSINE_ESIZE.  Every call on one GPU
+ * uses that GPU's array, which keeps the last call's contents (nothing in
+ * it needs to start at zero): calls that overlap on one GPU race.
+ * Arguments, checks and results otherwise as bvml_dsine_refiner_forward.
+ */
+int bvml_dsine_refiner_forward_noalloc(bvml_dsine_refiner* r, const float* normal,
+                                       const float* feature, const float* hidden, int h8,
+                                       int w8, float fx, float fy, float cx, float cy,
+                                       int orig_h, int orig_w, int pad_t, int pad_l, int out_h,
+                                       int out_w, float* out, float* coarse, void* stream);
+
 /* Message for the calling thread's last non-zero refiner status ("" if none). */
 const char* bvml_dsine_refiner_last_error(void);
 
