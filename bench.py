@@ -319,6 +319,7 @@ def roofline(bytes_per_call, launch_s, traffic, kernel, copy_gbps, read_gbps=Non
     }
     if read_gbps is not None:
         r["read_ceiling_gbps"] = round(read_gbps, 1)
+        r["frac_of_read_ceiling"] = round(achieved / read_gbps, 4)
     return r
 
 
