@@ -67,8 +67,13 @@ __device__ __forceinline__ float gru_mix(float z, float h, float q) {
 
 // K: kernel size; TH: tile rows; WM x WN waves (WM along the channels, WN
 // along the tile rows); each wave 4 M-blocks (64 output channels) x NB tile rows.
-template <int K, int TH, int WM, int WN, int EPI>
-__global__ __launch_bounds__(kThreads) void conv_kernel(ConvArgs a) {
+// KS: groups of those 4 waves that split the input channels (group g takes
+// chunks g, g + KS, ...; the other groups' sums meet group 0's in LDS before
+// its epilogue).  A grid with one workgroup per CU leaves each SIMD one wave
+// of 4-wave workgroups; with KS = 2 it has two, and one wave's MFMAs run
+// while the other waits for its operands.
+template <int K, int TH, int WM, int WN, int EPI, int KS>
+__global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
     constexpr int P = K / 2;
     constexpr int HR = TH + K - 1, HC = kTW + K - 1, HS = HR * HC;  // halo rows, cols, size
     constexpr int HALO = kCC * HS;                                   // floats per chunk
@@ -76,14 +81,20 @@ __global__ __launch_bounds__(kThreads) void conv_kernel(ConvArgs a) {
     constexpr int NB = TH / WN;                                      // tile rows per wave
     constexpr int TAPS = K * K;
     static_assert(WM * WN == kThreads / 64, "4 waves");
-    __shared__ float halo[2][HALO];
+    static_assert(KS == 1 || NB % 2 == 0, "the split's sums meet two N-blocks at a time");
+    __shared__ float halo[KS][2][HALO];
 
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int ks = (KS > 1) ? (int)threadIdx.x / kThreads : 0;  // the wave group's split
+    const int tid = (int)threadIdx.x - ks * kThreads, lane = tid & 63, wave = tid >> 6;
     const int g = lane >> 4, col = lane & 15;
     const int wm = wave % WM, wn = wave / WM;
     const int tx0 = (blockIdx.x % a.tiles_x) * kTW, ty0 = (blockIdx.x / a.tiles_x) * TH;
     const int mb0 = blockIdx.y * (4 * WM) + 4 * wm;  // the wave's first M-block
     const int nchunks = (a.cin + kCC - 1) / kCC;
+    // every group makes the same number of trips (the barriers are the
+    // workgroup's); a trip past the last chunk stages zeros and multiplies
+    // nothing
+    const int trips = (nchunks + KS - 1) / KS;
 
     // halo element e of a chunk: (channel, halo row, halo col), its source
     auto halo_load = [&](int chunk, float (&v)[PER_T]) {
@@ -104,7 +115,7 @@ __global__ __launch_bounds__(kThreads) void conv_kernel(ConvArgs a) {
 #pragma unroll
         for (int i = 0; i < PER_T; ++i) {
             const int e = tid + i * kThreads;
-            if (e < HALO) halo[buf][e] = v[i];
+            if (e < HALO) halo[ks][buf][e] = v[i];
         }
     };
 
@@ -115,16 +126,18 @@ __global__ __launch_bounds__(kThreads) void conv_kernel(ConvArgs a) {
         for (int n = 0; n < NB; ++n) acc[m][n] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
 
     float pre[PER_T];
-    halo_load(0, pre);
+    halo_load(ks, pre);
     halo_store(0, pre);
     __syncthreads();
     const float* wbase = a.wp + (size_t)mb0 * 64 + lane;
     const size_t tap_stride = (size_t)a.mblocks * 64;
-    for (int chunk = 0; chunk < nchunks; ++chunk) {
-        const int buf = chunk & 1;
-        const bool more = chunk + 1 < nchunks;
-        if (more) halo_load(chunk + 1, pre);
-        const float* hb = halo[buf] + g * HS + (wn * NB) * HC + col;
+    for (int trip = 0; trip < trips; ++trip) {
+        const int chunk = trip * KS + ks;
+        const int buf = trip & 1;
+        const bool more = trip + 1 < trips;
+        if (more) halo_load(chunk + KS, pre);
+        if (chunk < nchunks) {
+        const float* hb = halo[ks][buf] + g * HS + (wn * NB) * HC + col;
         const float* wc = wbase + (size_t)chunk * TAPS * tap_stride;
         // the A operands one tap ahead, the B operands (LDS) one tap ahead
         float af[3][4];
@@ -154,8 +167,33 @@ __global__ __launch_bounds__(kThreads) void conv_kernel(ConvArgs a) {
                     acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[t % 3][m], bf[t & 1][n],
                                                                     acc[m][n], 0, 0, 0);
         }
+        }
         if (more) halo_store(buf ^ 1, pre);
         __syncthreads();
+    }
+    if constexpr (KS > 1) {
+        // the other groups' sums into group 0's, two N-blocks at a time
+        __shared__ v4f xch[KS - 1][4][2][kThreads];
+#pragma unroll
+        for (int n0 = 0; n0 < NB; n0 += 2) {
+            if (ks > 0) {
+#pragma unroll
+                for (int m = 0; m < 4; ++m)
+#pragma unroll
+                    for (int j = 0; j < 2; ++j) xch[ks - 1][m][j][tid] = acc[m][n0 + j];
+            }
+            __syncthreads();
+            if (ks == 0) {
+#pragma unroll
+                for (int q = 0; q < KS - 1; ++q)
+#pragma unroll
+                    for (int m = 0; m < 4; ++m)
+#pragma unroll
+                        for (int j = 0; j < 2; ++j) acc[m][n0 + j] += xch[q][m][j][tid];
+            }
+            __syncthreads();
+        }
+        if (ks > 0) return;
     }
 
     // epilogue: lane (g, col), register r of acc[m][n] is output channel
@@ -207,6 +245,10 @@ __global__ __launch_bounds__(kThreads) void conv_kernel(ConvArgs a) {
     }
 }
 
+// Workgroups below which a launch splits the input channels over two wave
+// groups (fewer than two 4-wave workgroups per CU).
+constexpr long long kSplitGrid = 512;
+
 template <int K, int TH, int WM, int WN, int EPI>
 int launch(const ConvArgs& a0, hipStream_t stream, const char* op) {
     ConvArgs a = a0;
@@ -215,8 +257,19 @@ int launch(const ConvArgs& a0, hipStream_t stream, const char* op) {
     const int mtiles = a.mblocks / (4 * WM);
     const long long tiles = (long long)a.tiles_x * tiles_y;
     if (tiles > INT_MAX) return fail(BVML_DSINE_ESIZE, std::string(op) + ": too many tiles");
-    hipLaunchKernelGGL((conv_kernel<K, TH, WM, WN, EPI>), dim3((unsigned)tiles, (unsigned)mtiles),
-                       dim3(kThreads), 0, stream, a);
+    const dim3 grid((unsigned)tiles, (unsigned)mtiles);
+    // (waves of 8 tile rows hold 128 accumulators: two of them per SIMD
+    // would spill, so those tiles never split)
+    bool split = false;
+    if constexpr (TH / WN <= 4) split = tiles * mtiles < kSplitGrid;
+    if constexpr (TH / WN <= 4) {
+        if (split)
+            hipLaunchKernelGGL((conv_kernel<K, TH, WM, WN, EPI, 2>), grid, dim3(2 * kThreads), 0,
+                               stream, a);
+    }
+    if (!split)
+        hipLaunchKernelGGL((conv_kernel<K, TH, WM, WN, EPI, 1>), grid, dim3(kThreads), 0, stream,
+                           a);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess)
         return fail((int)e, std::string(op) + " launch: " + hipGetErrorString(e));
