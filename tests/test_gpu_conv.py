@@ -47,6 +47,8 @@ def _dev(a, dev):
 @pytest.mark.parametrize("cin,cout,k,H,W", [
     (130, 64, 5, 24, 32), (66, 256, 3, 20, 36), (66, 192, 3, 13, 19), (7, 20, 5, 9, 5),
     (130, 128, 5, 1, 1), (66, 192, 3, 64, 80),
+    # one chunk of input channels: the second wave group of a split launch has none
+    (3, 20, 5, 9, 5), (4, 64, 5, 17, 33),
 ])
 def test_conv_plain(cuda, cin, cout, k, H, W):
     import torch
