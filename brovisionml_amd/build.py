@@ -10,7 +10,7 @@
                           subset below
   libbvml_dsine_refine.so the native NRN refiner (refiner.cpp,
                           refiner_cpu.cpp, include/bvml_dsine_refine.h): C++
-                          over the C ABI and MIOpen; extern "C" symbols only
+                          over the C ABI; extern "C" symbols only
   libbvml_dsine_refine_cxx.so  the C++ drop-in brovisionml::dsine::Refiner
                           (dsine_refine.cpp, include/brovisionml/dsine_refine.h)
                           over the refiner's C ABI; brotensor::Tensor left
@@ -80,7 +80,7 @@ REFINE_SOURCES = [os.path.join(CSRC, "refiner.cpp"),      # device path, weights
                   os.path.join(CSRC, "refiner_cpu.cpp")]  # host path
 # the allocation-free forward and its device scratch array (hipcc)
 REFINE_HIP_SOURCE = os.path.join(CSRC, "refiner_noalloc.hip")
-# host C++ against the HIP runtime and MIOpen headers
+# host C++ against the HIP runtime headers
 HIP_HOST_FLAGS = ["-D__HIP_PLATFORM_AMD__", "-isystem", os.path.join(ROCM, "include")]
 
 
@@ -113,7 +113,7 @@ def build_library() -> str:
     _run([HIPCC, *HIP_FLAGS, "-I", INCLUDE, "-c", REFINE_HIP_SOURCE, "-o", noalloc_obj])
     _run([CXX, *CXX_FLAGS, *HIP_HOST_FLAGS, "-I", INCLUDE, "-shared", "-o", LIB_REFINE + ".tmp",
           *REFINE_SOURCES, noalloc_obj, "-L", LIBDIR, "-lbvml_dsine", "-L", os.path.join(ROCM, "lib"),
-          "-lMIOpen", "-lamdhip64", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath," + os.path.join(ROCM, "lib"),
+          "-lamdhip64", "-Wl,-rpath,$ORIGIN", "-Wl,-rpath," + os.path.join(ROCM, "lib"),
           "-Wl,--version-script=" + os.path.join(CSRC, "libbvml_dsine_refine.map")])
     _install(LIB_REFINE + ".tmp", LIB_REFINE)
     _run([CXX, *CXX_FLAGS, "-I", INCLUDE, "-shared", "-o", LIB_REFINE_CXX + ".tmp",
@@ -130,14 +130,22 @@ def build_library() -> str:
     return LIB
 
 
+# The language standards the drop-in C++ is checked against: brovisionml
+# builds as C++20 (its CMakeLists.txt sets CMAKE_CXX_STANDARD 20); the
+# library's own build uses C++17, so the sources take both.
+CXX_STANDARDS = ("c++17", "c++20")
+
+
 def check_brotensor_api() -> None:
     """Compiles the C++ layer and the launchers header against a header that
     declares only what brovisionml's sources use of brotensor::Tensor
-    (tests/cpp/brotensor_api/brotensor/tensor.h)."""
+    (tests/cpp/brotensor_api/brotensor/tensor.h), warnings as errors, under
+    each of CXX_STANDARDS."""
     api = os.path.join(ROOT, "tests", "cpp", "brotensor_api")
-    for src in (*CXX_SOURCES, *REFINE_CXX_SOURCES, os.path.join(api, "launchers_check.cpp")):
-        _run([CXX, "-std=c++17", "-fsyntax-only", "-Wall", "-Wextra", "-I", api, "-I", INCLUDE,
-              src])
+    for std in CXX_STANDARDS:
+        for src in (*CXX_SOURCES, *REFINE_CXX_SOURCES, os.path.join(api, "launchers_check.cpp")):
+            _run([CXX, "-std=" + std, "-fsyntax-only", "-Wall", "-Wextra", "-Werror", "-I", api,
+                  "-I", INCLUDE, src])
 
 
 if __name__ == "__main__":

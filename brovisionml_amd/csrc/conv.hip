@@ -345,10 +345,13 @@ int bvml_dsine_conv_gru_update_f32(const float* x, int cin, int H, int W, const 
     const long long HW = (long long)H * W;
     if (HW == 0) return BVML_DSINE_OK;
     const size_t xb = (size_t)cin * HW * 4, cb = (size_t)C * HW * 4;
+    // h_new may be h itself (each element is read, then written, by the same
+    // lane), but not a partial overlap of it: another lane's write would race
+    // this lane's read
     if (overlaps(h_new, cb, x, xb) || (h_copy && overlaps(h_copy, cb, x, xb)) ||
-        overlaps(h_new, cb, z, cb) || (h_copy && (overlaps(h_copy, cb, z, cb) ||
-                                                 overlaps(h_copy, cb, h, cb) ||
-                                                 overlaps(h_copy, cb, h_new, cb))))
+        overlaps(h_new, cb, z, cb) || (h_new != h && overlaps(h_new, cb, h, cb)) ||
+        (h_copy && (overlaps(h_copy, cb, z, cb) || overlaps(h_copy, cb, h, cb) ||
+                    overlaps(h_copy, cb, h_new, cb))))
         return fail(BVML_DSINE_EALIAS, "conv_gru_update: outputs overlap an input");
     ConvArgs a{};
     a.x = x; a.wp = wp; a.cin = cin; a.cout = C; a.H = H; a.W = W; a.HW = HW;

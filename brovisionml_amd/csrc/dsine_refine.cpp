@@ -12,6 +12,7 @@
 #include "brovisionml/dsine_refine.h"
 
 #include <cstddef>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 
@@ -44,10 +45,15 @@ void need_map(const Tensor& t, Device dev, std::size_t n, const char* name) {
 
 }  // namespace
 
+// The engine's device buffers, uploaded weights and grid-size state are
+// shared by every forward of the object, so each call holds `mu` while it
+// uses the engine: forward is const (the reference's signature) and may be
+// called from several threads.
 struct Refiner::Impl {
     bvml_dsine_refiner* engine = nullptr;
     bool loaded = false;
     Device device = Device::CPU;
+    mutable std::mutex mu;
 
     Impl() {
         if (const int st = bvml_dsine_refiner_create(&engine)) fail_status(st);
@@ -65,22 +71,28 @@ Refiner& Refiner::operator=(Refiner&&) noexcept = default;
 void Refiner::load(const std::string& dir) { load_file(dir + "/model.safetensors"); }
 
 void Refiner::load_file(const std::string& path) {
+    std::lock_guard<std::mutex> lock(impl_->mu);
     if (const int st = bvml_dsine_refiner_load_file(impl_->engine, path.c_str())) fail_status(st);
     impl_->loaded = true;
 }
 
 void Refiner::to(Device dev) {
+    std::lock_guard<std::mutex> lock(impl_->mu);
     if (!impl_->loaded) fail("to() called before load()");
     if (dev != Device::CPU && dev != Device::CUDA)
         fail("to(): a device this library does not run (CPU and the HIP GPU only)");
     impl_->device = dev;
 }
 
-Device Refiner::device() const { return impl_->device; }
+Device Refiner::device() const {
+    std::lock_guard<std::mutex> lock(impl_->mu);
+    return impl_->device;
+}
 
 Tensor Refiner::forward(const DecoderOutput& dec, const Intrinsics& intrins, int origH, int origW,
                         const DsineTransform& tf) const {
     const Impl& m = *impl_;
+    std::lock_guard<std::mutex> lock(m.mu);
     if (!m.loaded) fail("forward() called before load()");
     if (dec.h8 < 1 || dec.w8 < 1) fail("forward(): the decoder grid is empty");
     const std::size_t hw = static_cast<std::size_t>(dec.h8) * static_cast<std::size_t>(dec.w8);

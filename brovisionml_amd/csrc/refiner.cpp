@@ -1,12 +1,12 @@
 // The native NRN refiner (include/bvml_dsine_refine.h): brovisionml's Refiner
 // (src/dsine_refine.cpp:161-294) on one HIP device, over this library's C ABI
-// (include/bvml_dsine.h) and MIOpen.
+// (include/bvml_dsine.h).
 //
 // Per iteration (src/dsine_refine.cpp:255-287), on persistent per-grid maps:
 //   z, r*h = gates of conv5x5([h | feature | uv], [W_z; W_r])  bvml_dsine_conv_gru_gates_f32
 //   h    = (1 - z) h + z tanh(conv5x5([r*h | feature | uv], W_q) + b_q),
 //          also into [h | uv]                                bvml_dsine_conv_gru_update_f32
-//   t0   = conv3x3([h | uv], the heads' first layers)        MIOpen, 66 -> 192 or 256
+//   t0   = conv3x3([h | uv], the heads' first layers)        bvml_dsine_conv_f32, 66 -> 192 or 256
 //   prob, xy, angle = the heads' 1x1 layers on relu(t0 + b0) bvml_dsine_heads_mlp_f32
 //   pred = angmf_propagate(pred, prob, xy, angle) on logits  bvml_dsine_angmf_propagate_f32
 // and, in the last iteration only, the up-mask head (its 1x1 layers in the
@@ -19,17 +19,18 @@
 // (256).  The convolutions run without their bias; the fused kernels add it
 // in the reference's rounding (a bias add after the convolution's sum).
 //
-// The 5x5 convolutions are this library's implicit GEMMs on the fp32 matrix
-// cores (conv.hip); the heads' 3x3 layer is MIOpen's immediate mode, the
-// solution with the lowest time estimate, as PyTorch picks it on ROCm without
-// benchmarking (its Winograd kernel beats the direct product there); the
-// plans are made once per grid size.
+// Every convolution is this library's implicit GEMM on the fp32 matrix cores
+// (conv.hip): the kernels, their launch shapes and so their summation order
+// depend on the grid size only, so a forward's result is the same in every
+// process and from both forward entry points (a library that picks its
+// algorithm by measured or estimated time, as MIOpen's immediate mode does,
+// changes its rounding with the process's history).  The maps are allocated
+// once per grid size.
 
 #include "bvml_dsine_refine.h"
 #include "refiner_common.h"
 
 #include <hip/hip_runtime.h>
-#include <miopen/miopen.h>
 
 #include <cmath>
 #include <cstdint>
@@ -475,26 +476,6 @@ int hip_fail(hipError_t e, const std::string& what) {
     return fail((int)e, "forward: " + what + ": " + hipGetErrorString(e));
 }
 
-int mio_fail(miopenStatus_t s, const std::string& what) {
-    return fail(BVML_DSINE_ELIB,
-                "forward: MIOpen " + what + ": " + miopenGetErrorString(s));
-}
-
-struct ConvPlan {
-    miopenTensorDescriptor_t x = nullptr, w = nullptr, y = nullptr;
-    miopenConvolutionDescriptor_t conv = nullptr;
-    uint64_t solution = 0;
-    size_t ws = 0;
-
-    void reset() {
-        if (x) miopenDestroyTensorDescriptor(x);
-        if (w) miopenDestroyTensorDescriptor(w);
-        if (y) miopenDestroyTensorDescriptor(y);
-        if (conv) miopenDestroyConvolutionDescriptor(conv);
-        *this = ConvPlan{};
-    }
-};
-
 // Restores the caller's current device on scope exit.
 class DeviceScope {
 public:
@@ -523,13 +504,12 @@ struct bvml_dsine_refiner {
     bool dirty = true;  // host weights newer than the device copy
 
     int device = -1;  // bound at the first forward
-    miopenHandle_t mio = nullptr;
 
     // weights on the device, one allocation
     float* warena = nullptr;
     // convz + convr and convq, packed for the implicit-GEMM kernels
     const float *w_zr = nullptr, *b_z = nullptr, *b_r = nullptr, *w_q = nullptr, *b_q = nullptr;
-    const float *w_h0 = nullptr, *b_h0 = nullptr, *w2p = nullptr, *b_h2 = nullptr;
+    const float *b_h0 = nullptr, *w2p = nullptr, *b_h2 = nullptr;
     const float* w_h0p[2] = {};  // the 3x3 layer packed for bvml_dsine_conv_f32 (192, 256 filters)
     const float* w4p[kHeads] = {};  // the 1x1 layers packed for bvml_dsine_heads_mlp_f32
     const float* b4[kHeads] = {};
@@ -538,18 +518,10 @@ struct bvml_dsine_refiner {
     int H = 0, W = 0;
     float* arena = nullptr;
     Maps maps{};  // the maps' places in `arena` (maps_at)
-    void* ws = nullptr;
-    size_t ws_bytes = 0;
-    // [0]: the three heads the propagate reads, [1]: all four
-    ConvPlan h0_p[2];
 
     void drop_grid() {
-        for (auto& p : h0_p) p.reset();
         if (arena) (void)hipFree(arena);
-        if (ws) (void)hipFree(ws);
         arena = nullptr;
-        ws = nullptr;
-        ws_bytes = 0;
         H = W = 0;
     }
 
@@ -558,19 +530,17 @@ struct bvml_dsine_refiner {
         DeviceScope scope(device);
         drop_grid();
         if (warena) (void)hipFree(warena);
-        if (mio) miopenDestroy(mio);
     }
 
     int upload();
     int plan(int H, int W);
-    int make_plan(ConvPlan& p, int cin, int cout, int k, int groups, int H, int W);
-    int conv(const ConvPlan& p, const float* w, const float* x, float* y);
 };
 
 // Copies the host weights into the device arena, in the layout the kernels
 // read: [W_z; W_r] as one 128-filter weight, the four heads' first layers as
-// one 256-filter weight (each head's filters contiguous, prob, xy, angle,
-// up_mask: the first three heads are a prefix), their 1x1 layers packed for
+// one 192- and one 256-filter weight (each head's filters contiguous, prob,
+// xy, angle, up_mask: the first three heads are a prefix), all three packed
+// for bvml_dsine_conv_*, and the heads' 1x1 layers packed for
 // bvml_dsine_heads_mlp_f32.
 int bvml_dsine_refiner::upload() {
     std::vector<float> w2(kHeads * kMid * kMid), w2p_h((size_t)kHeads * 4096);
@@ -613,13 +583,11 @@ int bvml_dsine_refiner::upload() {
     parts.push_back({&b_r, {&host[kRb]}});
     parts.push_back({&w_q, {&wq_p}});
     parts.push_back({&b_q, {&host[kQb]}});
-    Src h0w, h0b, h2b;
+    Src h0b, h2b;
     for (int h = 0; h < kHeads; ++h) {
-        h0w.push_back(&host[head_w(h, 0)]);
         h0b.push_back(&host[head_b(h, 0)]);
         h2b.push_back(&host[head_b(h, 1)]);
     }
-    parts.push_back({&w_h0, h0w});
     parts.push_back({&w_h0p[0], {&wh0_p[0]}});
     parts.push_back({&w_h0p[1], {&wh0_p[1]}});
     parts.push_back({&b_h0, h0b});
@@ -651,6 +619,11 @@ int bvml_dsine_refiner::upload() {
             warena = nullptr;
             return hip_fail(e, "hipMalloc of the weights");
         }
+    } else {
+        // a forward queued earlier, on any stream of the device, may still be
+        // reading the weights: wait for it before overwriting them
+        const hipError_t e = hipDeviceSynchronize();
+        if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
     }
     const hipError_t e = hipMemcpy(warena, staging.data(), total * sizeof(float),
                                    hipMemcpyHostToDevice);
@@ -660,79 +633,26 @@ int bvml_dsine_refiner::upload() {
     return BVML_DSINE_OK;
 }
 
-int bvml_dsine_refiner::make_plan(ConvPlan& p, int cin, int cout, int k, int groups, int H,
-                                  int W) {
-    miopenStatus_t st;
-    if ((st = miopenCreateTensorDescriptor(&p.x)) != miopenStatusSuccess ||
-        (st = miopenSet4dTensorDescriptor(p.x, miopenFloat, 1, cin, H, W)) != miopenStatusSuccess ||
-        (st = miopenCreateTensorDescriptor(&p.w)) != miopenStatusSuccess ||
-        (st = miopenSet4dTensorDescriptor(p.w, miopenFloat, cout, cin / groups, k, k)) !=
-            miopenStatusSuccess ||
-        (st = miopenCreateTensorDescriptor(&p.y)) != miopenStatusSuccess ||
-        (st = miopenSet4dTensorDescriptor(p.y, miopenFloat, 1, cout, H, W)) != miopenStatusSuccess ||
-        (st = miopenCreateConvolutionDescriptor(&p.conv)) != miopenStatusSuccess ||
-        (st = miopenInitConvolutionDescriptor(p.conv, miopenConvolution, k / 2, k / 2, 1, 1, 1,
-                                              1)) != miopenStatusSuccess ||
-        (groups > 1 &&
-         (st = miopenSetConvolutionGroupCount(p.conv, groups)) != miopenStatusSuccess))
-        return mio_fail(st, "descriptors");
-    size_t count = 0;
-    if ((st = miopenConvolutionForwardGetSolutionCount(mio, p.w, p.x, p.conv, p.y, &count)) !=
-        miopenStatusSuccess)
-        return mio_fail(st, "solution count");
-    if (count == 0) return fail(BVML_DSINE_ELIB, "forward: MIOpen has no solution for a convolution");
-    std::vector<miopenConvSolution_t> sols(count);
-    size_t got = 0;
-    if ((st = miopenConvolutionForwardGetSolution(mio, p.w, p.x, p.conv, p.y, count, &got,
-                                                  sols.data())) != miopenStatusSuccess)
-        return mio_fail(st, "solutions");
-    if (got == 0) return fail(BVML_DSINE_ELIB, "forward: MIOpen has no solution for a convolution");
-    size_t best = 0;
-    for (size_t i = 1; i < got; ++i)
-        if (sols[i].time < sols[best].time) best = i;
-    p.solution = sols[best].solution_id;
-    p.ws = sols[best].workspace_size;
-    if ((st = miopenConvolutionForwardCompileSolution(mio, p.w, p.x, p.conv, p.y, p.solution)) !=
-        miopenStatusSuccess)
-        return mio_fail(st, "compile");
-    return BVML_DSINE_OK;
-}
-
-// Allocates the maps of an H x W grid and plans its convolutions.
+// Allocates the maps of an H x W grid.  The maps of the previous size are
+// freed first, once every forward queued on any stream of the device (which
+// may still be reading them) has finished.
 int bvml_dsine_refiner::plan(int h, int w) {
     if (arena && H == h && W == w) return BVML_DSINE_OK;
+    if (arena) {
+        const hipError_t e = hipDeviceSynchronize();
+        if (e != hipSuccess) return hip_fail(e, "hipDeviceSynchronize");
+    }
     drop_grid();
     const size_t hw = (size_t)h * w;
-    hipError_t e = hipMalloc(&arena, maps_floats(hw) * sizeof(float));
+    const hipError_t e = hipMalloc(&arena, maps_floats(hw) * sizeof(float));
     if (e != hipSuccess) {
         arena = nullptr;
         return hip_fail(e, "hipMalloc of the maps");
     }
     maps = maps_at(arena, hw);
-    int st;
-    for (int i = 0; i < 2; ++i)
-        if ((st = make_plan(h0_p[i], kHin, (3 + i) * kMid, 3, 1, h, w))) return drop_grid(), st;
-    size_t need = 0;
-    for (const ConvPlan* p : {&h0_p[0], &h0_p[1]})
-        need = p->ws > need ? p->ws : need;
-    if (need) {
-        e = hipMalloc(&ws, need);
-        if (e != hipSuccess) {
-            ws = nullptr;
-            drop_grid();
-            return hip_fail(e, "hipMalloc of the MIOpen workspace");
-        }
-        ws_bytes = need;
-    }
     H = h;
     W = w;
     return BVML_DSINE_OK;
-}
-
-int bvml_dsine_refiner::conv(const ConvPlan& p, const float* w, const float* x, float* y) {
-    const miopenStatus_t st = miopenConvolutionForwardImmediate(mio, p.w, w, p.x, x, p.conv, p.y, y,
-                                                                ws, ws_bytes, p.solution);
-    return st == miopenStatusSuccess ? BVML_DSINE_OK : mio_fail(st, "convolution");
 }
 
 const std::vector<std::vector<float>>& bvml_refine::host_weights(const bvml_dsine_refiner* r) {
@@ -740,11 +660,9 @@ const std::vector<std::vector<float>>& bvml_refine::host_weights(const bvml_dsin
 }
 
 // The loop of Refiner::forward on the maps `m`, after forward's checks, with
-// the refiner's device current and its weights on it: the 3x3 heads layer on
-// MIOpen (its plans made for this grid size) or, with own_h0, on this
-// library's convolution kernel.
+// the refiner's device current and its weights on it.
 int bvml_refine::forward_maps(bvml_dsine_refiner* r, const Maps& m, const ForwardArgs& a,
-                              void* stream, bool own_h0) {
+                              void* stream) {
     const int h8 = a.h8, w8 = a.w8, pad_t = a.pad_t, pad_l = a.pad_l;
     const int out_h = a.out_h, out_w = a.out_w;
     float* out = a.out;
@@ -800,10 +718,8 @@ int bvml_refine::forward_maps(bvml_dsine_refiner* r, const Maps& m, const Forwar
         // the heads (:119-127, :257-267, :276): the 3x3 layers, then the rest
         // in one pass; the up-mask head's last bias is the upsample's
         const float* b4[kHeads] = {r->b4[0], r->b4[1], r->b4[2], nullptr};
-        const int st0 = own_h0 ? ck(bvml_dsine_conv_f32(m.hin, kHin, h8, w8, r->w_h0p[last ? 1 : 0],
-                                                        nh * kMid, 3, m.t0, stream), "conv")
-                               : r->conv(r->h0_p[last ? 1 : 0], r->w_h0, m.hin, m.t0);
-        if ((st = st0) ||
+        if ((st = ck(bvml_dsine_conv_f32(m.hin, kHin, h8, w8, r->w_h0p[last ? 1 : 0], nh * kMid,
+                                         3, m.t0, stream), "conv")) ||
             (st = ck(bvml_dsine_heads_mlp_f32(m.t0, r->b_h0, r->w2p, r->b_h2, r->w4p, b4, kHeadOut,
                                               nh, h8, w8, m.head, stream), "heads_mlp")))
             return st;
@@ -924,17 +840,10 @@ int bvml_dsine_refiner_forward(bvml_dsine_refiner* r, const float* normal, const
     }
     DeviceScope scope(r->device);
     if (scope.status() != hipSuccess) return hip_fail(scope.status(), "hipSetDevice");
-    miopenStatus_t ms;
-    if (!r->mio && (ms = miopenCreate(&r->mio)) != miopenStatusSuccess) {
-        r->mio = nullptr;
-        return mio_fail(ms, "handle");
-    }
     int st;
     if (r->dirty && (st = r->upload()) != BVML_DSINE_OK) return st;
     if ((st = r->plan(h8, w8)) != BVML_DSINE_OK) return st;
-    if ((ms = miopenSetStream(r->mio, static_cast<hipStream_t>(stream))) != miopenStatusSuccess)
-        return mio_fail(ms, "stream");
-    return bvml_refine::forward_maps(r, r->maps, args, stream, false);
+    return bvml_refine::forward_maps(r, r->maps, args, stream);
 }
 
 }  // extern "C"

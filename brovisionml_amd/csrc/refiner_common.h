@@ -98,10 +98,8 @@ inline Maps maps_at(float* base, size_t hw) {
 }
 
 // The loop of the device forward on the maps m (refiner.cpp), after the
-// checks, with the refiner's device current and its weights uploaded;
-// own_h0: the heads' 3x3 layer on bvml_dsine_conv_f32 instead of MIOpen.
-int forward_maps(bvml_dsine_refiner* r, const Maps& m, const ForwardArgs& a, void* stream,
-                 bool own_h0);
+// checks, with the refiner's device current and its weights uploaded.
+int forward_maps(bvml_dsine_refiner* r, const Maps& m, const ForwardArgs& a, void* stream);
 int refiner_device(const bvml_dsine_refiner* r);    // -1 before the first forward
 bool refiner_uploaded(const bvml_dsine_refiner* r);  // weights on the device and current
 

@@ -1,13 +1,15 @@
 // The native refiner's allocation-free forward
 // (bvml_dsine_refiner_forward_noalloc): the loop of bvml_dsine_refiner_forward
 // on maps placed in `scratch`, a fixed device array of this library, for
-// callers that cannot allocate device memory.  It makes no hipMalloc, hipFree
-// or MIOpen call: the heads' 3x3 layer runs on this library's convolution
-// kernel (bvml_dsine_conv_f32) instead of MIOpen, and the weights must
-// already be on the device (a bvml_dsine_refiner_forward since the last
+// callers that cannot allocate device memory.  It makes no hipMalloc or hipFree
+// call (the same kernels as bvml_dsine_refiner_forward, so the same result,
+// bit for bit), and the weights must already be on the device (a bvml_dsine_refiner_forward since the last
 // weight change uploads them).  Every call on one GPU uses that GPU's copy of
-// `scratch`: calls that overlap on one GPU race.  Nothing in `scratch` needs
-// to start at zero: each forward writes every map before it reads it.
+// `scratch`, so calls on one GPU are put in order: each call's stream waits
+// for an event recorded after the previous call's work, whatever stream that
+// ran on (inside a stream capture the caller orders the replays).  Nothing in
+// `scratch` needs to start at zero: each forward writes every map before it
+// reads it.
 
 #include <hip/hip_runtime.h>
 
@@ -29,23 +31,36 @@ constexpr size_t kScratchFloats = size_t(8) << 20;
 static __device__ __align__(256) float scratch[kScratchFloats];
 
 constexpr int kMaxDevices = 64;
-std::once_flag g_once[kMaxDevices];
-hipError_t g_status[kMaxDevices];
-void* g_scratch[kMaxDevices];  // each device's address of its copy of `scratch`
 
-// Set-up, once per device, with that device current: the address of this
-// device's copy of `scratch` (host code uses it, never the array's name).
-int scratch_on(int dev, float** out) {
+// Per device: the address of its copy of `scratch` (host code uses it, never
+// the array's name), an event recorded after the last call's work, and a
+// lock held while a call waits for that event, enqueues its work and records
+// the event again.
+struct DeviceSlot {
+    std::once_flag once;
+    hipError_t status = hipSuccess;
+    void* scratch = nullptr;
+    hipEvent_t done = nullptr;
+    bool recorded = false;
+    std::mutex mu;
+};
+DeviceSlot g_slot[kMaxDevices];
+
+// Set-up, once per device, with that device current.
+int slot_on(int dev, DeviceSlot** out) {
     if (dev < 0 || dev >= kMaxDevices)
         return fail(BVML_DSINE_EUNSUP, "forward_noalloc: device index beyond " +
                                            std::to_string(kMaxDevices - 1));
-    std::call_once(g_once[dev], [dev] {
-        g_status[dev] = hipGetSymbolAddress(&g_scratch[dev], HIP_SYMBOL(scratch));
+    DeviceSlot& s = g_slot[dev];
+    std::call_once(s.once, [&s] {
+        s.status = hipGetSymbolAddress(&s.scratch, HIP_SYMBOL(scratch));
+        if (s.status == hipSuccess)
+            s.status = hipEventCreateWithFlags(&s.done, hipEventDisableTiming);
     });
-    if (g_status[dev] != hipSuccess)
-        return fail((int)g_status[dev], std::string("forward_noalloc: hipGetSymbolAddress: ") +
-                                            hipGetErrorString(g_status[dev]));
-    *out = static_cast<float*>(g_scratch[dev]);
+    if (s.status != hipSuccess)
+        return fail((int)s.status, std::string("forward_noalloc: set-up: ") +
+                                       hipGetErrorString(s.status));
+    *out = &s;
     return BVML_DSINE_OK;
 }
 
@@ -77,9 +92,32 @@ extern "C" int bvml_dsine_refiner_forward_noalloc(bvml_dsine_refiner* r, const f
     if (e != hipSuccess) return fail((int)e, "forward_noalloc: hipGetDevice failed");
     if (prev != dev && (e = hipSetDevice(dev)) != hipSuccess)
         return fail((int)e, "forward_noalloc: hipSetDevice failed");
-    float* base = nullptr;
-    int st = scratch_on(dev, &base);
-    if (st == BVML_DSINE_OK) st = forward_maps(r, maps_at(base, hw), args, stream, true);
+    DeviceSlot* slot = nullptr;
+    int st = slot_on(dev, &slot);
+    if (st == BVML_DSINE_OK) {
+        std::lock_guard<std::mutex> lock(slot->mu);
+        const hipStream_t strm = static_cast<hipStream_t>(stream);
+        hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+        e = hipStreamIsCapturing(strm, &cap);
+        const bool chain = e == hipSuccess && cap == hipStreamCaptureStatusNone;
+        if (e != hipSuccess)
+            st = fail((int)e, "forward_noalloc: hipStreamIsCapturing failed");
+        else if (chain && slot->recorded &&
+                 (e = hipStreamWaitEvent(strm, slot->done, 0)) != hipSuccess)
+            st = fail((int)e, "forward_noalloc: hipStreamWaitEvent failed");
+        if (st == BVML_DSINE_OK) {
+            st = forward_maps(r, maps_at(static_cast<float*>(slot->scratch), hw), args, stream);
+            // (recorded after a failed call too: the next call waits for
+            // whatever this one enqueued)
+            if (chain) {
+                e = hipEventRecord(slot->done, strm);
+                if (e == hipSuccess)
+                    slot->recorded = true;
+                else if (st == BVML_DSINE_OK)
+                    st = fail((int)e, "forward_noalloc: hipEventRecord failed");
+            }
+        }
+    }
     if (prev != dev) (void)hipSetDevice(prev);
     return st;
 }

@@ -21,8 +21,12 @@ What runs where:
     the upsample fuses convex_upsample_forward and l2_normalize_nchw_forward
     (:278-282); the ray map comes from bvml_dsine_build_ray8_f32 on the device.
   * The ConvGRU and the heads' convolutions (the reference's brotensor
-    conv2d_forward, :94-101) are torch's F.conv2d, i.e. MIOpen / hipBLASLt on
-    ROCm, in fp32 and without bias; their biases, activations and the GRU's
+    conv2d_forward, :94-101) are torch's F.conv2d in fp32 and without bias,
+    with MIOpen switched off, so torch runs them as im2col + an fp32 GEMM: a
+    fixed algorithm per shape, the same rounding in every process (MIOpen
+    picks its algorithm by estimated or measured time, which changes with
+    the process's history, and its Winograd kernels round differently from a
+    direct sum); their biases, activations and the GRU's
     gate arithmetic run in the package's fused elementwise kernels
     (bvml_dsine_gru_gates_f32, bvml_dsine_gru_update_f32,
     bvml_dsine_bias_act_f32), the up-mask head's last bias in the upsample
@@ -128,8 +132,9 @@ class Refiner:
     """Refiner::forward on the device.  `weights` as weight_shapes() names
     them (numpy or torch); hidden / feature are the checkpoint's widths.
 
-    The convolutions run without their bias on MIOpen / hipBLASLt (torch's
-    F.conv2d): convz and convr as one 2*hidden-channel convolution, the four
+    The convolutions run without their bias as torch's F.conv2d with MIOpen
+    off (im2col + an fp32 GEMM, the same algorithm in every process): convz
+    and convr as one 2*hidden-channel convolution, the four
     heads' first 3x3 convolutions as one, their 1x1 middle convolutions as one
     grouped convolution.  Biases, activations and the gate arithmetic run in
     this package's fused kernels (bvml_dsine_gru_gates_f32,
@@ -186,13 +191,21 @@ class Refiner:
 
     def forward(self, dec: DecoderOutput, intr: workloads.Intrinsics, orig_h: int, orig_w: int,
                 crop: Crop | None = None, trace: list | None = None, cond=None,
-                hidden_trace: list | None = None):
+                hidden_trace: list | None = None, heads_trace: list | None = None):
         """The refined normals (1, 3, h, w) at the unpadded resolution
         (crop.orig_h x crop.orig_w; the whole 8*h8 x 8*w8 map without crop).
         trace, when given, receives each iteration's (pred_norm, up) pair,
-        hidden_trace a copy of each iteration's h_new (1, C, h8, w8);
+        hidden_trace a copy of each iteration's h_new (1, C, h8, w8),
+        heads_trace each iteration's propagate inputs (pred_norm before the
+        iteration, and the prob, xy and angle heads' raw logits);
         cond, when given, is conditioning()'s result for these intrinsics (so
         the call does no host-to-device copy and can be captured in a graph)."""
+        import torch
+        with torch.backends.cudnn.flags(enabled=False):
+            return self._forward(dec, intr, orig_h, orig_w, crop, trace, cond, hidden_trace,
+                                 heads_trace)
+
+    def _forward(self, dec, intr, orig_h, orig_w, crop, trace, cond, hidden_trace, heads_trace):
         import torch
         import torch.nn.functional as F
         _, _, H, W = dec.normal.shape
@@ -223,6 +236,8 @@ class Refiner:
             qp = F.conv2d(rhx, self.w_q, None, padding=2)
             dsine.gru_update(qp, self.b_q, z, h, C, HW, h, hin[:, :C])
             prob, xy, angle, up_mask = self._heads(hin, H, W)
+            if heads_trace is not None:
+                heads_trace.append((pred_norm, prob, xy, angle))
             pred_norm = dsine.angmf_propagate(pred_norm, prob, xy, angle, ray8, fu, cu, fv, cv,
                                               H, W, logits=True)
             up = dsine.convex_upsample_normalize(pred_norm, up_mask, 1, 3, H, W, K_UP,
@@ -242,10 +257,10 @@ class NativeRefiner:
     """Refiner::forward in C++ (libbvml_dsine_refine.so, the C ABI of
     include/bvml_dsine_refine.h): the same loop as Refiner above, with no
     Python or torch in it: the 5x5 ConvGRU convolutions on this package's
-    fp32 matrix-core kernels with the gates and update fused, the heads
-    after their 3x3 layer (MIOpen) in one fused pass, the rest this
-    package's kernels, the up-mask head and the upsample in the last
-    iteration only.  Weights from a safetensors file (`path`, read by
+    fp32 matrix-core kernels with the gates and update fused, the heads'
+    3x3 layer on the same kernels, the rest of the heads in one fused pass,
+    the rest this package's kernels, the up-mask head and the upsample in
+    the last iteration only: the same bits in every process.  Weights from a safetensors file (`path`, read by
     the library) or a dict as weight_shapes() names them."""
 
     def __init__(self, weights: dict | None = None, path: str | None = None):

@@ -8,10 +8,14 @@
 // iteration's up-sampled normals cropped to the unpadded image.
 //
 // On the GPU (brotensor's CUDA tag, the HIP device) the loop is the native
-// refiner of include/bvml_dsine_refine.h: this library's gfx950 kernels and
-// MIOpen's convolutions, asynchronously on the null stream.  On the CPU it
-// is the library's host path: fp32 convolutions and the CPU branch of the
-// ops, on host threads.
+// refiner of include/bvml_dsine_refine.h: this library's gfx950 kernels,
+// asynchronously on the null stream.  On the CPU it is the library's host
+// path: fp32 convolutions and the CPU branch of the ops, on host threads.
+//
+// Threads: forward is const, as the reference's, and may be called on one
+// Refiner from several threads; the calls take a lock of the object's own
+// (load, load_file and to take it too), since the device buffers, the
+// uploaded weights and the grid-size state are shared by its forwards.
 //
 // Weights load from a safetensors file (F32, F16 or BF16, widened to fp32)
 // under the top-level keys gru.conv{z,r,q}.*, {prob,xy,angle,up_prob}_head.*

@@ -9,18 +9,23 @@
  * convolutions as fp32 matrix-core implicit GEMMs with the gates and the
  * update fused, the heads after their 3x3 layer in one fused pass, the
  * propagate on the heads' raw logits, the convex upsample with its mask
- * bias -- and the heads' 3x3 layer on MIOpen (fp32, immediate mode).  The
- * C++ class of include/brovisionml/dsine_refine.h sits on top of it.
+ * bias -- and the heads' 3x3 layer on the same fp32 matrix-core convolution.
+ * Its kernels and their launch shapes depend on the grid size only, so a
+ * forward gives the same bits in every process.  The C++ class of
+ * include/brovisionml/dsine_refine.h sits on top of it.
  *
  * Lifecycle: create (no HIP call) -> weights (load_file, or set_tensor per
  * tensor) -> forward, any number of times, at any grid size -> destroy.
  * The first forward binds the refiner to the calling thread's current HIP
  * device; later forwards make that device current and restore the caller's.
  * The first forward after a weight change uploads the weights (a
- * synchronous copy), and the first forward at a grid size allocates its
- * buffers and plans its convolutions: run one forward eagerly before
- * capturing forwards into a HIP graph.  Calls on one refiner must not
- * overlap; distinct refiners are independent.
+ * synchronous copy, after the device has finished any forward still
+ * reading the old weights), and the first forward at a grid size allocates
+ * its buffers (after the device has finished any forward still using the
+ * previous size's): run one forward eagerly before capturing forwards into
+ * a HIP graph.  Calls on one refiner from two host threads at once are not
+ * allowed (the C++ Refiner class serializes its own); distinct refiners are
+ * independent.
  *
  * Return value: 0 on success, a negative BVML_DSINE_E* code for a rejected
  * argument or missing weights (nothing is launched), a positive hipError_t
@@ -38,14 +43,15 @@ extern "C" {
 
 #define BVML_DSINE_EWEIGHTS (-9)  /* a checkpoint tensor missing, of the wrong size or dtype */
 #define BVML_DSINE_EFILE (-10)    /* the checkpoint cannot be read or is not safetensors */
-#define BVML_DSINE_ELIB (-11)     /* MIOpen reported an error */
+#define BVML_DSINE_ELIB (-11)     /* reserved (no longer returned: the refiner uses no library
+                                     convolution) */
 
 typedef struct bvml_dsine_refiner bvml_dsine_refiner;
 
 /* A refiner with no weights; makes no HIP call. */
 int bvml_dsine_refiner_create(bvml_dsine_refiner** out);
 
-/* Frees the refiner's device memory and MIOpen state (NULL is a no-op). */
+/* Frees the refiner's device memory (NULL is a no-op). */
 void bvml_dsine_refiner_destroy(bvml_dsine_refiner* r);
 
 /*
@@ -117,15 +123,19 @@ int bvml_dsine_refiner_forward_cpu(bvml_dsine_refiner* r, const float* normal,
  * instead of allocated ones: the variant for callers that cannot allocate
  * device memory (code under HIP graph capture, tight serving loops,
  * harnesses that forbid hipMalloc).  No counterpart in the reference.  It
- * calls no hipMalloc, hipFree or MIOpen routine: the heads' 3x3 layer runs
- * on bvml_dsine_conv_f32 (the same fp32 convolution within rounding), and
- * the weights must already be on the device: a bvml_dsine_refiner_forward
- * after the last load_file / set_tensor uploads them (else
- * BVML_DSINE_EWEIGHTS).  The array holds 8,388,608 floats (32 MiB) per GPU,
- * the maps of a grid of up to about 5,500 pixels (1,523 planes; a 60 x 80
- * grid needs 7,310,400 floats); a larger grid returns BVML_DSINE_ESIZE.  Every call on one GPU
- * uses that GPU's array, which keeps the last call's contents (nothing in
- * it needs to start at zero): calls that overlap on one GPU race.
+ * calls no hipMalloc or hipFree (the same kernels as
+ * bvml_dsine_refiner_forward: the same result, bit for bit), and the weights
+ * must already be on the device: a bvml_dsine_refiner_forward after the last
+ * load_file / set_tensor uploads them (else BVML_DSINE_EWEIGHTS).  The array
+ * holds 8,388,608 floats (32 MiB) per GPU, the maps of a grid of up to about
+ * 5,500 pixels (1,523 planes; a 60 x 80 grid needs 7,310,400 floats); a
+ * larger grid returns BVML_DSINE_ESIZE.  Every call on one GPU uses that
+ * GPU's array, which keeps the last call's contents (nothing in it needs to
+ * start at zero), so calls on one GPU run in the order they were made: each
+ * call's stream first waits for an event this library records after the
+ * previous call's work, whatever stream that ran on.  Under stream capture
+ * the call neither waits nor records (the caller orders the graph's
+ * replays).  The first call on a device creates that event (set-up, once).
  * Arguments, checks and results otherwise as bvml_dsine_refiner_forward.
  */
 int bvml_dsine_refiner_forward_noalloc(bvml_dsine_refiner* r, const float* normal,

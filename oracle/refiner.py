@@ -22,17 +22,30 @@ def _sigmoid_f32(x):
     return (1.0 / (1.0 + np.exp(-np.asarray(x, np.float64)))).astype(np.float32)
 
 
+def angle_from_logits(x):
+    """The angle head's activation, sigmoid(x) * pi (src/dsine_refine.cpp:265-267),
+    each step rounded to float."""
+    return (_sigmoid_f32(x).astype(np.float64) * np.float64(K_PI32)).astype(np.float32)
+
+
 MUTATIONS = (None, "swap_zr", "swap_xy")
 
 
 def refine_forward(weights, normal, feature, hidden, intr, fuv, ray8, uv8, trace=None,
-                   nthreads: int = 1, hidden_trace=None, mutation=None):
+                   nthreads: int = 1, hidden_trace=None, mutation=None, cond_trace=None):
     """weights: name -> OIHW / (C,) float32 arrays; normal (3, H, W), feature
     and hidden (C, H, W) float32; intr unused beyond fuv = (fu, cu, fv, cv);
     ray8 (3, H, W) and uv8 (2, H, W) float32 as build_ray8 / build_uv give
     them.  Returns the last up-sampled map (3, 8H, 8W) float32; trace, when
     given, receives each iteration's (pred_norm, up), hidden_trace each
-    iteration's h_new (C, H, W) float64.  mutation plants a mistake, for the
+    iteration's h_new (C, H, W) float64, cond_trace each iteration's
+    propagate conditioning per pixel, a dict of (H, W) maps: "ratio",
+    |acc| / sqrt(sum (prob/|p|)^2) from the oracle's double sums (small where
+    the sum cancels: the output then moves by about 1/ratio times a relative
+    change of the terms), and "min_xy", the smallest |(xs, ys)| of the
+    pixel's k*k pairs (the rotation axis's direction moves by about an
+    absolute change of the pair over |(xs, ys)|).  mutation plants a mistake,
+    for the
     tests that show the checks catch one: "swap_zr" exchanges the GRU's z and
     r gates, "swap_xy" the propagate's xs and ys planes."""
     assert mutation in MUTATIONS
@@ -70,12 +83,20 @@ def refine_forward(weights, normal, feature, hidden, intr, fuv, ray8, uv8, trace
         xy = head("xy_head", hin)
         if mutation == "swap_xy":
             xy = np.concatenate([xy[PS * PS:], xy[:PS * PS]])
-        angle = (_sigmoid_f32(head("angle_head", hin)).astype(np.float64)
-                 * np.float64(K_PI32)).astype(np.float32)
-        pred = angmf_propagate(pred.reshape(1, 3, -1), prob.reshape(1, PS * PS, -1),
-                               xy.reshape(1, 2 * PS * PS, -1), angle.reshape(1, PS * PS, -1),
-                               ray8.reshape(3, -1), fuv, H, W, PS, nthreads=nthreads)
-        pred = pred.reshape(3, -1)
+        angle = angle_from_logits(head("angle_head", hin))
+        res = angmf_propagate(pred.reshape(1, 3, -1), prob.reshape(1, PS * PS, -1),
+                              xy.reshape(1, 2 * PS * PS, -1), angle.reshape(1, PS * PS, -1),
+                              ray8.reshape(3, -1), fuv, H, W, PS, nthreads=nthreads,
+                              return_acc=cond_trace is not None,
+                              return_qs=cond_trace is not None)
+        if cond_trace is not None:
+            res, acc, qs = res
+            a2 = (np.asarray(acc, np.float64).reshape(3, -1) ** 2).sum(axis=0)
+            ratio = np.sqrt(a2 / np.maximum(np.asarray(qs, np.float64).reshape(-1), 1e-300))
+            xy64 = xy.astype(np.float64).reshape(2, PS * PS, H, W)
+            cond_trace.append({"ratio": ratio.reshape(H, W),
+                               "min_xy": np.sqrt((xy64 ** 2).sum(axis=0)).min(axis=0)})
+        pred = res.reshape(3, -1)
         mask = head("up_prob_head", hin)
         up = convex_upsample(pred.reshape(1, 3, H, W), mask[None], H, W, K_UP, normalize=True,
                              eps=float(np.float32(1e-12)), nthreads=nthreads)[0]

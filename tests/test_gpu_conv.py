@@ -145,5 +145,14 @@ def test_conv_rejects(cuda):
     assert lib.bvml_dsine_conv_f32(0, 130, 4, 4, p, 64, 5, p, None) == _lib.ENULL
     assert lib.bvml_dsine_conv_gru_update_f32(p, 130, 4, 4, p, 48, p, p, p, p, None, None) == \
         _lib.ESHAPE
+    # h_new partly over h (one plane on): another lane's write would race this
+    # lane's read, so it is refused before any launch (h_new == h is allowed)
+    xs = torch.zeros(130 * 16, device=cuda)
+    zs = torch.zeros(64 * 16, device=cuda)
+    hs = torch.zeros(65 * 16, device=cuda)
+    bq = torch.zeros(64, device=cuda)
+    assert lib.bvml_dsine_conv_gru_update_f32(
+        xs.data_ptr(), 130, 4, 4, p, 64, bq.data_ptr(), zs.data_ptr(), hs.data_ptr(),
+        hs.data_ptr() + 16 * 4, None, None) == _lib.EALIAS
     assert lib.bvml_dsine_conv_packed_size(64, 130, 5) == 33 * 25 * 4 * 64
     assert lib.bvml_dsine_conv_packed_size(192, 66, 3) == 17 * 9 * 12 * 64

@@ -1,29 +1,40 @@
 """The refiner loop on the device (brovisionml_amd/refiner.py: Refiner::forward,
 src/dsine_refine.cpp:212-294, driving this package's kernels with the ConvGRU
-and heads on MIOpen) against its CPU restatement (oracle/refiner.py: float64
-convolutions, the C oracle's ops), iteration by iteration, on synthetic
-weights and decoder outputs (no checkpoint ships here).
+and heads on torch's fp32 convolutions, MIOpen off) against its CPU
+restatement (oracle/refiner.py: float64 convolutions, the C oracle's ops),
+on synthetic weights and decoder outputs (no checkpoint ships here).
 
-The device convolutions run in fp32, the restatement's in float64, so the
-heads' outputs differ by float rounding and the differences pass through five
-recurrent iterations.  How much they differ depends on the convolution
-algorithm MIOpen picks, which can change with the process's history (the
-same forward measured 6.8e-6 on its own and 2.7e-5 after the rest of the GPU
-suite, at a pixel with no cancellation, while the propagate kernel alone is
-within 2.6e-7 of the oracle on those heads' outputs): the bar here is 1e-4
-per component on every iteration's propagated and up-sampled normals.  The
-ops alone hold 1e-5 on identical inputs (tests/test_gpu_parity.py), and the
-closed-form pins below, whose heads are exact, hold 1e-5 through the loop."""
+Two checks per iteration:
+  * stepwise: the iteration's propagate against the C oracle on the device's
+    own inputs (the previous iteration's device output and the device's
+    heads, activated as correctly rounded floats): the op's bar, 1e-5;
+  * end to end, against the float64 restatement: the returned map within
+    5e-6 (the reference reports its whole pipeline "exact to FP32 round-off
+    -- max-abs ~2-5e-6", docs/dsine.md:75-77), each iteration's up-sampled
+    map within 2e-5, each iteration's propagated /8 normals within 1e-4.
+    The heads are fp32 convolutions, here as in the reference, and where a
+    pixel's window holds a small xy pair (|(xs, ys)| down to 1e-3 in these
+    draws) their ~1e-7 rounding moves that neighbour's rotation axis by
+    about 1e-7/|(xs, ys)| rad: measured up to 5.6e-5 on the /8 normals of
+    such pixels (and of their neighbours in the next iteration), while every
+    pixel whose pairs are all >= 0.05 stays within 4.8e-6.
+The convolutions are a fixed algorithm per shape (im2col + an fp32 GEMM), so
+the result does not depend on the process's history.  The closed-form pins
+below, whose heads are exact, hold 1e-5 through the loop."""
 from __future__ import annotations
 
 import numpy as np
 import pytest
 
+import oracle
 from brovisionml_amd import refiner as rf, workloads as wl
 from oracle import refiner as oref
 
 pytestmark = pytest.mark.gpu
-TOL = 1e-4
+TOL_STEP = 1e-5     # an iteration's propagate against the oracle on the device's own inputs
+TOL_RESULT = 5e-6   # the returned map against the float64 restatement
+TOL_UP = 2e-5       # each iteration's up-sampled map against the float64 restatement
+TOL_COARSE = 1e-4   # each iteration's /8 normals against the float64 restatement
 
 
 def say(msg: str) -> None:
@@ -51,20 +62,31 @@ def test_refiner_iterations(cuda, H, W, fov, seed):
     dev = torch.device(cuda)
     model = rf.Refiner(weights, dev)
     dec = rf.DecoderOutput(*(torch.from_numpy(a)[None].to(dev) for a in (n, feature, hidden)))
-    trace = []
-    out = model.forward(dec, intr, 8 * H, 8 * W, trace=trace)
+    trace, heads = [], []
+    out = model.forward(dec, intr, 8 * H, 8 * W, trace=trace, heads_trace=heads)
     torch.cuda.synchronize()
     ray8 = wl.build_ray8(intr, H, W, 8 * H, 8 * W).reshape(3, H, W)
     uv8 = rf.uv_map(intr, H, W, 8 * H, 8 * W)
     want_trace = []
     want = oref.refine_forward(weights, n, feature, hidden, intr, fuv, ray8, uv8,
                                trace=want_trace, nthreads=16)
-    assert len(trace) == len(want_trace) == rf.N_ITER
-    for it, ((gp, gu), (wp, wu)) in enumerate(zip(trace, want_trace)):
-        ep = float(np.abs(gp.cpu().numpy().reshape(3, H, W).astype(np.float64) - wp).max())
+    assert len(trace) == len(heads) == len(want_trace) == rf.N_ITER
+    for it, ((gp, gu), (wp, wu), (pin, prob, xy, angle)) in enumerate(
+            zip(trace, want_trace, heads)):
+        gp = gp.cpu().numpy().reshape(3, H, W)
+        step = oracle.angmf_propagate(
+            pin.cpu().numpy().reshape(1, 3, -1), oref._sigmoid_f32(prob.cpu().numpy()),
+            xy.cpu().numpy(), oref.angle_from_logits(angle.cpu().numpy()), ray8.reshape(3, -1),
+            fuv, H, W, rf.PS, nthreads=16).reshape(3, H, W)
+        es = float(np.abs(gp.astype(np.float64) - step).max())
+        ep = float(np.abs(gp.astype(np.float64) - wp).max())
         eu = float(np.abs(gu.cpu().numpy()[0].astype(np.float64) - wu).max())
-        say(f"    iteration {it}: propagate max-abs {ep:.3e}  upsample max-abs {eu:.3e}")
-        assert ep <= TOL and eu <= TOL
+        say(f"    iteration {it}: propagate stepwise max-abs {es:.3e}, against float64 "
+            f"{ep:.3e}; upsample against float64 {eu:.3e}")
+        assert es <= TOL_STEP and ep <= TOL_COARSE and eu <= TOL_UP
+    er = float(np.abs(out.cpu().numpy()[0].astype(np.float64) - want).max())
+    say(f"    result max-abs {er:.3e}")
+    assert er <= TOL_RESULT
     assert out.shape == (1, 3, 8 * H, 8 * W)
     assert np.array_equal(out.cpu().numpy(), trace[-1][1].cpu().numpy())
 

@@ -4,10 +4,16 @@ against the CPU restatement (oracle/refiner.py: float64 convolutions, the C
 oracle's ops), the closed-form pins of tests/refiner_pins.py and the Python
 driver (brovisionml_amd/refiner.py), on synthetic weights and decoder maps.
 
-The bars are those of tests/test_gpu_refiner.py: 1e-4 per component where
-fp32 convolutions meet the float64 restatement through five recurrent
-iterations (MIOpen's algorithm choice sets how far apart they land), 1e-5
-where the pins' heads are exact."""
+The bars against the float64 restatement are those of
+tests/test_gpu_refiner.py: the returned map within 5e-6 (the reference's
+"exact to FP32 round-off -- max-abs ~2-5e-6", docs/dsine.md:75-77), each
+iteration's propagated /8 normals within 1e-4 (fp32 heads whose rounding a
+small xy pair amplifies), 1e-5 where the pins' heads are exact.  Every
+convolution of the
+native refiner is this library's kernel, whose launch shape depends on the
+grid size only, so forwards of the same weights and maps are bit-identical:
+in one process, across a change of grid size and back, from a checkpoint
+file, and in another process (the C++ class's test binary)."""
 from __future__ import annotations
 
 import os
@@ -20,7 +26,8 @@ from oracle import refiner as oref
 from tests import refiner_pins as pins
 
 pytestmark = pytest.mark.gpu
-TOL = 1e-4
+TOL_RESULT = 5e-6   # the returned map against the float64 restatement
+TOL_COARSE = 1e-4   # each iteration's /8 normals against the float64 restatement
 
 
 def say(msg: str) -> None:
@@ -52,15 +59,17 @@ def test_native_matches_oracle(cuda, H, W, fov, seed):
     for it, (wp, _) in enumerate(want):
         ep = float(np.abs(coarse[it].astype(np.float64) - wp).max())
         say(f"    iteration {it}: propagate max-abs {ep:.3e}")
-        assert ep <= TOL
+        assert ep <= TOL_COARSE
     eu = float(np.abs(out.cpu().numpy()[0].astype(np.float64) - want[-1][1]).max())
     say(f"    result max-abs {eu:.3e}")
-    assert eu <= TOL
+    assert eu <= TOL_RESULT
     assert out.shape == (1, 3, 8 * H, 8 * W)
 
 
 def test_native_matches_python_driver(cuda):
-    """The C++ loop and the Python loop on the same weights and maps."""
+    """The C++ loop and the Python loop on the same weights and maps (fp32
+    convolutions of two algorithms: their results, each within a few 1e-6 of
+    the float64 restatement, within 1e-5 of each other)."""
     import torch
     H, W = 32, 40
     say(f"[gpu] native refiner vs Python driver {H}x{W}")
@@ -74,13 +83,13 @@ def test_native_matches_python_driver(cuda):
     ep = max(float((coarse[i] - trace[i][0].reshape(3, H, W)).abs().max()) for i in range(rf.N_ITER))
     eu = float((nat - py).abs().max())
     say(f"    propagate max-abs {ep:.3e}  result max-abs {eu:.3e}")
-    assert ep <= TOL and eu <= TOL
+    assert ep <= TOL_COARSE and eu <= 1e-5
 
 
 def test_native_crop_and_grid_change(cuda):
     """The crop (src/dsine_refine.cpp:289-293) is the slice of the whole map,
     and a refiner re-planned for another grid size gives what a fresh one
-    gives (to 1e-5: a re-plan may pick another convolution algorithm)."""
+    gives, bit for bit."""
     import torch
     weights = rf.random_weights(5)
     model = rf.NativeRefiner(weights)
@@ -101,8 +110,8 @@ def test_native_crop_and_grid_change(cuda):
     again = model.forward(dec, intr, 8 * H, 8 * W)
     fresh = rf.NativeRefiner(weights).forward(dec2, intr2, 72, 112)
     torch.cuda.synchronize()
-    assert float((again - full).abs().max()) <= 1e-5
-    assert float((other - fresh).abs().max()) <= 1e-5
+    assert torch.equal(again, full)
+    assert torch.equal(other, fresh)
 
 
 def test_native_pin_constant_heads(cuda):
@@ -145,8 +154,8 @@ def test_native_pin_onehot_upsample(cuda, n0):
 @pytest.mark.parametrize("dtype", ["F32", "F16"])
 def test_native_load_file(cuda, tmp_path, dtype):
     """Weights read from a safetensors file give the forward of the same
-    weights set from memory (F16 files: the F16-rounded weights), to 1e-5
-    (two refiners may pick different convolution algorithms)."""
+    weights set from memory (F16 files: the F16-rounded weights), bit for
+    bit."""
     import torch
     from safetensors.numpy import save_file
     say(f"[gpu] native refiner load_file {dtype}")
@@ -162,13 +171,14 @@ def test_native_load_file(cuda, tmp_path, dtype):
     b = rf.NativeRefiner({k: v.astype(np.float32) for k, v in weights.items()}).forward(
         dec, intr, 8 * H, 8 * W)
     torch.cuda.synchronize()
-    assert float((a - b).abs().max()) <= 1e-5
+    assert torch.equal(a, b)
 
 
 def test_cpp_refiner_on_device(cuda, tmp_path):
     """brovisionml::dsine::Refiner (tests/cpp/test_dsine_refine.cpp, run on
-    brotensor's CUDA tag) against the native refiner's device forward in
-    this process, and its host path against its device path."""
+    brotensor's CUDA tag, in its own process) against the native refiner's
+    device forward in this process, bit for bit, and its host path against
+    its device path."""
     import torch
     from tests.test_refiner_native_host import _cpu_dec, cpp_case, run_cpp_refine
     wpath, cpath, weights, maps, intr, crop = cpp_case(tmp_path)
@@ -186,4 +196,5 @@ def test_cpp_refiner_on_device(cuda, tmp_path):
     e_cpp = float(np.abs(got - dev).max())
     e_host = float(np.abs(host.numpy() - dev).max())
     say(f"    C++ class vs device forward max-abs {e_cpp:.3e}; host vs device {e_host:.3e}")
-    assert e_cpp <= 1e-5 and e_host <= TOL
+    assert np.array_equal(got, dev), e_cpp
+    assert e_host <= 1e-5

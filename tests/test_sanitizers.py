@@ -67,7 +67,7 @@ def sanitized_refine_exe(sanitized_exe):
               "-I", INCLUDE, "-c", src, "-o", obj])
         objs.append(obj)
     exe = os.path.join(OUT, "test_dsine_refine_san")
-    _run(["g++", *SAN, "-pthread", *objs, "-L", "/opt/rocm/lib", "-lMIOpen", "-lamdhip64",
+    _run(["g++", *SAN, "-pthread", *objs, "-L", "/opt/rocm/lib", "-lamdhip64",
           "-Wl,-rpath,/opt/rocm/lib", "-o", exe])
     return exe
 
