@@ -10,11 +10,19 @@ together exceed 512 MB, so the 256 MB Infinity Cache cannot serve them; the
 timed replay starts after a 512 MB flush.  The warm figure (one set, read by
 every step) is measured after the cold ones, on a set of its own.
 
-The K timed steps are the K kernel launches of one captured HIP graph,
-replayed once between two HIP events on the replay stream: the kernels run
-back to back, so the region measures the GPU, not Python's launch overhead.
-Per-launch durations come from a second, eager pass over the same rotation
-with an event pair around every launch (median and max reported).
+The K timed steps of the propagate are K calls of its C ABI enqueued back to
+back from C++ (tests/hw/probe.hip, bvml_probe_angmf_loop), as a C++ caller
+such as the refiner issues them: a short bounded spin kernel holds the stream
+while the host enqueues the K calls, and two HIP events on that stream, one
+right after the spin and one after the last call, bracket exactly the K
+launches on the GPU.  The same K launches captured in one HIP graph and
+replayed between two events are reported beside it ("graph"): a replay
+carries a fixed cost of its own (about 9 us on the GPU at 256 x 256, so
+0.45 us per launch at K = 20), and the first replay timed in a process read
+about 20% slow, with a host-side gap inside its events.  The upsample and
+the refiner forward are timed as graph replays.  Per-launch durations come
+from an eager pass over the same rotation with an event pair around every
+launch (median and max reported).
 
 Prints one JSON line (rank 0):
   value         Mpixel/s over the timed region (K steps / event time)
@@ -51,6 +59,14 @@ HBM_PEAK_GBPS = 8000.0
 FLUSH_BYTES = 512 << 20
 # Back-to-back work before each timed region, to bring the clocks up (Timer.ramp).
 RAMP_SECONDS = 0.3
+# The ramp before the process's first timed region (Timer.timed_graph): on a
+# box that has just been idle, the first timed regions ran about 20% slower
+# than every later one after a 0.3 s ramp (a 256 x 256 call: 10.5 and 10.1 us
+# per launch in the first two regions of a process, 8.7-8.9 in the next
+# sixteen, each after its own ramp of graph replays), and 2 s of Python-launched
+# work before the first ramp did not change that (10.4 us): the GPU needs
+# longer at full load the first time.
+SETTLE_SECONDS = 2.0
 
 
 def cpu_model() -> str:
@@ -129,12 +145,17 @@ class Timer:
     footprint."""
 
     ramp_seconds = RAMP_SECONDS
+    settled = False  # whether this process has run its SETTLE_SECONDS ramp
 
     def __init__(self, dev, launch, nsets: int, steps: int, warmup: int, bytes_per_call: int,
-                 warm_index: int | None = None):
+                 warm_index: int | None = None, loop=None):
         import torch
         self.torch, self.dev = torch, dev
         self.launch, self.nsets, self.steps = launch, nsets, steps
+        # loop(indices) -> seconds: the launches of those sets enqueued back
+        # to back from C++ and timed on the GPU (angmf_loop); None: time
+        # graph replays
+        self.loop = loop
         self.bytes_per_call = bytes_per_call
         self.warm_index = warm_index
         self._flush_buf = torch.ones(FLUSH_BYTES // 4, dtype=torch.float32, device=dev)
@@ -162,19 +183,20 @@ class Timer:
                 self.launch(i)
         return g
 
-    def ramp(self, work) -> None:
-        """Run `work` back to back for ramp_seconds: the GPU lowers its clocks
+    def ramp(self, work, seconds: float | None = None) -> None:
+        """Run `work` back to back for ramp_seconds (or `seconds`): the GPU lowers its clocks
         when idle (input generation on the host leaves it idle for seconds)
         and takes tens of milliseconds of load to raise them again, so a
         timed replay straight after idle time measures the clock ramp, not
         the kernel (4 x 512 x 512, k = 7: 184 us per launch right after 5 s of
         idle, 152 us at steady clocks)."""
         torch = self.torch
+        limit = self.ramp_seconds if seconds is None else seconds
         t0 = time.perf_counter()
         while True:
             work()
             torch.cuda.synchronize()
-            if time.perf_counter() - t0 >= self.ramp_seconds:
+            if time.perf_counter() - t0 >= limit:
                 return
 
     def timed_graph(self, g, flush: bool):
@@ -182,7 +204,8 @@ class Timer:
         stream = torch.cuda.current_stream(self.dev)
         e0 = torch.cuda.Event(enable_timing=True)
         e1 = torch.cuda.Event(enable_timing=True)
-        self.ramp(g.replay)
+        self.ramp(g.replay, None if Timer.settled else SETTLE_SECONDS)
+        Timer.settled = True
         if flush:
             self.flush()
         self.mark()
@@ -193,9 +216,31 @@ class Timer:
         torch.cuda.synchronize()
         return e0.elapsed_time(e1) * 1e-3
 
+    def timed_loop(self, idx, flush: bool) -> float:
+        """Seconds for the launches of sets idx enqueued from C++ (self.loop),
+        after the ramp (the same loop back to back) and, if asked, a flush."""
+        torch = self.torch
+        self.ramp(lambda: self.loop(idx), None if Timer.settled else SETTLE_SECONDS)
+        Timer.settled = True
+        if flush:
+            self.flush()
+        self.mark()
+        torch.cuda.synchronize()
+        t = self.loop(idx)
+        torch.cuda.synchronize()
+        return t
+
     def cold(self) -> float:
-        """Seconds for self.steps launches rotating over the sets, the replay
-        starting after a flush."""
+        """Seconds for self.steps launches rotating over the sets, starting
+        after a flush: the C++ loop where the Timer has one, else one graph
+        replay."""
+        idx = [i % self.nsets for i in range(self.steps)]
+        if self.loop is not None:
+            return self.timed_loop(idx, flush=True)
+        return self.cold_graph()
+
+    def cold_graph(self) -> float:
+        """cold() as one replay of a graph of the launches."""
         g = self.capture([i % self.nsets for i in range(self.steps)])
         g.replay()
         return self.timed_graph(g, flush=True)
@@ -203,6 +248,8 @@ class Timer:
     def warm(self) -> float:
         """Seconds for self.steps launches of one set (Infinity Cache warm)."""
         w = self.warm_index if self.warm_index is not None else 0
+        if self.loop is not None:
+            return self.timed_loop([w] * self.steps, flush=False)
         g = self.capture([w] * self.steps)
         g.replay()
         return self.timed_graph(g, flush=False)
@@ -408,6 +455,40 @@ def angmf_launcher(sets: AngmfSets, dev, flags: int, ray_from_intrinsics: bool, 
     return launch
 
 
+def angmf_loop_timer(sets: AngmfSets, dev, flags: int, ray_from_intrinsics: bool, calls: int):
+    """loop(indices) -> seconds: the calls of those sets (a chain of `calls`
+    per set, each output feeding the next) enqueued back to back from C++
+    through the C ABI's function pointer (tests/hw/probe.hip), timed by HIP
+    events on the current stream right after a bounded spin that holds the
+    stream while they are enqueued."""
+    import ctypes
+    import torch
+    from brovisionml_amd import _lib
+    from tests.hw import probe
+    w = sets.w
+    fn = ctypes.cast(_lib.load().bvml_dsine_angmf_propagate_f32, ctypes.c_void_p).value
+    if calls > 1 and not hasattr(sets, "outs2"):
+        sets.outs2 = [torch.empty_like(o) for o in sets.outs]
+
+    def rows(i):
+        s = sets.sets[i]
+        pn, out = s["pred_norm"].data_ptr(), []
+        for c in range(calls):
+            dst = (sets.outs[i] if c % 2 == 0 else sets.outs2[i]).data_ptr()
+            out.append([pn, s["prob"].data_ptr(), s["xy"].data_ptr(), s["angle"].data_ptr(),
+                        0 if ray_from_intrinsics else s["ray"].data_ptr(), dst])
+            pn = dst
+        return out
+
+    def loop(idx) -> float:
+        ptrs = [r for i in idx for r in rows(i)]
+        # the spin covers the host's enqueueing: about 5 us per call, doubled
+        spin_us = min(1e5, 10.0 * len(ptrs) + 100.0)
+        return probe.angmf_loop(fn, ptrs, sets.intr, w.B, w.H, w.W, w.k, flags, spin_us,
+                                torch.cuda.current_stream(dev).cuda_stream)
+    return loop
+
+
 def recompute_counts(sets: AngmfSets, flags: int, nthreads: int):
     """Per set: pixels below the fast path's cancellation threshold, from
     the oracle's double sums (|acc|^2 / sum (prob/|p|)^2)."""
@@ -464,10 +545,14 @@ def measure_angmf(args, dev, w, steps, warmup, flags=0, ray_from_intrinsics=Fals
     nsets = args.sets or nsets_for(bytes_per_call * w.calls)
     sets = AngmfSets(w, nsets, dev, logits=logits)
     launch = angmf_launcher(sets, dev, flags, ray_from_intrinsics, w.calls)
-    tm = Timer(dev, launch, nsets, steps, warmup, bytes_per_call, warm_index=sets.warm_index)
+    loop = angmf_loop_timer(sets, dev, flags, ray_from_intrinsics, w.calls)
+    tm = Timer(dev, launch, nsets, steps, warmup, bytes_per_call, warm_index=sets.warm_index,
+               loop=loop)
     t_cold = tm.cold()
     res = {"sets": sets, "timer": tm, "bytes_per_call": bytes_per_call, "nsets": nsets,
            "launch_s": t_cold / (steps * w.calls), "t_cold": t_cold}
+    if with_eager:
+        res["t_cold_graph"] = tm.cold_graph()
     if with_eager:
         t_eager, per = tm.eager()
         res["t_eager"], res["per_launch_us"] = t_eager, per
@@ -507,7 +592,9 @@ def bench_angmf(args, dev) -> dict:
             "prob_angle": "logits, activated in the kernel" if args.logits else "activated",
             "inputs": f"{nsets} independent seeded draws, rotating "
                       f"({nsets * bytes_per_call * w.calls / 1e6:.0f} MB > 256 MB Infinity "
-                      "Cache); timed replay after a 512 MB flush",
+                      "Cache); timed after a 512 MB flush",
+            "timing": "K calls enqueued back to back from C++ behind a spin that holds the "
+                      "stream; HIP events around the K launches on the GPU",
         })
     line["roofline"] = roofline(
         bytes_per_call, m["launch_s"],
@@ -531,6 +618,12 @@ def bench_angmf(args, dev) -> dict:
         "us_per_step": round(m["t_eager"] / args.steps * 1e6, 3),
         "note": "the same steps launched one by one from Python with per-launch events",
     }
+    line["graph"] = {
+        "value": round(px / m["t_cold_graph"] / 1e6, 2),
+        "us_per_step": round(m["t_cold_graph"] / args.steps * 1e6, 3),
+        "note": "the same K launches captured in one HIP graph, one replay between two events "
+                "after a flush (a replay carries a fixed cost of its own)",
+    }
     line["gpu"] = torch.cuda.get_device_name(dev)
     nt = host_share()
     t_ratio, counts = recompute_counts(sets, flags, nt)
@@ -549,7 +642,8 @@ def bench_angmf(args, dev) -> dict:
         fl = flags | _lib.FP64
         launch64 = angmf_launcher(sets, dev, fl, False, w.calls)
         k64 = max(4, args.steps // 4)
-        t64 = Timer(dev, launch64, nsets, k64, 1, bytes_per_call, warm_index=sets.warm_index)
+        t64 = Timer(dev, launch64, nsets, k64, 1, bytes_per_call, warm_index=sets.warm_index,
+                    loop=angmf_loop_timer(sets, dev, fl, False, w.calls))
         t = t64.cold()
         line["fp64"] = {
             "kernel": f"angmf_f64_kernel<{k}>",
@@ -612,7 +706,39 @@ def bench_angmf(args, dev) -> dict:
     if args.configs and not (args.logits or args.ray_from_intrinsics):
         line["configs"] = bench_configs(args, dev, [i for i in (0, 1, 2, 3, 4)
                                                     if i != args.workload])
+        # the propagate as the refiner runs it: on the heads' raw logits
+        # (BVML_DSINE_LOGITS), whose planes the heads pass has just written
+        # (warm), and cold for comparison
+        ml = measure_angmf(args, dev, w, args.steps, args.warmup, flags | _lib.LOGITS,
+                           logits=True, with_ceilings=False, with_eager=False)
+        line["logits"] = {
+            "kernel": angmf_kernel_name(w, flags | _lib.LOGITS),
+            "warm_us_per_call": round(ml["t_warm"] / (args.steps * w.calls) * 1e6, 3),
+            "cold_us_per_call": round(ml["launch_s"] * 1e6, 3),
+            "bytes_per_call": ml["bytes_per_call"],
+            "note": "prob and angle as the heads' raw logits, the activations applied in the "
+                    "kernel; warm: one set read by every launch, as the refiner's propagate "
+                    "reads what its heads pass has just written",
+        }
+        del ml
+        torch.cuda.empty_cache()
+        # the refiner's next steps on the same line: the fused convex
+        # upsample x8 + normalise, and the whole native refiner forward
+        sub = argparse.Namespace(**vars(args))
+        sub.workload, sub.sets, sub.precise, sub.calib = 0, 0, False, False
+        sub.cpu_seconds = args.cpu_seconds / 2
+        line["upsample"] = sub_line(bench_upsample(sub, dev))
+        sub.workload, sub.driver = None, "native"
+        line["refiner"] = sub_line(bench_refiner(sub, dev))
     return line
+
+
+def sub_line(line: dict) -> dict:
+    """Another op's bench line as a sub-object of the default line: the
+    run-wide keys dropped."""
+    run_keys = ("n_gpus", "steps", "warmup", "higher_is_better", "scaling", "vs_baseline",
+                "dtype", "data")
+    return {k: v for k, v in line.items() if k not in run_keys}
 
 
 def bench_configs(args, dev, indices) -> dict:
@@ -638,7 +764,7 @@ def bench_configs(args, dev, indices) -> dict:
             "bytes_per_call": bpc,
             "traffic": traffic_from_profile("angmf", w.name),
             "inputs": f"{nsets} independent draws ({nsets * bpc * w.calls / 1e6:.0f} MB), "
-                      "timed after a 512 MB flush",
+                      "timed after a 512 MB flush; K calls enqueued from C++",
         }
         if w.calls > 1:
             entry["note"] = f"{w.calls} chained calls per step (each output feeds the next call)"
@@ -876,11 +1002,12 @@ def bench_refiner(args, dev) -> dict:
     """The whole NRN refiner forward at a 256x256 grid (a 2048x2048 image),
     synthetic weights and decoder outputs, one forward per step, `steps`
     forwards captured in one graph: the native refiner
-    (libbvml_dsine_refine.so: the loop in C++, ConvGRU + heads on MIOpen,
-    the package's propagate with fused activations and its upsample +
-    normalise; the line's value) and the Python driver
-    (brovisionml_amd/refiner.py, the same kernels and convolutions, with the
-    up-mask head and upsample in every iteration) beside it.  The CPU leg is
+    (libbvml_dsine_refine.so: the loop in C++, every convolution on the
+    package's fp32 matrix-core kernels, the propagate with fused activations
+    and the upsample + normalise; the line's value) and the Python driver
+    (brovisionml_amd/refiner.py: torch's im2col + GEMM convolutions, the
+    package's other kernels, with the up-mask head and upsample in every
+    iteration) beside it.  The CPU leg is
     the restatement in oracle/refiner.py (float64 convolutions, the C
     oracle's ops) on a 24x32 grid."""
     import torch
@@ -933,7 +1060,8 @@ def bench_refiner(args, dev) -> dict:
                      t * 1e3 / args.steps,
                      {"workload": f"dsine-refiner-{H}x{W}", "H": H, "W": W, "iterations": 5,
                       "weights": "synthetic (uniform +-1/sqrt(fan_in))",
-                      "driver": driver, "convolutions": "5x5: implicit-GEMM fp32 MFMA kernels; 3x3: MIOpen immediate mode, fp32"})
+                      "driver": driver,
+                      "convolutions": "5x5 and 3x3: implicit-GEMM fp32 MFMA kernels"})
     if t_py is not None:
         line["python_driver"] = {"ms_per_step": round(t_py * 1e3 / args.steps, 4),
                                  "value": round(opx / t_py / 1e6, 2)}

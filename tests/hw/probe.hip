@@ -5,9 +5,15 @@
 //     range: the error bounds the kernels' budgets assume
 //     (tests/test_gpu_hw_bounds.py);
 //   * a streaming read of a buffer, the same-box read ceiling bench.py
-//     reports beside the kernels' bandwidth.
+//     reports beside the kernels' bandwidth;
+//   * a launch loop: K calls of a C-ABI entry point (bvml_dsine_angmf_propagate_f32,
+//     reached through the function pointer the caller passes) enqueued back
+//     to back from C++ between two events, behind a short bounded spin
+//     kernel that holds the stream while the host enqueues them, so the
+//     events time the K launches on the GPU, not the host's enqueueing.
 // Every kernel writes one result per workgroup (the read: per wave), into
-// arrays the host sizes to the grid, with vector stores.
+// arrays the host sizes to the grid, with vector stores (the spin kernel
+// writes nothing).
 
 #include <hip/hip_runtime.h>
 
@@ -101,6 +107,17 @@ __global__ __launch_bounds__(kBlock) void stream_read(const f4v* p, size_t n4, c
     if ((threadIdx.x & 63) == 0) out[(size_t)blockIdx.x * (kBlock / 64) + (threadIdx.x >> 6)] = acc;
 }
 
+// One wave that waits until `ticks` of the 100 MHz real-time counter have
+// passed since it started (bounded: the host caps ticks), then exits.
+__global__ __launch_bounds__(64) void spin(uint64_t ticks) {
+    const uint64_t t0 = __builtin_amdgcn_s_memrealtime();
+    while (__builtin_amdgcn_s_memrealtime() - t0 < ticks) __builtin_amdgcn_s_sleep(8);
+}
+
+typedef int (*angmf_fn)(const float*, const float*, const float*, const float*, const float*,
+                        double, double, double, double, int, int, int, int, long long, float*,
+                        unsigned, void*);
+
 size_t read_grid(size_t n4, int u) { return (n4 + (size_t)kBlock * u - 1) / ((size_t)kBlock * u); }
 
 uint32_t bits_of(float f) {
@@ -178,6 +195,44 @@ int bvml_probe_stream_read(const float* p, size_t n, int u, float* out, size_t o
         default: return -1;
     }
     return (int)hipGetLastError();
+}
+
+// K calls of `fn` (an angmf_propagate_f32 entry point), call i on the six
+// device pointers ptrs[6 i .. 6 i + 5] (pred_norm, prob, xy, angle, ray, out),
+// enqueued back to back on `stream` after a spin of spin_us microseconds
+// (at most 100 ms), with events right after the spin and after the last
+// call: *ms = the events' elapsed time.  Returns 0, the first non-zero
+// status of fn, or a hipError_t.
+int bvml_probe_angmf_loop(void* fn, const unsigned long long* ptrs, int K, double fu, double cu,
+                          double fv, double cv, int B, int H, int W, int k, unsigned flags,
+                          double spin_us, void* stream, float* ms) {
+    if (!fn || !ptrs || K < 1 || !ms || !(spin_us >= 0.0) || spin_us > 1e5) return -1;
+    const angmf_fn call = reinterpret_cast<angmf_fn>(fn);
+    const hipStream_t st = static_cast<hipStream_t>(stream);
+    hipEvent_t e0 = nullptr, e1 = nullptr;
+    hipError_t e = hipEventCreate(&e0);
+    if (e == hipSuccess) e = hipEventCreate(&e1);
+    int status = (int)e;
+    if (e == hipSuccess) {
+        hipLaunchKernelGGL(spin, dim3(1), dim3(64), 0, st, (uint64_t)(spin_us * 100.0));
+        e = hipGetLastError();
+        if (e == hipSuccess) e = hipEventRecord(e0, st);
+        status = (int)e;
+        for (int i = 0; i < K && status == 0; ++i) {
+            const unsigned long long* p = ptrs + 6 * (size_t)i;
+            status = call(reinterpret_cast<const float*>(p[0]), reinterpret_cast<const float*>(p[1]),
+                          reinterpret_cast<const float*>(p[2]), reinterpret_cast<const float*>(p[3]),
+                          reinterpret_cast<const float*>(p[4]), fu, cu, fv, cv, B, H, W, k, 0,
+                          reinterpret_cast<float*>(p[5]), flags, stream);
+        }
+        if (status == 0 && (e = hipEventRecord(e1, st)) != hipSuccess) status = (int)e;
+        if (status == 0 && (e = hipEventSynchronize(e1)) != hipSuccess) status = (int)e;
+        if (status == 0 && (e = hipEventElapsedTime(ms, e0, e1)) != hipSuccess) status = (int)e;
+        if (status != 0) (void)hipStreamSynchronize(st);
+    }
+    if (e0) (void)hipEventDestroy(e0);
+    if (e1) (void)hipEventDestroy(e1);
+    return status;
 }
 
 // The number of partials bvml_probe_stream_read writes for n floats.

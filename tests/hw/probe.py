@@ -27,6 +27,10 @@ def load() -> ctypes.CDLL:
         lib.bvml_probe_stream_read.restype = i
         lib.bvml_probe_read_partials.argtypes = [sz, i]
         lib.bvml_probe_read_partials.restype = sz
+        lib.bvml_probe_angmf_loop.argtypes = [vp, ctypes.POINTER(ctypes.c_ulonglong), i, d, d, d, d,
+                                              i, i, i, i, ctypes.c_uint, d, vp,
+                                              ctypes.POINTER(f)]
+        lib.bvml_probe_angmf_loop.restype = i
         _lib = lib
     return _lib
 
@@ -53,3 +57,20 @@ def stream_read(ptr: int, n: int, unroll: int, out_ptr: int, out_len: int,
 
 def read_partials(n: int, unroll: int) -> int:
     return load().bvml_probe_read_partials(n, unroll)
+
+
+def angmf_loop(fn_ptr: int, ptrs, intr, B: int, H: int, W: int, k: int, flags: int,
+               spin_us: float, stream: int = 0) -> float:
+    """Seconds for len(ptrs) calls of the angmf_propagate_f32 entry point at
+    fn_ptr enqueued back to back from C++ (call i on the six pointers
+    ptrs[i]: pred_norm, prob, xy, angle, ray, out), timed by events after a
+    spin of spin_us microseconds that holds the stream while they are
+    enqueued."""
+    flat = (ctypes.c_ulonglong * (6 * len(ptrs)))(*[int(p) for row in ptrs for p in row])
+    ms = ctypes.c_float()
+    fu, cu, fv, cv = intr
+    st = load().bvml_probe_angmf_loop(fn_ptr, flat, len(ptrs), fu, cu, fv, cv, B, H, W, k, flags,
+                                      spin_us, stream, ctypes.byref(ms))
+    if st != 0:
+        raise RuntimeError(f"bvml_probe_angmf_loop failed: {st}")
+    return ms.value * 1e-3
