@@ -173,6 +173,7 @@ struct AngmfArgs {
     // G waves per group (one run of the window's neighbours each) -> 64*M*G
     // threads.
     int G, TW, TH, M, tiles_x, tiles_per_img;
+    int range;            // range tiles: 64 M consecutive pixels (TW = W; TH the rows they span)
     double ifu64, ifv64;  // 1/fu, 1/fv
     double tu_c, tv_c;    // (0.5 - cu)/fu, (0.5 - cv)/fv: source ray tu0 = sx/fu + tu_c
     double dd_min;        // tier 1: |dd| below this sends a pixel to the recompute
@@ -239,9 +240,14 @@ __global__ __launch_bounds__(256) void angmf_f64_kernel(AngmfArgs a) {
 // fp32 fast kernel
 // ---------------------------------------------------------------------------
 
-// Workgroups go to the 8 XCDs round-robin (blockIdx % 8).  Give each XCD a
-// contiguous run of logical tiles so tiles that share halo rows and columns
-// share that XCD's L2.
+// Workgroups go to the 8 XCDs round-robin by their linear index (x fastest).
+// Give each XCD a contiguous run of an image's logical tiles so tiles that
+// share halo rows and columns share that XCD's L2.  (A launch of several
+// samples is remapped per image, along x only.  Remapping its linear index
+// instead, so that each XCD takes whole images, cut 32 x 60 x 80's traffic
+// from 1.067x to 1.047x the algorithmic bytes but ran slower, cold and warm:
+// 18.2-19.1 against 17.5-18.3 us, 15.3-15.8 against 14.1-14.2 warm, and
+// 4 x 512 x 512 at k = 7 161 against 156-157 us.)
 __device__ __forceinline__ int xcd_remap(int bid, int nb) {
     const int q = nb >> 3, r = nb & 7;
     const int xcd = bid & 7, i = bid >> 3;
@@ -609,7 +615,11 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     // loop fully unrolled), or a ring of LA slots (G = 1, rolled loop)
     constexpr int SL = (G == 1) ? LA : NR;
     extern __shared__ float4 smem[];
-    const int TW = (int)(tile & 0x7ffu), TH = (int)((tile >> 11) & 0x7ffu);
+    // a tile width of 0 marks a range tile: 64 M consecutive pixels of the
+    // row-major image, its halo the full-width rows they span (TH of them at
+    // most) and P more on each side
+    const bool range = (tile & 0x7ffu) == 0u;
+    const int TW = range ? W : (int)(tile & 0x7ffu), TH = (int)((tile >> 11) & 0x7ffu);
     const int M = (int)((tile >> 22) & 0x1fu), LX = (int)(tile >> 27);
     const int npx = 64 * M;
     const int nrow = TH + 2 * P;
@@ -622,9 +632,31 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
 
     const int b = blockIdx.y;
     const int lb = xcd_remap(blockIdx.x, tiles_per_img);
-    const int tyi = magic_div(lb, tx_magic, LX);
-    const int ty0 = tyi * TH;
-    const int tx0 = (lb - tyi * tiles_x) * TW;
+    // the tile's first row and column, and (range tiles) its first pixel;
+    // tx_magic and LX divide by tiles_x (rectangular tiles) or W (ranges)
+    int ty0, tx0, p0 = 0;
+    if (range) {
+        p0 = lb * npx;
+        ty0 = magic_div(p0, tx_magic, LX);
+        tx0 = 0;
+    } else {
+        const int tyi = magic_div(lb, tx_magic, LX);
+        ty0 = tyi * TH;
+        tx0 = (lb - tyi * tiles_x) * TW;
+    }
+    const float rtw = __builtin_amdgcn_rcpf((float)TW);
+    // image row and column of the tile's pixel jj (0 <= jj < 64 M)
+    auto tile_px = [&](int jj, int& yy, int& xx) {
+        if (range) {
+            const int pp = p0 + jj;
+            yy = magic_div(pp, tx_magic, LX);
+            xx = pp - yy * W;
+        } else {
+            const int t = small_div(jj, rtw);
+            yy = ty0 + t;
+            xx = tx0 + (jj - t * TW);
+        }
+    };
     const long long HW = (long long)H * W;
     const uint32_t HW4 = (uint32_t)HW * 4u;  // plane bytes; max(NR, 3) * HW4 < 2^32
 
@@ -636,9 +668,9 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     const int n0 = role * RUN + (role < REM ? role : REM);  // first neighbour of the run
     const int nrun = RUN + (role < REM ? 1 : 0);
     const int j = gi * 64 + lane;
-    const float rtw = __builtin_amdgcn_rcpf((float)TW);
-    const int ty = small_div(j, rtw), tx = j - ty * TW;
-    const int y = ty0 + ty, x = tx0 + tx;
+    int y, x;
+    tile_px(j, y, x);
+    const int ty = y - ty0, tx = x - tx0;
     const bool valid = (ty < TH) && (y < H) && (x < W);
     const uint32_t pb = valid ? (uint32_t)(y * W + x) * 4u : 0u;
 
@@ -733,9 +765,10 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
         // each tile pixel's ray, once (pixels past the image: clamped ones)
         if ((int)threadIdx.x < npx) {
             const int t = threadIdx.x;
-            const int rty = small_div(t, rtw), rtx = t - rty * TW;
-            const bvml::Ray3f r3 = synth_ray(min(tx0 + rtx, W - 1), min(ty0 + rty, H - 1), a.fu, a.cu,
-                                        a.fv, a.cv);
+            int ry, rx;
+            tile_px(t, ry, rx);
+            const bvml::Ray3f r3 = synth_ray(min(rx, W - 1), min(ry, H - 1), a.fu, a.cu, a.fv,
+                                             a.cv);
             rayl[t] = make_float4(r3.x, r3.y, r3.z, 0.0f);
         }
     }
@@ -915,8 +948,6 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     constexpr int PPP = 64 / LP;
     const int slot = lane / LP, il = lane - slot * LP;
     const bool lead = il == LP - 1;  // the lane slot_sum leaves a slot's sums in
-    int tw = TW;
-    asm volatile("" : "+s"(tw));
     const float* pn = pred_norm + (size_t)b * 3 * HW;
     const float* pr = prob + (size_t)b * K2 * HW;
     const float* xyp = xy + (size_t)b * 2 * K2 * HW;
@@ -933,8 +964,8 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
         }
         const bool act = src >= 0;
         const int jj = gi * 64 + (act ? src : 0);
-        const int fty = jj / tw, ftx = jj - fty * tw;
-        const int fy = ty0 + fty, fx = tx0 + ftx;
+        int fy, fx;
+        tile_px(jj, fy, fx);
         const uint32_t fb = (uint32_t)(fy * W + fx) * 4u;
         // one tier over this lane's neighbours of its pixel; returns false
         // (tier 2) when a neighbour is outside the reduced form's domain
@@ -1132,14 +1163,16 @@ auto angmf_f32_for(bool synth_ray, bool logits) {
 }
 
 // Candidate G values per window size, in order of preference (the first
-// wins ties in lane utilisation).  Runs longer than lookahead(K, G)
-// neighbours keep only that many of them in flight.
-//   K = 5: 4 (runs of 6-7) on wide images; 2 (runs of 12-13) gives narrow
-//          images (W = 60, 80) full-width tiles of 3-4 rows with few idle lanes
-//   K = 7, 9: 4 (runs of 12-13 / 20-21; 64 x 2 tiles halve the halo per pixel
-//          against 8 waves of runs of 6-7 on 64 x 1 tiles)
+// wins ties in lane utilisation, except between range tiles).  Runs longer
+// than lookahead(K, G) neighbours keep only that many of them in flight.
+//   K = 5: 4 (runs of 6-7) on wide images; 2 (runs of 12-13) on large narrow
+//          launches (range tiles of 256 pixels)
+//   K = 7: 4 (runs of 12-13; 64 x 2 tiles halve the halo per pixel against 8
+//          waves of runs of 6-7 on 64 x 1 tiles)
+//   K = 9: 8 (a 64 x 2 tile's halo does not fit 4 waves' LDS share, and
+//          narrow images take range tiles, where 8 wins)
 constexpr int kGChoices[10][2] = {{0, 0}, {1, 1}, {0, 0}, {2, 2}, {0, 0},
-                                  {4, 2}, {0, 0}, {4, 8}, {0, 0}, {4, 8}};
+                                  {4, 2}, {0, 0}, {4, 8}, {0, 0}, {8, 8}};
 
 // A G with more waves per group for launches that leave CUs idle (fewer
 // workgroups than CUs with the first choice): the shorter runs shorten each
@@ -1177,8 +1210,8 @@ constexpr double kStreamBytes = 256.0 * (1 << 20);
 
 // LDS one workgroup may use: 64 KB for the run-split kernels (G > 1), so
 // that two to three of them share a CU; the whole-window kernel's 64 x 8
-// tiles take up to 80 KB, two per CU (gfx950 has 160 KB per CU and allows it
-// all to one workgroup).
+// tiles and the range tiles of narrow images take up to 80 KB, two per CU
+// (gfx950 has 160 KB per CU and allows it all to one workgroup).
 constexpr int kMaxLdsBytes = 65536;
 constexpr int kMaxLdsBytesG1 = 81920;
 
@@ -1226,7 +1259,7 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
     unsigned mag;
     int L;
     div_magic(a.tiles_x, mag, L);
-    const unsigned tile = pack_tile(a.TW, a.TH, a.M, L);
+    const unsigned tile = pack_tile(a.range ? 0 : a.TW, a.TH, a.M, L);
     constexpr int G0 = kGChoices[K][0], G1 = kGChoices[K][1];
     auto kern = (a.G == G0) ? angmf_f32_for<K, G0>(a.synth_ray != 0, a.logits != 0)
                             : angmf_f32_for<K, G1>(a.synth_ray != 0, a.logits != 0);
@@ -1264,25 +1297,68 @@ hipError_t launch_angmf(AngmfArgs a, bool fp64, hipStream_t s) {
 }
 
 // Whether a TW x TH tile of M groups of G waves fits the kernel: its LDS, and
-// at most two halo records per thread.
-bool tile_fits(int K, int G, int M, int TW, int TH, bool synth_ray) {
-    return lds_units(K, G, M, TW, TH, synth_ray) * 16 <= (G == 1 ? kMaxLdsBytesG1 : kMaxLdsBytes) &&
+// at most two halo records per thread.  Range tiles (narrow images) may take
+// the whole-window tiles' LDS: their halo is full rows.
+bool tile_fits(int K, int G, int M, int TW, int TH, bool synth_ray, bool range = false) {
+    const int lim = (G == 1 || range) ? kMaxLdsBytesG1 : kMaxLdsBytes;
+    return lds_units(K, G, M, TW, TH, synth_ray) * 16 <= lim &&
            halo_count(K, TW, TH) <= 2 * 64 * M * G;
+}
+
+int gcd_int(int a, int b) {
+    while (b != 0) {
+        const int t = a % b;
+        a = b;
+        b = t;
+    }
+    return a;
+}
+
+// Rows spanned by a range tile of npx pixels of a W-wide image, at most: its
+// first pixel is a multiple of npx, so it starts at a column that is a
+// multiple of gcd(npx, W).
+int range_rows(int npx, int W) {
+    const int g = gcd_int(npx, W);
+    return (W - g + npx - 1) / W + 1;
+}
+
+// Tiles per image of a launch plan.
+long long tiles_per_image(const AngmfArgs& c) {
+    if (c.range) return (c.HW + 64LL * c.M - 1) / (64LL * c.M);
+    return (long long)((c.W + c.TW - 1) / c.TW) * ((c.H + c.TH - 1) / c.TH);
 }
 
 // Tile of the fp32 kernel for G waves per group: wide images (and rows longer
 // than a workgroup's 64 * M pixels) take 64 x M tiles (each wave one 256 B row
-// segment per plane); narrow ones full-width tiles of TH rows with the fewest
-// idle lanes among those that fit.  Returns the fraction of lanes that hold a
-// pixel (0 if nothing fits).
+// segment per plane).  Narrow images (W <= 128) whose rows are not a whole
+// number of 64-pixel groups take range tiles: 64 M consecutive pixels of the
+// row-major image, so that every group reads exactly two whole 128 B lines
+// per plane and no line is split between tiles (full-width tiles of whole
+// rows split every other line at W = 80: 1.11x the algorithmic traffic), the
+// largest M that fits.  Other narrow images take full-width tiles of TH rows
+// with the fewest idle lanes among those that fit.  Returns the fraction of
+// lanes that hold a pixel (0 if nothing fits).
 double tile_for(AngmfArgs& a, int K, int G) {
     const int mmax = kWgWaves / G;
     a.G = G;
+    a.range = 0;
     a.TW = 64;
     a.M = mmax;
     while (a.M > 1 && !tile_fits(K, G, a.M, 64, a.M, a.synth_ray != 0)) --a.M;
     a.TH = a.M;
     double best = tile_fits(K, G, a.M, 64, a.M, a.synth_ray != 0) ? 1.0 : 0.0;
+    if (a.W <= 128 && a.W % 64 != 0) {
+        for (int m = mmax; m >= 1; --m) {
+            const int th = range_rows(64 * m, a.W);
+            if (!tile_fits(K, G, m, a.W, th, a.synth_ray != 0, true)) continue;
+            a.range = 1;
+            a.TW = a.W;
+            a.TH = th;
+            a.M = m;
+            const long long tiles = (a.HW + 64LL * m - 1) / (64LL * m);
+            return (double)a.HW / (double)(tiles * 64LL * m);
+        }
+    }
     if (a.W > 128 || a.W > 64 * mmax) return best;
     best = -1.0;
     for (int th = 1; th <= a.H && th <= 64 * mmax; ++th) {
@@ -1308,11 +1384,12 @@ constexpr long long kSmallGrid = 512;
 // pixel, takes G = 1.  Otherwise, of the two run-split candidates, a launch of
 // fewer than kSmallGrid workgroups takes the one with more of them (its runs are
 // shorter, so its waves finish sooner); a larger one the one with the most
-// lanes holding a pixel, the preferred G on ties.
+// lanes holding a pixel, the preferred G on ties, except between range tiles,
+// where the second (fewer, larger workgroups) wins ties: 32 x 60 x 80 at
+// k = 5 ran 18.0-18.3 us with G = 2 (608 workgroups) against 19.2-19.4 with
+// G = 4 (1,216).
 void choose_tile(AngmfArgs& a, int K) {
-    auto wgs = [](const AngmfArgs& c) {
-        return (long long)((c.W + c.TW - 1) / c.TW) * ((c.H + c.TH - 1) / c.TH) * c.B;
-    };
+    auto wgs = [](const AngmfArgs& c) { return tiles_per_image(c) * c.B; };
     if (kWholeWindowOk[K] && (long long)K * K * a.HW * 4 < (1LL << 32)) {
         AngmfArgs one = a;
         const double util = tile_for(one, K, 1);
@@ -1335,7 +1412,7 @@ void choose_tile(AngmfArgs& a, int K) {
                 a = alt;
             else if (w0 < kSmallGrid || w1 < kSmallGrid)
                 a = (w1 > w0) ? alt : a;
-            else if (u1 > u0 + 1e-9)
+            else if (u1 > u0 + 1e-9 || (alt.range && u1 >= u0 - 1e-9))
                 a = alt;
         }
     }
@@ -1379,11 +1456,11 @@ int plan_angmf(AngmfArgs& a, int B, int H, int W, int k, double fu, double cu, d
                              (synth ? 0.0 : (double)HW * 4.0 * 3.0);
         a.stream_planes = (a.G == 1 && bytes > kStreamBytes) ? 1 : 0;
     }
-    if (!tile_fits(k, a.G, a.M, a.TW, a.TH, synth))
+    if (!tile_fits(k, a.G, a.M, a.TW, a.TH, synth, a.range != 0))
         return fail(BVML_DSINE_ESIZE, "angmf_propagate: no tile fits the kernel's LDS");
-    a.tiles_x = (W + a.TW - 1) / a.TW;
-    const long long tiles_y = (H + a.TH - 1) / a.TH;
-    const long long tpi = (long long)a.tiles_x * tiles_y;
+    // (range tiles: the kernel divides pixel indices by W with tiles_x's magic)
+    a.tiles_x = a.range ? W : (W + a.TW - 1) / a.TW;
+    const long long tpi = tiles_per_image(a);
     a.tiles_per_img = (int)(tpi < INT_MAX ? tpi : INT_MAX);
 
     // The fp32 path assumes intrinsics in the range real cameras produce;
@@ -1503,8 +1580,8 @@ int bvml_dsine_angmf_plan(int B, int H, int W, int k, double fu, double cu, doub
     const int st = plan_angmf(a, B, H, W, k, fu, cu, fv, cv, flags, fp64);
     if (st != BVML_DSINE_OK) return st;
     if (waves_per_group) *waves_per_group = a.G;
-    if (tile_w) *tile_w = a.TW;
-    if (tile_h) *tile_h = a.TH;
+    if (tile_w) *tile_w = a.range ? 64 * a.M : a.TW;
+    if (tile_h) *tile_h = a.range ? 0 : a.TH;
     if (stream_planes) *stream_planes = a.stream_planes;
     return fp64 ? 0 : 1;
 }

@@ -103,7 +103,8 @@ int bvml_dsine_angmf_propagate_f32(const float* pred_norm, const float* prob,
  * runs the double-precision kernel, or a negative BVML_DSINE_E* status.
  * *waves_per_group receives the waves that share one 64-pixel group (1: each
  * wave evaluates the whole window; 2, 4, 8: the window's neighbours split
- * into runs), *tile_w and *tile_h the workgroup's tile, *stream_planes 1
+ * into runs), *tile_w and *tile_h the workgroup's tile (*tile_h 0: a range
+ * tile, *tile_w consecutive pixels of the row-major image), *stream_planes 1
  * when the launch reads its neighbour planes with the non-temporal cache
  * policy (a whole-window launch larger than the Infinity Cache); any of the
  * four may be NULL.  No counterpart in the reference: for tests and tuning.

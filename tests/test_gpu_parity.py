@@ -122,6 +122,7 @@ SHAPES = [
     (1, 33, 65, 3), (2, 17, 200, 7), (1, 12, 20, 9), (3, 5, 6, 1), (1, 64, 64, 5),
     (1, 10, 64, 9), (1, 5, 128, 7), (1, 6, 100, 9), (2, 512, 512, 5), (3, 500, 333, 7),
     (1, 256, 256, 3), (4, 384, 80, 5), (1, 256, 256, 7), (4, 384, 40, 9), (1, 800, 800, 5),
+    (16, 130, 70, 5),
 ]
 
 
