@@ -8,7 +8,8 @@
 //     reports beside the kernels' bandwidth;
 //   * a launch loop: K calls of a C-ABI entry point (bvml_dsine_angmf_propagate_f32,
 //     reached through the function pointer the caller passes) enqueued back
-//     to back from C++ between two events, behind a short bounded spin
+//     to back from C++ between two events (device-scope release, the HIP
+//     flag for timing commands between events), behind a short bounded spin
 //     kernel that holds the stream while the host enqueues them, so the
 //     events time the K launches on the GPU, not the host's enqueueing.
 // Every kernel writes one result per workgroup (the read: per wave), into
@@ -209,9 +210,11 @@ int bvml_probe_angmf_loop(void* fn, const unsigned long long* ptrs, int K, doubl
     if (!fn || !ptrs || K < 1 || !ms || !(spin_us >= 0.0) || spin_us > 1e5) return -1;
     const angmf_fn call = reinterpret_cast<angmf_fn>(fn);
     const hipStream_t st = static_cast<hipStream_t>(stream);
+    // device-scope release: the events time the launches without a system-scope
+    // cache writeback of their own inside the timed region
     hipEvent_t e0 = nullptr, e1 = nullptr;
-    hipError_t e = hipEventCreate(&e0);
-    if (e == hipSuccess) e = hipEventCreate(&e1);
+    hipError_t e = hipEventCreateWithFlags(&e0, hipEventReleaseToDevice);
+    if (e == hipSuccess) e = hipEventCreateWithFlags(&e1, hipEventReleaseToDevice);
     int status = (int)e;
     if (e == hipSuccess) {
         hipLaunchKernelGGL(spin, dim3(1), dim3(64), 0, st, (uint64_t)(spin_us * 100.0));
