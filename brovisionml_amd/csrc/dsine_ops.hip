@@ -514,12 +514,14 @@ __device__ __forceinline__ void stage_halo(float mx, float my, float mz, int sx,
 // neighbours' planes in flight, issuing the next neighbour's loads as it
 // finishes one.
 constexpr int kWgWaves = 8;
-// Measured best: 3 at k <= 5 (a 256 x 256 call in one round of waves wants
-// each wave's first neighbours' data first), 7 at k >= 7 (many rounds); 5
-// with G = 1 (large launches, every wave runs the whole window; 2 to 6
-// measured on 4 x 512 x 512 at k = 7).
+// Measured best: at k <= 5, 2 with G = 4 (a 256 x 256 call in one round of
+// waves wants each wave's first neighbours' data first: 8.41 against 8.46-8.50
+// us with 3, 9.8 with 1) and 3 with G = 2 or 8 (32 x 60 x 80: 17.7-18.4 us
+// against 19.7 with 2); 7 at k >= 7 (many rounds); 5 with G = 1 (large
+// launches, every wave runs the whole window; 2 to 6 measured on 4 x 512 x 512
+// at k = 7).
 __host__ __device__ constexpr int lookahead(int K, int G) {
-    return G == 1 ? 5 : (K <= 5 ? 3 : 7);
+    return G == 1 ? 5 : (K <= 5 ? (G == 4 ? 2 : 3) : 7);
 }
 
 // Neighbours whose planes a wave loads before the halo staging and its
