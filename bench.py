@@ -837,6 +837,17 @@ def bench_ray_relu(args, dev) -> dict:
 # convex upsample
 # ---------------------------------------------------------------------------
 
+def upsample_kernel_name(C: int, H: int, W: int, s: int, mask_ptr: int) -> str:
+    """The kernel bvml_dsine_convex_upsample_f32 runs: at s = 8 the LDS-staged
+    one when H*W is a multiple of 4 and the mask 16-byte aligned (the outputs
+    here are fresh allocations, 16-byte aligned), else the register one."""
+    if s != 8:
+        return f"upsample_kernel<{C}>"
+    if (H * W) % 4 == 0 and mask_ptr % 16 == 0:
+        return f"upsample8_lds_kernel<{C}>"
+    return f"upsample8_kernel<{C}>"
+
+
 def bench_upsample(args, dev) -> dict:
     import torch
     import oracle
@@ -896,7 +907,7 @@ def bench_upsample(args, dev) -> dict:
     line["roofline"] = roofline(
         bytes_per_call, launch_s,
         None if args.precise else traffic_from_profile("upsample", w.name),
-        f"upsample8_kernel<{C}>" if s == 8 else f"upsample_kernel<{C}>", copy_gbps, read_gbps)
+        upsample_kernel_name(C, H, W, s, ms[0].data_ptr()), copy_gbps, read_gbps)
     line["per_launch"] = {"us_median": round(float(np.median(per)), 3),
                           "us_max": round(float(per.max()), 3)}
     line["warm"] = {

@@ -82,10 +82,14 @@ def check(got, want, normalize=True, scale=1.0, exact=False):
 # (B, C, H, W, s): the refiner's shapes (C = 3, s = 8, the /8 grid of 480x640
 # and 2048x2048 images), ragged widths (pixel groups that straddle rows and
 # partial last groups), other channel counts, a batch, and other scales
-# (the generic kernel).
+# (the generic kernel).  At s = 8, H*W a multiple of 4 takes the LDS-staged
+# kernel (60x80: a partial last 128-pixel group; 3x4 and 2x2: fewer pixels
+# than one group; 16x24: whole groups, B = 3), other H*W the register kernel.
 CASES = [
     (1, 3, 60, 80, 8), (1, 3, 256, 256, 8), (2, 3, 7, 13, 8), (1, 1, 5, 3, 8),
     (1, 2, 33, 17, 8), (1, 4, 9, 65, 8), (3, 3, 1, 1, 8), (1, 3, 2, 31, 8),
+    (1, 3, 3, 4, 8), (2, 1, 20, 20, 8), (1, 2, 12, 36, 8), (1, 4, 17, 12, 8),
+    (3, 3, 16, 24, 8), (2, 3, 2, 2, 8),
     (1, 3, 10, 12, 4), (2, 2, 6, 7, 2), (1, 3, 5, 5, 1), (1, 3, 4, 6, 16), (1, 4, 3, 3, 3),
 ]
 
@@ -197,6 +201,43 @@ def test_upsample_unaligned_out(cuda):
     b = run_gpu(x, mask, 8, cuda, misalign=True)
     assert np.array_equal(a.view(np.uint32), b.view(np.uint32))
     check(b, run_oracle(x, mask, 8))
+
+
+@pytest.mark.parametrize("B,C,H,W", [(1, 3, 60, 80), (2, 1, 20, 20), (1, 4, 17, 12), (2, 3, 2, 2)])
+@pytest.mark.parametrize("normalize,precise,bias", [(True, False, False), (False, False, False),
+                                                    (True, True, False), (True, False, True)])
+def test_upsample_staged_matches_register_kernel(cuda, B, C, H, W, normalize, precise, bias):
+    """At s = 8 the LDS-staged kernel (a 16-byte-aligned mask and H*W a
+    multiple of 4) and the register kernel (the same mask 4 bytes past
+    16-byte alignment) compute every sub-pixel in the same order: the same
+    bits, fast and double paths, with and without a mask bias."""
+    import torch
+    say(f"[gpu] upsample staged vs register kernel B={B} C={C} {H}x{W} normalize={normalize} "
+        f"precise={precise} bias={bias}")
+    rng = np.random.default_rng(400 + H + W + C + 3 * precise + 5 * bias)
+    x, mask = _inputs(rng, B, C, H, W, 8)
+    xt = to_dev(x, cuda)
+    n = mask.size
+    buf = torch.empty(n + 4, dtype=torch.float32, device=cuda)
+    assert buf.data_ptr() % 16 == 0
+    aligned = buf[:n].view(mask.shape)
+    shifted = buf[1:n + 1].view(mask.shape)
+    bt = to_dev((3.0 * rng.standard_normal(576)).astype(np.float32), cuda) if bias else None
+    outs = []
+    for m in (aligned, shifted):
+        m.copy_(torch.from_numpy(mask))
+        g = Guarded(B * C * 64 * H * W, cuda)
+        if normalize:
+            r = dsine.convex_upsample_normalize(xt, m, B, C, H, W, 8, EPS, g.out,
+                                                precise=precise, mask_bias=bt)
+        else:
+            r = dsine.convex_upsample(xt, m, B, C, H, W, 8, g.out, precise=precise, mask_bias=bt)
+        torch.cuda.synchronize()
+        assert g.intact(), "convex upsample wrote outside its output"
+        outs.append(r.cpu().numpy().reshape(B, C, 8 * H, 8 * W))
+    assert np.array_equal(outs[0].view(np.uint32), outs[1].view(np.uint32))
+    if not bias:
+        check(outs[0], run_oracle(x, mask, 8, normalize), normalize, exact=precise)
 
 
 def test_upsample_many_samples(cuda):
