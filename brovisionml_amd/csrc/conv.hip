@@ -9,8 +9,10 @@
 // chunk's loads in flight during the current chunk's products), then for each
 // tap runs v_mfma_f32_16x16x4_f32 steps with
 //   A = the packed weights of 16 output channels x the chunk's 4 channels at
-//       that tap (one coalesced 256-byte load per step, from L2; see
-//       bvml_dsine_conv_pack_f32),
+//       that tap (bvml_dsine_conv_pack_f32's layout): the chunk's weights
+//       staged in LDS (double-buffered, copied by direct-to-LDS loads) or,
+//       for the 5x5 launches of 8 M-blocks, one coalesced 256-byte L2 load
+//       per step (stage_weights),
 //   B = the halo at the tap's shift: 4 channels x 16 pixels of one tile row.
 // Each sum is fp32 in the matrix instruction's order.  The epilogues fuse
 // what the refiner does next (src/dsine_refine.cpp:138-159):
@@ -72,6 +74,17 @@ __device__ __forceinline__ float gru_mix(float z, float h, float q) {
 // its epilogue).  A grid with one workgroup per CU leaves each SIMD one wave
 // of 4-wave workgroups; with KS = 2 it has two, and one wave's MFMAs run
 // while the other waits for its operands.
+// Whether a launch stages each chunk's weights in LDS with direct-to-LDS
+// loads (the products then wait on LDS reads only) or has every wave read
+// its A operands from L2 two taps ahead.  Staged, at 256 x 256 (same-box
+// A/B, bit-identical results): convq (5x5, 64 channels, KS = 2) 253-259
+// against 274-276 us; the heads' 3x3 layer 130-131 against 167 us (192
+// channels), 166-168 against 193-195 (256).  The 5x5 kernels of 8 M-blocks
+// per workgroup (convz + convr) keep the L2 reads: their waves already reuse
+// each A operand for 8 tile rows, their 115 KB of staged weights per chunk
+// leave one workgroup per CU, and staged they ran 524-531 against 508-512 us.
+constexpr bool stage_weights(int K, int WM) { return !(K == 5 && WM == 2); }
+
 template <int K, int TH, int WM, int WN, int EPI, int KS>
 __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
     constexpr int P = K / 2;
@@ -82,10 +95,17 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
     constexpr int TAPS = K * K;
     static_assert(WM * WN == kThreads / 64, "4 waves");
     static_assert(KS == 1 || NB % 2 == 0, "the split's sums meet two N-blocks at a time");
+    // the workgroup's weights of one chunk, [tap][its 4 WM M-blocks][64 lanes],
+    // staged in LDS (SW) or read by each wave from L2
+    constexpr bool SW = stage_weights(K, WM);
+    constexpr int WCH = SW ? TAPS * 4 * WM * 64 : 1;
     __shared__ float halo[KS][2][HALO];
+    __shared__ float wts[KS][2][WCH];
 
     const int ks = (KS > 1) ? (int)threadIdx.x / kThreads : 0;  // the wave group's split
     const int tid = (int)threadIdx.x - ks * kThreads, lane = tid & 63, wave = tid >> 6;
+    // the wave's index as a scalar (the weight copies' LDS addresses are per wave)
+    const int wave_s = __builtin_amdgcn_readfirstlane(wave);
     const int g = lane >> 4, col = lane & 15;
     const int wm = wave % WM, wn = wave / WM;
     const int tx0 = (blockIdx.x % a.tiles_x) * kTW, ty0 = (blockIdx.x / a.tiles_x) * TH;
@@ -118,6 +138,22 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
             if (e < HALO) halo[ks][buf][e] = v[i];
         }
     };
+    // a chunk's weights for the workgroup's M-blocks, copied to LDS with
+    // direct-to-LDS loads (one M-block of one tap, 256 bytes, per wave-wide
+    // load; the group's 4 waves take every 4th): they use no registers, and
+    // the products then wait on LDS reads only
+    const float* wsrc = a.wp + (size_t)blockIdx.y * (4 * WM) * 64 + lane;
+    auto w_load = [&](int chunk, int buf) {
+        const float* wc = wsrc + (size_t)chunk * TAPS * a.mblocks * 64;
+        for (int i = wave_s; i < TAPS * 4 * WM; i += 4) {
+            const int tap = i / (4 * WM), j = i - tap * (4 * WM);
+            __builtin_amdgcn_global_load_lds(
+                static_cast<const void*>(wc + ((size_t)tap * a.mblocks + j) * 64),
+                reinterpret_cast<__attribute__((address_space(3))) void*>(
+                    reinterpret_cast<uintptr_t>(&wts[ks][buf][i * 64])),
+                4, 0, 0);
+        }
+    };
 
     v4f acc[4][NB];
 #pragma unroll
@@ -127,19 +163,26 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
 
     float pre[PER_T];
     halo_load(ks, pre);
+    if (SW && ks < nchunks) w_load(ks, 0);
     halo_store(0, pre);
+    __builtin_amdgcn_s_waitcnt(0);  // the weight copies (counted with the loads)
     __syncthreads();
-    const float* wbase = a.wp + (size_t)mb0 * 64 + lane;
-    const size_t tap_stride = (size_t)a.mblocks * 64;
     for (int trip = 0; trip < trips; ++trip) {
         const int chunk = trip * KS + ks;
         const int buf = trip & 1;
         const bool more = trip + 1 < trips;
-        if (more) halo_load(chunk + KS, pre);
+        // the next chunk's halo (to registers) and weights (to the other LDS
+        // buffer, which every wave finished reading before the last barrier)
+        if (more) {
+            halo_load(chunk + KS, pre);
+            if (SW && chunk + KS < nchunks) w_load(chunk + KS, buf ^ 1);
+        }
         if (chunk < nchunks) {
         const float* hb = halo[ks][buf] + g * HS + (wn * NB) * HC + col;
-        const float* wc = wbase + (size_t)chunk * TAPS * tap_stride;
-        // the A operands one tap ahead, the B operands (LDS) one tap ahead
+        if constexpr (!SW) {
+        const size_t tap_stride = (size_t)a.mblocks * 64;
+        const float* wc = a.wp + (size_t)mb0 * 64 + lane + (size_t)chunk * TAPS * tap_stride;
+        // the A operands (L2) two taps ahead, the B operands (LDS) one
         float af[3][4];
 #pragma unroll
         for (int q = 0; q < 2; ++q)
@@ -167,8 +210,38 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
                     acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[t % 3][m], bf[t & 1][n],
                                                                     acc[m][n], 0, 0, 0);
         }
+        } else {
+        const float* wl = wts[ks][buf] + (4 * wm) * 64 + lane;
+        // the A and B operands (LDS) one tap ahead
+        float af[2][4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m) af[0][m] = wl[m * 64];
+        float bf[2][NB];
+#pragma unroll
+        for (int n = 0; n < NB; ++n) bf[0][n] = hb[n * HC];
+#pragma unroll
+        for (int t = 0; t < TAPS; ++t) {
+            if (t + 1 < TAPS) {
+                const int ky = (t + 1) / K, kx = (t + 1) % K;
+#pragma unroll
+                for (int n = 0; n < NB; ++n) bf[(t + 1) & 1][n] = hb[(n + ky) * HC + kx];
+#pragma unroll
+                for (int m = 0; m < 4; ++m) af[(t + 1) & 1][m] = wl[((t + 1) * 4 * WM + m) * 64];
+            }
+            // the next tap's reads stay ahead of this tap's products (a
+            // single wave per SIMD would otherwise wait on each read)
+            __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int n = 0; n < NB; ++n)
+                    acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[t & 1][m], bf[t & 1][n],
+                                                                    acc[m][n], 0, 0, 0);
+        }
+        }
         }
         if (more) halo_store(buf ^ 1, pre);
+        __builtin_amdgcn_s_waitcnt(0);  // the next chunk's weight copies
         __syncthreads();
     }
     if constexpr (KS > 1) {
