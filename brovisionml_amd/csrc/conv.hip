@@ -10,9 +10,9 @@
 // tap runs v_mfma_f32_16x16x4_f32 steps with
 //   A = the packed weights of 16 output channels x the chunk's 4 channels at
 //       that tap (bvml_dsine_conv_pack_f32's layout): the chunk's weights
-//       staged in LDS (double-buffered, copied by direct-to-LDS loads) or,
-//       for the 5x5 launches of 8 M-blocks, one coalesced 256-byte L2 load
-//       per step (stage_weights),
+//       read from L2 (one coalesced 256-byte load per step) or, in the 3x3
+//       launches of 4 M-blocks, staged in LDS (double-buffered, copied by
+//       direct-to-LDS loads; stage_weights),
 //   B = the halo at the tap's shift: 4 channels x 16 pixels of one tile row.
 // Each sum is fp32 in the matrix instruction's order.  The epilogues fuse
 // what the refiner does next (src/dsine_refine.cpp:138-159):
@@ -76,14 +76,13 @@ __device__ __forceinline__ float gru_mix(float z, float h, float q) {
 // while the other waits for its operands.
 // Whether a launch stages each chunk's weights in LDS with direct-to-LDS
 // loads (the products then wait on LDS reads only) or has every wave read
-// its A operands from L2 two taps ahead.  Staged, at 256 x 256 (same-box
-// A/B, bit-identical results): convq (5x5, 64 channels, KS = 2) 253-259
-// against 274-276 us; the heads' 3x3 layer 130-131 against 167 us (192
-// channels), 166-168 against 193-195 (256).  The 5x5 kernels of 8 M-blocks
-// per workgroup (convz + convr) keep the L2 reads: their waves already reuse
-// each A operand for 8 tile rows, their 115 KB of staged weights per chunk
-// leave one workgroup per CU, and staged they ran 524-531 against 508-512 us.
-constexpr bool stage_weights(int K, int WM) { return !(K == 5 && WM == 2); }
+// its A operands from L2 two taps ahead.  Same-box A/B at 256 x 256, both
+// with the operands two taps ahead of the products, bit-identical results:
+// only the 3x3 launches of 4 M-blocks per workgroup (the heads' first layer
+// at 192 channels) gain by staging, 131 against 156-157 us; staged, the
+// others lose: convz + convr 524-531 against 466-472 us, convq 263-266
+// against 246-250, the 3x3 layer at 256 channels 167 against 163.
+constexpr bool stage_weights(int K, int WM) { return K == 3 && WM == 1; }
 
 template <int K, int TH, int WM, int WN, int EPI, int KS>
 __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
