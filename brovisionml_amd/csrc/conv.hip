@@ -90,6 +90,11 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
     constexpr int HR = TH + K - 1, HC = kTW + K - 1, HS = HR * HC;  // halo rows, cols, size
     constexpr int HALO = kCC * HS;                                   // floats per chunk
     constexpr int PER_T = (HALO + kThreads - 1) / kThreads;
+    // a channel's halo in LDS starts 16 banks (mod 64) after the previous
+    // one's, so the 4 channels a B read takes (16 lanes each) hit disjoint
+    // banks: 400 floats at k = 5 already; 324 padded to 336 at k = 3 (1,224
+    // and 2,448 bank conflicts per wave unpadded)
+    constexpr int HSP = HS + ((16 - HS % 64) + 64) % 64;
     constexpr int NB = TH / WN;                                      // tile rows per wave
     constexpr int TAPS = K * K;
     static_assert(WM * WN == kThreads / 64, "4 waves");
@@ -98,7 +103,7 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
     // staged in LDS (SW) or read by each wave from L2
     constexpr bool SW = stage_weights(K, WM);
     constexpr int WCH = SW ? TAPS * 4 * WM * 64 : 1;
-    __shared__ float halo[KS][2][HALO];
+    __shared__ float halo[KS][2][kCC * HSP];
     __shared__ float wts[KS][2][WCH];
 
     const int ks = (KS > 1) ? (int)threadIdx.x / kThreads : 0;  // the wave group's split
@@ -134,7 +139,7 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
 #pragma unroll
         for (int i = 0; i < PER_T; ++i) {
             const int e = tid + i * kThreads;
-            if (e < HALO) halo[ks][buf][e] = v[i];
+            if (e < HALO) halo[ks][buf][(e / HS) * HSP + e % HS] = v[i];
         }
     };
     // a chunk's weights for the workgroup's M-blocks, copied to LDS with
@@ -177,7 +182,7 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
             if (SW && chunk + KS < nchunks) w_load(chunk + KS, buf ^ 1);
         }
         if (chunk < nchunks) {
-        const float* hb = halo[ks][buf] + g * HS + (wn * NB) * HC + col;
+        const float* hb = halo[ks][buf] + g * HSP + (wn * NB) * HC + col;
         if constexpr (!SW) {
         const size_t tap_stride = (size_t)a.mblocks * 64;
         const float* wc = a.wp + (size_t)mb0 * 64 + lane + (size_t)chunk * TAPS * tap_stride;
