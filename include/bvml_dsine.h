@@ -156,7 +156,9 @@ int bvml_dsine_build_uv8_f32(float* uv, double fu, double cu, double fv, double 
  * makes that sub-pixel NaN.  Within 7.2e-6 per component of the
  * double-precision result (a bound; typically 1e-7); flags BVML_DSINE_FP64
  * computes every sub-pixel in double.  `out` is caller-allocated and must not
- * overlap x or mask.
+ * overlap x or mask.  Any alignment works; at scale 8 a 16-byte-aligned `out`
+ * and mask with H*W a multiple of 4 take the fastest kernel (the result is
+ * the same bit for bit).
  */
 int bvml_dsine_convex_upsample_f32(const float* x, const float* mask, int B, int C, int H,
                                    int W, int scale, int normalize, float eps, float* out,
