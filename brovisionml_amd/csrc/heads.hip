@@ -52,6 +52,13 @@ constexpr int kW2Floats = bvml::pack::kHeadsW2Floats;  // one head's packed midd
 constexpr int kLdsOb = 8;
 constexpr int kChunkOb = 8;    // a large last layer passes through LDS this many blocks at a time
 constexpr int kLdsFloats = kMaxHeads * kW2Floats + (kLdsOb + kChunkOb) * 16 * 64;
+// The biases in LDS too: b0 and b2 of every head, and the last layers'
+// biases up to kB4Lds floats in all (the others are read from global memory).
+// A bias read from global memory inside the products would wait for the next
+// head's inputs, whose loads were issued before it (vector loads complete in
+// order): 3 heads of 25, 50 and 25 outputs at 256 x 256 took 48.7 us so.
+constexpr int kB4Lds = 1024;
+constexpr int kBiasFloats = 2 * kMaxHeads * kHid + kB4Lds;
 
 typedef float v4f __attribute__((ext_vector_type(4)));
 
@@ -65,6 +72,7 @@ struct HeadsArgs {
     float* out[kMaxHeads];
     int outs[kMaxHeads];
     int lds_off[kMaxHeads];           // W4p's offset in LDS, -1: read from global
+    int b4_off[kMaxHeads];            // b4's offset in the LDS bias region, -1: global or none
     int lds_floats;                   // floats staged in LDS
     int nheads;
     long long HW;
@@ -87,9 +95,10 @@ __device__ __forceinline__ void load_head_inputs(const HeadsArgs& a, int h, int 
 }
 
 // The last layer on the middle layer's registers t (see above): kOb output
-// blocks of 16 at a time, W4 packed at w4, plus the bias, into out.
+// blocks of 16 at a time, W4 packed at w4, plus the bias b4 (when has_b4),
+// into out.
 __device__ __forceinline__ void last_layer(const float* __restrict__ w4, const v4f (&t)[4][2],
-                                           int n, const float* __restrict__ b4,
+                                           int n, const float* __restrict__ b4, bool has_b4,
                                            float* __restrict__ out, long long HW, int lane, int g,
                                            const long long* p, const bool* in) {
     const int nob = (n + 15) / 16;
@@ -121,10 +130,10 @@ __device__ __forceinline__ void last_layer(const float* __restrict__ w4, const v
                 const int o = 16 * (ob0 + i) + 4 * g + r;
                 if (o >= n) continue;
                 float* oc = out + (size_t)o * HW;
-                const float bias = b4 ? b4[o] : 0.0f;
+                const float bias = has_b4 ? b4[o] : 0.0f;
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb)
-                    if (in[nb]) oc[p[nb]] = b4 ? oacc[i][nb][r] + bias : oacc[i][nb][r];
+                    if (in[nb]) oc[p[nb]] = has_b4 ? oacc[i][nb][r] + bias : oacc[i][nb][r];
             }
         }
     }
@@ -132,6 +141,21 @@ __device__ __forceinline__ void last_layer(const float* __restrict__ w4, const v
 
 __global__ __launch_bounds__(kWaves * 64) void heads_mlp_kernel(HeadsArgs a) {
     __shared__ float lds[kLdsFloats];
+    // [b0 of every head | b2 of every head | the staged last-layer biases]
+    __shared__ float bl[kBiasFloats];
+    {
+        const int nb2 = a.nheads * kHid;
+        for (int i = threadIdx.x; i < nb2; i += kWaves * 64) {
+            bl[i] = a.b0[i];
+            bl[kMaxHeads * kHid + i] = a.b2[i];
+        }
+#pragma unroll
+        for (int h = 0; h < kMaxHeads; ++h) {
+            if (h >= a.nheads || a.b4_off[h] < 0) continue;
+            for (int i = threadIdx.x; i < a.outs[h]; i += kWaves * 64)
+                bl[2 * kMaxHeads * kHid + a.b4_off[h] + i] = a.b4[h][i];
+        }
+    }
     // stage the packed middle layers and the small last layers
     {
         const int n = a.lds_floats;
@@ -182,7 +206,7 @@ __global__ __launch_bounds__(kWaves * 64) void heads_mlp_kernel(HeadsArgs a) {
         const float* w2 = lds + h * kW2Floats;
 #pragma unroll
         for (int j = 0; j < 16; ++j) {
-            const float bias = a.b0[kHid * h + 4 * j + g];
+            const float bias = bl[kHid * h + 4 * j + g];
             float bf[2];
 #pragma unroll
             for (int nb = 0; nb < 2; ++nb) bf[nb] = in[nb] ? relu(cur[j][nb] + bias) : 0.0f;
@@ -200,15 +224,19 @@ __global__ __launch_bounds__(kWaves * 64) void heads_mlp_kernel(HeadsArgs a) {
         for (int mb = 0; mb < 4; ++mb)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
-                const float bias = a.b2[kHid * h + 16 * mb + 4 * g + r];
+                const float bias = bl[kMaxHeads * kHid + kHid * h + 16 * mb + 4 * g + r];
 #pragma unroll
                 for (int nb = 0; nb < 2; ++nb) acc[mb][nb][r] = relu(acc[mb][nb][r] + bias);
             }
-        // last layer, from LDS or (a large layer) from global memory: two
-        // calls, so each reads through its own address space
-        if (a.lds_off[h] >= 0)
-            last_layer(lds + a.lds_off[h], acc, a.outs[h], a.b4[h], a.out[h], a.HW, lane, g, p,
-                       in);
+        // last layer, from LDS or (a large layer) from global memory: separate
+        // calls, so each reads its weights and bias through its own address
+        // space
+        if (a.lds_off[h] >= 0 && a.b4_off[h] >= 0)
+            last_layer(lds + a.lds_off[h], acc, a.outs[h], bl + 2 * kMaxHeads * kHid + a.b4_off[h],
+                       true, a.out[h], a.HW, lane, g, p, in);
+        else if (a.lds_off[h] >= 0)
+            last_layer(lds + a.lds_off[h], acc, a.outs[h], a.b4[h], a.b4[h] != nullptr, a.out[h],
+                       a.HW, lane, g, p, in);
         else {
             // a large last layer: kChunkOb blocks at a time through the chunk
             // buffer after the staged weights (uniform across the workgroup)
@@ -223,8 +251,8 @@ __global__ __launch_bounds__(kWaves * 64) void heads_mlp_kernel(HeadsArgs a) {
                 __syncthreads();
                 const int n = a.outs[h] - 16 * c0 < 16 * cb ? a.outs[h] - 16 * c0 : 16 * cb;
                 const float* b4 = a.b4[h] ? a.b4[h] + 16 * c0 : nullptr;
-                last_layer(chunk, acc, n, b4, a.out[h] + (size_t)16 * c0 * a.HW, a.HW, lane, g, p,
-                           in);
+                last_layer(chunk, acc, n, b4, b4 != nullptr, a.out[h] + (size_t)16 * c0 * a.HW,
+                           a.HW, lane, g, p, in);
             }
         }
         if (h + 1 < a.nheads) {
@@ -289,6 +317,14 @@ int bvml_dsine_heads_mlp_f32(const float* t0, const float* b0, const float* w2p,
         }
     }
     a.lds_floats = at;
+    // the last layers' biases in LDS while they fit
+    int b4_at = 0;
+    for (int h = 0; h < kMaxHeads; ++h) a.b4_off[h] = -1;
+    for (int h = 0; h < nheads; ++h)
+        if (b4[h] && b4_at + outs[h] <= kB4Lds) {
+            a.b4_off[h] = b4_at;
+            b4_at += outs[h];
+        }
     for (int h = 0; h < nheads; ++h)
         if ((reinterpret_cast<uintptr_t>(w4p[h]) & 15u) != 0)
             return fail(BVML_DSINE_EPARAM, "heads_mlp: w4p must be 16-byte aligned");
