@@ -954,37 +954,53 @@ def bench_upsample(args, dev) -> dict:
 # ---------------------------------------------------------------------------
 
 def refiner_kernel_rooflines(dev, H: int, W: int, reps: int):
-    """The refiner's two 5x5 ConvGRU convolutions (the implicit-GEMM kernels
-    of brovisionml_amd/csrc/conv.hip, gates and update epilogues) timed alone
+    """The refiner's 5x5 ConvGRU convolutions (the implicit-GEMM kernels of
+    brovisionml_amd/csrc/conv.hip) as its forward runs them, each timed alone
     on the refiner's map size with HIP events on their stream, against the
-    fp32 matrix peak: algorithmic flops per launch = 2 * cout * cin * 25 *
-    H * W (convz + convr: cout 128; convq: 64; cin 130).  Returns (the
-    convz + convr kernel's roofline, both kernels' figures)."""
+    fp32 matrix peak: every iteration convz + convr and convq over the hidden
+    state's 64 channels (cin 64; the gates and the update in their
+    epilogues, with the part over the other 66 channels added), and once per
+    forward those parts over [feature | uv] (cin 66, plain convolutions).
+    Algorithmic flops per launch = 2 * cout * cin * 25 * H * W.  Returns (the
+    per-iteration convz + convr kernel's roofline, every kernel's figures)."""
     import torch
     from brovisionml_amd import _lib
     lib = _lib.load()
-    C, cin = 64, 130
+    C, ch, cx = 64, 64, 66
     g = torch.Generator().manual_seed(0)
-    x = torch.randn(cin, H, W, generator=g).to(dev)
+    x = torch.randn(ch + cx, H, W, generator=g).to(dev)
     h = x[:C]
-    w = (torch.rand(3 * C, cin, 5, 5, generator=g) - 0.5) / math.sqrt(cin * 25)
-    wzr = torch.from_numpy(_lib.conv_pack_f32(w[:2 * C].numpy(), interleave=True)).to(dev)
-    wq = torch.from_numpy(_lib.conv_pack_f32(w[2 * C:].numpy())).to(dev)
+    xf = x[ch:]
+    w = (torch.rand(3 * C, ch + cx, 5, 5, generator=g) - 0.5) / math.sqrt((ch + cx) * 25)
+    wzr_h = torch.from_numpy(_lib.conv_pack_f32(w[:2 * C, :ch].numpy(), interleave=True)).to(dev)
+    wzr_f = torch.from_numpy(_lib.conv_pack_f32(w[:2 * C, ch:].numpy(), interleave=True)).to(dev)
+    wq_h = torch.from_numpy(_lib.conv_pack_f32(w[2 * C:, :ch].numpy())).to(dev)
+    wq_f = torch.from_numpy(_lib.conv_pack_f32(w[2 * C:, ch:].numpy())).to(dev)
     b = torch.zeros(C, device=dev)
     z, rh, hn, hc = (torch.empty(C, H, W, device=dev) for _ in range(4))
+    s_zr = torch.empty(2 * C, H, W, device=dev)
+    s_q = torch.empty(C, H, W, device=dev)
     stream = torch.cuda.current_stream(dev)
     sp = stream.cuda_stream
     calls = {
-        "conv_gru_gates (convz + convr, 5x5, 130 -> 128)": (
-            2 * 2 * C * cin * 25 * H * W,
-            lambda: lib.bvml_dsine_conv_gru_gates_f32(x.data_ptr(), cin, H, W, wzr.data_ptr(), C,
-                                                       b.data_ptr(), b.data_ptr(), h.data_ptr(),
-                                                       z.data_ptr(), rh.data_ptr(), sp)),
-        "conv_gru_update (convq, 5x5, 130 -> 64)": (
-            2 * C * cin * 25 * H * W,
-            lambda: lib.bvml_dsine_conv_gru_update_f32(x.data_ptr(), cin, H, W, wq.data_ptr(), C,
-                                                        b.data_ptr(), z.data_ptr(), h.data_ptr(),
-                                                        hn.data_ptr(), hc.data_ptr(), sp)),
+        "conv_gru_gates (convz + convr over h, 5x5, 64 -> 128, + the [feature, uv] part)": (
+            2 * 2 * C * ch * 25 * H * W,
+            lambda: lib.bvml_dsine_conv_gru_gates_sum_f32(
+                x.data_ptr(), ch, H, W, wzr_h.data_ptr(), C, s_zr.data_ptr(), b.data_ptr(),
+                b.data_ptr(), h.data_ptr(), z.data_ptr(), rh.data_ptr(), sp)),
+        "conv_gru_update (convq over r*h, 5x5, 64 -> 64, + the [feature, uv] part)": (
+            2 * C * ch * 25 * H * W,
+            lambda: lib.bvml_dsine_conv_gru_update_sum_f32(
+                rh.data_ptr(), ch, H, W, wq_h.data_ptr(), C, s_q.data_ptr(), b.data_ptr(),
+                z.data_ptr(), h.data_ptr(), hn.data_ptr(), hc.data_ptr(), sp)),
+        "conv (convz + convr over [feature, uv], 5x5, 66 -> 128, once per forward)": (
+            2 * 2 * C * cx * 25 * H * W,
+            lambda: lib.bvml_dsine_conv_f32(xf.data_ptr(), cx, H, W, wzr_f.data_ptr(), 2 * C, 5,
+                                            s_zr.data_ptr(), sp)),
+        "conv (convq over [feature, uv], 5x5, 66 -> 64, once per forward)": (
+            2 * C * cx * 25 * H * W,
+            lambda: lib.bvml_dsine_conv_f32(xf.data_ptr(), cx, H, W, wq_f.data_ptr(), C, 5,
+                                            s_q.data_ptr(), sp)),
     }
     out = {}
     for name, (flops, call) in calls.items():
@@ -1072,7 +1088,8 @@ def bench_refiner(args, dev) -> dict:
                      {"workload": f"dsine-refiner-{H}x{W}", "H": H, "W": W, "iterations": 5,
                       "weights": "synthetic (uniform +-1/sqrt(fan_in))",
                       "driver": driver,
-                      "convolutions": "5x5 and 3x3: implicit-GEMM fp32 MFMA kernels"})
+                      "convolutions": "5x5 and 3x3: implicit-GEMM fp32 MFMA kernels; the "
+                                      "ConvGRU's parts over [feature, uv] once per forward"})
     if t_py is not None:
         line["python_driver"] = {"ms_per_step": round(t_py * 1e3 / args.steps, 4),
                                  "value": round(opx / t_py / 1e6, 2)}

@@ -49,6 +49,8 @@ EXPORTS = (
     "bvml_dsine_conv_f32",
     "bvml_dsine_conv_gru_gates_f32",
     "bvml_dsine_conv_gru_update_f32",
+    "bvml_dsine_conv_gru_gates_sum_f32",
+    "bvml_dsine_conv_gru_update_sum_f32",
     "bvml_dsine_last_error",
     "bvml_dsine_version",
 )
@@ -133,6 +135,12 @@ def load(path: str = LIB) -> ctypes.CDLL:
     lib.bvml_dsine_conv_gru_gates_f32.restype = i
     lib.bvml_dsine_conv_gru_update_f32.argtypes = [vp, i, i, i, vp, i, vp, vp, vp, vp, vp, vp]
     lib.bvml_dsine_conv_gru_update_f32.restype = i
+    lib.bvml_dsine_conv_gru_gates_sum_f32.argtypes = [vp, i, i, i, vp, i, vp, vp, vp, vp, vp, vp,
+                                                      vp]
+    lib.bvml_dsine_conv_gru_gates_sum_f32.restype = i
+    lib.bvml_dsine_conv_gru_update_sum_f32.argtypes = [vp, i, i, i, vp, i, vp, vp, vp, vp, vp, vp,
+                                                       vp]
+    lib.bvml_dsine_conv_gru_update_sum_f32.restype = i
     lib.bvml_dsine_last_error.argtypes = []
     lib.bvml_dsine_last_error.restype = ctypes.c_char_p
     lib.bvml_dsine_version.argtypes = []

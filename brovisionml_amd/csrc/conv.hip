@@ -55,6 +55,7 @@ struct ConvArgs {
     const float* z;     // kUpdate: the update gate
     float* o0;          // kGates: z, kUpdate: h_new
     float* o1;          // kGates: rh, kUpdate: h_copy (may be NULL)
+    const float* s0;    // kGates, kUpdate: sums to add before the bias (packed order), or NULL
     int cin, cout, H, W, mblocks, tiles_x;
     long long HW;
 };
@@ -308,8 +309,13 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
                     const int c = 16 * ((mb0 + m) / 2) + 4 * g + r;
                     if (c >= a.cout / 2) continue;
                     const size_t i = (size_t)c * a.HW + px;
-                    const float zz = sigmoid(acc[m][n][r] + a.b0[c]);
-                    const float rr = sigmoid(acc[m + 1][n][r] + a.b1[c]);
+                    float sz = acc[m][n][r], sr = acc[m + 1][n][r];
+                    if (a.s0) {
+                        sz += a.s0[(size_t)(16 * (mb0 + m) + 4 * g + r) * a.HW + px];
+                        sr += a.s0[(size_t)(16 * (mb0 + m + 1) + 4 * g + r) * a.HW + px];
+                    }
+                    const float zz = sigmoid(sz + a.b0[c]);
+                    const float rr = sigmoid(sr + a.b1[c]);
                     a.o0[i] = zz;
                     a.o1[i] = rr * a.h[i];
                 }
@@ -321,7 +327,9 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
                     const int c = 16 * (mb0 + m) + 4 * g + r;
                     if (c >= a.cout) continue;
                     const size_t i = (size_t)c * a.HW + px;
-                    const float v = gru_mix(a.z[i], a.h[i], tanhf(acc[m][n][r] + a.b0[c]));
+                    float sq = acc[m][n][r];
+                    if (a.s0) sq += a.s0[i];
+                    const float v = gru_mix(a.z[i], a.h[i], tanhf(sq + a.b0[c]));
                     a.o0[i] = v;
                     if (a.o1) a.o1[i] = v;
                 }
@@ -395,9 +403,10 @@ int bvml_dsine_conv_f32(const float* x, int cin, int H, int W, const float* wp, 
                   : launch<3, 16, 1, 4, kPlain>(a, s, "conv");
 }
 
-int bvml_dsine_conv_gru_gates_f32(const float* x, int cin, int H, int W, const float* wp,
-                                  int C, const float* bias_z, const float* bias_r,
-                                  const float* h, float* z, float* rh, void* stream) {
+int bvml_dsine_conv_gru_gates_sum_f32(const float* x, int cin, int H, int W, const float* wp,
+                                      int C, const float* sum0, const float* bias_z,
+                                      const float* bias_r, const float* h, float* z, float* rh,
+                                      void* stream) {
     if (int st = check_common("conv_gru_gates", x, cin, H, W, wp, 5)) return st;
     if (C < 1 || C % 32 != 0)
         return fail(BVML_DSINE_ESHAPE, "conv_gru_gates: C must be a multiple of 32");
@@ -407,20 +416,30 @@ int bvml_dsine_conv_gru_gates_f32(const float* x, int cin, int H, int W, const f
     if (HW == 0) return BVML_DSINE_OK;
     const size_t xb = (size_t)cin * HW * 4, cb = (size_t)C * HW * 4;
     if (overlaps(z, cb, x, xb) || overlaps(rh, cb, x, xb) || overlaps(z, cb, rh, cb) ||
-        overlaps(z, cb, h, cb) || overlaps(rh, cb, h, cb))
-        return fail(BVML_DSINE_EALIAS, "conv_gru_gates: z and rh must not overlap x, h or each other");
+        overlaps(z, cb, h, cb) || overlaps(rh, cb, h, cb) ||
+        (sum0 && (overlaps(z, cb, sum0, 2 * cb) || overlaps(rh, cb, sum0, 2 * cb))))
+        return fail(BVML_DSINE_EALIAS,
+                    "conv_gru_gates: z and rh must not overlap x, h, sum0 or each other");
     ConvArgs a{};
     a.x = x; a.wp = wp; a.cin = cin; a.cout = 2 * C; a.H = H; a.W = W; a.HW = HW;
-    a.b0 = bias_z; a.b1 = bias_r; a.h = h; a.o0 = z; a.o1 = rh;
+    a.b0 = bias_z; a.b1 = bias_r; a.h = h; a.o0 = z; a.o1 = rh; a.s0 = sum0;
     a.mblocks = conv_mblocks(2 * C);
     if (a.mblocks % 8 == 0)
         return launch<5, 16, 2, 2, kGates>(a, static_cast<hipStream_t>(stream), "conv_gru_gates");
     return launch<5, 16, 1, 4, kGates>(a, static_cast<hipStream_t>(stream), "conv_gru_gates");
 }
 
-int bvml_dsine_conv_gru_update_f32(const float* x, int cin, int H, int W, const float* wp, int C,
-                                   const float* bias_q, const float* z, const float* h,
-                                   float* h_new, float* h_copy, void* stream) {
+int bvml_dsine_conv_gru_gates_f32(const float* x, int cin, int H, int W, const float* wp,
+                                  int C, const float* bias_z, const float* bias_r,
+                                  const float* h, float* z, float* rh, void* stream) {
+    return bvml_dsine_conv_gru_gates_sum_f32(x, cin, H, W, wp, C, nullptr, bias_z, bias_r, h, z,
+                                             rh, stream);
+}
+
+int bvml_dsine_conv_gru_update_sum_f32(const float* x, int cin, int H, int W, const float* wp,
+                                       int C, const float* sum0, const float* bias_q,
+                                       const float* z, const float* h, float* h_new,
+                                       float* h_copy, void* stream) {
     if (int st = check_common("conv_gru_update", x, cin, H, W, wp, 5)) return st;
     if (C < 1 || C % 64 != 0)
         return fail(BVML_DSINE_ESHAPE, "conv_gru_update: C must be a multiple of 64");
@@ -435,14 +454,22 @@ int bvml_dsine_conv_gru_update_f32(const float* x, int cin, int H, int W, const 
     if (overlaps(h_new, cb, x, xb) || (h_copy && overlaps(h_copy, cb, x, xb)) ||
         overlaps(h_new, cb, z, cb) || (h_new != h && overlaps(h_new, cb, h, cb)) ||
         (h_copy && (overlaps(h_copy, cb, z, cb) || overlaps(h_copy, cb, h, cb) ||
-                    overlaps(h_copy, cb, h_new, cb))))
+                    overlaps(h_copy, cb, h_new, cb))) ||
+        (sum0 && (overlaps(h_new, cb, sum0, cb) || (h_copy && overlaps(h_copy, cb, sum0, cb)))))
         return fail(BVML_DSINE_EALIAS, "conv_gru_update: outputs overlap an input");
     ConvArgs a{};
     a.x = x; a.wp = wp; a.cin = cin; a.cout = C; a.H = H; a.W = W; a.HW = HW;
-    a.b0 = bias_q; a.z = z; a.h = h; a.o0 = h_new; a.o1 = h_copy;
+    a.b0 = bias_q; a.z = z; a.h = h; a.o0 = h_new; a.o1 = h_copy; a.s0 = sum0;
     a.mblocks = conv_mblocks(C);
     // 64 channels: one M tile of 4 blocks per wave, all four waves along the rows
     return launch<5, 16, 1, 4, kUpdate>(a, static_cast<hipStream_t>(stream), "conv_gru_update");
+}
+
+int bvml_dsine_conv_gru_update_f32(const float* x, int cin, int H, int W, const float* wp, int C,
+                                   const float* bias_q, const float* z, const float* h,
+                                   float* h_new, float* h_copy, void* stream) {
+    return bvml_dsine_conv_gru_update_sum_f32(x, cin, H, W, wp, C, nullptr, bias_q, z, h, h_new,
+                                              h_copy, stream);
 }
 
 }  // extern "C"

@@ -2,10 +2,15 @@
 // (src/dsine_refine.cpp:161-294) on one HIP device, over this library's C ABI
 // (include/bvml_dsine.h).
 //
+// Once per forward, the ConvGRU convolutions' parts over [feature | uv], the
+// channels no iteration changes (conv(cat(h, x), W) = conv(h, W_h) + conv(x,
+// W_x)):
+//   cf_zr = conv5x5([feature | uv], [W_z; W_r] over those channels), cf_q likewise
+//                                                            bvml_dsine_conv_f32
 // Per iteration (src/dsine_refine.cpp:255-287), on persistent per-grid maps:
-//   z, r*h = gates of conv5x5([h | feature | uv], [W_z; W_r])  bvml_dsine_conv_gru_gates_f32
-//   h    = (1 - z) h + z tanh(conv5x5([r*h | feature | uv], W_q) + b_q),
-//          also into [h | uv]                                bvml_dsine_conv_gru_update_f32
+//   z, r*h = gates of conv5x5(h, [W_z; W_r] over h) + cf_zr  bvml_dsine_conv_gru_gates_sum_f32
+//   h    = (1 - z) h + z tanh(conv5x5(r*h, W_q over h) + cf_q + b_q),
+//          also into [h | uv]                                bvml_dsine_conv_gru_update_sum_f32
 //   t0   = conv3x3([h | uv], the heads' first layers)        bvml_dsine_conv_f32, 66 -> 192 or 256
 //   prob, xy, angle = the heads' 1x1 layers on relu(t0 + b0) bvml_dsine_heads_mlp_f32
 //   pred = angmf_propagate(pred, prob, xy, angle) on logits  bvml_dsine_angmf_propagate_f32
@@ -507,8 +512,11 @@ struct bvml_dsine_refiner {
 
     // weights on the device, one allocation
     float* warena = nullptr;
-    // convz + convr and convq, packed for the implicit-GEMM kernels
-    const float *w_zr = nullptr, *b_z = nullptr, *b_r = nullptr, *w_q = nullptr, *b_q = nullptr;
+    // convz + convr and convq, each split by input channels into the part
+    // over h (every iteration) and the part over [feature | uv] (once per
+    // forward), packed for the implicit-GEMM kernels
+    const float *w_zr_h = nullptr, *w_zr_f = nullptr, *b_z = nullptr, *b_r = nullptr;
+    const float *w_q_h = nullptr, *w_q_f = nullptr, *b_q = nullptr;
     const float *b_h0 = nullptr, *w2p = nullptr, *b_h2 = nullptr;
     const float* w_h0p[2] = {};  // the 3x3 layer packed for bvml_dsine_conv_f32 (192, 256 filters)
     const float* w4p[kHeads] = {};  // the 1x1 layers packed for bvml_dsine_heads_mlp_f32
@@ -557,15 +565,33 @@ int bvml_dsine_refiner::upload() {
     if (const int st = bvml_dsine_heads_pack_f32(w2.data(), w4src, kHeadOut, kHeads, w2p_h.data(),
                                                  w4dst))
         return fail(st, std::string("forward: heads_pack: ") + bvml_dsine_last_error());
-    // [W_z; W_r] with their 16-channel blocks interleaved, W_q
+    // [W_z; W_r] with their 16-channel blocks interleaved, and W_q, each as
+    // its input channels [0, kHidden) (h) and [kHidden, kHx) (feature, uv):
+    // conv(cat(h, x), W) = conv(h, W_h) + conv(x, W_x)
     std::vector<float> wzr(host[kZw]);
     wzr.insert(wzr.end(), host[kRw].begin(), host[kRw].end());
-    std::vector<float> wzr_p((size_t)bvml_dsine_conv_packed_size(2 * kHidden, kHx, 5));
-    std::vector<float> wq_p((size_t)bvml_dsine_conv_packed_size(kHidden, kHx, 5));
-    if (const int st = bvml_dsine_conv_pack_f32(wzr.data(), 2 * kHidden, kHx, 5, 1, wzr_p.data()))
-        return fail(st, std::string("forward: conv_pack: ") + bvml_dsine_last_error());
-    if (const int st = bvml_dsine_conv_pack_f32(host[kQw].data(), kHidden, kHx, 5, 0, wq_p.data()))
-        return fail(st, std::string("forward: conv_pack: ") + bvml_dsine_last_error());
+    auto in_slice = [](const std::vector<float>& w, int cout, int c0, int c1) {
+        std::vector<float> out;
+        out.reserve((size_t)cout * (c1 - c0) * 25);
+        for (int o = 0; o < cout; ++o)
+            out.insert(out.end(), w.begin() + ((size_t)o * kHx + c0) * 25,
+                       w.begin() + ((size_t)o * kHx + c1) * 25);
+        return out;
+    };
+    std::vector<float> wsplit_p[4];
+    {
+        const std::vector<float>* src[4] = {&wzr, &wzr, &host[kQw], &host[kQw]};
+        const int cout[4] = {2 * kHidden, 2 * kHidden, kHidden, kHidden};
+        const int c0[4] = {0, kHidden, 0, kHidden}, c1[4] = {kHidden, kHx, kHidden, kHx};
+        const int il[4] = {1, 1, 0, 0};
+        for (int i = 0; i < 4; ++i) {
+            const std::vector<float> w = in_slice(*src[i], cout[i], c0[i], c1[i]);
+            wsplit_p[i].resize((size_t)bvml_dsine_conv_packed_size(cout[i], c1[i] - c0[i], 5));
+            if (const int st = bvml_dsine_conv_pack_f32(w.data(), cout[i], c1[i] - c0[i], 5, il[i],
+                                                        wsplit_p[i].data()))
+                return fail(st, std::string("forward: conv_pack: ") + bvml_dsine_last_error());
+        }
+    }
     std::vector<float> wh0;
     for (int h = 0; h < kHeads; ++h)
         wh0.insert(wh0.end(), host[head_w(h, 0)].begin(), host[head_w(h, 0)].end());
@@ -578,10 +604,12 @@ int bvml_dsine_refiner::upload() {
     }
     using Src = std::vector<const std::vector<float>*>;
     std::vector<std::pair<const float**, Src>> parts;
-    parts.push_back({&w_zr, {&wzr_p}});
+    parts.push_back({&w_zr_h, {&wsplit_p[0]}});
+    parts.push_back({&w_zr_f, {&wsplit_p[1]}});
     parts.push_back({&b_z, {&host[kZb]}});
     parts.push_back({&b_r, {&host[kRb]}});
-    parts.push_back({&w_q, {&wq_p}});
+    parts.push_back({&w_q_h, {&wsplit_p[2]}});
+    parts.push_back({&w_q_f, {&wsplit_p[3]}});
     parts.push_back({&b_q, {&host[kQb]}});
     Src h0b, h2b;
     for (int h = 0; h < kHeads; ++h) {
@@ -685,19 +713,27 @@ int bvml_refine::forward_maps(bvml_dsine_refiner* r, const Maps& m, const Forwar
                    : fail(status, std::string("forward: ") + what + ": " + bvml_dsine_last_error());
     };
     hipError_t e;
-    // hx = [h | feature | uv], rhx = [r*h | feature | uv], hin = [h_new | uv]
+    // hx = [h | feature | uv], rh = r*h, hin = [h_new | uv]
     float* uv = m.hx + (size_t)(kHidden + kFeature) * hw;
     if ((st = ck(bvml_dsine_build_uv8_f32(uv, fu, cu, fv, cv, h8, w8, stream), "build_uv8")) ||
         (st = ck(bvml_dsine_build_ray8_f32(m.ray, fu, cu, fv, cv, h8, w8, stream), "build_ray8")))
         return st;
     if ((e = copy(m.hx, a.hidden, kHidden)) != hipSuccess ||
         (e = copy(m.hx + (size_t)kHidden * hw, a.feature, kFeature)) != hipSuccess ||
-        (e = copy(m.rhx + (size_t)kHidden * hw, m.hx + (size_t)kHidden * hw, kX)) != hipSuccess ||
         (e = copy(m.hin + (size_t)kHidden * hw, uv, 2)) != hipSuccess ||
         (e = copy(m.pred[0], a.normal, 3)) != hipSuccess)
         return hip_fail(e, "hipMemcpyAsync");
     // pred_norm = RayReLU(decoder.normal, ray_8)  (:240-242)
     if ((st = ck(bvml_dsine_ray_relu_f32(m.pred[0], m.ray, 1, h8, w8, 0, stream), "ray_relu")))
+        return st;
+    // the ConvGRU convolutions' parts over [feature | uv], which no
+    // iteration changes: once per forward instead of once per iteration
+    float* cf_zr = m.cf;
+    float* cf_q = m.cf + (size_t)2 * kHidden * hw;
+    const float* xf = m.hx + (size_t)kHidden * hw;
+    if ((st = ck(bvml_dsine_conv_f32(xf, kX, h8, w8, r->w_zr_f, 2 * kHidden, 5, cf_zr, stream),
+                 "conv")) ||
+        (st = ck(bvml_dsine_conv_f32(xf, kX, h8, w8, r->w_q_f, kHidden, 5, cf_q, stream), "conv")))
         return st;
 
     const bool direct = pad_t == 0 && pad_l == 0 && out_h == fh && out_w == fw;
@@ -705,14 +741,14 @@ int bvml_refine::forward_maps(bvml_dsine_refiner* r, const Maps& m, const Forwar
     for (int it = 0; it < kIter; ++it) {
         const bool last = it == kIter - 1;
         const int nh = last ? kHeads : kHeads - 1;
-        // ConvGRU (:138-159): the two 5x5 convolutions with the gates and
-        // the update in their epilogues; h_new overwrites h in hx and is
-        // copied into hin
-        if ((st = ck(bvml_dsine_conv_gru_gates_f32(m.hx, kHx, h8, w8, r->w_zr, C, r->b_z, r->b_r,
-                                                   m.hx, m.z, m.rhx, stream),
+        // ConvGRU (:138-159): the two 5x5 convolutions over h (r*h) plus
+        // their parts over [feature | uv], with the gates and the update in
+        // their epilogues; h_new overwrites h in hx and is copied into hin
+        if ((st = ck(bvml_dsine_conv_gru_gates_sum_f32(m.hx, kHidden, h8, w8, r->w_zr_h, C, cf_zr,
+                                                       r->b_z, r->b_r, m.hx, m.z, m.rh, stream),
                      "conv_gru_gates")) ||
-            (st = ck(bvml_dsine_conv_gru_update_f32(m.rhx, kHx, h8, w8, r->w_q, C, r->b_q, m.z,
-                                                    m.hx, m.hx, m.hin, stream),
+            (st = ck(bvml_dsine_conv_gru_update_sum_f32(m.rh, kHidden, h8, w8, r->w_q_h, C, cf_q,
+                                                        r->b_q, m.z, m.hx, m.hx, m.hin, stream),
                      "conv_gru_update")))
             return st;
         // the heads (:119-127, :257-267, :276): the 3x3 layers, then the rest

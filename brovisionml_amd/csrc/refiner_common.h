@@ -68,18 +68,21 @@ int check_forward(const std::vector<std::vector<float>>& host, const ForwardArgs
 // The host copy of the refiner's weights, one vector per spec.
 const std::vector<std::vector<float>>& host_weights(const bvml_dsine_refiner* r);
 
-// The device maps of one forward: [h | feature | uv], [r*h | feature | uv],
-// [h_new | uv], the update gate, the heads' 3x3 output, the heads' outputs,
-// the two propagate buffers, the ray map, the full-resolution result before
-// the crop.
+// The device maps of one forward: [h | feature | uv], r*h, [h_new | uv], the
+// update gate, the heads' 3x3 output, the heads' outputs, the two propagate
+// buffers, the ray map, the full-resolution result before the crop, and the
+// ConvGRU convolutions' parts over [feature | uv] (constant through the
+// iterations: convz + convr's 128 channels in their packed order, then
+// convq's 64).
 struct Maps {
-    float *hx, *rhx, *hin, *z, *t0, *head[kHeads], *pred[2], *ray, *up;
+    float *hx, *rh, *hin, *z, *t0, *head[kHeads], *pred[2], *ray, *up, *cf;
 };
 
 // The planes of each map in Maps order (up: 3 * kUp^2 planes); each map
 // starts on a 64-float boundary.
-constexpr int kMapPlanes[] = {kHx, kHx, kHin, kHidden, kHeads * kMid, kHeadOut[0], kHeadOut[1],
-                              kHeadOut[2], kHeadOut[3], 3, 3, 3, 3 * kUp * kUp};
+constexpr int kMapPlanes[] = {kHx, kHidden, kHin, kHidden, kHeads * kMid, kHeadOut[0],
+                              kHeadOut[1], kHeadOut[2], kHeadOut[3], 3, 3, 3, 3 * kUp * kUp,
+                              3 * kHidden};
 inline size_t maps_floats(size_t hw) {
     size_t total = 0;
     for (int c : kMapPlanes) total += ((size_t)c * hw + 63) & ~(size_t)63;
@@ -87,10 +90,13 @@ inline size_t maps_floats(size_t hw) {
 }
 inline Maps maps_at(float* base, size_t hw) {
     Maps m{};
-    float** order[] = {&m.hx, &m.rhx, &m.hin, &m.z, &m.t0, &m.head[0], &m.head[1], &m.head[2],
-                       &m.head[3], &m.pred[0], &m.pred[1], &m.ray, &m.up};
+    float** order[] = {&m.hx,      &m.rh,      &m.hin,     &m.z,       &m.t0,
+                       &m.head[0], &m.head[1], &m.head[2], &m.head[3], &m.pred[0],
+                       &m.pred[1], &m.ray,     &m.up,      &m.cf};
+    static_assert(sizeof(order) / sizeof(order[0]) == sizeof(kMapPlanes) / sizeof(kMapPlanes[0]),
+                  "one plane count per map");
     size_t at = 0;
-    for (int i = 0; i < 13; ++i) {
+    for (size_t i = 0; i < sizeof(order) / sizeof(order[0]); ++i) {
         *order[i] = base + at;
         at += ((size_t)kMapPlanes[i] * hw + 63) & ~(size_t)63;
     }

@@ -24,9 +24,9 @@ namespace {
 
 using namespace bvml_refine;
 
-// 32 MiB: the maps of a grid of up to about 5,500 pixels (1,523 planes per
+// 32 MiB: the maps of a grid of up to 5,086 pixels (1,649 planes per
 // pixel; a 60 x 80 grid, the refiner's size for a 480 x 640 image, needs
-// 7,310,400 floats).
+// 7,915,200 floats).
 constexpr size_t kScratchFloats = size_t(8) << 20;
 static __device__ __align__(256) float scratch[kScratchFloats];
 
@@ -81,7 +81,7 @@ extern "C" int bvml_dsine_refiner_forward_noalloc(bvml_dsine_refiner* r, const f
         return fail(BVML_DSINE_ESIZE,
                     "forward_noalloc: a " + std::to_string(h8) + " x " + std::to_string(w8) +
                         " grid needs " + std::to_string(need) + " floats of scratch; the maximum is " +
-                        std::to_string(kScratchFloats) + " (about 5,500 pixels)");
+                        std::to_string(kScratchFloats) + " (about 5,000 pixels)");
     const int dev = refiner_device(r);
     if (dev < 0 || !refiner_uploaded(r))
         return fail(BVML_DSINE_EWEIGHTS,

@@ -276,6 +276,15 @@ long long bvml_dsine_heads_packed_size(int out);
  *   bvml_dsine_conv_gru_update_f32 convq (C filters, 5x5); writes
  *     h_new = (1 - z) h + z tanh(s + bias_q) to h_new and, when non-NULL,
  *     h_copy, as bvml_dsine_gru_update_f32 does; h_new may be h; C % 64 == 0
+ *   bvml_dsine_conv_gru_gates_sum_f32, bvml_dsine_conv_gru_update_sum_f32
+ *     the same with sums to add before the bias: sum0 holds 2C (gates) or C
+ *     (update) planes in the packed channel order, i.e. what
+ *     bvml_dsine_conv_f32 writes with the same packing (interleave = 1 for
+ *     the gates), or NULL.  By linearity, conv(x, W) = conv(x_a, W_a) +
+ *     conv(x_b, W_b) over a split of the input channels: the refiner
+ *     computes the part over its constant channels (feature, uv) once per
+ *     forward and passes it as sum0 to every iteration's convolution over
+ *     the hidden state (each sum still fp32, in another order)
  * Outputs must not overlap x (or, for the fused ones, the other inputs and
  * each other).  No counterpart in the reference (brotensor's conv2d_forward
  * followed by its elementwise ops).
@@ -291,6 +300,14 @@ int bvml_dsine_conv_gru_gates_f32(const float* x, int cin, int H, int W, const f
 int bvml_dsine_conv_gru_update_f32(const float* x, int cin, int H, int W, const float* wp, int C,
                                    const float* bias_q, const float* z, const float* h,
                                    float* h_new, float* h_copy, void* stream);
+int bvml_dsine_conv_gru_gates_sum_f32(const float* x, int cin, int H, int W, const float* wp,
+                                      int C, const float* sum0, const float* bias_z,
+                                      const float* bias_r, const float* h, float* z, float* rh,
+                                      void* stream);
+int bvml_dsine_conv_gru_update_sum_f32(const float* x, int cin, int H, int W, const float* wp,
+                                       int C, const float* sum0, const float* bias_q,
+                                       const float* z, const float* h, float* h_new,
+                                       float* h_copy, void* stream);
 
 /* Message for the calling thread's last non-zero status ("" if none). */
 const char* bvml_dsine_last_error(void);

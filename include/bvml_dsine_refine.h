@@ -127,8 +127,8 @@ int bvml_dsine_refiner_forward_cpu(bvml_dsine_refiner* r, const float* normal,
  * bvml_dsine_refiner_forward: the same result, bit for bit), and the weights
  * must already be on the device: a bvml_dsine_refiner_forward after the last
  * load_file / set_tensor uploads them (else BVML_DSINE_EWEIGHTS).  The array
- * holds 8,388,608 floats (32 MiB) per GPU, the maps of a grid of up to about
- * 5,500 pixels (1,523 planes; a 60 x 80 grid needs 7,310,400 floats); a
+ * holds 8,388,608 floats (32 MiB) per GPU, the maps of a grid of up to
+ * 5,086 pixels (1,649 planes; a 60 x 80 grid needs 7,915,200 floats); a
  * larger grid returns BVML_DSINE_ESIZE.  Every call on one GPU uses that
  * GPU's array, which keeps the last call's contents (nothing in it needs to
  * start at zero), so calls on one GPU run in the order they were made: each

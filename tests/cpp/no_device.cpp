@@ -81,4 +81,16 @@ int bvml_dsine_conv_gru_update_f32(const float*, int, int, int, const float*, in
     no_device("bvml_dsine_conv_gru_update_f32");
 }
 
+int bvml_dsine_conv_gru_gates_sum_f32(const float*, int, int, int, const float*, int,
+                                      const float*, const float*, const float*, const float*,
+                                      float*, float*, void*) {
+    no_device("bvml_dsine_conv_gru_gates_sum_f32");
+}
+
+int bvml_dsine_conv_gru_update_sum_f32(const float*, int, int, int, const float*, int,
+                                       const float*, const float*, const float*, const float*,
+                                       float*, float*, void*) {
+    no_device("bvml_dsine_conv_gru_update_sum_f32");
+}
+
 }  // extern "C"

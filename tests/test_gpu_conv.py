@@ -135,6 +135,77 @@ def test_conv_gru(cuda, H, W):
     assert np.array_equal(ghn, hc.out.cpu().numpy().reshape(C, H, W))
 
 
+@pytest.mark.parametrize("H,W", [(24, 32), (13, 19)])
+def test_conv_gru_split_sums(cuda, H, W):
+    """The _sum entry points: convz + convr and convq over the hidden state's
+    64 channels, with the part over the other 66 (feature, uv) computed by
+    bvml_dsine_conv_f32 from the same split weights and passed as sum0, as
+    the refiner runs them; against the float64 restatement of the whole
+    130-channel convolutions, to the whole convolutions' bars."""
+    import torch
+    say(f"[gpu] conv gru split sums {H}x{W}")
+    C, cin, ch = 64, 130, 64
+    rng = np.random.default_rng(7 * H + W)
+    hx = rng.standard_normal((cin, H, W)).astype(np.float32)
+    h = hx[:C].copy()
+    wz, wr, wq = (rng.uniform(-1, 1, (C, cin, 5, 5)).astype(np.float32) / np.sqrt(cin * 25)
+                  for _ in range(3))
+    bz, br, bq = (rng.uniform(-0.3, 0.3, C).astype(np.float32) for _ in range(3))
+    dev = torch.device(cuda)
+    lib = _lib.load()
+    stream = torch.cuda.current_stream().cuda_stream
+    wzr = np.concatenate([wz, wr])
+    wzr_h = _dev(_lib.conv_pack_f32(wzr[:, :ch], interleave=True), dev)
+    wzr_f = _dev(_lib.conv_pack_f32(wzr[:, ch:], interleave=True), dev)
+    wq_h = _dev(_lib.conv_pack_f32(wq[:, :ch]), dev)
+    wq_f = _dev(_lib.conv_pack_f32(wq[:, ch:]), dev)
+    hxd, hd = _dev(hx, dev), _dev(h, dev)
+    bzd, brd, bqd = _dev(bz, dev), _dev(br, dev), _dev(bq, dev)
+    s_zr = torch.empty(2 * C * H * W, device=dev)
+    s_q = torch.empty(C * H * W, device=dev)
+    xf = hxd[ch:]
+    assert lib.bvml_dsine_conv_f32(xf.data_ptr(), cin - ch, H, W, wzr_f.data_ptr(), 2 * C, 5,
+                                   s_zr.data_ptr(), stream) == _lib.OK, _lib.last_error()
+    assert lib.bvml_dsine_conv_f32(xf.data_ptr(), cin - ch, H, W, wq_f.data_ptr(), C, 5,
+                                   s_q.data_ptr(), stream) == _lib.OK, _lib.last_error()
+    z = Guarded(C * H * W, dev)
+    rh = Guarded(C * H * W, dev, shift=3)
+    st = lib.bvml_dsine_conv_gru_gates_sum_f32(hxd.data_ptr(), ch, H, W, wzr_h.data_ptr(), C,
+                                               s_zr.data_ptr(), bzd.data_ptr(), brd.data_ptr(),
+                                               hd.data_ptr(), z.out.data_ptr(), rh.out.data_ptr(),
+                                               stream)
+    assert st == _lib.OK, _lib.last_error()
+    hn = Guarded(C * H * W, dev, shift=2)
+    st = lib.bvml_dsine_conv_gru_update_sum_f32(rh.out.data_ptr(), ch, H, W, wq_h.data_ptr(), C,
+                                                s_q.data_ptr(), bqd.data_ptr(), z.out.data_ptr(),
+                                                hd.data_ptr(), hn.out.data_ptr(), None, stream)
+    assert st == _lib.OK, _lib.last_error()
+    torch.cuda.synchronize()
+    assert z.intact() and rh.intact() and hn.intact()
+    sz, ez = conv64(hx, wz)
+    sr, er = conv64(hx, wr)
+    gz = z.out.cpu().numpy().reshape(C, H, W)
+    grh = rh.out.cpu().numpy().reshape(C, H, W)
+    want_z = _sig(sz + bz[:, None, None])
+    want_rh = _sig(sr + br[:, None, None]) * h
+    say(f"    gates: z max-abs {np.abs(gz - want_z).max():.3e}, rh max-abs "
+        f"{np.abs(grh - want_rh).max():.3e}")
+    assert (np.abs(gz - want_z) <= ez / 4 + 8 * U).all()
+    assert (np.abs(grh - want_rh) <= np.abs(h) * (er / 4 + 8 * U)).all()
+    rhx_h = np.concatenate([grh, hx[C:]])
+    sq, eq = conv64(rhx_h, wq)
+    q = np.tanh(sq + bq[:, None, None])
+    want_h = (1 - gz.astype(np.float64)) * h + gz * q
+    ghn = hn.out.cpu().numpy().reshape(C, H, W)
+    say(f"    update: max-abs {np.abs(ghn - want_h).max():.3e}")
+    assert (np.abs(ghn - want_h) <= np.abs(gz) * eq + 16 * U * (np.abs(h) + np.abs(q))).all()
+    # sum0 must not overlap an output
+    assert lib.bvml_dsine_conv_gru_gates_sum_f32(hxd.data_ptr(), ch, H, W, wzr_h.data_ptr(), C,
+                                                 z.out.data_ptr(), bzd.data_ptr(),
+                                                 brd.data_ptr(), hd.data_ptr(), z.out.data_ptr(),
+                                                 rh.out.data_ptr(), stream) == _lib.EALIAS
+
+
 def test_conv_rejects(cuda):
     import torch
     lib = _lib.load()
