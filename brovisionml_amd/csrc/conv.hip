@@ -55,7 +55,7 @@ struct ConvArgs {
     const float* z;     // kUpdate: the update gate
     float* o0;          // kGates: z, kUpdate: h_new
     float* o1;          // kGates: rh, kUpdate: h_copy (may be NULL)
-    const float* s0;    // kGates, kUpdate: sums to add before the bias (packed order), or NULL
+    const float* s0;    // kGates, kUpdate: sums to add (packed order, the accumulators' start), or NULL
     int cin, cout, H, W, mblocks, tiles_x;
     long long HW;
 };
@@ -165,6 +165,24 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
     for (int m = 0; m < 4; ++m)
 #pragma unroll
         for (int n = 0; n < NB; ++n) acc[m][n] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+    // sums to add (the fused launches' sum0) start group 0's accumulators:
+    // their loads overlap the first halo's, where a read in the epilogue
+    // would stall every workgroup at once (convq over r*h at 256 x 256: 145
+    // against 157 us; convz + convr over h 260 against 265)
+    if (EPI != kPlain && a.s0 && ks == 0) {
+        const int x = tx0 + col;
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            const int y = ty0 + wn * NB + n;
+            if (x >= a.W || y >= a.H) continue;
+            const size_t px = (size_t)y * a.W + x;
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+                    acc[m][n][r] = a.s0[(size_t)(16 * (mb0 + m) + 4 * g + r) * a.HW + px];
+        }
+    }
 
     float pre[PER_T];
     halo_load(ks, pre);
@@ -310,10 +328,6 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
                     if (c >= a.cout / 2) continue;
                     const size_t i = (size_t)c * a.HW + px;
                     float sz = acc[m][n][r], sr = acc[m + 1][n][r];
-                    if (a.s0) {
-                        sz += a.s0[(size_t)(16 * (mb0 + m) + 4 * g + r) * a.HW + px];
-                        sr += a.s0[(size_t)(16 * (mb0 + m + 1) + 4 * g + r) * a.HW + px];
-                    }
                     const float zz = sigmoid(sz + a.b0[c]);
                     const float rr = sigmoid(sr + a.b1[c]);
                     a.o0[i] = zz;
@@ -328,7 +342,6 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
                     if (c >= a.cout) continue;
                     const size_t i = (size_t)c * a.HW + px;
                     float sq = acc[m][n][r];
-                    if (a.s0) sq += a.s0[i];
                     const float v = gru_mix(a.z[i], a.h[i], tanhf(sq + a.b0[c]));
                     a.o0[i] = v;
                     if (a.o1) a.o1[i] = v;
