@@ -113,7 +113,14 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
     const int wave_s = __builtin_amdgcn_readfirstlane(wave);
     const int g = lane >> 4, col = lane & 15;
     const int wm = wave % WM, wn = wave / WM;
-    const int tx0 = (blockIdx.x % a.tiles_x) * kTW, ty0 = (blockIdx.x / a.tiles_x) * TH;
+    // (k = 5) each XCD takes a contiguous run of tiles, so neighbouring tiles
+    // share their halo lines and output lines in that XCD's L2 (workgroups go
+    // to the XCDs in turn): convz + convr over h at 256 x 256 237 against
+    // 242-246 us, convq 135-136 against 137-138; the 3x3 layers lose by it
+    const int nbx = (int)gridDim.x, bx = (int)blockIdx.x, xcd = bx & 7;
+    const int tile = K != 5 ? bx
+                            : xcd * (nbx >> 3) + (xcd < (nbx & 7) ? xcd : (nbx & 7)) + (bx >> 3);
+    const int tx0 = (tile % a.tiles_x) * kTW, ty0 = (tile / a.tiles_x) * TH;
     const int mb0 = blockIdx.y * (4 * WM) + 4 * wm;  // the wave's first M-block
     const int nchunks = (a.cin + kCC - 1) / kCC;
     // every group makes the same number of trips (the barriers are the
@@ -184,12 +191,56 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
         }
     }
 
+    // The A operands from L2 (!SW): a ring of AR register slots, AR - 1 taps
+    // ahead of the products.  At k = 5 the ring runs across chunk boundaries
+    // (AR = 5 divides the 25 taps, so tap t of every chunk takes slot t % AR):
+    // a chunk's first taps are loaded during the previous chunk, ahead of
+    // that chunk's halo loads, which the products would otherwise wait for
+    // (vector loads complete in issue order), and the barrier between chunks
+    // waits for the LDS writes only, leaving those loads in flight across it
+    // (convz + convr over h at 256 x 256, with the tile order above: 233-234
+    // against 237 us; the [feature, uv] part 232 against 235).  At k = 3,
+    // two taps ahead within each chunk (the 256-channel 3x3 layer: 169
+    // against 173-175 us with the ring).
+    constexpr bool XC = !SW && K == 5;
+    constexpr int AR = XC ? 5 : 3;
+    static_assert(TAPS % AR == 0, "ring slots divide the taps");
+    const size_t tap_stride = (size_t)a.mblocks * 64;
+    const float* wbase = a.wp + (size_t)mb0 * 64 + lane;
+    float aw[SW ? 1 : AR][4];
+    auto a_load = [&](int chunk, int tap, int slot) {
+        const float* wc = wbase + ((size_t)chunk * TAPS + tap) * tap_stride;
+#pragma unroll
+        for (int m = 0; m < 4; ++m) aw[slot][m] = wc[m * 64];
+    };
+    auto chunk_barrier = [&]() {
+        if constexpr (SW) {
+            __builtin_amdgcn_s_waitcnt(0);  // the weight copies (counted with the loads)
+            __syncthreads();
+        } else if constexpr (!XC) {
+            __syncthreads();
+        } else {
+            // this wave's halo writes done (lgkmcnt(0)), then the barrier;
+            // the compiler keeps every LDS access on its side of it (the
+            // barrier builtin alone is no memory fence to it)
+            asm volatile("" ::: "memory");
+            __builtin_amdgcn_s_waitcnt(0xc07f);
+            __builtin_amdgcn_s_barrier();
+            asm volatile("" ::: "memory");
+        }
+    };
+
     float pre[PER_T];
     halo_load(ks, pre);
     if (SW && ks < nchunks) w_load(ks, 0);
+    if constexpr (XC) {
+        if (ks < nchunks) {
+#pragma unroll
+            for (int q = 0; q < AR - 1; ++q) a_load(ks, q, q);
+        }
+    }
     halo_store(0, pre);
-    __builtin_amdgcn_s_waitcnt(0);  // the weight copies (counted with the loads)
-    __syncthreads();
+    chunk_barrier();
     for (int trip = 0; trip < trips; ++trip) {
         const int chunk = trip * KS + ks;
         const int buf = trip & 1;
@@ -203,18 +254,18 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
         if (chunk < nchunks) {
         const float* hb = halo[ks][buf] + g * HSP + (wn * NB) * HC + col;
         if constexpr (!SW) {
-        const size_t tap_stride = (size_t)a.mblocks * 64;
-        const float* wc = a.wp + (size_t)mb0 * 64 + lane + (size_t)chunk * TAPS * tap_stride;
-        // the A operands (L2) and the B operands (LDS) two taps ahead, the
+        // (the ring's taps past this chunk's last: the next chunk's first;
+        // after the last chunk, the last chunk's again, unused)
+        const int next_chunk = chunk + KS < nchunks ? chunk + KS : nchunks - 1;
+        // the B operands (LDS) two taps ahead, the A operands AR - 1, the
         // loads of each tap issued before the previous tap's products (a
         // scheduling barrier keeps them there: convz + convr at 256 x 256
         // 466-468 us against 504-509 with the compiler's own order and the B
         // operands one tap ahead)
-        float af[3][4];
+        if constexpr (!XC) {
 #pragma unroll
-        for (int q = 0; q < 2; ++q)
-#pragma unroll
-            for (int m = 0; m < 4; ++m) af[q][m] = wc[(size_t)q * tap_stride + m * 64];
+            for (int q = 0; q < AR - 1; ++q) a_load(chunk, q, q);
+        }
         float bf[3][NB];
 #pragma unroll
         for (int n = 0; n < NB; ++n) bf[0][n] = hb[n * HC];
@@ -227,17 +278,16 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
 #pragma unroll
                 for (int n = 0; n < NB; ++n) bf[(t + 2) % 3][n] = hb[(n + ky) * HC + kx];
             }
-            if (t + 2 < TAPS) {
-#pragma unroll
-                for (int m = 0; m < 4; ++m)
-                    af[(t + 2) % 3][m] = wc[(size_t)(t + 2) * tap_stride + m * 64];
-            }
+            if (t + AR - 1 < TAPS)
+                a_load(chunk, t + AR - 1, (t + AR - 1) % AR);
+            else if (XC)
+                a_load(next_chunk, t + AR - 1 - TAPS, (t + AR - 1) % AR);
             __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
             for (int m = 0; m < 4; ++m)
 #pragma unroll
                 for (int n = 0; n < NB; ++n)
-                    acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(af[t % 3][m], bf[t % 3][n],
+                    acc[m][n] = __builtin_amdgcn_mfma_f32_16x16x4f32(aw[t % AR][m], bf[t % 3][n],
                                                                     acc[m][n], 0, 0, 0);
         }
         } else {
@@ -271,8 +321,7 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
         }
         }
         if (more) halo_store(buf ^ 1, pre);
-        __builtin_amdgcn_s_waitcnt(0);  // the next chunk's weight copies
-        __syncthreads();
+        chunk_barrier();
     }
     if constexpr (KS > 1) {
         // the other groups' sums into group 0's, two N-blocks at a time
