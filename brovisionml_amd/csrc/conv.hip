@@ -71,10 +71,10 @@ __device__ __forceinline__ float gru_mix(float z, float h, float q) {
 // K: kernel size; TH: tile rows; WM x WN waves (WM along the channels, WN
 // along the tile rows); each wave 4 M-blocks (64 output channels) x NB tile rows.
 // KS: groups of those 4 waves that split the input channels (group g takes
-// chunks g, g + KS, ...; the other groups' sums meet group 0's in LDS before
-// its epilogue).  A grid with one workgroup per CU leaves each SIMD one wave
-// of 4-wave workgroups; with KS = 2 it has two, and one wave's MFMAs run
-// while the other waits for its operands.
+// chunks g, g + KS, ...; with KS = 2 the two groups' sums meet in LDS and
+// each group finishes half of the tile rows).  A grid with one workgroup per
+// CU leaves each SIMD one wave of 4-wave workgroups; with KS = 2 it has two,
+// and one wave's MFMAs run while the other waits for its operands.
 // Whether a launch stages each chunk's weights in LDS with direct-to-LDS
 // loads (the products then wait on LDS reads only) or has every wave read
 // its A operands from L2 two taps ahead.  Same-box A/B at 256 x 256, both
@@ -99,7 +99,7 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
     constexpr int NB = TH / WN;                                      // tile rows per wave
     constexpr int TAPS = K * K;
     static_assert(WM * WN == kThreads / 64, "4 waves");
-    static_assert(KS == 1 || NB % 2 == 0, "the split's sums meet two N-blocks at a time");
+    static_assert(KS == 1 || NB % 2 == 0, "each group of the split finishes NB / 2 rows");
     // the workgroup's weights of one chunk, [tap][its 4 WM M-blocks][64 lanes],
     // staged in LDS (SW) or read by each wave from L2
     constexpr bool SW = stage_weights(K, WM);
@@ -323,29 +323,42 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
         if (more) halo_store(buf ^ 1, pre);
         chunk_barrier();
     }
+    // (KS = 2) the groups' sums meet in LDS and each group finishes half of
+    // the tile rows, group 0 the first NB/2 and group 1 the rest: each hands
+    // the other its partial of the other's rows (the sums are the same either
+    // way round, a + b = b + a), so the epilogue's loads and stores run on
+    // all 8 waves (convq over r*h at 256 x 256: 127 against 136-137 us when
+    // group 0 finished every row)
+    int n_lo = 0, n_hi = NB;
     if constexpr (KS > 1) {
-        // the other groups' sums into group 0's, two N-blocks at a time
-        __shared__ v4f xch[KS - 1][4][2][kThreads];
+        static_assert(KS == 2, "two wave groups");
+        constexpr int HN = NB / 2;
+        __shared__ v4f xch[2][4][HN][kThreads];
+        if (ks == 0) {
 #pragma unroll
-        for (int n0 = 0; n0 < NB; n0 += 2) {
-            if (ks > 0) {
+            for (int m = 0; m < 4; ++m)
 #pragma unroll
-                for (int m = 0; m < 4; ++m)
+                for (int j = 0; j < HN; ++j) xch[0][m][j][tid] = acc[m][HN + j];
+        } else {
 #pragma unroll
-                    for (int j = 0; j < 2; ++j) xch[ks - 1][m][j][tid] = acc[m][n0 + j];
-            }
-            __syncthreads();
-            if (ks == 0) {
+            for (int m = 0; m < 4; ++m)
 #pragma unroll
-                for (int q = 0; q < KS - 1; ++q)
-#pragma unroll
-                    for (int m = 0; m < 4; ++m)
-#pragma unroll
-                        for (int j = 0; j < 2; ++j) acc[m][n0 + j] += xch[q][m][j][tid];
-            }
-            __syncthreads();
+                for (int j = 0; j < HN; ++j) xch[1][m][j][tid] = acc[m][j];
         }
-        if (ks > 0) return;
+        __syncthreads();
+        if (ks == 0) {
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int j = 0; j < HN; ++j) acc[m][j] += xch[1][m][j][tid];
+        } else {
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int j = 0; j < HN; ++j) acc[m][HN + j] += xch[0][m][j][tid];
+        }
+        n_lo = ks == 0 ? 0 : HN;
+        n_hi = n_lo + HN;
     }
 
     // epilogue: lane (g, col), register r of acc[m][n] is output channel
@@ -356,7 +369,7 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
         const int y = ty0 + wn * NB + n;
-        if (y >= a.H) continue;
+        if (n < n_lo || n >= n_hi || y >= a.H) continue;
         const size_t px = (size_t)y * a.W + x;
         if constexpr (EPI == kPlain) {
 #pragma unroll
