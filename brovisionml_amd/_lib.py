@@ -51,6 +51,7 @@ EXPORTS = (
     "bvml_dsine_conv_gru_update_f32",
     "bvml_dsine_conv_gru_gates_sum_f32",
     "bvml_dsine_conv_gru_update_sum_f32",
+    "bvml_dsine_conv_heads_f32",
     "bvml_dsine_last_error",
     "bvml_dsine_version",
 )
@@ -141,6 +142,8 @@ def load(path: str = LIB) -> ctypes.CDLL:
     lib.bvml_dsine_conv_gru_update_sum_f32.argtypes = [vp, i, i, i, vp, i, vp, vp, vp, vp, vp, vp,
                                                        vp]
     lib.bvml_dsine_conv_gru_update_sum_f32.restype = i
+    lib.bvml_dsine_conv_heads_f32.argtypes = [vp, i, i, i, vp, i, vp, vp, vp, vp, vp, vp, vp, vp]
+    lib.bvml_dsine_conv_heads_f32.restype = i
     lib.bvml_dsine_last_error.argtypes = []
     lib.bvml_dsine_last_error.restype = ctypes.c_char_p
     lib.bvml_dsine_version.argtypes = []
@@ -328,6 +331,27 @@ def heads_mlp_f32(t0: int, b0: int, w2p: int, b2: int, w4p, b4, outs, H: int, W:
     return load().bvml_dsine_heads_mlp_f32(
         t0, b0, w2p, b2, (vp * nh)(*w4p), (vp * nh)(*[b or None for b in b4]),
         (ctypes.c_int * nh)(*outs), nh, H, W, (vp * nh)(*out), stream)
+
+
+def heads_w2q_f32(w2):
+    """Each head's middle-layer weights (nheads, 64, 64[, 1, 1]) in the
+    last-layer layout bvml_dsine_conv_heads_f32 reads (W2 packed as a
+    64-output last layer), back to back; a float32 numpy array."""
+    import numpy as np
+    w2 = np.asarray(w2, np.float32).reshape(-1, 64, 64)
+    return np.concatenate(heads_pack_f32(w2, list(w2))[1])
+
+
+def conv_heads_f32(x: int, cin: int, H: int, W: int, wp: int, b0: int, w2q: int, b2: int, w4p,
+                   b4, outs, out, stream: int = 0) -> int:
+    """Raw call of bvml_dsine_conv_heads_f32; pointers are integer device
+    addresses, w4p / b4 / out lists of them (0 in b4 for no bias), outs the
+    output counts. Returns the status."""
+    vp = ctypes.c_void_p
+    nh = len(outs)
+    return load().bvml_dsine_conv_heads_f32(
+        x, cin, H, W, wp, nh, b0, w2q, b2, (vp * nh)(*w4p), (vp * nh)(*[b or None for b in b4]),
+        (ctypes.c_int * nh)(*outs), (vp * nh)(*out), stream)
 
 
 def conv_pack_f32(w, interleave: bool = False):

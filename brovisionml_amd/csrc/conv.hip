@@ -43,7 +43,7 @@ constexpr int kTW = 16;      // tile width: one MFMA column block per tile row
 constexpr int kCC = bvml::pack::kConvChunk;  // input channels per chunk (one k-step per tap)
 constexpr int kThreads = 256;
 
-enum Epi : int { kPlain = 0, kGates = 1, kUpdate = 2 };
+enum Epi : int { kPlain = 0, kGates = 1, kUpdate = 2, kHeads = 3 };
 
 struct ConvArgs {
     const float* x;     // cin planes of H x W
@@ -56,9 +56,36 @@ struct ConvArgs {
     float* o0;          // kGates: z, kUpdate: h_new
     float* o1;          // kGates: rh, kUpdate: h_copy (may be NULL)
     const float* s0;    // kGates, kUpdate: sums to add (packed order, the accumulators' start), or NULL
+    // kHeads (b0: the 3x3 layer's bias, b1: the middle layers' bias)
+    const float* w2q;   // the middle layers, 4096 floats per head in the last-layer layout
+    const float* w4p[4];
+    const float* b4[4];  // NULL: no bias
+    float* hout[4];
+    int outs[4];
     int cin, cout, H, W, mblocks, tiles_x;
     long long HW;
 };
+
+__device__ __forceinline__ float relu(float v) { return v < 0.0f ? 0.0f : v; }
+
+// base[byte_off / 4] with a uniform base pointer and a 32-bit per-lane byte
+// offset: the scalar-base + vector-offset load form, no 64-bit address per load
+__device__ __forceinline__ float ldo(const float* base, uint32_t byte_off) {
+    return *reinterpret_cast<const float*>(reinterpret_cast<const char*>(base) + byte_off);
+}
+
+// Raw buffer loads of packed weights: the descriptor (base, bytes) in scalar
+// registers, a per-lane byte offset and a wave-uniform one (a scalar
+// register), so a run of weight loads keeps no address registers of its own.
+constexpr int kBufferWord3 = 0x00020000;  // gfx9 raw-buffer descriptor word 3
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t weights_rsrc(const float* w, uint32_t bytes) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<float*>(w), (short)0, (int)bytes,
+                                             kBufferWord3);
+}
+__device__ __forceinline__ float ldw(__amdgpu_buffer_rsrc_t r, uint32_t byte_off, uint32_t soff) {
+    return __builtin_bit_cast(float,
+                              __builtin_amdgcn_raw_buffer_load_b32(r, (int)byte_off, (int)soff, 0));
+}
 
 __device__ __forceinline__ float sigmoid(float x) { return 1.0f / (1.0f + expf(-x)); }
 
@@ -86,7 +113,10 @@ __device__ __forceinline__ float gru_mix(float z, float h, float q) {
 constexpr bool stage_weights(int K, int WM) { return K == 3 && WM == 1; }
 
 template <int K, int TH, int WM, int WN, int EPI, int KS>
-__global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
+// (the fused heads launch holds three 4-wave workgroups per CU, one wave
+// per SIMD each, so its registers stay within a third of a SIMD's)
+__global__ __launch_bounds__(kThreads * KS)
+__attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : 1))) void conv_kernel(ConvArgs a) {
     constexpr int P = K / 2;
     constexpr int HR = TH + K - 1, HC = kTW + K - 1, HS = HR * HC;  // halo rows, cols, size
     constexpr int HALO = kCC * HS;                                   // floats per chunk
@@ -176,7 +206,7 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
     // their loads overlap the first halo's, where a read in the epilogue
     // would stall every workgroup at once (convq over r*h at 256 x 256: 145
     // against 157 us; convz + convr over h 260 against 265)
-    if (EPI != kPlain && a.s0 && ks == 0) {
+    if ((EPI == kGates || EPI == kUpdate) && a.s0 && ks == 0) {
         const int x = tx0 + col;
 #pragma unroll
         for (int n = 0; n < NB; ++n) {
@@ -365,6 +395,126 @@ __global__ __launch_bounds__(kThreads * KS) void conv_kernel(ConvArgs a) {
     // 16 (mb0 + m) + 4 g + r (in the packed order) at pixel
     // (ty0 + wn NB + n, tx0 + col)
     const int x = tx0 + col;
+    if constexpr (EPI == kHeads) {
+        // The rest of head h = blockIdx.y (the wave's 64 channels, WM = 1) on
+        // the matrix cores, every lane taking part (lanes past the map
+        // compute on the zero padding and store nothing):
+        //   a = relu(acc + b0);  t = relu(W2 a + b2);  out = W4 t + b4.
+        // acc[m][n] holds channels {16 m + 4 g + r} at lane (g, col), which
+        // is the B operand of a step whose 4 inputs are those channels, so
+        // both 1x1 layers read the previous layer's registers directly, their
+        // weights packed in that input order (the last-layer layout).
+        static_assert(WM == 1, "one head per wave");
+        const int h = blockIdx.y;
+        const __amdgpu_buffer_rsrc_t w2 =
+            weights_rsrc(a.w2q + (size_t)h * (16 * 4 * 64), 16 * 4 * 64 * 4);
+        const float* b0 = a.b0 + 64 * h;
+        const float* b2 = a.b1 + 64 * h;
+        const int nout = a.outs[h];
+        const int nob = (nout + 15) / 16;
+        const __amdgpu_buffer_rsrc_t w4 = weights_rsrc(a.w4p[h], 4096u * nob);
+        const uint32_t lb = 4u * lane, gb = 16u * g;  // this lane's byte offsets
+        const float* b4 = a.b4[h];
+        float* out = a.hout[h];
+        // Each step's 4 weights are loaded one step ahead of its products
+        // from buffer descriptors (a scheduling barrier keeps them there and
+        // keeps the compiler from hoisting every weight load at once, and
+        // the descriptors keep 64-bit addresses out of the registers): 141
+        // VGPRs, three workgroups per CU.  (256 x 256, 3 heads: 172 us
+        // against 182 for the 3x3 layer and bvml_dsine_heads_mlp_f32; two
+        // tile rows per pass, 173-174.)
+        {
+            // a = relu(acc + b0), in place
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float bias = ldo(b0, gb + 4u * (16 * m + r));
+#pragma unroll
+                    for (int j = 0; j < NB; ++j)
+                        acc[m][j][r] = relu(acc[m][j][r] + bias);
+                }
+            // t = W2 a: output block mo, step (m, r) takes channels {16 m + 4 g + r}
+            v4f t[4][NB];
+#pragma unroll
+            for (int mo = 0; mo < 4; ++mo)
+#pragma unroll
+                for (int j = 0; j < NB; ++j) t[mo][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+            float cw[2][4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cw[0][r] = ldw(w2, lb, 256u * r);
+#pragma unroll
+            for (int st = 0; st < 16; ++st) {  // st = 4 mo + m
+                if (st + 1 < 16) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+                        cw[(st + 1) & 1][r] = ldw(w2, lb, 256u * ((st + 1) * 4 + r));
+                }
+                __builtin_amdgcn_sched_barrier(0);
+                const int mo = st / 4, m = st % 4;
+#pragma unroll
+                for (int r = 0; r < 4; ++r)
+#pragma unroll
+                    for (int j = 0; j < NB; ++j)
+                        t[mo][j] = __builtin_amdgcn_mfma_f32_16x16x4f32(
+                            cw[st & 1][r], acc[m][j][r], t[mo][j], 0, 0, 0);
+            }
+            // t = relu(t + b2)
+#pragma unroll
+            for (int mo = 0; mo < 4; ++mo)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const float bias = ldo(b2, gb + 4u * (16 * mo + r));
+#pragma unroll
+                    for (int j = 0; j < NB; ++j) t[mo][j][r] = relu(t[mo][j][r] + bias);
+                }
+            // out = W4 t + b4, 16 outputs at a time
+            for (int ob = 0; ob < nob; ++ob) {
+                const uint32_t wb = 4096u * ob;
+                v4f o[NB];
+#pragma unroll
+                for (int j = 0; j < NB; ++j) o[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
+                float cw4[2][4];
+#pragma unroll
+                for (int r = 0; r < 4; ++r) cw4[0][r] = ldw(w4, lb, wb + 256u * r);
+#pragma unroll
+                for (int mo = 0; mo < 4; ++mo) {
+                    if (mo + 1 < 4) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r)
+                            cw4[(mo + 1) & 1][r] = ldw(w4, lb, wb + 256u * ((mo + 1) * 4 + r));
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r)
+#pragma unroll
+                        for (int j = 0; j < NB; ++j)
+                            o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(cw4[mo & 1][r], t[mo][j][r],
+                                                                        o[j], 0, 0, 0);
+                }
+                if (x >= a.W) continue;
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int oc = 16 * ob + 4 * g + r;
+                    if (oc >= nout) continue;
+                    const float bias = b4 ? ldo(b4, 4u * oc) : 0.0f;
+                    // plane 16 ob + r from a uniform base, plus this lane's
+                    // 4 g planes and pixel as a 32-bit byte offset (the map is
+                    // at most 2^26 pixels)
+                    float* ob_base = out + (size_t)(16 * ob + r) * a.HW;
+#pragma unroll
+                    for (int j = 0; j < NB; ++j) {
+                        const int n = j, y = ty0 + wn * NB + n;
+                        if (n < n_lo || n >= n_hi || y >= a.H) continue;
+                        const uint32_t off = 4u * (uint32_t)(4 * g * a.HW + y * a.W + x);
+                        *reinterpret_cast<float*>(reinterpret_cast<char*>(ob_base) + off) =
+                            b4 ? o[j][r] + bias : o[j][r];
+                    }
+                }
+            }
+        }
+        return;
+    }
     if (x >= a.W) return;
 #pragma unroll
     for (int n = 0; n < NB; ++n) {
@@ -476,6 +626,42 @@ int bvml_dsine_conv_f32(const float* x, int cin, int H, int W, const float* wp, 
                       : launch<3, 16, 2, 2, kPlain>(a, s, "conv");
     return k == 5 ? launch<5, 16, 1, 4, kPlain>(a, s, "conv")
                   : launch<3, 16, 1, 4, kPlain>(a, s, "conv");
+}
+
+int bvml_dsine_conv_heads_f32(const float* x, int cin, int H, int W, const float* wp, int nheads,
+                              const float* b0, const float* w2q, const float* b2,
+                              const float* const* w4p, const float* const* b4, const int* outs,
+                              float* const* out, void* stream) {
+    if (int st = check_common("conv_heads", x, cin, H, W, wp, 3)) return st;
+    if (nheads < 1 || nheads > 4)
+        return fail(BVML_DSINE_EPARAM, "conv_heads: nheads must be 1..4");
+    if (!b0 || !w2q || !b2 || !w4p || !b4 || !outs || !out)
+        return fail(BVML_DSINE_ENULL, "conv_heads: pointers must be non-NULL");
+    const long long HW = (long long)H * W;
+    if (HW > (1LL << 26)) return fail(BVML_DSINE_ESIZE, "conv_heads: more than 2^26 pixels");
+    ConvArgs a{};
+    const size_t xb = (size_t)cin * HW * 4;
+    for (int h = 0; h < nheads; ++h) {
+        if (outs[h] < 1 || outs[h] > 4096)
+            return fail(BVML_DSINE_EPARAM, "conv_heads: outs must be 1..4096");
+        if (!w4p[h] || !out[h])
+            return fail(BVML_DSINE_ENULL, "conv_heads: w4p and out must be non-NULL");
+        const size_t ob = (size_t)outs[h] * HW * 4;
+        if (overlaps(out[h], ob, x, xb))
+            return fail(BVML_DSINE_EALIAS, "conv_heads: an output overlaps x");
+        for (int e = 0; e < h; ++e)
+            if (overlaps(out[h], ob, out[e], (size_t)outs[e] * HW * 4))
+                return fail(BVML_DSINE_EALIAS, "conv_heads: outputs overlap");
+        a.w4p[h] = w4p[h];
+        a.b4[h] = b4[h];
+        a.hout[h] = out[h];
+        a.outs[h] = outs[h];
+    }
+    if (HW == 0) return BVML_DSINE_OK;
+    a.x = x; a.wp = wp; a.cin = cin; a.cout = 64 * nheads; a.H = H; a.W = W; a.HW = HW;
+    a.b0 = b0; a.b1 = b2; a.w2q = w2q;
+    a.mblocks = conv_mblocks(64 * nheads);
+    return launch<3, 16, 1, 4, kHeads>(a, static_cast<hipStream_t>(stream), "conv_heads");
 }
 
 int bvml_dsine_conv_gru_gates_sum_f32(const float* x, int cin, int H, int W, const float* wp,

@@ -11,8 +11,11 @@
 //   z, r*h = gates of conv5x5(h, [W_z; W_r] over h) + cf_zr  bvml_dsine_conv_gru_gates_sum_f32
 //   h    = (1 - z) h + z tanh(conv5x5(r*h, W_q over h) + cf_q + b_q),
 //          also into [h | uv]                                bvml_dsine_conv_gru_update_sum_f32
-//   t0   = conv3x3([h | uv], the heads' first layers)        bvml_dsine_conv_f32, 66 -> 192 or 256
-//   prob, xy, angle = the heads' 1x1 layers on relu(t0 + b0) bvml_dsine_heads_mlp_f32
+//   prob, xy, angle = the three heads (conv3x3 -> ReLU -> conv1x1 -> ReLU -> conv1x1)
+//          on [h | uv], the 1x1 layers in the 3x3 layer's epilogue
+//                                                            bvml_dsine_conv_heads_f32, 66 -> 192
+//          (last iteration, all four heads: t0 = conv3x3, 66 -> 256, then the 1x1 layers
+//          on relu(t0 + b0)                     bvml_dsine_conv_f32, bvml_dsine_heads_mlp_f32)
 //   pred = angmf_propagate(pred, prob, xy, angle) on logits  bvml_dsine_angmf_propagate_f32
 // and, in the last iteration only, the up-mask head (its 1x1 layers in the
 // same heads pass) and the convex upsample + normalise with its bias (the
@@ -518,6 +521,9 @@ struct bvml_dsine_refiner {
     const float *w_zr_h = nullptr, *w_zr_f = nullptr, *b_z = nullptr, *b_r = nullptr;
     const float *w_q_h = nullptr, *w_q_f = nullptr, *b_q = nullptr;
     const float *b_h0 = nullptr, *w2p = nullptr, *b_h2 = nullptr;
+    // the three propagate heads' middle layers in the last-layer layout, for
+    // bvml_dsine_conv_heads_f32
+    const float* w2q = nullptr;
     const float* w_h0p[2] = {};  // the 3x3 layer packed for bvml_dsine_conv_f32 (192, 256 filters)
     const float* w4p[kHeads] = {};  // the 1x1 layers packed for bvml_dsine_heads_mlp_f32
     const float* b4[kHeads] = {};
@@ -549,7 +555,8 @@ struct bvml_dsine_refiner {
 // one 192- and one 256-filter weight (each head's filters contiguous, prob,
 // xy, angle, up_mask: the first three heads are a prefix), all three packed
 // for bvml_dsine_conv_*, and the heads' 1x1 layers packed for
-// bvml_dsine_heads_mlp_f32.
+// bvml_dsine_heads_mlp_f32 (and the first three heads' middle layers again,
+// in the last-layer layout, for bvml_dsine_conv_heads_f32).
 int bvml_dsine_refiner::upload() {
     std::vector<float> w2(kHeads * kMid * kMid), w2p_h((size_t)kHeads * 4096);
     std::vector<std::vector<float>> w4p_h(kHeads);
@@ -565,6 +572,23 @@ int bvml_dsine_refiner::upload() {
     if (const int st = bvml_dsine_heads_pack_f32(w2.data(), w4src, kHeadOut, kHeads, w2p_h.data(),
                                                  w4dst))
         return fail(st, std::string("forward: heads_pack: ") + bvml_dsine_last_error());
+    // W2 of each of the first three heads packed as a 64-output last layer
+    constexpr int kProp = kHeads - 1;
+    const long long w2q_n = bvml_dsine_heads_packed_size(kMid);
+    std::vector<float> w2q_h((size_t)kProp * w2q_n), w2p_tmp((size_t)kProp * 4096);
+    {
+        const float* src[kProp];
+        float* dst[kProp];
+        int outs[kProp];
+        for (int h = 0; h < kProp; ++h) {
+            src[h] = &w2[(size_t)h * kMid * kMid];
+            dst[h] = &w2q_h[(size_t)h * w2q_n];
+            outs[h] = kMid;
+        }
+        if (const int st = bvml_dsine_heads_pack_f32(w2.data(), src, outs, kProp, w2p_tmp.data(),
+                                                     dst))
+            return fail(st, std::string("forward: heads_pack: ") + bvml_dsine_last_error());
+    }
     // [W_z; W_r] with their 16-channel blocks interleaved, and W_q, each as
     // its input channels [0, kHidden) (h) and [kHidden, kHx) (feature, uv):
     // conv(cat(h, x), W) = conv(h, W_h) + conv(x, W_x)
@@ -620,6 +644,7 @@ int bvml_dsine_refiner::upload() {
     parts.push_back({&w_h0p[1], {&wh0_p[1]}});
     parts.push_back({&b_h0, h0b});
     parts.push_back({&w2p, {&w2p_h}});
+    parts.push_back({&w2q, {&w2q_h}});
     parts.push_back({&b_h2, h2b});
     for (int h = 0; h < kHeads; ++h) {
         parts.push_back({&w4p[h], {&w4p_h[h]}});
@@ -751,14 +776,24 @@ int bvml_refine::forward_maps(bvml_dsine_refiner* r, const Maps& m, const Forwar
                                                         r->b_q, m.z, m.hx, m.hx, m.hin, stream),
                      "conv_gru_update")))
             return st;
-        // the heads (:119-127, :257-267, :276): the 3x3 layers, then the rest
-        // in one pass; the up-mask head's last bias is the upsample's
+        // the heads (:119-127, :257-267, :276): in the first four iterations
+        // the three the propagate reads, as their 3x3 layer with the rest in
+        // its epilogue; in the last all four, the 3x3 layers, then the rest
+        // in one pass (the up-mask head's last layer, 576 outputs, is too
+        // large to fuse); the up-mask head's last bias is the upsample's
         const float* b4[kHeads] = {r->b4[0], r->b4[1], r->b4[2], nullptr};
-        if ((st = ck(bvml_dsine_conv_f32(m.hin, kHin, h8, w8, r->w_h0p[last ? 1 : 0], nh * kMid,
-                                         3, m.t0, stream), "conv")) ||
-            (st = ck(bvml_dsine_heads_mlp_f32(m.t0, r->b_h0, r->w2p, r->b_h2, r->w4p, b4, kHeadOut,
-                                              nh, h8, w8, m.head, stream), "heads_mlp")))
+        if (!last) {
+            if ((st = ck(bvml_dsine_conv_heads_f32(m.hin, kHin, h8, w8, r->w_h0p[0], nh, r->b_h0,
+                                                   r->w2q, r->b_h2, r->w4p, b4, kHeadOut, m.head,
+                                                   stream), "conv_heads")))
+                return st;
+        } else if ((st = ck(bvml_dsine_conv_f32(m.hin, kHin, h8, w8, r->w_h0p[1], nh * kMid, 3,
+                                                m.t0, stream), "conv")) ||
+                   (st = ck(bvml_dsine_heads_mlp_f32(m.t0, r->b_h0, r->w2p, r->b_h2, r->w4p, b4,
+                                                     kHeadOut, nh, h8, w8, m.head, stream),
+                            "heads_mlp"))) {
             return st;
+        }
         // the propagate on the logits (:262-274)
         if ((st = ck(bvml_dsine_angmf_propagate_f32(m.pred[cur], m.head[0], m.head[1],
                                                     m.head[2], m.ray, fu, cu, fv, cv, 1, h8, w8,

@@ -309,6 +309,30 @@ int bvml_dsine_conv_gru_update_sum_f32(const float* x, int cin, int H, int W, co
                                        const float* z, const float* h, float* h_new,
                                        float* h_copy, void* stream);
 
+/*
+ * The heads' 3x3 first layers with the rest of the heads in the
+ * convolution's epilogue: what bvml_dsine_conv_f32 (k = 3, cout = 64 nheads)
+ * followed by bvml_dsine_heads_mlp_f32 computes, without the 64 nheads-plane
+ * map between them.  For heads h < nheads and every pixel p:
+ *   a = relu(conv3x3(x)[64h + c][p] + b0[64h + c])   c < 64
+ *   t = relu(W2_h a + b2_h)
+ *   out[h][o][p] = (W4_h t)[o] + b4[h][o]             o < outs[h]; b4[h] NULL: no bias
+ * wp: the 3x3 weights of the nheads x 64 filters (bvml_dsine_conv_pack_f32,
+ * k = 3); w2q: each head's W2 in the last-layer layout, nheads *
+ * bvml_dsine_heads_packed_size(64) floats back to back (bvml_dsine_heads_pack_f32
+ * with W2_h as a 64-output last layer); w4p[h], b0, b2, b4, outs as
+ * bvml_dsine_heads_mlp_f32 takes them.  Each sum fp32 (the middle layer's
+ * products in another order than bvml_dsine_heads_mlp_f32's), then its
+ * bias added once.  nheads 1..4, outs 1..4096, at most 2^26 pixels; the
+ * outputs must not overlap x or each other.  No counterpart in the
+ * reference (src/dsine_refine.cpp:119-127 runs each head as three
+ * convolutions and two ReLUs of brotensor ops).
+ */
+int bvml_dsine_conv_heads_f32(const float* x, int cin, int H, int W, const float* wp, int nheads,
+                              const float* b0, const float* w2q, const float* b2,
+                              const float* const* w4p, const float* const* b4, const int* outs,
+                              float* const* out, void* stream);
+
 /* Message for the calling thread's last non-zero status ("" if none). */
 const char* bvml_dsine_last_error(void);
 

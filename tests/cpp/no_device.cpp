@@ -93,4 +93,10 @@ int bvml_dsine_conv_gru_update_sum_f32(const float*, int, int, int, const float*
     no_device("bvml_dsine_conv_gru_update_sum_f32");
 }
 
+int bvml_dsine_conv_heads_f32(const float*, int, int, int, const float*, int, const float*,
+                              const float*, const float*, const float* const*,
+                              const float* const*, const int*, float* const*, void*) {
+    no_device("bvml_dsine_conv_heads_f32");
+}
+
 }  // extern "C"

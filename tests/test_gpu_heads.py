@@ -134,3 +134,105 @@ def test_heads_mlp_rejects(cuda):
     assert _lib.heads_mlp_f32(0, p, p, p, [p], [0], [25], 4, 4, [p]) == _lib.ENULL
     assert _lib.heads_mlp_f32(p, p, p, p, [p], [0], [25], -1, 4, [p]) == _lib.ESHAPE
     assert rf.N_ITER == 5
+
+
+def reference_fused(x, w3, b0, w2, b2, w4s, b4s):
+    """float64 restatement of the 3x3 layer and the heads after it, with the
+    rounding bound carried through: the convolution's own bound (conv64), the
+    bias adds, then the two 1x1 layers as in reference() with the middle
+    layer's inputs uncertain by the 3x3 layer's bound."""
+    from tests.test_gpu_conv import conv64
+    s3, e3 = conv64(x, w3)
+    nh = len(w4s)
+    s3 = s3.reshape(64 * nh, -1)
+    e3 = e3.reshape(64 * nh, -1)
+    outs, bounds = [], []
+    for h in range(nh):
+        pre = s3[64 * h:64 * (h + 1)] + b0[64 * h:64 * (h + 1), None]
+        a = np.maximum(pre, 0)
+        ea = e3[64 * h:64 * (h + 1)] + U * np.abs(pre)
+        W2 = w2[h].astype(np.float64)
+        s = W2 @ a + b2[64 * h:64 * (h + 1), None].astype(np.float64)
+        t = np.maximum(s, 0)
+        et = 64 * U * (np.abs(W2) @ a) + np.abs(W2) @ ea + U * np.abs(s)
+        W4 = w4s[h].astype(np.float64)
+        o = W4 @ t
+        if b4s[h] is not None:
+            o = o + b4s[h].astype(np.float64)[:, None]
+        eo = 64 * U * (np.abs(W4) @ t) + np.abs(W4) @ et + U * np.abs(o)
+        outs.append(o)
+        bounds.append(4 * eo + 1e-30)
+    return outs, bounds
+
+
+@pytest.mark.parametrize("H,W,outs,with_bias", [
+    (24, 32, (25, 50, 25), True),       # two wave groups per workgroup (a small grid)
+    (13, 19, (25, 50, 25), True),       # ragged tiles
+    (224, 240, (25, 50, 25), True),     # one wave group, three workgroups per CU
+    (16, 20, (25, 50, 25, 576), True),  # the up-mask head too
+    (7, 9, (1, 17, 33, 64), False),
+])
+def test_conv_heads(cuda, H, W, outs, with_bias):
+    """bvml_dsine_conv_heads_f32 (the 3x3 layer with the heads in its
+    epilogue) against the float64 restatement, and against the unfused
+    bvml_dsine_conv_f32 + bvml_dsine_heads_mlp_f32 to the same bound."""
+    import torch
+    nh = len(outs)
+    say(f"[gpu] conv_heads {H}x{W} outs {outs}")
+    rng = np.random.default_rng(H * 7 + W + nh)
+    HW, cin = H * W, 66
+    x = rng.standard_normal((cin, H, W)).astype(np.float32)
+    w3 = rng.uniform(-1, 1, (64 * nh, cin, 3, 3)).astype(np.float32) / np.sqrt(cin * 9)
+    b0 = rng.uniform(-0.5, 0.5, 64 * nh).astype(np.float32)
+    w2 = rng.uniform(-1 / 8, 1 / 8, (nh, 64, 64)).astype(np.float32)
+    b2 = rng.uniform(-1 / 8, 1 / 8, 64 * nh).astype(np.float32)
+    w4s = [rng.uniform(-1 / 8, 1 / 8, (n, 64)).astype(np.float32) for n in outs]
+    b4s = [rng.uniform(-1 / 8, 1 / 8, n).astype(np.float32) if with_bias else None for n in outs]
+    w2p, w4p = _lib.heads_pack_f32(w2, w4s)
+    dev = torch.device(cuda)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    xd, w3d = T(x), T(_lib.conv_pack_f32(w3))
+    b0d, b2d, w2pd, w2qd = T(b0), T(b2), T(w2p), T(_lib.heads_w2q_f32(w2))
+    w4pd = [T(w) for w in w4p]
+    b4d = [T(b) if b is not None else None for b in b4s]
+    b4p = [b.data_ptr() if b is not None else 0 for b in b4d]
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    outd = [Guarded(n * HW, dev, shift=h + 1) for h, n in enumerate(outs)]
+    st = _lib.conv_heads_f32(xd.data_ptr(), cin, H, W, w3d.data_ptr(), b0d.data_ptr(),
+                             w2qd.data_ptr(), b2d.data_ptr(), [w.data_ptr() for w in w4pd], b4p,
+                             list(outs), [o.out.data_ptr() for o in outd], stream)
+    assert st == _lib.OK, _lib.last_error()
+    # the unfused path
+    t0 = torch.empty(64 * nh * HW, device=dev)
+    lib = _lib.load()
+    assert lib.bvml_dsine_conv_f32(xd.data_ptr(), cin, H, W, w3d.data_ptr(), 64 * nh, 3,
+                                   t0.data_ptr(), stream) == _lib.OK, _lib.last_error()
+    unf = [torch.empty(n * HW, device=dev) for n in outs]
+    assert _lib.heads_mlp_f32(t0.data_ptr(), b0d.data_ptr(), w2pd.data_ptr(), b2d.data_ptr(),
+                              [w.data_ptr() for w in w4pd], b4p, list(outs), H, W,
+                              [u.data_ptr() for u in unf], stream) == _lib.OK, _lib.last_error()
+    torch.cuda.synchronize()
+    want, bound = reference_fused(x, w3, b0, w2, b2, w4s, b4s)
+    for h in range(nh):
+        assert outd[h].intact(), f"head {h} wrote outside its output"
+        got = outd[h].out.cpu().numpy().reshape(outs[h], HW).astype(np.float64)
+        ref = unf[h].cpu().numpy().reshape(outs[h], HW).astype(np.float64)
+        err = np.abs(got - want[h])
+        say(f"    head {h}: max-abs {err.max():.3e}, max err/bound {(err / bound[h]).max():.3f}, "
+            f"against the unfused path {np.abs(got - ref).max():.3e}")
+        assert (err <= bound[h]).all()
+        assert (np.abs(ref - want[h]) <= bound[h]).all()
+
+
+def test_conv_heads_rejects(cuda):
+    import torch
+    dev = torch.device(cuda)
+    x = torch.zeros(66 * 16 * 4, device=dev)
+    p = x.data_ptr()
+    f = _lib.conv_heads_f32
+    assert f(p, 66, 4, 4, p, p, p, p, [p], [0], [25], [p]) == _lib.EALIAS
+    assert f(p, 66, 4, 4, p, p, p, p, [p] * 5, [0] * 5, [1] * 5, [p] * 5) == _lib.EPARAM
+    assert f(p, 66, 4, 4, p, p, p, p, [p], [0], [0], [p]) == _lib.EPARAM
+    assert f(0, 66, 4, 4, p, p, p, p, [p], [0], [25], [p]) == _lib.ENULL
+    assert f(p, 66, -1, 4, p, p, p, p, [p], [0], [25], [p]) == _lib.ESHAPE
+    assert f(p, 66, 8193, 8193, p, p, p, p, [p], [0], [25], [p]) == _lib.ESIZE
