@@ -20,7 +20,11 @@
 //   kGates   convz and convr as one convolution whose 16-channel blocks
 //            alternate z, r: z = sigmoid(s_z + b_z), rh = sigmoid(s_r + b_r) h
 //   kUpdate  convq: h_new = (1 - z) h + z tanh(s + b_q), to h_new and h_copy
-// in the rounding of bvml_dsine_gru_gates_f32 / bvml_dsine_gru_update_f32.
+// in the rounding of bvml_dsine_gru_gates_f32 / bvml_dsine_gru_update_f32;
+//   kHeads   the heads' 3x3 first layers with the rest of each head
+//            (src/dsine_refine.cpp:119-127): relu(s + b0), a 64 x 64 1x1
+//            layer, relu, the last 1x1 layer, on the matrix cores from the
+//            accumulators' registers (bvml_dsine_conv_heads_f32).
 
 #include <hip/hip_runtime.h>
 
