@@ -743,8 +743,9 @@ int bvml_refine::forward_maps(bvml_dsine_refiner* r, const Maps& m, const Forwar
     if ((st = ck(bvml_dsine_build_uv8_f32(uv, fu, cu, fv, cv, h8, w8, stream), "build_uv8")) ||
         (st = ck(bvml_dsine_build_ray8_f32(m.ray, fu, cu, fv, cv, h8, w8, stream), "build_ray8")))
         return st;
-    if ((e = copy(m.hx, a.hidden, kHidden)) != hipSuccess ||
-        (e = copy(m.hx + (size_t)kHidden * hw, a.feature, kFeature)) != hipSuccess ||
+    // (h itself is not copied: the first iteration reads the decoder's
+    // hidden state, and its update writes h_new into hx)
+    if ((e = copy(m.hx + (size_t)kHidden * hw, a.feature, kFeature)) != hipSuccess ||
         (e = copy(m.hin + (size_t)kHidden * hw, uv, 2)) != hipSuccess ||
         (e = copy(m.pred[0], a.normal, 3)) != hipSuccess)
         return hip_fail(e, "hipMemcpyAsync");
@@ -768,12 +769,14 @@ int bvml_refine::forward_maps(bvml_dsine_refiner* r, const Maps& m, const Forwar
         const int nh = last ? kHeads : kHeads - 1;
         // ConvGRU (:138-159): the two 5x5 convolutions over h (r*h) plus
         // their parts over [feature | uv], with the gates and the update in
-        // their epilogues; h_new overwrites h in hx and is copied into hin
-        if ((st = ck(bvml_dsine_conv_gru_gates_sum_f32(m.hx, kHidden, h8, w8, r->w_zr_h, C, cf_zr,
-                                                       r->b_z, r->b_r, m.hx, m.z, m.rh, stream),
+        // their epilogues; h_new goes to hx (over h after the first
+        // iteration, which reads the decoder's hidden state) and into hin
+        const float* h = it == 0 ? a.hidden : m.hx;
+        if ((st = ck(bvml_dsine_conv_gru_gates_sum_f32(h, kHidden, h8, w8, r->w_zr_h, C, cf_zr,
+                                                       r->b_z, r->b_r, h, m.z, m.rh, stream),
                      "conv_gru_gates")) ||
             (st = ck(bvml_dsine_conv_gru_update_sum_f32(m.rh, kHidden, h8, w8, r->w_q_h, C, cf_q,
-                                                        r->b_q, m.z, m.hx, m.hx, m.hin, stream),
+                                                        r->b_q, m.z, h, m.hx, m.hin, stream),
                      "conv_gru_update")))
             return st;
         // the heads (:119-127, :257-267, :276): in the first four iterations
