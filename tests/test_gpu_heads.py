@@ -236,3 +236,50 @@ def test_conv_heads_rejects(cuda):
     assert f(0, 66, 4, 4, p, p, p, p, [p], [0], [25], [p]) == _lib.ENULL
     assert f(p, 66, -1, 4, p, p, p, p, [p], [0], [25], [p]) == _lib.ESHAPE
     assert f(p, 66, 8193, 8193, p, p, p, p, [p], [0], [25], [p]) == _lib.ESIZE
+
+
+def test_conv_heads_nan_pattern(cuda):
+    """A NaN in the 3x3 layer's input reaches exactly the outputs of the
+    pixels whose 3x3 window holds it, in the fused and the unfused path
+    alike; every other output of the two paths agrees."""
+    import torch
+    H, W, outs, cin = 20, 24, (25, 50, 25), 66
+    nh = len(outs)
+    rng = np.random.default_rng(5)
+    x = rng.standard_normal((cin, H, W)).astype(np.float32)
+    x[7, 9, 13] = np.nan
+    w3 = rng.uniform(-1, 1, (64 * nh, cin, 3, 3)).astype(np.float32) / np.sqrt(cin * 9)
+    b0 = rng.uniform(-0.5, 0.5, 64 * nh).astype(np.float32)
+    w2 = rng.uniform(-1 / 8, 1 / 8, (nh, 64, 64)).astype(np.float32)
+    b2 = rng.uniform(-1 / 8, 1 / 8, 64 * nh).astype(np.float32)
+    w4s = [rng.uniform(-1 / 8, 1 / 8, (n, 64)).astype(np.float32) for n in outs]
+    b4s = [rng.uniform(-1 / 8, 1 / 8, n).astype(np.float32) for n in outs]
+    w2p, w4p = _lib.heads_pack_f32(w2, w4s)
+    dev = torch.device(cuda)
+    T = lambda a: torch.from_numpy(np.ascontiguousarray(a)).to(dev)  # noqa: E731
+    xd, w3d = T(x), T(_lib.conv_pack_f32(w3))
+    b0d, b2d, w2pd, w2qd = T(b0), T(b2), T(w2p), T(_lib.heads_w2q_f32(w2))
+    w4pd = [T(w) for w in w4p]
+    b4d = [T(b) for b in b4s]
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    fused = [torch.empty(n * H * W, device=dev) for n in outs]
+    assert _lib.conv_heads_f32(xd.data_ptr(), cin, H, W, w3d.data_ptr(), b0d.data_ptr(),
+                               w2qd.data_ptr(), b2d.data_ptr(), [w.data_ptr() for w in w4pd],
+                               [b.data_ptr() for b in b4d], list(outs),
+                               [o.data_ptr() for o in fused], stream) == _lib.OK
+    t0 = torch.empty(64 * nh * H * W, device=dev)
+    assert _lib.load().bvml_dsine_conv_f32(xd.data_ptr(), cin, H, W, w3d.data_ptr(), 64 * nh, 3,
+                                           t0.data_ptr(), stream) == _lib.OK
+    unf = [torch.empty(n * H * W, device=dev) for n in outs]
+    assert _lib.heads_mlp_f32(t0.data_ptr(), b0d.data_ptr(), w2pd.data_ptr(), b2d.data_ptr(),
+                              [w.data_ptr() for w in w4pd], [b.data_ptr() for b in b4d],
+                              list(outs), H, W, [u.data_ptr() for u in unf], stream) == _lib.OK
+    torch.cuda.synchronize()
+    window = np.zeros((H, W), bool)
+    window[8:11, 12:15] = True
+    for h, n in enumerate(outs):
+        f = fused[h].cpu().numpy().reshape(n, H, W)
+        u = unf[h].cpu().numpy().reshape(n, H, W)
+        assert np.isnan(f[:, window]).all() and np.isnan(u[:, window]).all()
+        assert np.isfinite(f[:, ~window]).all()
+        assert np.abs(f[:, ~window] - u[:, ~window]).max() <= 1e-5
