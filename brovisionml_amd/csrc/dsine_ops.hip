@@ -1008,8 +1008,14 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
                 double ox, oy, oz, pinv;
                 if constexpr (TIER == 2) {
                     const double rxd = frx, ryd = fry, rzd = frz;
-                    const double ird =
-                        1.0 / smax(sqrt(fma(rxd, rxd, fma(ryd, ryd, rzd * rzd))), 1e-8);
+                    // 1 / max(|r|, 1e-8) from the reciprocal square root
+                    // (two Newton steps) rather than a square root and a
+                    // division, whose long sequences sit on the flagged
+                    // group's path (256 x 256 at k = 5: 8.34 against 8.47 us
+                    // per call, same bits); |r|^2 of float components stays
+                    // finite in double, and NaN rays go to tier 3 below
+                    const double r2d = fma(rxd, rxd, fma(ryd, ryd, rzd * rzd));
+                    const double ird = (r2d < 1e-16) ? 1e8 : rsq64(r2d);
                     if (!nbr_red_f64(mx, my, mz, fsx, fsy, xsv, ysv, thv, wv, rxd, ryd, rzd, ird,
                                      a, ox, oy, oz, pinv)) {
                         q2 = __builtin_nan("");
