@@ -526,10 +526,13 @@ __host__ __device__ constexpr int lookahead(int K, int G) {
 
 // Neighbours whose planes a wave loads before the halo staging and its
 // barrier; the rest are loaded after it.
-// Measured best: 1 at k <= 5; at k >= 7 all of the lookahead (7), which
-// overlaps the halo's staging with the first neighbours' loads; 3 with G = 1.
+// Measured best: at k <= 5, 1 with G = 2 or 4 and 2 with G = 8 (the small
+// launches, latency-bound: 60 x 80 4.03 against 4.14 us cold, 128 x 128
+// 4.04-4.06 against 4.08-4.09; 3 or 4 slower); at k >= 7 all of the
+// lookahead (7), which overlaps the halo's staging with the first
+// neighbours' loads; 3 with G = 1.
 __host__ __device__ constexpr int preloads(int K, int G) {
-    return G == 1 ? 3 : (K <= 5 ? 1 : 7);
+    return G == 1 ? 3 : (K <= 5 ? (G == 8 ? 2 : 1) : 7);
 }
 
 // Source-normal halo records of a TW x TH tile.
@@ -703,7 +706,7 @@ void angmf_f32_kernel(const float* __restrict__ pred_norm, const float* __restri
     // addresses and discard the result).
     // Loads in consumption order: ray, then per neighbour its 4 planes, at
     // most LA neighbours ahead of the one being evaluated; the planes of the
-    // first kPreLoads neighbours go out before the staging.  Vector loads
+    // first PRE neighbours go out before the staging.  Vector loads
     // complete in issue order, so the loop consumes them one neighbour at a
     // time: a scheduling barrier after each neighbour's loads keeps them in
     // that order, and the loop's register fences keep the compiler from
