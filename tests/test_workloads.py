@@ -76,3 +76,19 @@ def test_make_sample_distributions():
     assert (zn > 0).all()
     # deterministic
     assert np.array_equal(wl.make_sample(wl.WORKLOADS[0])["xy"], wl.make_sample(wl.WORKLOADS[0])["xy"])
+
+
+def test_every_workload_finds_its_traffic_profile():
+    # the bench line's roofline.traffic comes from the committed rocprofv3
+    # summary whose workload field names the workload exactly
+    import os
+    import sys
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    import bench
+    for w in wl.WORKLOADS:
+        t = bench.traffic_from_profile("angmf", w.name)
+        assert t is not None, w.name
+        algo = w.algorithmic_bytes(shared_ray=True) // w.calls
+        assert algo <= t <= 1.2 * algo, (w.name, t, algo)
+    up = bench.traffic_from_profile("upsample", "dsine-upsample-256x256-s8")
+    assert up is not None
