@@ -423,20 +423,31 @@ __attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : 1))) void conv
         // Each step's 4 weights are loaded one step ahead of its products
         // from buffer descriptors (a scheduling barrier keeps them there and
         // keeps the compiler from hoisting every weight load at once, and
-        // the descriptors keep 64-bit addresses out of the registers): 141
+        // the descriptors keep 64-bit addresses out of the registers): 162
         // VGPRs, three workgroups per CU.  (256 x 256, 3 heads: 172 us
-        // against 182 for the 3x3 layer and bvml_dsine_heads_mlp_f32; two
-        // tile rows per pass, 173-174.)
+        // against 182 for the 3x3 layer and bvml_dsine_heads_mlp_f32, 166
+        // with the loads below issued ahead; two tile rows per pass,
+        // 173-174.)
         {
+            // the loads the epilogue's first steps wait on go out together:
+            // b0, then the middle layer's first weights
+            float b0v[4][4];
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) b0v[m][r] = ldo(b0, gb + 4u * (16 * m + r));
+            float cw[2][4];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) cw[0][r] = ldw(w2, lb, 256u * r);
+            __builtin_amdgcn_sched_barrier(0);
             // a = relu(acc + b0), in place
 #pragma unroll
             for (int m = 0; m < 4; ++m)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float bias = ldo(b0, gb + 4u * (16 * m + r));
 #pragma unroll
                     for (int j = 0; j < NB; ++j)
-                        acc[m][j][r] = relu(acc[m][j][r] + bias);
+                        acc[m][j][r] = relu(acc[m][j][r] + b0v[m][r]);
                 }
             // t = W2 a: output block mo, step (m, r) takes channels {16 m + 4 g + r}
             v4f t[4][NB];
@@ -444,15 +455,34 @@ __attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : 1))) void conv
             for (int mo = 0; mo < 4; ++mo)
 #pragma unroll
                 for (int j = 0; j < NB; ++j) t[mo][j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-            float cw[2][4];
-#pragma unroll
-            for (int r = 0; r < 4; ++r) cw[0][r] = ldw(w2, lb, 256u * r);
+            // b2 and the last layer's first weights and biases, loaded during
+            // the middle layer's products (at steps 8 and 12), so that no
+            // step waits on a load of its own: with each of them loaded where
+            // it is used, every workgroup of the launch stalled on the same
+            // round trips at once (256 x 256, 3 heads: 171 against 166 us,
+            // same bits)
+            float b2v[4][4], cw4[2][4], b4cur[4], b4nxt[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
             for (int st = 0; st < 16; ++st) {  // st = 4 mo + m
                 if (st + 1 < 16) {
 #pragma unroll
                     for (int r = 0; r < 4; ++r)
                         cw[(st + 1) & 1][r] = ldw(w2, lb, 256u * ((st + 1) * 4 + r));
+                }
+                if (st == 8) {
+#pragma unroll
+                    for (int mo = 0; mo < 4; ++mo)
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) b2v[mo][r] = ldo(b2, gb + 4u * (16 * mo + r));
+                }
+                if (st == 12) {
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) cw4[0][r] = ldw(w4, lb, 256u * r);
+#pragma unroll
+                    for (int r = 0; r < 4; ++r) {
+                        const int oc = 4 * g + r;
+                        b4cur[r] = (b4 && oc < nout) ? ldo(b4, 4u * oc) : 0.0f;
+                    }
                 }
                 __builtin_amdgcn_sched_barrier(0);
                 const int mo = st / 4, m = st % 4;
@@ -468,25 +498,30 @@ __attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : 1))) void conv
             for (int mo = 0; mo < 4; ++mo)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
-                    const float bias = ldo(b2, gb + 4u * (16 * mo + r));
 #pragma unroll
-                    for (int j = 0; j < NB; ++j) t[mo][j][r] = relu(t[mo][j][r] + bias);
+                    for (int j = 0; j < NB; ++j) t[mo][j][r] = relu(t[mo][j][r] + b2v[mo][r]);
                 }
-            // out = W4 t + b4, 16 outputs at a time
+            // out = W4 t + b4, 16 outputs at a time; the next block's first
+            // weights and biases load during this block's last step
             for (int ob = 0; ob < nob; ++ob) {
                 const uint32_t wb = 4096u * ob;
                 v4f o[NB];
 #pragma unroll
                 for (int j = 0; j < NB; ++j) o[j] = v4f{0.0f, 0.0f, 0.0f, 0.0f};
-                float cw4[2][4];
-#pragma unroll
-                for (int r = 0; r < 4; ++r) cw4[0][r] = ldw(w4, lb, wb + 256u * r);
 #pragma unroll
                 for (int mo = 0; mo < 4; ++mo) {
                     if (mo + 1 < 4) {
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
                             cw4[(mo + 1) & 1][r] = ldw(w4, lb, wb + 256u * ((mo + 1) * 4 + r));
+                    } else if (ob + 1 < nob) {
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) cw4[0][r] = ldw(w4, lb, wb + 4096u + 256u * r);
+#pragma unroll
+                        for (int r = 0; r < 4; ++r) {
+                            const int oc = 16 * (ob + 1) + 4 * g + r;
+                            b4nxt[r] = (b4 && oc < nout) ? ldo(b4, 4u * oc) : 0.0f;
+                        }
                     }
                     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
@@ -496,12 +531,11 @@ __attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : 1))) void conv
                             o[j] = __builtin_amdgcn_mfma_f32_16x16x4f32(cw4[mo & 1][r], t[mo][j][r],
                                                                         o[j], 0, 0, 0);
                 }
-                if (x >= a.W) continue;
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                     const int oc = 16 * ob + 4 * g + r;
-                    if (oc >= nout) continue;
-                    const float bias = b4 ? ldo(b4, 4u * oc) : 0.0f;
+                    if (x >= a.W || oc >= nout) continue;
+                    const float bias = b4cur[r];
                     // plane 16 ob + r from a uniform base, plus this lane's
                     // 4 g planes and pixel as a 32-bit byte offset (the map is
                     // at most 2^26 pixels)
@@ -515,6 +549,8 @@ __attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : 1))) void conv
                             b4 ? o[j][r] + bias : o[j][r];
                     }
                 }
+#pragma unroll
+                for (int r = 0; r < 4; ++r) b4cur[r] = b4nxt[r];
             }
         }
         return;
