@@ -118,9 +118,12 @@ constexpr bool stage_weights(int K, int WM) { return K == 3 && WM == 1; }
 
 template <int K, int TH, int WM, int WN, int EPI, int KS>
 // (the fused heads launch holds three 4-wave workgroups per CU, one wave
-// per SIMD each, so its registers stay within a third of a SIMD's)
+// per SIMD each, so its registers stay within a third of a SIMD's; convq
+// with one wave group, on maps of two or more workgroups per CU, within
+// half, where its epilogue's loads, all issued before its stores, would
+// otherwise take more)
 __global__ __launch_bounds__(kThreads * KS)
-__attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : 1))) void conv_kernel(ConvArgs a) {
+__attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : (EPI == kUpdate && KS == 1 ? 2 : 1)))) void conv_kernel(ConvArgs a) {
     constexpr int P = K / 2;
     constexpr int HR = TH + K - 1, HC = kTW + K - 1, HS = HR * HC;  // halo rows, cols, size
     constexpr int HALO = kCC * HS;                                   // floats per chunk
@@ -556,12 +559,12 @@ __attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : 1))) void conv
         return;
     }
     if (x >= a.W) return;
+    if constexpr (EPI == kPlain) {
 #pragma unroll
-    for (int n = 0; n < NB; ++n) {
-        const int y = ty0 + wn * NB + n;
-        if (n < n_lo || n >= n_hi || y >= a.H) continue;
-        const size_t px = (size_t)y * a.W + x;
-        if constexpr (EPI == kPlain) {
+        for (int n = 0; n < NB; ++n) {
+            const int y = ty0 + wn * NB + n;
+            if (n < n_lo || n >= n_hi || y >= a.H) continue;
+            const size_t px = (size_t)y * a.W + x;
 #pragma unroll
             for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -569,23 +572,91 @@ __attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : 1))) void conv
                     const int o = 16 * (mb0 + m) + 4 * g + r;
                     if (o < a.cout) a.out[(size_t)o * a.HW + px] = acc[m][n][r];
                 }
-        } else if constexpr (EPI == kGates) {
-            // M-blocks alternate z, r: block 2i holds z channels 16i.., 2i + 1
-            // the r channels 16i.. (mb0 is a multiple of 4, so m = 0, 2 are z)
+        }
+        return;
+    }
+    // The ConvGRU epilogues read the biases and the maps h (and z) and store
+    // the gates (the new state).  Every load goes out before the first
+    // store: the outputs may not overlap the inputs (the entry points refuse
+    // that), but the compiler cannot know it, and with each element's loads
+    // after the previous element's stores a wave waited one round trip per
+    // element, every workgroup at once (convz + convr over h at 256 x 256:
+    // a 30 us epilogue of 64 such elements per lane).
+    if constexpr (EPI == kGates) {
+        // M-blocks alternate z, r: block 2i holds z channels 16i.., 2i + 1
+        // the r channels 16i.. (mb0 is a multiple of 4, so m = 0, 2 are z)
+        float bz[2][4], br[2][4], hv[NB][2][4];
 #pragma unroll
-            for (int m = 0; m < 4; m += 2)
+        for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int c = 16 * ((mb0 + 2 * mm) / 2) + 4 * g + r;
+                const bool ok = c < a.cout / 2;
+                bz[mm][r] = ok ? a.b0[c] : 0.0f;
+                br[mm][r] = ok ? a.b1[c] : 0.0f;
+            }
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            const int y = ty0 + wn * NB + n;
+            const bool row = n >= n_lo && n < n_hi && y < a.H;
+            const size_t px = row ? (size_t)y * a.W + x : 0;
+#pragma unroll
+            for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
+                    const int c = 16 * ((mb0 + 2 * mm) / 2) + 4 * g + r;
+                    hv[n][mm][r] = (row && c < a.cout / 2) ? a.h[(size_t)c * a.HW + px] : 0.0f;
+                }
+        }
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            const int y = ty0 + wn * NB + n;
+            if (n < n_lo || n >= n_hi || y >= a.H) continue;
+            const size_t px = (size_t)y * a.W + x;
+#pragma unroll
+            for (int mm = 0; mm < 2; ++mm)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int m = 2 * mm;
                     const int c = 16 * ((mb0 + m) / 2) + 4 * g + r;
                     if (c >= a.cout / 2) continue;
                     const size_t i = (size_t)c * a.HW + px;
-                    float sz = acc[m][n][r], sr = acc[m + 1][n][r];
-                    const float zz = sigmoid(sz + a.b0[c]);
-                    const float rr = sigmoid(sr + a.b1[c]);
+                    const float zz = sigmoid(acc[m][n][r] + bz[mm][r]);
+                    const float rr = sigmoid(acc[m + 1][n][r] + br[mm][r]);
                     a.o0[i] = zz;
-                    a.o1[i] = rr * a.h[i];
+                    a.o1[i] = rr * hv[n][mm][r];
                 }
-        } else {
+        }
+    } else {
+        float bq[4][4], zv[NB][4][4], hv[NB][4][4];
+#pragma unroll
+        for (int m = 0; m < 4; ++m)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+                const int c = 16 * (mb0 + m) + 4 * g + r;
+                bq[m][r] = c < a.cout ? a.b0[c] : 0.0f;
+            }
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            const int y = ty0 + wn * NB + n;
+            const bool row = n >= n_lo && n < n_hi && y < a.H;
+            const size_t px = row ? (size_t)y * a.W + x : 0;
+#pragma unroll
+            for (int m = 0; m < 4; ++m)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                    const int c = 16 * (mb0 + m) + 4 * g + r;
+                    const bool ok = row && c < a.cout;
+                    const size_t i = (size_t)c * a.HW + px;
+                    zv[n][m][r] = ok ? a.z[i] : 0.0f;
+                    hv[n][m][r] = ok ? a.h[i] : 0.0f;
+                }
+        }
+#pragma unroll
+        for (int n = 0; n < NB; ++n) {
+            const int y = ty0 + wn * NB + n;
+            if (n < n_lo || n >= n_hi || y >= a.H) continue;
+            const size_t px = (size_t)y * a.W + x;
 #pragma unroll
             for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -593,8 +664,7 @@ __attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : 1))) void conv
                     const int c = 16 * (mb0 + m) + 4 * g + r;
                     if (c >= a.cout) continue;
                     const size_t i = (size_t)c * a.HW + px;
-                    float sq = acc[m][n][r];
-                    const float v = gru_mix(a.z[i], a.h[i], tanhf(sq + a.b0[c]));
+                    const float v = gru_mix(zv[n][m][r], hv[n][m][r], tanhf(acc[m][n][r] + bq[m][r]));
                     a.o0[i] = v;
                     if (a.o1) a.o1[i] = v;
                 }
