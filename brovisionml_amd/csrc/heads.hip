@@ -90,7 +90,13 @@ __device__ __forceinline__ void load_head_inputs(const HeadsArgs& a, int h, int 
         const int c = kHid * h + 4 * j + g;
         const float* tc = a.t0 + (size_t)c * a.HW;
 #pragma unroll
-        for (int nb = 0; nb < 2; ++nb) bf[j][nb] = in[nb] ? tc[p[nb]] : 0.0f;
+        for (int nb = 0; nb < 2; ++nb) {
+            // every lane loads (a pixel past the map reads pixel 0; its
+            // value is masked where it is used): with the loads under
+            // branches, or zeroed here, the compiler waited for all of them,
+            // the next head's included, before the current head's products
+            bf[j][nb] = tc[in[nb] ? p[nb] : 0];
+        }
     }
 }
 
@@ -196,7 +202,11 @@ __global__ __launch_bounds__(kWaves * 64) void heads_mlp_kernel(HeadsArgs a) {
     for (int h = 0; h < kMaxHeads; ++h) {
         if (h >= a.nheads) break;
         float next[16][2];
-        if (h + 1 < a.nheads) load_head_inputs(a, h + 1, g, p, in, next);
+        // the next head's inputs (the last head re-reads its own, unused:
+        // loads under a branch would leave the compiler unable to count them,
+        // and it would wait for all of them before this head's products)
+        load_head_inputs(a, h + 1 < a.nheads ? h + 1 : h, g, p, in, next);
+        __builtin_amdgcn_sched_barrier(0);
         // middle layer: acc[mb][nb] = W2 (rows 16 mb..) x relu(t0 + b0) (pixels of nb)
         v4f acc[4][2];
 #pragma unroll
@@ -246,8 +256,18 @@ __global__ __launch_bounds__(kWaves * 64) void heads_mlp_kernel(HeadsArgs a) {
                 const int cb = nob - c0 < kChunkOb ? nob - c0 : kChunkOb;
                 const float* src = a.w4p[h] + (size_t)c0 * 16 * 64;
                 __syncthreads();
+                // direct-to-LDS loads, 1 KB per wave-wide load (lane l's 16 bytes
+                // at the wave's base + 16 l), all in flight at once; a chunk is a
+                // whole number of 256-float runs, so each wave's loads are
+                // all-lane (a copy through registers waited one round trip per
+                // 8 KB, every wave at once)
                 for (int i = threadIdx.x * 4; i < cb * 16 * 64; i += kWaves * 64 * 4)
-                    *reinterpret_cast<float4*>(chunk + i) = *reinterpret_cast<const float4*>(src + i);
+                    __builtin_amdgcn_global_load_lds(
+                        static_cast<const void*>(src + i),
+                        reinterpret_cast<__attribute__((address_space(3))) void*>(
+                            reinterpret_cast<uintptr_t>(chunk + (i - 4 * lane))),
+                        16, 0, 0);
+                __builtin_amdgcn_s_waitcnt(0);
                 __syncthreads();
                 const int n = a.outs[h] - 16 * c0 < 16 * cb ? a.outs[h] - 16 * c0 : 16 * cb;
                 const float* b4 = a.b4[h] ? a.b4[h] + 16 * c0 : nullptr;
