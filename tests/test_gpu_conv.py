@@ -75,7 +75,9 @@ def _sig(v):
     return 1.0 / (1.0 + np.exp(-v))
 
 
-@pytest.mark.parametrize("H,W", [(24, 32), (13, 19), (64, 64)])
+# (256 x 520: 528 tiles, so convq runs with one wave group, the launch for
+# maps of two or more workgroups per CU)
+@pytest.mark.parametrize("H,W", [(24, 32), (13, 19), (64, 64), (256, 520)])
 def test_conv_gru(cuda, H, W):
     """The fused gates (convz + convr) and update (convq) against the float64
     restatement of src/dsine_refine.cpp:145-157."""
