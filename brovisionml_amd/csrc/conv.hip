@@ -422,6 +422,11 @@ __attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : (EPI == kUpdat
         const __amdgpu_buffer_rsrc_t w4 = weights_rsrc(a.w4p[h], 4096u * nob);
         const uint32_t lb = 4u * lane, gb = 16u * g;  // this lane's byte offsets
         const float* b4 = a.b4[h];
+        // (the biases' loads are unconditional, from the weights when there is
+        // no bias, at a clamped index, and masked where used: under a branch
+        // the compiler could not count them, and the products waited for the
+        // next block's weights with them)
+        const float* b4s = b4 ? b4 : a.w4p[h];
         float* out = a.hout[h];
         // Each step's 4 weights are loaded one step ahead of its products
         // from buffer descriptors (a scheduling barrier keeps them there and
@@ -484,7 +489,7 @@ __attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : (EPI == kUpdat
 #pragma unroll
                     for (int r = 0; r < 4; ++r) {
                         const int oc = 4 * g + r;
-                        b4cur[r] = (b4 && oc < nout) ? ldo(b4, 4u * oc) : 0.0f;
+                        b4cur[r] = ldo(b4s, 4u * (uint32_t)(oc < nout ? oc : nout - 1));
                     }
                 }
                 __builtin_amdgcn_sched_barrier(0);
@@ -517,13 +522,18 @@ __attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : (EPI == kUpdat
 #pragma unroll
                         for (int r = 0; r < 4; ++r)
                             cw4[(mo + 1) & 1][r] = ldw(w4, lb, wb + 256u * ((mo + 1) * 4 + r));
-                    } else if (ob + 1 < nob) {
+                    } else {
+                        // (the last block loads its own again, unused: under a
+                        // branch these loads would leave the compiler waiting
+                        // for them before this step's products)
+                        const int nx = ob + 1 < nob ? ob + 1 : ob;
 #pragma unroll
-                        for (int r = 0; r < 4; ++r) cw4[0][r] = ldw(w4, lb, wb + 4096u + 256u * r);
+                        for (int r = 0; r < 4; ++r)
+                            cw4[0][r] = ldw(w4, lb, 4096u * (uint32_t)nx + 256u * r);
 #pragma unroll
                         for (int r = 0; r < 4; ++r) {
-                            const int oc = 16 * (ob + 1) + 4 * g + r;
-                            b4nxt[r] = (b4 && oc < nout) ? ldo(b4, 4u * oc) : 0.0f;
+                            const int oc = 16 * nx + 4 * g + r;
+                            b4nxt[r] = ldo(b4s, 4u * (uint32_t)(oc < nout ? oc : nout - 1));
                         }
                     }
                     __builtin_amdgcn_sched_barrier(0);
@@ -608,6 +618,9 @@ __attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : (EPI == kUpdat
                     hv[n][mm][r] = (row && c < a.cout / 2) ? a.h[(size_t)c * a.HW + px] : 0.0f;
                 }
         }
+        // (all of them here: a use after some of the stores below would wait
+        // for those stores too, the loads being conditional)
+        __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
         for (int n = 0; n < NB; ++n) {
             const int y = ty0 + wn * NB + n;
@@ -652,6 +665,7 @@ __attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : (EPI == kUpdat
                     hv[n][m][r] = ok ? a.h[i] : 0.0f;
                 }
         }
+        __builtin_amdgcn_s_waitcnt(0);
 #pragma unroll
         for (int n = 0; n < NB; ++n) {
             const int y = ty0 + wn * NB + n;
