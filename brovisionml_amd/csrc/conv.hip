@@ -600,10 +600,12 @@ __attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : (EPI == kUpdat
         for (int mm = 0; mm < 2; ++mm)
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
+                // (a clamped index, no branch: a load under a per-lane
+                // condition made the next one wait for everything before it)
                 const int c = 16 * ((mb0 + 2 * mm) / 2) + 4 * g + r;
-                const bool ok = c < a.cout / 2;
-                bz[mm][r] = ok ? a.b0[c] : 0.0f;
-                br[mm][r] = ok ? a.b1[c] : 0.0f;
+                const int cc = c < a.cout / 2 ? c : a.cout / 2 - 1;
+                bz[mm][r] = a.b0[cc];
+                br[mm][r] = a.b1[cc];
             }
 #pragma unroll
         for (int n = 0; n < NB; ++n) {
@@ -647,7 +649,7 @@ __attribute__((amdgpu_waves_per_eu(EPI == kHeads && KS == 1 ? 3 : (EPI == kUpdat
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
                 const int c = 16 * (mb0 + m) + 4 * g + r;
-                bq[m][r] = c < a.cout ? a.b0[c] : 0.0f;
+                bq[m][r] = a.b0[c < a.cout ? c : a.cout - 1];
             }
 #pragma unroll
         for (int n = 0; n < NB; ++n) {
